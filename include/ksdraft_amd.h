@@ -1,0 +1,119 @@
+/*
+ * ksdraft_amd.h — C ABI of libksdraft_amd.so, the MI355X (gfx950) kernels behind
+ * KSDraft's INT8 tier (the reference's ksdraft/kernels package).
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are device pointers (HBM) unless stated otherwise. The library
+ *     allocates nothing: callers own inputs and outputs.
+ *   - `stream` is a hipStream_t passed as void*; work is enqueued on it and the call
+ *     returns without synchronising.
+ *   - Tensors are dense row-major. int8 codes, fp16 scales (passed as uint16_t bit
+ *     patterns), fp32 accumulators.
+ *   - Return value: KSD_OK (0) or an error class. The message of the last error on the
+ *     calling thread is copied out by ksd_last_error(). Calls keep no global mutable
+ *     state besides that thread-local message, so they are reentrant.
+ *   - "group" is the quantisation group size along the quantised axis; 32, 64 and
+ *     128 are supported (128 is the KSDraft default, GROUP_SIZE in
+ *     reference ksdraft/kernels/quant.py:20).
+ */
+#ifndef KSDRAFT_AMD_H
+#define KSDRAFT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes (mapped to Python exception classes by the host wrapper) */
+#define KSD_OK 0
+#define KSD_EINVAL 1   /* ValueError: shape / group / argument mismatch */
+#define KSD_ETYPE 2    /* TypeError: unsupported dtype                  */
+#define KSD_EHIP 3     /* RuntimeError: HIP launch / runtime failure     */
+
+/* element types for typed float buffers */
+#define KSD_F32 0
+#define KSD_BF16 1
+#define KSD_F16 2
+#define KSD_F16_SAT 3  /* output only: fp16 rounded then clamped to +-65504 */
+
+/* ABI version, bumped on any signature change. */
+int ksd_abi_version(void);
+
+/* Copies the calling thread's last error message (NUL-terminated) into buf. */
+int ksd_last_error(char *buf, size_t len);
+
+/*
+ * Q1 / Q3 — quantize along the last dim.
+ * Replaces quantize_last_dim (reference ksdraft/kernels/quant.py:30-52) and, with
+ * noise != NULL, quantize_last_dim_dithered (reference ksdraft/train/stages.py:27-50).
+ *   x       (rows, K) of type x_dtype, row stride x_stride elements
+ *   codes   (rows, K) int8, dense
+ *   scales  (rows, ceil(K/group)) fp16
+ *   noise   NULL, or (rows, ceil(K/group)*group) fp32 uniform [0,1) draws (torch.rand of
+ *           the padded grouped shape); code_value += (noise - 0.5) * dither2 before rounding,
+ *           dither2 = fp32(2 * dither).
+ */
+int ksd_quantize_lastdim(const void *x, int x_dtype, int64_t rows, int64_t K,
+                         int64_t x_stride, int group, int8_t *codes, uint16_t *scales,
+                         const float *noise, float dither2, void *stream);
+
+/*
+ * Q2 — dequantize along the last dim: out = float(code) * float(scale) per group.
+ * Replaces dequantize_last_dim (reference ksdraft/kernels/quant.py:55-67).
+ *   codes (rows, K) int8; scales (rows, n_scales) fp16; out (rows, K) fp32.
+ *   group is already resolved by the caller (the reference's group=None inference).
+ */
+int ksd_dequantize_lastdim(const int8_t *codes, const uint16_t *scales, int64_t rows,
+                           int64_t K, int64_t n_scales, int group, float *out,
+                           void *stream);
+
+/*
+ * Transposed quantization: quantize_last_dim(x.t().contiguous(), group) without the
+ * transpose copy. Used for the dW operands (reference ksdraft/kernels/ks3_int8.py:418,422).
+ *   x       (R, C) of type x_dtype, dense
+ *   codes   (C, R) int8; scales (C, ceil(R/group)) fp16
+ */
+int ksd_quantize_transpose(const void *x, int x_dtype, int64_t R, int64_t C, int group,
+                           int8_t *codes, uint16_t *scales, void *stream);
+
+/*
+ * Requant-transpose: quantize_last_dim(dequantize_last_dim(codes, scales).t(), group).
+ * Replaces the dequantize -> transpose -> requantize operand builds of
+ * reference ksdraft/kernels/ks3_int8.py:349-351, 407-408, 417-419, 423.
+ *   codes (R, C) int8 with scales (R, ceil(C/group_in)) fp16
+ *   out_codes (C, R) int8; out_scales (C, ceil(R/group)) fp16
+ */
+int ksd_requant_transpose(const int8_t *codes, const uint16_t *scales, int64_t R,
+                          int64_t C, int group_in, int group, int8_t *out_codes,
+                          uint16_t *out_scales, void *stream);
+
+/*
+ * G1 / G2 — W8A8 GEMM, "NT" layout: Y = dequant(A) . dequant(W)^T with the ordered
+ * per-group contract
+ *     acc = 0;  for g in 0..K/group-1:  acc = fmaf(float(P_g), sa[m,g]*sw[n,g], acc)
+ * where P_g = sum_{k in g} A[m,k]*W[n,k] is exact int32 and sa*sw is exact in fp32.
+ * Replaces _w8a8_gemm_kernel / w8a8_gemm (reference ksdraft/kernels/gemm.py:18-50, 53-90).
+ *   a (M, K) int8, a_scales (M, K/group) fp16; w (N, K) int8, w_scales (N, K/group)
+ *   K must be a multiple of 128 (the host wrapper zero-pads like gemm.py:71-73).
+ *   bias    NULL or (N,) fp32, added in fp32 after the group sum (linear.py:71-72)
+ *   y       (M, N) of type y_dtype (KSD_F32, KSD_BF16, KSD_F16, KSD_F16_SAT)
+ */
+int ksd_w8a8_gemm_nt(const int8_t *a, const uint16_t *a_scales, const int8_t *w,
+                     const uint16_t *w_scales, int64_t M, int64_t N, int64_t K, int group,
+                     const float *bias, void *y, int y_dtype, void *stream);
+
+/*
+ * Test-only export of the exact int32 group partials P_g of the GEMM above
+ * (the tl.dot result of reference ksdraft/kernels/gemm.py:42).
+ *   partials (K/group, M, N) int32
+ */
+int ksd_w8a8_group_partials(const int8_t *a, const int8_t *w, int64_t M, int64_t N,
+                            int64_t K, int group, int32_t *partials, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KSDRAFT_AMD_H */

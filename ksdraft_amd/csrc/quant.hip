@@ -1,0 +1,264 @@
+// GS symmetric int8 quantization kernels for gfx950.
+//
+// Contract (reference ksdraft/kernels/quant.py:30-52): per row, per `group`-wide slice
+// of the last dim, amax -> scale = fp16(clamp(amax/127, 2^-24, 65504)) -> code =
+// clamp(rne(x/scale), -127, 127). A partial last group is zero-padded for the amax and
+// its padded lanes are not stored. These kernels are HBM-streaming: coalesced 16-byte
+// loads, wave shuffles for the group amax, no LDS for the row-wise form.
+#include "ksd_common.h"
+
+namespace ksd {
+
+// ----------------------------------------------------------------------------------
+// Row-wise quantization: one group is owned by G/8 consecutive lanes, 8 elements each.
+template <int DT, int G, bool VEC>
+__global__ __launch_bounds__(256) void quant_rows_kernel(
+    const void *__restrict__ xv, int64_t rows, int64_t K, int64_t stride, int64_t ngroups,
+    int8_t *__restrict__ codes, uint16_t *__restrict__ scales,
+    const float *__restrict__ noise, float dither2) {
+  using T = typename Elem<DT>::T;
+  constexpr int LPG = G / 8;
+  const T *x = (const T *)xv;
+  const int64_t gid = ((int64_t)blockIdx.x * 256 + threadIdx.x) / LPG;
+  const int sub = threadIdx.x % LPG;
+  const bool active = gid < rows * ngroups;
+  const int64_t row = active ? gid / ngroups : 0;
+  const int64_t grp = active ? gid % ngroups : 0;
+  const int64_t k0 = grp * G + sub * 8;
+  const T *xr = x + row * stride;
+
+  float v[8];
+  const bool full = active && (k0 + 8 <= K);
+  if (VEC && full) {
+    if constexpr (sizeof(T) == 4) {
+      const float4 *p = (const float4 *)(xr + k0);
+      float4 a = p[0], b = p[1];
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+      uint4 a = *(const uint4 *)(xr + k0);
+      const uint16_t *h = (const uint16_t *)&a;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = Elem<DT>::load(h + i);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      v[i] = (active && k0 + i < K) ? Elem<DT>::load(xr + k0 + i) : 0.0f;
+  }
+
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int off = LPG / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  const float s = group_scale(amax);
+
+  int8_t q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float c = v[i] / s;
+    if (noise != nullptr && active) {
+      // stages.py:44-47: codes + (rand - 0.5) * (2*dither), fp32 ops, separately rounded
+      const float r = noise[row * ngroups * G + k0 + i];
+      c = c + (r - 0.5f) * dither2;
+    }
+    q[i] = code_of(c);
+  }
+  if (!active) return;
+  int8_t *cr = codes + row * K;
+  if (VEC && full) {
+    *(uint2 *)(cr + k0) = *(const uint2 *)q;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (k0 + i < K) cr[k0 + i] = q[i];
+  }
+  if (sub == 0) scales[row * ngroups + grp] = f16_bits(s);
+}
+
+// ----------------------------------------------------------------------------------
+// Dequantization: out = float(code) * float(scale), exact in fp32 (quant.py:66).
+__global__ __launch_bounds__(256) void dequant_rows_kernel(
+    const int8_t *__restrict__ codes, const uint16_t *__restrict__ scales, int64_t rows,
+    int64_t K, int64_t nsc, int group, float *__restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows * K) return;
+  const int64_t r = i / K, k = i % K;
+  const int64_t g = k / group;
+  const float s = g < nsc ? f16_to_f32(scales[r * nsc + g]) : 0.0f;
+  out[i] = (float)codes[i] * s;
+}
+
+// ----------------------------------------------------------------------------------
+// Transposed quantization: codes (C, R) = quantize along R of x (R, C). A block owns one
+// G-row group by 64 columns; the tile goes through LDS so both the loads (along C) and
+// the code stores (along R) are contiguous.
+struct LoadF32 {
+  const float *x; int64_t C;
+  __device__ float operator()(int64_t r, int64_t c) const { return x[r * C + c]; }
+};
+struct LoadBF16 {
+  const uint16_t *x; int64_t C;
+  __device__ float operator()(int64_t r, int64_t c) const { return bf16_to_f32(x[r * C + c]); }
+};
+struct LoadF16 {
+  const uint16_t *x; int64_t C;
+  __device__ float operator()(int64_t r, int64_t c) const { return f16_to_f32(x[r * C + c]); }
+};
+// dequantized codes: float(code) * float(scale) (the exact product of quant.py:66)
+struct LoadDequant {
+  const int8_t *q; const uint16_t *s; int64_t C; int64_t nsc; int gin;
+  __device__ float operator()(int64_t r, int64_t c) const {
+    return (float)q[r * C + c] * f16_to_f32(s[r * nsc + c / gin]);
+  }
+};
+
+template <class Loader, int G>
+__global__ __launch_bounds__(256) void quant_T_kernel(Loader ld, int64_t R, int64_t C,
+                                                      int64_t nbc, int64_t ngr,
+                                                      int8_t *__restrict__ codes,
+                                                      uint16_t *__restrict__ scales) {
+  __shared__ float tile[G][65];
+  __shared__ float cmax[4][64];
+  const int64_t bc = blockIdx.x % nbc, br = blockIdx.x / nbc;
+  const int64_t r0 = br * G, c0 = bc * 64;
+  const int c = threadIdx.x & 63, rq = threadIdx.x >> 6;
+  const bool cok = c0 + c < C;
+
+  float m = 0.0f;
+#pragma unroll 4
+  for (int i = 0; i < G / 4; ++i) {
+    const int r = rq + 4 * i;
+    const float v = (cok && r0 + r < R) ? ld(r0 + r, c0 + c) : 0.0f;
+    tile[r][c] = v;
+    m = fmaxf(m, fabsf(v));
+  }
+  cmax[rq][c] = m;
+  __syncthreads();
+  const float amax = fmaxf(fmaxf(cmax[0][c], cmax[1][c]), fmaxf(cmax[2][c], cmax[3][c]));
+  const float s = group_scale(amax);
+  if (!cok) return;
+  if (rq == 0) scales[(c0 + c) * ngr + br] = f16_bits(s);
+
+  constexpr int RPT = G / 4;  // rows (output bytes) per thread
+  int8_t q[RPT];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) q[j] = code_of(tile[rq * RPT + j][c] / s);
+  int8_t *dst = codes + (c0 + c) * R + r0 + rq * RPT;
+  const int64_t rbase = r0 + rq * RPT;
+  if (rbase + RPT <= R && (((uintptr_t)dst) & 7) == 0) {
+#pragma unroll
+    for (int j = 0; j < RPT; j += 8) *(uint2 *)(dst + j) = *(const uint2 *)(q + j);
+  } else {
+#pragma unroll
+    for (int j = 0; j < RPT; ++j)
+      if (rbase + j < R) dst[j] = q[j];
+  }
+}
+
+template <class Loader>
+static int launch_quant_T(Loader ld, int64_t R, int64_t C, int group, int8_t *codes,
+                          uint16_t *scales, hipStream_t st) {
+  const int64_t nbc = cdiv(C, 64), ngr = cdiv(R, group);
+  const int64_t blocks = nbc * ngr;
+  if (blocks > 0x7fffffffLL) return fail(KSD_EINVAL, "quantize_transpose: tensor too large");
+  switch (group) {
+    case 32: quant_T_kernel<Loader, 32><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(ld, R, C, nbc, ngr, codes, scales); break;
+    case 64: quant_T_kernel<Loader, 64><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(ld, R, C, nbc, ngr, codes, scales); break;
+    default: quant_T_kernel<Loader, 128><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(ld, R, C, nbc, ngr, codes, scales); break;
+  }
+  return check_launch("quantize_transpose");
+}
+
+template <int DT, int G>
+static void launch_rows(const void *x, int64_t rows, int64_t K, int64_t stride,
+                        int8_t *codes, uint16_t *scales, const float *noise, float d2,
+                        bool vec, hipStream_t st) {
+  const int64_t ng = cdiv(K, G);
+  const int64_t lanes = rows * ng * (G / 8);
+  const unsigned blocks = (unsigned)cdiv(lanes, 256);
+  if (vec)
+    quant_rows_kernel<DT, G, true><<<blocks, 256, 0, st>>>(x, rows, K, stride, ng, codes, scales, noise, d2);
+  else
+    quant_rows_kernel<DT, G, false><<<blocks, 256, 0, st>>>(x, rows, K, stride, ng, codes, scales, noise, d2);
+}
+
+template <int DT>
+static void launch_rows_g(int group, const void *x, int64_t rows, int64_t K, int64_t stride,
+                          int8_t *codes, uint16_t *scales, const float *noise, float d2,
+                          bool vec, hipStream_t st) {
+  if (group == 32) launch_rows<DT, 32>(x, rows, K, stride, codes, scales, noise, d2, vec, st);
+  else if (group == 64) launch_rows<DT, 64>(x, rows, K, stride, codes, scales, noise, d2, vec, st);
+  else launch_rows<DT, 128>(x, rows, K, stride, codes, scales, noise, d2, vec, st);
+}
+
+}  // namespace ksd
+
+using namespace ksd;
+
+extern "C" int ksd_quantize_lastdim(const void *x, int x_dtype, int64_t rows, int64_t K,
+                                    int64_t x_stride, int group, int8_t *codes,
+                                    uint16_t *scales, const float *noise, float dither2,
+                                    void *stream) {
+  if (!valid_group(group)) return fail(KSD_EINVAL, "group must be 32, 64 or 128, got %d", group);
+  if (rows < 0 || K < 0 || x_stride < K) return fail(KSD_EINVAL, "bad quantize shape");
+  if (rows == 0 || K == 0) return KSD_OK;
+  if (cdiv(rows * cdiv(K, group) * (group / 8), 256) > 0x7fffffffLL)
+    return fail(KSD_EINVAL, "quantize: tensor too large");
+  hipStream_t st = (hipStream_t)stream;
+  const int esz = x_dtype == KSD_F32 ? 4 : 2;
+  const bool vec = (((uintptr_t)x) % 16 == 0) && ((x_stride * esz) % 16 == 0) &&
+                   (K % 8 == 0) && (((uintptr_t)codes) % 8 == 0);
+  switch (x_dtype) {
+    case KSD_F32: launch_rows_g<KSD_F32>(group, x, rows, K, x_stride, codes, scales, noise, dither2, vec, st); break;
+    case KSD_BF16: launch_rows_g<KSD_BF16>(group, x, rows, K, x_stride, codes, scales, noise, dither2, vec, st); break;
+    case KSD_F16: launch_rows_g<KSD_F16>(group, x, rows, K, x_stride, codes, scales, noise, dither2, vec, st); break;
+    default: return fail(KSD_ETYPE, "quantize expects float32, bfloat16 or float16 input");
+  }
+  return check_launch("quantize_lastdim");
+}
+
+extern "C" int ksd_dequantize_lastdim(const int8_t *codes, const uint16_t *scales,
+                                      int64_t rows, int64_t K, int64_t n_scales, int group,
+                                      float *out, void *stream) {
+  if (group <= 0) return fail(KSD_EINVAL, "dequantize: group must be positive");
+  if (rows == 0 || K == 0) return KSD_OK;
+  const int64_t n = rows * K;
+  if (cdiv(n, 256) > 0x7fffffffLL) return fail(KSD_EINVAL, "dequantize: tensor too large");
+  dequant_rows_kernel<<<(unsigned)cdiv(n, 256), 256, 0, (hipStream_t)stream>>>(
+      codes, scales, rows, K, n_scales, group, out);
+  return check_launch("dequantize_lastdim");
+}
+
+extern "C" int ksd_quantize_transpose(const void *x, int x_dtype, int64_t R, int64_t C,
+                                      int group, int8_t *codes, uint16_t *scales,
+                                      void *stream) {
+  if (!valid_group(group)) return fail(KSD_EINVAL, "group must be 32, 64 or 128, got %d", group);
+  if (R == 0 || C == 0) return KSD_OK;
+  hipStream_t st = (hipStream_t)stream;
+  switch (x_dtype) {
+    case KSD_F32: return launch_quant_T(LoadF32{(const float *)x, C}, R, C, group, codes, scales, st);
+    case KSD_BF16: return launch_quant_T(LoadBF16{(const uint16_t *)x, C}, R, C, group, codes, scales, st);
+    case KSD_F16: return launch_quant_T(LoadF16{(const uint16_t *)x, C}, R, C, group, codes, scales, st);
+    default: return fail(KSD_ETYPE, "quantize expects float32, bfloat16 or float16 input");
+  }
+}
+
+extern "C" int ksd_requant_transpose(const int8_t *codes, const uint16_t *scales, int64_t R,
+                                     int64_t C, int group_in, int group, int8_t *out_codes,
+                                     uint16_t *out_scales, void *stream) {
+  if (!valid_group(group) || !valid_group(group_in))
+    return fail(KSD_EINVAL, "group must be 32, 64 or 128");
+  if (R == 0 || C == 0) return KSD_OK;
+  LoadDequant ld{codes, scales, C, cdiv(C, group_in), group_in};
+  return launch_quant_T(ld, R, C, group, out_codes, out_scales, (hipStream_t)stream);
+}
+
+extern "C" int ksd_abi_version(void) { return 1; }
+
+extern "C" int ksd_last_error(char *buf, size_t len) {
+  if (buf == nullptr || len == 0) return KSD_EINVAL;
+  snprintf(buf, len, "%s", ksd::g_err);
+  return KSD_OK;
+}

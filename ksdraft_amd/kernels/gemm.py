@@ -1,0 +1,120 @@
+"""W8A8 GS128 GEMM on the gfx950 int8 matrix cores (mirror of reference ksdraft/kernels/gemm.py).
+
+``w8a8_gemm`` keeps the reference signature, validation and errors (gemm.py:53-90) and
+returns fp32 (M, N). The kernel computes, per output element, the ordered per-group
+contract acc = fmaf(float(P_g), sa*sw, acc) for g ascending, with P_g the exact int32
+group dot product. ``w8a8_gemm_out`` exposes the fused epilogue (fp32 bias, bf16/fp16
+output) used by the linear layer and the KS3 cell.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from .. import _lib
+from .quant import GROUP_SIZE, SCALE_DTYPE
+
+_OUT_CODE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+
+
+def _validate(a_codes, a_scales, w_codes, w_scales, group):
+    """gemm.py:60-70: the reference's checks, in its order, with its messages."""
+    M, K = a_codes.shape
+    N = w_codes.shape[0]
+    if w_codes.shape[1] != K:
+        raise ValueError(f"K mismatch: A {K} vs W {w_codes.shape[1]}")
+    n_groups = a_scales.shape[-1]
+    if w_scales.shape[-1] != n_groups:
+        raise ValueError(
+            f"scale group mismatch: A {n_groups} vs W {w_scales.shape[-1]}")
+    Kp = n_groups * group
+    if Kp < K:
+        raise ValueError(f"K {K} exceeds the scales' padded length {Kp}")
+    return M, N, K, n_groups, Kp
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def _prepare(a_codes, a_scales, w_codes, w_scales, group):
+    M, N, K, n_groups, Kp = _validate(a_codes, a_scales, w_codes, w_scales, group)
+    dev = _lib.require_gpu(a_codes, a_scales, w_codes, w_scales)
+    if a_codes.dtype != torch.int8 or w_codes.dtype != torch.int8:
+        raise TypeError("w8a8_gemm expects int8 codes")
+    if a_scales.dtype != SCALE_DTYPE or w_scales.dtype != SCALE_DTYPE:
+        raise TypeError("w8a8_gemm expects float16 scales")
+    # The kernel steps K by 128. Zero-pad codes (gemm.py:71-73) and, for groups smaller
+    # than 128, the scale columns of the padding groups (their codes are zero, so any
+    # finite scale leaves the sum unchanged).
+    K128 = -(-Kp // 128) * 128
+    if K128 != K:
+        a_codes = F.pad(a_codes, (0, K128 - K))
+        w_codes = F.pad(w_codes, (0, K128 - K))
+    g128 = K128 // group
+    if g128 != n_groups:
+        a_scales = F.pad(a_scales, (0, g128 - n_groups))
+        w_scales = F.pad(w_scales, (0, g128 - n_groups))
+    return (dev, M, N, K128, _aligned(a_codes), a_scales.contiguous(), _aligned(w_codes),
+            w_scales.contiguous())
+
+
+def w8a8_gemm_out(a_codes: torch.Tensor, a_scales: torch.Tensor, w_codes: torch.Tensor,
+                  w_scales: torch.Tensor, group: int = GROUP_SIZE, *,
+                  bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
+                  fp16_saturate: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+    """(M,K)x(N,K)^T -> (M,N) with the fused epilogue: + bias (fp32) then cast.
+
+    fp16_saturate: fp16 output clamped to +-65504 (ks3_int8.py:241-242)."""
+    dev, M, N, K, a, as_, w, ws = _prepare(a_codes, a_scales, w_codes, w_scales, group)
+    if fp16_saturate:
+        out_dtype = torch.float16
+    code = _lib.F16_SAT if fp16_saturate else _OUT_CODE.get(out_dtype)
+    if code is None:
+        raise TypeError(f"unsupported output dtype {out_dtype}")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=dev)
+    elif out.shape != (M, N) or out.dtype != out_dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous (M, N) tensor of the output dtype")
+    if bias is not None:
+        bias = bias.to(device=dev, dtype=torch.float32).contiguous()
+        if bias.numel() != N:
+            raise ValueError(f"bias has {bias.numel()} elements, expected {N}")
+    if K == 0:
+        out.zero_()
+        if bias is not None:
+            out += bias.to(out_dtype)
+        return out
+    _lib.call("ksd_w8a8_gemm_nt", a.data_ptr(), as_.data_ptr(), w.data_ptr(), ws.data_ptr(),
+              M, N, K, group, _lib.ptr(bias), out.data_ptr(), code, _lib.stream_ptr(dev))
+    return out
+
+
+def w8a8_gemm(a_codes: torch.Tensor, a_scales: torch.Tensor, w_codes: torch.Tensor,
+              w_scales: torch.Tensor, group: int = GROUP_SIZE) -> torch.Tensor:
+    """(M,K)x(N,K)^T -> (M,N) fp32. Inputs as produced by quantize_last_dim with the
+    matching `group` (gemm.py:53-90)."""
+    return w8a8_gemm_out(a_codes, a_scales, w_codes, w_scales, group)
+
+
+def w8a8_group_partials(a_codes: torch.Tensor, w_codes: torch.Tensor,
+                        group: int = GROUP_SIZE) -> torch.Tensor:
+    """Test-only export of the exact int32 group partials (K/group, M, N) of the GEMM
+    (the int32 tl.dot of gemm.py:42), from the same MFMA code path."""
+    dev = _lib.require_gpu(a_codes, w_codes)
+    M, K = a_codes.shape
+    N = w_codes.shape[0]
+    if w_codes.shape[1] != K:
+        raise ValueError(f"K mismatch: A {K} vs W {w_codes.shape[1]}")
+    if K % 128:
+        raise ValueError("w8a8_group_partials needs K % 128 == 0")
+    a = _aligned(a_codes)
+    w = _aligned(w_codes)
+    out = torch.empty((K // group, M, N), dtype=torch.int32, device=dev)
+    _lib.call("ksd_w8a8_group_partials", a.data_ptr(), w.data_ptr(), M, N, K, group,
+              out.data_ptr(), _lib.stream_ptr(dev))
+    return out

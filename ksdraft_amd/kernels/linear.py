@@ -1,0 +1,148 @@
+"""Int8Linear — W8A8 GS128 drop-in for nn.Linear (mirror of reference ksdraft/kernels/linear.py).
+
+Same constructor, attributes and methods as the reference (linear.py:23-97): fp32
+masters ``weight``/``bias`` stay authoritative and are requantized (per-output-row
+groups along the input dim) on every call into non-persistent ``weight_codes`` /
+``weight_scales`` buffers.
+
+Training differs from the reference on purpose: where the reference runs an fp32
+straight-through estimator (``fake_quant_forward``, linear.py:75-97), this layer runs
+the INT8-native autograd function ``W8A8LinearFunction`` — int8 forward GEMM and int8
+backward GEMMs built with the recipe of reference ksdraft/kernels/ks3_int8.py:403-424:
+
+    dX = quant_N(dY) . requant_N(W)^T              (W^T requantized along N)
+    dW = quant_M(dY)^T . requant_M(dequant(quant(X)))^T   (both along tokens M)
+
+Setting ``ste_training = True`` on a module restores the reference's STE behaviour.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from .gemm import w8a8_gemm, w8a8_gemm_out
+from .quant import (GROUP_SIZE, dequantize_last_dim, quantize_last_dim,
+                    quantize_last_dim_dithered, quantize_transpose, requant_transpose)
+
+
+class W8A8LinearFunction(torch.autograd.Function):
+    """y = W8A8(x, W) + b with int8 backward GEMMs; returns fp32-master gradients."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, wq, ws, group):
+        K = x.shape[-1]
+        N = wq.shape[0]
+        x2 = x.reshape(-1, K)
+        xq, xs = quantize_last_dim(x2, group)        # == quantize_last_dim(x2.float())
+        y = w8a8_gemm_out(xq, xs, wq, ws, group, bias=bias,
+                          out_dtype=x.dtype if x.dtype in (torch.float32, torch.bfloat16,
+                                                           torch.float16) else torch.float32)
+        ctx.save_for_backward(xq, xs, wq, ws)
+        ctx.x_shape = x.shape
+        ctx.x_dtype = x.dtype
+        ctx.group = group
+        ctx.has_bias = bias is not None
+        return y.reshape(*x.shape[:-1], N)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        xq, xs, wq, ws = ctx.saved_tensors
+        group = ctx.group
+        N, K = wq.shape
+        g = grad_out.reshape(-1, N)
+        if g.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            g = g.float()
+        g = g.contiguous()
+        dx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            gq, gs = quantize_last_dim(g, group)                    # along N (per token)
+            wtq, wts = requant_transpose(wq, ws, group, group)      # W^T (K, N) along N
+            dx = w8a8_gemm_out(gq, gs, wtq, wts, group, out_dtype=ctx.x_dtype
+                               if ctx.x_dtype in (torch.float32, torch.bfloat16,
+                                                  torch.float16) else torch.float32)
+            dx = dx.reshape(ctx.x_shape).to(ctx.x_dtype)
+        if ctx.needs_input_grad[1]:
+            gtq, gts = quantize_transpose(g, group)                 # dY^T (N, M) along M
+            xtq, xts = requant_transpose(xq, xs, group, group)      # X^T (K, M) along M
+            dw = w8a8_gemm(gtq, gts, xtq, xts, group)                # (N, K) fp32
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            db = g.float().sum(0)
+        return dx, dw, db, None, None, None
+
+
+class Int8Linear(nn.Module):
+    ste_training = False  # True: reference fp32 STE training path (fake_quant_forward)
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True):
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        # zeros, not empty: uninitialised memory could hold NaN patterns (linear.py:27-28)
+        self.weight = nn.Parameter(torch.zeros(out_features, in_features))
+        self.bias = nn.Parameter(torch.zeros(out_features)) if bias else None
+        self.register_buffer("weight_codes", None, persistent=False)
+        self.register_buffer("weight_scales", None, persistent=False)
+        if self.weight.is_cuda:
+            self._quantize_weight()
+
+    @classmethod
+    def from_float(cls, module: nn.Linear) -> "Int8Linear":
+        lin = cls(module.in_features, module.out_features, bias=module.bias is not None)
+        with torch.no_grad():
+            lin.weight.copy_(module.weight)
+            if module.bias is not None:
+                lin.bias.copy_(module.bias)
+        lin = lin.to(module.weight.device)
+        if lin.weight.is_cuda:
+            lin._quantize_weight()  # codes must reflect the copied masters
+        return lin
+
+    @torch.no_grad()
+    def _quantize_weight(self) -> None:
+        dither = float(getattr(self, "_dither", 0.0))
+        w = self.weight.detach()
+        if w.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            w = w.float()
+        if dither > 0:
+            codes, scales = quantize_last_dim_dithered(w.float(), GROUP_SIZE, dither)
+        else:
+            codes, scales = quantize_last_dim(w.float())
+        self.weight_codes = codes
+        self.weight_scales = scales
+
+    def _quantize_weight_dithered(self, dither: float) -> None:
+        self._dither = dither
+        self._quantize_weight()
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        self._quantize_weight()  # live fp32 masters stay authoritative (linear.py:66)
+        if torch.is_grad_enabled() and (self.weight.requires_grad or x.requires_grad):
+            if self.ste_training:
+                return self.fake_quant_forward(x)
+            return W8A8LinearFunction.apply(x, self.weight, self.bias, self.weight_codes,
+                                            self.weight_scales, GROUP_SIZE)
+        x2 = x.reshape(-1, x.shape[-1])
+        xq, xs = quantize_last_dim(x2)
+        out_dtype = x.dtype if x.dtype in (torch.float32, torch.bfloat16,
+                                           torch.float16) else torch.float32
+        # linear.py:69-73: fp32 GEMM, + bias in fp32, then cast to x.dtype (fused)
+        y = w8a8_gemm_out(xq, xs, self.weight_codes, self.weight_scales,
+                          bias=self.bias.detach() if self.bias is not None else None,
+                          out_dtype=out_dtype)
+        return y.reshape(*x.shape[:-1], self.out_features).to(x.dtype)
+
+    def fake_quant_forward(self, x: torch.Tensor) -> torch.Tensor:
+        """Reference STE path (linear.py:75-97): fp32 GEMM on quantize-dequantized
+        operands with straight-through gradients. Quantization runs on the HIP kernels;
+        the fp32 product is torch's."""
+        self._quantize_weight()
+        w = dequantize_last_dim(self.weight_codes.detach(), self.weight_scales.detach()) \
+            + (self.weight - self.weight.detach())
+        x2 = x.reshape(-1, x.shape[-1]).float()
+        codes, scales = quantize_last_dim(x2)
+        xq = dequantize_last_dim(codes, scales) + (x2 - x2.detach())
+        y = xq @ w.reshape(self.out_features, self.in_features).T
+        if self.bias is not None:
+            y = y + self.bias.float()
+        return y.reshape(*x.shape[:-1], self.out_features).to(x.dtype)

@@ -1,0 +1,149 @@
+"""GS128 symmetric INT8 quantization on gfx950 (mirror of reference ksdraft/kernels/quant.py).
+
+Contract (quant.py:1-17): symmetric per-group scales along the quantized dimension,
+group 128 by default; scales stored fp16, rounded BEFORE encoding and bounded to
+[2**-24, 65504]; codes saturate to [-127, 127] with round-half-even; a partial last group
+is zero-padded and its padded lanes are dropped from the codes.
+
+Every function runs one HIP kernel from libksdraft_amd.so on the tensor's current
+stream. There is no CPU path: CPU tensors raise after the reference's own argument
+checks (so its TypeError/ValueError conditions are identical on any device).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+GROUP_SIZE = 128
+SCALE_DTYPE = torch.float16
+SCALE_MIN = 2.0 ** -24
+SCALE_MAX = 65504.0
+
+
+def _padded_length(n: int, group: int = GROUP_SIZE) -> int:
+    """quant.py:26-27."""
+    return (n + group - 1) // group * group
+
+
+def _float_input(x: torch.Tensor) -> torch.Tensor:
+    if not torch.is_floating_point(x):
+        raise TypeError("quantize expects floating-point input")
+    if x.dtype == torch.float64:
+        raise TypeError("ksdraft_amd quantizes float32/bfloat16/float16 input (got float64)")
+    return x
+
+
+def _quantize(x: torch.Tensor, group: int, noise: torch.Tensor | None, dither: float):
+    x = _float_input(x)
+    if group not in (32, 64, 128):
+        raise ValueError(f"group must be 32, 64 or 128, got {group}")
+    dev = _lib.require_gpu(x)
+    K = x.shape[-1]
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K) if K else x.reshape(-1, 0)
+    rows = x2.shape[0]
+    # rows may be strided (a view), elements within a row must be dense
+    if K and (x2.stride(-1) != 1 or (rows > 1 and x2.stride(0) < K)):
+        x2 = x2.contiguous()
+    ng = -(-K // group) if group > 0 else 0
+    codes = torch.empty((rows, K), dtype=torch.int8, device=dev)
+    scales = torch.empty((rows, ng), dtype=SCALE_DTYPE, device=dev)
+    noise_ptr = None
+    if noise is not None:
+        noise = noise.to(device=dev, dtype=torch.float32).contiguous()
+        if noise.numel() != rows * ng * group:
+            raise ValueError("dither noise must cover the padded grouped shape")
+        noise_ptr = noise.data_ptr()
+    stride = x2.stride(0) if rows > 1 else K
+    _lib.call("ksd_quantize_lastdim", x2.data_ptr(), _lib.dtype_code(x2.dtype), rows, K,
+              stride, group, codes.data_ptr(), scales.data_ptr(), noise_ptr,
+              float(2.0 * dither), _lib.stream_ptr(dev))
+    return codes.reshape(*lead, K), scales.reshape(*lead, ng)
+
+
+def quantize_last_dim(x: torch.Tensor, group: int = GROUP_SIZE):
+    """x (..., K) fp -> (codes int8 (..., K), scales fp16 (..., Kp/group)). quant.py:30-52."""
+    return _quantize(x, group, None, 0.0)
+
+
+def quantize_last_dim_dithered(x: torch.Tensor, group: int, dither: float,
+                               generator: torch.Generator | None = None):
+    """Rounding-dither variant (reference ksdraft/train/stages.py:27-50).
+
+    The uniform draws come from torch.rand over the padded grouped shape on x's device
+    with `generator`, exactly the reference's RNG call, so codes are bit-identical for
+    identical generator state. dither == 0 is the exact grid (stages.py:43)."""
+    _float_input(x)
+    if dither > 0:
+        K = x.shape[-1]
+        Kp = _padded_length(K, group)
+        rows = x.numel() // K if K else 0
+        noise = torch.rand((rows, Kp), generator=generator, device=x.device,
+                           dtype=torch.float32)
+        return _quantize(x, group, noise, dither)
+    return _quantize(x, group, None, 0.0)
+
+
+def dequantize_last_dim(codes: torch.Tensor, scales: torch.Tensor,
+                        group: int | None = None) -> torch.Tensor:
+    """Inverse of quantize_last_dim, fp32 out (quant.py:55-67).
+
+    Keeps the reference's group inference: group = _padded_length(K) // n_scales."""
+    K = codes.shape[-1]
+    if group is None:
+        group = _padded_length(K) // max(scales.shape[-1], 1)
+    dev = _lib.require_gpu(codes, scales)
+    if codes.dtype != torch.int8:
+        codes = codes.to(torch.int8)  # float-typed integral codes (linear.py:79-80)
+    if scales.dtype != SCALE_DTYPE:
+        raise TypeError(f"scales must be {SCALE_DTYPE}, got {scales.dtype}")
+    lead = codes.shape[:-1]
+    c2 = codes.reshape(-1, K).contiguous() if K else codes.reshape(-1, 0)
+    nsc = scales.shape[-1]
+    s2 = scales.reshape(-1, nsc).contiguous()
+    out = torch.empty((c2.shape[0], K), dtype=torch.float32, device=dev)
+    _lib.call("ksd_dequantize_lastdim", c2.data_ptr(), s2.data_ptr(), c2.shape[0], K, nsc,
+              group, out.data_ptr(), _lib.stream_ptr(dev))
+    return out.reshape(*lead, K)
+
+
+def quantize_transpose(x: torch.Tensor, group: int = GROUP_SIZE):
+    """quantize_last_dim(x.t().contiguous(), group) for a 2-D x (R, C), without the copy.
+
+    Returns (codes (C, R) int8, scales (C, ceil(R/group)) fp16). Builds the dW operands
+    of reference ksdraft/kernels/ks3_int8.py:418, 422."""
+    x = _float_input(x)
+    dev = _lib.require_gpu(x)
+    if x.dim() != 2:
+        raise ValueError("quantize_transpose expects a 2-D tensor")
+    x = x.contiguous()
+    R, C = x.shape
+    codes = torch.empty((C, R), dtype=torch.int8, device=dev)
+    scales = torch.empty((C, -(-R // group)), dtype=SCALE_DTYPE, device=dev)
+    _lib.call("ksd_quantize_transpose", x.data_ptr(), _lib.dtype_code(x.dtype), R, C, group,
+              codes.data_ptr(), scales.data_ptr(), _lib.stream_ptr(dev))
+    return codes, scales
+
+
+def requant_transpose(codes: torch.Tensor, scales: torch.Tensor,
+                      group_in: int = GROUP_SIZE, group: int = GROUP_SIZE):
+    """quantize_last_dim(dequantize_last_dim(codes, scales).t(), group) in one pass.
+
+    The dequantize -> transpose -> requantize operand builds of reference
+    ksdraft/kernels/ks3_int8.py:349-351, 407-408, 417-419, 423."""
+    dev = _lib.require_gpu(codes, scales)
+    if codes.dim() != 2 or codes.dtype != torch.int8:
+        raise ValueError("requant_transpose expects 2-D int8 codes")
+    codes = codes.contiguous()
+    scales = scales.contiguous()
+    R, C = codes.shape
+    if scales.shape != (R, -(-C // group_in)):
+        raise ValueError(f"scales shape {tuple(scales.shape)} does not match codes {R}x{C} "
+                         f"with group {group_in}")
+    out_c = torch.empty((C, R), dtype=torch.int8, device=dev)
+    out_s = torch.empty((C, -(-R // group)), dtype=SCALE_DTYPE, device=dev)
+    _lib.call("ksd_requant_transpose", codes.data_ptr(), scales.data_ptr(), R, C, group_in,
+              group, out_c.data_ptr(), out_s.data_ptr(), _lib.stream_ptr(dev))
+    return out_c, out_s

@@ -1,0 +1,85 @@
+/*
+ * ksd_oracle.c — CPU restatement of KSDraft's INT8-tier arithmetic, used ONLY as the
+ * checker by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg. Nothing
+ * in the product (ksdraft_amd/) links or calls it.
+ *
+ * Plain C, built with gcc -O2 -ffp-contract=off (so a*b+c is two roundings unless
+ * written fmaf, which glibc rounds correctly). fp16 values are handled as uint16_t bit
+ * patterns with an exact decoder (half_to_float).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+/* exact fp16 -> fp32 decode (every fp16 value, subnormals included, is an fp32) */
+float ksd_half_to_float(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1fu;
+  const uint32_t man = h & 0x3ffu;
+  float f;
+  if (exp == 0) {
+    f = ldexpf((float)man, -24); /* subnormal: man * 2^-24 */
+  } else if (exp == 31) {
+    uint32_t bits = 0x7f800000u | (man << 13);
+    memcpy(&f, &bits, 4);
+  } else {
+    uint32_t bits = ((exp + 112u) << 23) | (man << 13);
+    memcpy(&f, &bits, 4);
+  }
+  uint32_t b;
+  memcpy(&b, &f, 4);
+  b |= sign;
+  memcpy(&f, &b, 4);
+  return f;
+}
+
+/*
+ * Exact int32 group partials P_g[m,n] = sum_{k in group g} a[m,k]*w[n,k]
+ * (the int32 tl.dot of reference ksdraft/kernels/gemm.py:42). out is (G, M, N).
+ */
+void ksd_oracle_partials(const int8_t *a, const int8_t *w, int64_t M, int64_t N, int64_t K,
+                         int group, int32_t *out) {
+  const int64_t G = K / group;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n) {
+      const int8_t *ar = a + m * K;
+      const int8_t *wr = w + n * K;
+      for (int64_t g = 0; g < G; ++g) {
+        int32_t p = 0;
+        for (int64_t k = g * group; k < (g + 1) * group; ++k) p += (int32_t)ar[k] * (int32_t)wr[k];
+        out[(g * M + m) * N + n] = p;
+      }
+    }
+}
+
+/*
+ * W8A8 GEMM in the ordered per-group contract the GPU kernel implements:
+ *   acc = 0; for g = 0..G-1: acc = fmaf((float)P_g, sa[m,g]*sw[n,g], acc); y = acc (+ bias[n])
+ * Per-group rescale order follows reference ksdraft/kernels/gemm.py:34-45; bias is
+ * added in fp32 afterwards as in ksdraft/kernels/linear.py:71-72.
+ * rows: optional list of `n_rows` row indices to evaluate (NULL = all M rows); y holds
+ * one output row per evaluated row.
+ */
+void ksd_oracle_gemm_ordered(const int8_t *a, const uint16_t *as, const int8_t *w,
+                             const uint16_t *ws, int64_t M, int64_t N, int64_t K, int group,
+                             const float *bias, const int64_t *rows, int64_t n_rows, float *y) {
+  const int64_t G = K / group;
+  const int64_t R = rows ? n_rows : M;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t r = 0; r < R; ++r)
+    for (int64_t n = 0; n < N; ++n) {
+      const int64_t m = rows ? rows[r] : r;
+      const int8_t *ar = a + m * K;
+      const int8_t *wr = w + n * K;
+      float acc = 0.0f;
+      for (int64_t g = 0; g < G; ++g) {
+        int32_t p = 0;
+        for (int64_t k = g * group; k < (g + 1) * group; ++k) p += (int32_t)ar[k] * (int32_t)wr[k];
+        const float s = ksd_half_to_float(as[m * G + g]) * ksd_half_to_float(ws[n * G + g]);
+        acc = fmaf((float)p, s, acc);
+      }
+      if (bias) acc = acc + bias[n];
+      y[r * N + n] = acc;
+    }
+}

@@ -1,0 +1,129 @@
+"""GPU parity: the W8A8 GEMM kernel.
+
+Bars: int32 group partials bit-exact (brute force oracle); fp32 output bit-exact vs the
+ordered-group contract oracle; within rtol/atol 1e-3 of the reference CPU path
+(dequantize + fp32 matmul, gemm.py:76-82) — the reference's own GPU test uses rtol 1e-4 /
+atol 1e-3 (tests/test_int8.py:80), which is asserted too.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from ksdraft_amd.kernels import gemm as kg
+from ksdraft_amd.kernels import quant as kq
+from oracle import gemm as og
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _operands(seed, M, K, N, wscale=0.1, group=128):
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randn(M, K, generator=g)
+    w = torch.randn(N, K, generator=g) * wscale
+    aq, as_ = oq.quantize_last_dim(a.numpy(), group)
+    wq, ws = oq.quantize_last_dim(w.numpy(), group)
+    return aq, as_, wq, ws
+
+
+def _gpu(*arrs):
+    return [torch.from_numpy(np.ascontiguousarray(a)).to(DEV) for a in arrs]
+
+
+# the reference's own GPU parity shapes, tests/test_int8.py:73
+REF_SHAPES = [(16, 256, 128), (64, 128, 96), (33, 384, 64), (128, 128, 128)]
+
+
+@pytest.mark.parametrize("M,K,N", REF_SHAPES + [(256, 1536, 1536), (1, 128, 1), (200, 640, 260)])
+def test_gemm_bit_exact_and_within_reference_tolerance(M, K, N):
+    aq, as_, wq, ws = _operands(3 + M, M, K, N)
+    y = kg.w8a8_gemm(*_gpu(aq, as_, wq, ws)).cpu().numpy()
+    ordered = og.gemm_ordered(aq, as_, wq, ws)
+    assert np.array_equal(y.view(np.uint32), ordered.view(np.uint32))
+    ref = og.gemm_reference(aq, as_, wq, ws)
+    np.testing.assert_allclose(y, ref, rtol=1e-4, atol=1e-3)
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("M,K,N", [(64, 256, 96), (40, 384, 130)])
+def test_group_partials_bit_exact(M, K, N, group):
+    aq, _, wq, _ = _operands(7, M, K, N, group=group)
+    p = kg.w8a8_group_partials(*_gpu(aq, wq), group=group).cpu().numpy()
+    assert np.array_equal(p, og.group_partials(aq, wq, group))
+
+
+@pytest.mark.parametrize("group", [32, 64])
+def test_small_groups(group):
+    aq, as_, wq, ws = _operands(9, 48, 320, 72, group=group)
+    y = kg.w8a8_gemm(*_gpu(aq, as_, wq, ws), group=group).cpu().numpy()
+    assert np.array_equal(y, og.gemm_ordered(aq, as_, wq, ws, group))
+    np.testing.assert_allclose(y, og.gemm_reference(aq, as_, wq, ws, group), rtol=1e-4, atol=1e-3)
+
+
+def test_ragged_k_is_zero_padded():
+    g = torch.Generator().manual_seed(1)
+    a = torch.randn(5, 100, generator=g)
+    w = torch.randn(6, 100, generator=g)
+    aq, as_ = oq.quantize_last_dim(a.numpy())
+    wq, ws = oq.quantize_last_dim(w.numpy())
+    y = kg.w8a8_gemm(*_gpu(aq, as_, wq, ws)).cpu().numpy()
+    assert np.array_equal(y, og.gemm_ordered(aq, as_, wq, ws))
+
+
+def test_epilogue_bias_and_output_dtypes():
+    aq, as_, wq, ws = _operands(11, 70, 512, 300)
+    bias = torch.randn(300, generator=torch.Generator().manual_seed(2))
+    ta = _gpu(aq, as_, wq, ws)
+    exp = torch.from_numpy(og.gemm_ordered(aq, as_, wq, ws, bias=bias.numpy()))
+    y32 = kg.w8a8_gemm_out(*ta, bias=bias.to(DEV)).cpu()
+    assert torch.equal(y32, exp)
+    ybf = kg.w8a8_gemm_out(*ta, bias=bias.to(DEV), out_dtype=torch.bfloat16).cpu()
+    assert torch.equal(ybf, exp.to(torch.bfloat16))
+    y16 = kg.w8a8_gemm_out(*ta, out_dtype=torch.float16).cpu()
+    assert torch.equal(y16, torch.from_numpy(og.gemm_ordered(aq, as_, wq, ws)).half())
+
+
+def test_fp16_saturating_output():
+    # coords = fp16(acc).clamp(+-65504) (ks3_int8.py:241-242)
+    a = np.full((4, 128), 127, np.int8)
+    w = np.full((4, 128), 127, np.int8)
+    sa = np.full((4, 1), 2.0, np.float16)
+    sw = np.array([[1.0], [-1.0], [1e-3], [0.5]], np.float16)
+    y = kg.w8a8_gemm_out(*_gpu(a, sa, w, sw), fp16_saturate=True).cpu()
+    ref = torch.from_numpy(og.gemm_ordered(a, sa, w, sw)).half().clamp(-65504, 65504)
+    assert torch.equal(y, ref)
+    assert y[0, 0].item() == 65504.0 and y[0, 1].item() == -65504.0
+
+
+def test_config1_forward_full_oracle():
+    """M=256, K=N=1536, X~N(0,1), W~N(0,0.02), seed 0, fp32 out."""
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(256, 1536, generator=g)
+    w = torch.randn(1536, 1536, generator=g) * 0.02
+    xq, xs = kq.quantize_last_dim(x.to(DEV))
+    wq, ws = kq.quantize_last_dim(w.to(DEV))
+    y = kg.w8a8_gemm(xq, xs, wq, ws).cpu().numpy()
+    exq, exs = oq.quantize_last_dim(x.numpy())
+    ewq, ews = oq.quantize_last_dim(w.numpy())
+    assert np.array_equal(xq.cpu().numpy(), exq) and np.array_equal(wq.cpu().numpy(), ewq)
+    assert np.array_equal(y, og.gemm_ordered(exq, exs, ewq, ews))
+    np.testing.assert_allclose(y, og.gemm_reference(exq, exs, ewq, ews), rtol=1e-3, atol=1e-3)
+
+
+def test_config2_forward_sampled_rows():
+    """BASELINE config 2 forward at full size (M=8192, K=N=1536): 96 sampled rows checked
+    bit-exactly against the ordered oracle; partials of 8 rows bit-exact."""
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(8192, 1536, generator=g)
+    w = torch.randn(1536, 1536, generator=g) * 0.02
+    xq, xs = kq.quantize_last_dim(x.to(DEV))
+    wq, ws = kq.quantize_last_dim(w.to(DEV))
+    y = kg.w8a8_gemm(xq, xs, wq, ws)
+    rows = np.sort(np.random.default_rng(0).choice(8192, 96, replace=False))
+    hq, hs, hwq, hws = (t.cpu().numpy() for t in (xq, xs, wq, ws))
+    exp = og.gemm_ordered(hq, hs, hwq, hws, rows=rows)
+    assert np.array_equal(y.cpu().numpy()[rows], exp)
+    p = kg.w8a8_group_partials(xq[:128], wq).cpu().numpy()
+    assert np.array_equal(p[:, :8], og.group_partials(hq[:8], hwq))

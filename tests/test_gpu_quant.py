@@ -1,0 +1,106 @@
+"""GPU parity: quantization kernels vs the oracle, bit-exact codes and fp16 scales."""
+
+import numpy as np
+import pytest
+import torch
+
+from ksdraft_amd.kernels import quant as kq
+from oracle import quant as oq
+from tests.test_oracle_quant import _adversarial_rows
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _check(x_cpu, group=128):
+    x = x_cpu.to(DEV)
+    codes, scales = kq.quantize_last_dim(x, group)
+    torch.cuda.synchronize()
+    ec, es = oq.quantize_last_dim(x_cpu.float().numpy(), group)
+    assert codes.dtype == torch.int8 and scales.dtype == torch.float16
+    assert np.array_equal(codes.cpu().numpy(), ec)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint16), es.view(np.uint16))
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("shape", [(64, 256), (4, 100), (33, 1536), (3, 7), (1, 1), (5, 136)])
+def test_quantize_matches_oracle(shape, group):
+    g = torch.Generator().manual_seed(hash((shape, group)) % 2**31)
+    _check(torch.randn(*shape, generator=g) * 3, group)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_quantize_half_inputs(dtype):
+    g = torch.Generator().manual_seed(11)
+    _check((torch.randn(17, 384, generator=g) * 2).to(dtype))
+
+
+@pytest.mark.parametrize("group", [32, 128])
+def test_quantize_adversarial_rounding(group):
+    x = _adversarial_rows(np.random.default_rng(99 + group), group)
+    _check(torch.from_numpy(x), group)
+
+
+def test_zero_row_and_extremes():
+    _check(torch.zeros(2, 128))
+    _check(torch.tensor([[1e-30] * 128, [3e38] * 128, [-7e-8] * 128]))
+
+
+def test_quantize_leading_dims_and_strided_rows():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 3, 256, generator=g).to(DEV)
+    c, s = kq.quantize_last_dim(x)
+    assert c.shape == (2, 3, 256) and s.shape == (2, 3, 2)
+    ec, es = oq.quantize_last_dim(x.cpu().numpy())
+    assert np.array_equal(c.cpu().numpy(), ec)
+    big = torch.randn(8, 512, generator=g).to(DEV)
+    view = big[:, 128:384]  # rows strided by 512
+    c, s = kq.quantize_last_dim(view)
+    ec, es = oq.quantize_last_dim(view.cpu().numpy())
+    assert np.array_equal(c.cpu().numpy(), ec) and np.array_equal(s.cpu().numpy(), es)
+
+
+def test_dither_matches_oracle_with_same_draws():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(8, 256, generator=g) * 3
+    noise = torch.rand(8, 256, generator=g)
+    codes, scales = kq._quantize(x.to(DEV), 128, noise.to(DEV), 0.5)
+    ec, es = oq.quantize_last_dim(x.numpy(), 128, noise=noise.numpy(), dither=0.5)
+    assert np.array_equal(codes.cpu().numpy(), ec) and np.array_equal(scales.cpu().numpy(), es)
+    c0, s0 = kq.quantize_last_dim_dithered(x.to(DEV), 128, 0.0)
+    ce, se = kq.quantize_last_dim(x.to(DEV), 128)
+    assert torch.equal(c0, ce) and torch.equal(s0, se)
+
+
+@pytest.mark.parametrize("K,nsc", [(256, 2), (100, 1), (6, 1), (256, 8)])
+def test_dequantize_matches_oracle(K, nsc):
+    g = torch.Generator().manual_seed(K)
+    codes = torch.randint(-127, 128, (9, K), generator=g, dtype=torch.int8)
+    scales = (torch.rand(9, nsc, generator=g) * 0.1).half()
+    out = kq.dequantize_last_dim(codes.to(DEV), scales.to(DEV))
+    ref = oq.dequantize_last_dim(codes.numpy(), scales.numpy())
+    assert np.array_equal(out.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("R,C", [(256, 192), (33, 70), (8192, 64), (130, 1)])
+def test_quantize_transpose_matches_oracle(R, C, dtype):
+    g = torch.Generator().manual_seed(R * 7 + C)
+    x = (torch.randn(R, C, generator=g) * 1e-2).to(dtype)
+    codes, scales = kq.quantize_transpose(x.to(DEV))
+    ec, es = oq.quantize_transpose(x.float().numpy())
+    assert np.array_equal(codes.cpu().numpy(), ec)
+    assert np.array_equal(scales.cpu().numpy(), es)
+
+
+@pytest.mark.parametrize("group_in,group", [(128, 128), (128, 32), (32, 128)])
+@pytest.mark.parametrize("R,C", [(200, 96), (1536, 1536), (64, 300)])
+def test_requant_transpose_matches_oracle(R, C, group_in, group):
+    g = torch.Generator().manual_seed(R + C)
+    w = torch.randn(R, C, generator=g) * 0.02
+    wq, ws = oq.quantize_last_dim(w.numpy(), group_in)
+    tq, ts = kq.requant_transpose(torch.from_numpy(wq).to(DEV), torch.from_numpy(ws).to(DEV),
+                                  group_in, group)
+    eq, es = oq.requant_transpose(wq, ws, group_in, group)
+    assert np.array_equal(tq.cpu().numpy(), eq)
+    assert np.array_equal(ts.cpu().numpy(), es)
