@@ -1,0 +1,313 @@
+#!/usr/bin/env python3
+"""Benchmark: KSDraft INT8 tier on one MI355X.
+
+Workload: one W8A8 GS128 linear layer at training shape,
+forward + both backward GEMMs, M = 8192 tokens (batch 4 x seq 2048), K = N = 1536.
+X ~ N(0,1), W ~ N(0,0.02) fp32 master, dY ~ N(0,1e-2), all fp32, seeded (torch CPU
+generator, seed 0) and resident in HBM before timing.
+
+One step = exactly what the training path runs for this layer:
+    quantize W -> quantize X -> GEMM Y = X W^T (fp32 out)
+    quantize dY (along N) -> requant W^T -> GEMM dX = dY W
+    quantize dY^T (along M) -> requant X^T -> GEMM dW = dY^T X   (fp32)
+value = algorithmic int8 ops of the three GEMMs (3 * 2*M*N*K) / step time, in TOPS.
+The step runs as a captured HIP graph (no host launch overhead; replays are checked
+bit-equal to the eager step); the eager step time is reported beside it.
+
+Also reported: per-kernel average launch times (HIP events around graphs of back-to-back
+launches on the launch stream), the GEMM roofline against the 5.0 POPS dense int8 peak,
+and the CPU oracle (the reference's CPU path: dequantize + fp32 matmul) timed on a
+bounded sample on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from ksdraft_amd.kernels.linear import w8a8_linear_backward, w8a8_linear_forward  # noqa: E402
+from ksdraft_amd.kernels.quant import (quantize_last_dim, quantize_transpose,  # noqa: E402
+                                       requant_transpose)
+from ksdraft_amd.kernels.gemm import w8a8_gemm_out  # noqa: E402
+
+METRIC = ("W8A8 GS128 GEMM TOPS fwd+bwd @d=1536 (% int8 peak); draft train-step tok/s")
+PEAK_INT8 = 5.0e15   # MI355X dense int8 MFMA, ops/s
+PEAK_HBM = 8.0e12    # MI355X HBM3E, bytes/s
+M, K, N = 8192, 1536, 1536
+GEMM_OPS = 2 * M * N * K
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--kernel-reps", type=int, default=20)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument("--pmc-probe", action="store_true",
+                   help="for rocprofv3 --pmc runs: a 256 MiB device copy (counter "
+                        "calibration), then 3 launches of each GEMM of the step; no timing")
+    return p.parse_args()
+
+
+def pmc_probe(x, w, dy):
+    """Workload for the HBM-traffic counters: torch's device copy of a known size
+    (256 MiB read + 256 MiB written) to calibrate FETCH_SIZE/WRITE_SIZE, then the
+    step's three GEMM launches on their real operands."""
+    src = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device=x.device).fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    wq, ws = quantize_last_dim(w)
+    xq, xs = quantize_last_dim(x)
+    gq, gs = quantize_last_dim(dy)
+    wtq, wts = requant_transpose(wq, ws)
+    gtq, gts = quantize_transpose(dy)
+    xtq, xts = requant_transpose(xq, xs)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        w8a8_gemm_out(xq, xs, wq, ws)
+        w8a8_gemm_out(gq, gs, wtq, wts)
+        w8a8_gemm_out(gtq, gts, xtq, xts)
+    torch.cuda.synchronize()
+    print("pmc probe done", flush=True)
+
+
+def make_inputs(dev):
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(M, K, generator=g)
+    w = torch.randn(N, K, generator=g) * 0.02
+    dy = torch.randn(M, N, generator=g) * 1e-2
+    return x, w, dy, x.to(dev), w.to(dev), dy.to(dev)
+
+
+def step(x, w, dy):
+    wq, ws = quantize_last_dim(w)
+    y, xq, xs = w8a8_linear_forward(x, wq, ws, None, out_dtype=torch.float32)
+    dx, dw = w8a8_linear_backward(dy, xq, xs, wq, ws, dx_dtype=torch.float32)
+    return y, dx, dw
+
+
+def time_graph(fn, reps, warm=3):
+    """Capture fn() once, replay; returns (graph, outputs, avg ms per replay)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(warm):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = fn()
+    for _ in range(warm):
+        graph.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return graph, out, e0.elapsed_time(e1) / reps
+
+
+def kernel_times(x, w, dy, reps):
+    """Average launch time (us) of every kernel of the step, each timed as a graph of
+    `reps` back-to-back launches bracketed by HIP events on the capture stream."""
+    wq, ws = quantize_last_dim(w)
+    xq, xs = quantize_last_dim(x)
+    gq, gs = quantize_last_dim(dy)
+    wtq, wts = requant_transpose(wq, ws)
+    gtq, gts = quantize_transpose(dy)
+    xtq, xts = requant_transpose(xq, xs)
+    stages = {
+        "quantize_W": (lambda: quantize_last_dim(w), 4 * N * K + N * K + 2 * N * K // 128),
+        "quantize_X": (lambda: quantize_last_dim(x), 4 * M * K + M * K + 2 * M * K // 128),
+        "gemm_fwd": (lambda: w8a8_gemm_out(xq, xs, wq, ws), None),
+        "quantize_dY": (lambda: quantize_last_dim(dy), 4 * M * N + M * N + 2 * M * N // 128),
+        "requant_WT": (lambda: requant_transpose(wq, ws), 2 * (N * K + 2 * N * K // 128)),
+        "gemm_dX": (lambda: w8a8_gemm_out(gq, gs, wtq, wts), None),
+        "quantize_T_dY": (lambda: quantize_transpose(dy), 4 * M * N + M * N + 2 * M * N // 128),
+        "requant_XT": (lambda: requant_transpose(xq, xs), 2 * (M * K + 2 * M * K // 128)),
+        "gemm_dW": (lambda: w8a8_gemm_out(gtq, gts, xtq, xts), None),
+    }
+    res = {}
+    for name, (fn, nbytes) in stages.items():
+        def rep(fn=fn):
+            for _ in range(reps):
+                fn()
+        _, _, ms = time_graph(rep, 3, warm=1)
+        us = ms * 1e3 / reps
+        ent = {"us": round(us, 3)}
+        if nbytes is None:
+            ent["tops"] = round(GEMM_OPS / (us * 1e-6) / 1e12, 1)
+        else:
+            ent["GBps"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+            ent["hbm_frac"] = round(nbytes / (us * 1e-6) / PEAK_HBM, 3)
+        res[name] = ent
+    return res
+
+
+def cpu_baseline(x, w, dy, budget_s):
+    """The oracle's restatement of the reference CPU path (quantize in numpy; GEMMs as
+    dequantize + fp32 BLAS matmul, reference ksdraft/kernels/gemm.py:76-82), timed on
+    this host's cores on a bounded sample of the same workload (full shape, as many
+    steps as fit the budget after one warm-up)."""
+    from oracle import gemm as og
+    from oracle import quant as oq
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = 1
+    X, W, DY = x.numpy(), w.numpy(), dy.numpy()
+
+    def cstep():
+        wq, ws = oq.quantize_last_dim(W)
+        xq, xs = oq.quantize_last_dim(X)
+        og.gemm_reference(xq, xs, wq, ws)
+        gq, gs = oq.quantize_last_dim(DY)
+        wtq, wts = oq.requant_transpose(wq, ws)
+        og.gemm_reference(gq, gs, wtq, wts)
+        gtq, gts = oq.quantize_transpose(DY)
+        xtq, xts = oq.requant_transpose(xq, xs)
+        og.gemm_reference(gtq, gts, xtq, xts)
+
+    cstep()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 10):
+        t0 = time.perf_counter()
+        cstep()
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    return {
+        "value": round(3 * GEMM_OPS / t / 1e12, 4), "unit": "TOPS", "cores": int(threads),
+        "kind": "port",
+        "sample": (f"full config-2 step (M={M}, K=N={K}) x {len(times)} after 1 warm-up, "
+                   f"median {t:.3f} s/step; numpy quantization passes single-threaded, "
+                   f"BLAS matmuls on {threads} threads"),
+    }
+
+
+def traffic_from_profiles():
+    path = os.path.join(ROOT, "profiles", "gemm_nt_c2_pmc.json")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        d = json.load(f)
+    return d.get("traffic_bytes_per_launch"), "profiles/gemm_nt_c2_pmc.json"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(one MI355X per box); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    xc, wc, dyc, x, w, dy = make_inputs(dev)
+    if args.pmc_probe:
+        pmc_probe(x, w, dy)
+        return
+
+    # eager: warm-up then K timed steps
+    for _ in range(args.warmup):
+        ref = step(x, w, dy)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step(x, w, dy)
+    e1.record()
+    torch.cuda.synchronize()
+    eager_ms = e0.elapsed_time(e1) / args.steps
+    eager_wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # graph: capture one step, check replays against the eager result, time K replays
+    ref = [t.clone() for t in step(x, w, dy)]
+    graph, outs, _ = time_graph(lambda: step(x, w, dy), 1)
+    for _ in range(3):
+        graph.replay()
+        step(x, w, dy)           # eager work between replays
+        torch.cuda.synchronize()
+        for a, b in zip(outs, ref):
+            if not torch.equal(a, b):
+                raise SystemExit("graph replay differs from the eager step")
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    g0.record()
+    for _ in range(args.steps):
+        graph.replay()
+    g1.record()
+    torch.cuda.synchronize()
+    ms = g0.elapsed_time(g1) / args.steps
+
+    kern = kernel_times(x, w, dy, args.kernel_reps)
+    gemm_us = [kern[k]["us"] for k in ("gemm_fwd", "gemm_dX", "gemm_dW")]
+    gemm_avg_us = float(np.mean(gemm_us))
+    achieved = GEMM_OPS / (gemm_avg_us * 1e-6)
+    traffic, tsrc = traffic_from_profiles()
+
+    value = 3 * GEMM_OPS / (ms * 1e-3) / 1e12
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: seeded X~N(0,1), W~N(0,0.02), dY~N(0,1e-2), fp32, resident in HBM",
+        "config": {"workload": "BASELINE config 2: W8A8 GS128 linear fwd + dX + dW, "
+                               "M=8192 (4x2048), K=N=1536, fp32 in/out, step as HIP graph",
+                   "M": M, "K": K, "N": N, "group": 128},
+        "pct_int8_peak": round(100 * value * 1e12 / PEAK_INT8, 2),
+        "tok_per_s": round(M / (ms * 1e-3), 1),
+        "gemm_only_tops": round(3 * GEMM_OPS / (sum(gemm_us) * 1e-6) / 1e12, 1),
+        "eager_ms_per_step": round(eager_ms, 4),
+        "eager_wall_ms_per_step": round(eager_wall_ms, 4),
+        "draft_train_step_tok_s": None,
+        "kernels": kern,
+        "roofline": {
+            "kernel": "gemm_nt_kernel<128,f32> (fwd, dX, dW launches averaged)",
+            "bound": "mfma",
+            "achieved": round(achieved / 1e12, 1),
+            "peak": PEAK_INT8 / 1e12,
+            "unit": "TOPS",
+            "frac": round(achieved / PEAK_INT8, 4),
+            "traffic": traffic,
+            "traffic_source": tsrc,
+            "avg_launch_us": round(gemm_avg_us, 3),
+            "ops_per_launch": GEMM_OPS,
+        },
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(xc, wc, dyc, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -43,7 +43,16 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+  // Workgroups are dispatched round-robin over the 8 XCDs (block b -> XCD b % 8), each
+  // with its own L2. Renumber so that XCD x owns a contiguous range of tiles in
+  // row-major tile order: the tiles sharing an A row panel then share one L2.
+  int bid = blockIdx.x;
+  {
+    const int nb = gridDim.x, per = nb / 8, rem = nb % 8, x = bid % 8, i = bid / 8;
+    // XCD x receives per (+1 if x < rem) blocks; they take tiles [start_x, start_x + cnt)
+    bid = x * per + min(x, rem) + i;
+  }
+  const int tm = bid / tiles_n, tn = bid % tiles_n;
   const int m0 = tm * BM, n0 = tn * BN;
   const int G = K / GROUP;
   const int KT = K / BK;
@@ -67,7 +76,7 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_kernel(
                             : WS + (int64_t)min(n0 + sc_r, N - 1) * G;
 
   v4i ra[4], rw[4];
-  float rs[GPT];
+  uint16_t rs[GPT];  // raw fp16 bits: converting here would force an early vmcnt wait
   auto gload = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -76,7 +85,7 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_kernel(
     }
     if (MODE == 0) {
 #pragma unroll
-      for (int g = 0; g < GPT; ++g) rs[g] = f16_to_f32(gS[kt * GPT + g]);
+      for (int g = 0; g < GPT; ++g) rs[g] = gS[kt * GPT + g];
     }
   };
   auto lstore = [&](int buf) {
@@ -88,8 +97,8 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_kernel(
     if (MODE == 0) {
 #pragma unroll
       for (int g = 0; g < GPT; ++g) {
-        if (sc_a) sSA[buf][g][sc_r] = rs[g];
-        else sSW[buf][g][sc_r] = rs[g];
+        if (sc_a) sSA[buf][g][sc_r] = f16_to_f32(rs[g]);
+        else sSW[buf][g][sc_r] = f16_to_f32(rs[g]);
       }
     }
   };

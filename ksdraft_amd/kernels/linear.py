@@ -26,6 +26,45 @@ from .quant import (GROUP_SIZE, dequantize_last_dim, quantize_last_dim,
                     quantize_last_dim_dithered, quantize_transpose, requant_transpose)
 
 
+_OUT_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _out_dtype(dtype: torch.dtype) -> torch.dtype:
+    return dtype if dtype in _OUT_DTYPES else torch.float32
+
+
+def w8a8_linear_forward(x2: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
+                        bias: torch.Tensor | None, group: int = GROUP_SIZE,
+                        out_dtype: torch.dtype | None = None):
+    """y = W8A8(x2, W) + bias in one quantize + one GEMM launch (linear.py:68-73).
+
+    Returns (y, xq, xs); the activation codes are what the backward keeps."""
+    xq, xs = quantize_last_dim(x2, group)          # == quantize_last_dim(x2.float())
+    y = w8a8_gemm_out(xq, xs, wq, ws, group, bias=bias,
+                      out_dtype=_out_dtype(out_dtype or x2.dtype))
+    return y, xq, xs
+
+
+def w8a8_linear_backward(g: torch.Tensor, xq: torch.Tensor, xs: torch.Tensor,
+                         wq: torch.Tensor, ws: torch.Tensor, group: int = GROUP_SIZE,
+                         dx_dtype: torch.dtype = torch.float32, need_dx: bool = True,
+                         need_dw: bool = True):
+    """INT8 backward GEMMs of the linear layer (recipe of ks3_int8.py:403-424).
+
+    g (M, N) upstream gradient; xq/xs the forward's activation codes; wq/ws the weight
+    codes. Returns (dx (M, K) in dx_dtype or None, dw (N, K) fp32 or None)."""
+    dx = dw = None
+    if need_dx:
+        gq, gs = quantize_last_dim(g, group)                    # along N (per token)
+        wtq, wts = requant_transpose(wq, ws, group, group)      # W^T (K, N) along N
+        dx = w8a8_gemm_out(gq, gs, wtq, wts, group, out_dtype=_out_dtype(dx_dtype))
+    if need_dw:
+        gtq, gts = quantize_transpose(g, group)                 # dY^T (N, M) along M
+        xtq, xts = requant_transpose(xq, xs, group, group)      # X^T (K, M) along M
+        dw = w8a8_gemm(gtq, gts, xtq, xts, group)                # (N, K) fp32
+    return dx, dw
+
+
 class W8A8LinearFunction(torch.autograd.Function):
     """y = W8A8(x, W) + b with int8 backward GEMMs; returns fp32-master gradients."""
 
@@ -33,11 +72,7 @@ class W8A8LinearFunction(torch.autograd.Function):
     def forward(ctx, x, weight, bias, wq, ws, group):
         K = x.shape[-1]
         N = wq.shape[0]
-        x2 = x.reshape(-1, K)
-        xq, xs = quantize_last_dim(x2, group)        # == quantize_last_dim(x2.float())
-        y = w8a8_gemm_out(xq, xs, wq, ws, group, bias=bias,
-                          out_dtype=x.dtype if x.dtype in (torch.float32, torch.bfloat16,
-                                                           torch.float16) else torch.float32)
+        y, xq, xs = w8a8_linear_forward(x.reshape(-1, K), wq, ws, bias, group, x.dtype)
         ctx.save_for_backward(xq, xs, wq, ws)
         ctx.x_shape = x.shape
         ctx.x_dtype = x.dtype
@@ -48,24 +83,16 @@ class W8A8LinearFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         xq, xs, wq, ws = ctx.saved_tensors
-        group = ctx.group
-        N, K = wq.shape
+        N = wq.shape[0]
         g = grad_out.reshape(-1, N)
-        if g.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        if g.dtype not in _OUT_DTYPES:
             g = g.float()
         g = g.contiguous()
-        dx = dw = db = None
-        if ctx.needs_input_grad[0]:
-            gq, gs = quantize_last_dim(g, group)                    # along N (per token)
-            wtq, wts = requant_transpose(wq, ws, group, group)      # W^T (K, N) along N
-            dx = w8a8_gemm_out(gq, gs, wtq, wts, group, out_dtype=ctx.x_dtype
-                               if ctx.x_dtype in (torch.float32, torch.bfloat16,
-                                                  torch.float16) else torch.float32)
+        dx, dw = w8a8_linear_backward(g, xq, xs, wq, ws, ctx.group, ctx.x_dtype,
+                                      ctx.needs_input_grad[0], ctx.needs_input_grad[1])
+        if dx is not None:
             dx = dx.reshape(ctx.x_shape).to(ctx.x_dtype)
-        if ctx.needs_input_grad[1]:
-            gtq, gts = quantize_transpose(g, group)                 # dY^T (N, M) along M
-            xtq, xts = requant_transpose(xq, xs, group, group)      # X^T (K, M) along M
-            dw = w8a8_gemm(gtq, gts, xtq, xts, group)                # (N, K) fp32
+        db = None
         if ctx.has_bias and ctx.needs_input_grad[2]:
             db = g.float().sum(0)
         return dx, dw, db, None, None, None
@@ -122,14 +149,10 @@ class Int8Linear(nn.Module):
                 return self.fake_quant_forward(x)
             return W8A8LinearFunction.apply(x, self.weight, self.bias, self.weight_codes,
                                             self.weight_scales, GROUP_SIZE)
-        x2 = x.reshape(-1, x.shape[-1])
-        xq, xs = quantize_last_dim(x2)
-        out_dtype = x.dtype if x.dtype in (torch.float32, torch.bfloat16,
-                                           torch.float16) else torch.float32
-        # linear.py:69-73: fp32 GEMM, + bias in fp32, then cast to x.dtype (fused)
-        y = w8a8_gemm_out(xq, xs, self.weight_codes, self.weight_scales,
-                          bias=self.bias.detach() if self.bias is not None else None,
-                          out_dtype=out_dtype)
+        # linear.py:68-73: fp32 GEMM, + bias in fp32, then cast to x.dtype (fused)
+        y, _, _ = w8a8_linear_forward(
+            x.reshape(-1, x.shape[-1]), self.weight_codes, self.weight_scales,
+            self.bias.detach() if self.bias is not None else None)
         return y.reshape(*x.shape[:-1], self.out_features).to(x.dtype)
 
     def fake_quant_forward(self, x: torch.Tensor) -> torch.Tensor:
