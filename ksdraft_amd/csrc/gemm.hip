@@ -3,233 +3,357 @@
 //   Y[m,n] = sum_g float(P_g[m,n]) * (sa[m,g] * sw[n,g]),  P_g = sum_{k in g} A[m,k] W[n,k]
 //
 // computed in the ordered contract acc = fmaf(float(P_g), sa*sw, acc), g = 0,1,...
-// (the per-group rescale of reference ksdraft/kernels/gemm.py:42-45; sa*sw is exact in
-// fp32 because both factors are fp16 values, and float(P_g) is exact because
-// |P_g| <= 128*127^2 < 2^24).
+// (the per-group rescale of reference ksdraft/kernels/gemm.py:42-45). sa*sw is exact in
+// fp32 (both factors are fp16 values) and float(P_g) is exact (|P_g| <= 128*127^2 < 2^24).
 //
 // Layout "NT": A (M,K) and W (N,K) both K-contiguous int8; scales (rows, K/group) fp16.
-// Block tile 128x128, K step 128 (a whole number of groups), 4 waves each owning a
-// 64x64 sub-tile = 2x2 MFMA 32x32 tiles. A/W tiles are staged global -> registers ->
-// LDS (double buffered, one barrier per K step); the LDS rows are 128 bytes and the
-// 16-byte chunk index is XOR-swizzled with (row & 7) so that the ds_read_b128 operand
-// fetches of 8 consecutive rows hit 8 distinct bank groups.
+//
+// Kernel structure (one 512-thread workgroup per CU, persistent):
+//   * 128x128 output tiles; every workgroup owns a contiguous chunk of tiles in row-major
+//     order, and the workgroups of one XCD (dispatched round-robin over 8 XCDs) own
+//     neighbouring chunks, so tiles sharing an A row panel share one L2.
+//   * K advances 128 per step through a 3-slot LDS ring filled by global_load_lds_dwordx4
+//     (no VGPR staging); the DMA for step q+2 is issued at step q into the slot every
+//     wave finished reading at step q-1. Each wave waits only for its own DMA of the
+//     current step (s_waitcnt vmcnt = one later stage), then a bare s_barrier.
+//   * 8 waves as 2 (M) x 4 (N), each owning 64x32 = two 32x32 MFMA tiles.
+//   * Per group: 4 x v_mfma_i32_32x32x32_i8 per tile give the exact int32 partial; the
+//     scale products sa[m]*sw[n] of the whole 32x32 tile come from one
+//     v_mfma_f32_32x32x8_f16 outer product (a single non-zero k slot, so exact); the VALU
+//     then does cvt + fma per element. The int32 partials are double buffered so the
+//     MFMAs of group g overlap the VALU epilogue of group g-1.
+//   * LDS rows are 128 bytes; the 16-byte chunk index is XOR-swizzled with (row & 7).
 #include "ksd_common.h"
 
 namespace ksd {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 128, BN = 128, BK = 128;
+#define KSD_LDS(p) ((__attribute__((address_space(3))) void *)(p))
+// s_waitcnt vmcnt(n) lgkmcnt(0) as inline asm with a memory clobber: a hard compiler
+// barrier, so no DMA of an earlier step can be sunk below the wait (the builtin is not a
+// memory barrier for the optimizer). lgkmcnt(0): this wave's LDS reads of the slot about
+// to be refilled have returned before it enters the barrier.
+#define KSD_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ") lgkmcnt(0)" ::: "memory")
+
+constexpr int BM = 128, BN = 128, BK = 128, NSLOT = 4, NTHREADS = 512;
 
 __device__ __forceinline__ int swz(int row, int chunk) {
   return row * BK + ((chunk ^ (row & 7)) << 4);
 }
 
-// MODE 0: fp32 epilogue into Y with output type OUT (and optional bias).
-// MODE 1: export the int32 group partials P_g to `partials` (G, M, N).
+// LDS-DMA loads as inline asm (M0 = LDS destination, set in the same statement). The
+// compiler does not model these as pending LDS writes, so it does not add its own
+// vmcnt(0) before LDS reads; the kernel's explicit KSD_WAIT_VM waits carry correctness.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)KSD_LDS(p);
+}
+// `lds` must be wave-uniform (kept in an SGPR).
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(g), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma2(const void *g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_ushort %0, off"
+               :: "v"(g), "s"(lds) : "memory", "m0");
+}
+
+__device__ __forceinline__ void wg_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// MODE 0: fp32 epilogue into Y (output type OUT, optional bias).
+// MODE 1: export the int32 group partials P_g to `partials` (G, M, N) (test path).
 template <int GROUP, int OUT, bool BIAS, int MODE>
-__global__ __launch_bounds__(256, 2) void gemm_nt_kernel(
+__global__ __launch_bounds__(NTHREADS, 1) void gemm_nt_kernel(
     const int8_t *__restrict__ A, const uint16_t *__restrict__ AS,
     const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int M, int N, int K,
-    int tiles_n, const float *__restrict__ bias, void *__restrict__ Y,
+    int tiles_n, int ntiles, const float *__restrict__ bias, void *__restrict__ Y,
     int32_t *__restrict__ partials) {
-  constexpr int GPT = BK / GROUP;  // groups per K step
-  constexpr int MPG = GROUP / 32;  // 32-deep MFMAs per group
-  __shared__ __attribute__((aligned(16))) int8_t sA[2][BM * BK];
-  __shared__ __attribute__((aligned(16))) int8_t sW[2][BN * BK];
-  __shared__ __attribute__((aligned(16))) float sSA[2][GPT][BM];
-  __shared__ __attribute__((aligned(16))) float sSW[2][GPT][BN];
+  constexpr int GPT = BK / GROUP;   // groups per K step
+  constexpr int MPG = GROUP / 32;   // 32-deep int8 MFMAs per group
+  __shared__ __attribute__((aligned(16))) int8_t sA[NSLOT][BM * BK];
+  __shared__ __attribute__((aligned(16))) int8_t sW[NSLOT][BN * BK];
+  // fp16 scales in the low half of dword slots (the ushort DMA writes one dword per
+  // lane): [0,128) rows of A, [128,256) rows of W
+  __shared__ __attribute__((aligned(16))) uint32_t sS[NSLOT][GPT][256];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  // Workgroups are dispatched round-robin over the 8 XCDs (block b -> XCD b % 8), each
-  // with its own L2. Renumber so that XCD x owns a contiguous range of tiles in
-  // row-major tile order: the tiles sharing an A row panel then share one L2.
-  int bid = blockIdx.x;
+  const int wm = wave >> 2, wn = wave & 3, half = lane >> 5, l32 = lane & 31;
+  const int G = K / GROUP, KT = K / BK;
+
+  int lb;  // logical block: consecutive on one XCD
   {
-    const int nb = gridDim.x, per = nb / 8, rem = nb % 8, x = bid % 8, i = bid / 8;
-    // XCD x receives per (+1 if x < rem) blocks; they take tiles [start_x, start_x + cnt)
-    bid = x * per + min(x, rem) + i;
+    const int nb = gridDim.x, per = nb / 8, rem = nb % 8, x = blockIdx.x % 8, i = blockIdx.x / 8;
+    lb = x * per + min(x, rem) + i;
   }
-  const int tm = bid / tiles_n, tn = bid % tiles_n;
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int G = K / GROUP;
-  const int KT = K / BK;
+  const int t_begin = (int)((int64_t)ntiles * lb / gridDim.x);
+  const int t_end = (int)((int64_t)ntiles * (lb + 1) / gridDim.x);
+  const int total = (t_end - t_begin) * KT;
+  if (total == 0) return;
 
-  // global -> register staging: 1024 16-byte chunks per operand tile, 4 per thread
-  const int lrow = tid >> 3, lch = tid & 7;
-  const int8_t *gA[4];
-  const int8_t *gW[4];
-  int soff[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = lrow + 32 * i;
-    gA[i] = A + (int64_t)min(m0 + r, M - 1) * K + lch * 16;
-    gW[i] = W + (int64_t)min(n0 + r, N - 1) * K + lch * 16;
-    soff[i] = swz(r, lch);
-  }
-  // scale staging: threads 0..127 own A rows, 128..255 own W rows
-  const bool sc_a = tid < 128;
-  const int sc_r = tid & 127;
-  const uint16_t *gS = sc_a ? AS + (int64_t)min(m0 + sc_r, M - 1) * G
-                            : WS + (int64_t)min(n0 + sc_r, N - 1) * G;
-
-  v4i ra[4], rw[4];
-  uint16_t rs[GPT];  // raw fp16 bits: converting here would force an early vmcnt wait
-  auto gload = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ra[i] = *(const v4i *)(gA[i] + kt * BK);
-      rw[i] = *(const v4i *)(gW[i] + kt * BK);
-    }
-    if (MODE == 0) {
-#pragma unroll
-      for (int g = 0; g < GPT; ++g) rs[g] = gS[kt * GPT + g];
-    }
+  // DMA issue state for the stage being prefetched: per-lane source pointers of this
+  // wave's two A rows, two W rows and one scale row, advanced by one K step per issue
+  // and re-based only when the issue cursor crosses into the next tile.
+  const int ii0 = wave * 2, w4 = wave & 3;
+  const int drow0 = ii0 * 8 + (lane >> 3), drow1 = drow0 + 8;
+  const int dchunk0 = ((lane & 7) ^ (drow0 & 7)) << 4, dchunk1 = ((lane & 7) ^ (drow1 & 7)) << 4;
+  const int srow = (w4 & 1) * 64 + lane;
+  const bool s_isA = w4 < 2;
+  // wave-uniform LDS destinations, moved to SGPRs once
+  const uint32_t ldsA = __builtin_amdgcn_readfirstlane(lds_addr(&sA[0][0]) + ii0 * 1024);
+  const uint32_t ldsW = __builtin_amdgcn_readfirstlane(lds_addr(&sW[0][0]) + ii0 * 1024);
+  const uint32_t ldsS = __builtin_amdgcn_readfirstlane(
+      lds_addr(&sS[0][0][0]) + ((s_isA ? 0 : 128) + (w4 & 1) * 64) * 4);
+  const int8_t *pa0, *pa1, *pw0, *pw1;
+  const uint16_t *ps;
+  int is_tile = t_begin, is_kt = 0, is_slot = 0;
+  auto rebase = [&]() {
+    const int m0 = (is_tile / tiles_n) * BM, n0 = (is_tile % tiles_n) * BN;
+    pa0 = A + (int64_t)min(m0 + drow0, M - 1) * K + dchunk0;
+    pa1 = A + (int64_t)min(m0 + drow1, M - 1) * K + dchunk1;
+    pw0 = W + (int64_t)min(n0 + drow0, N - 1) * K + dchunk0;
+    pw1 = W + (int64_t)min(n0 + drow1, N - 1) * K + dchunk1;
+    ps = s_isA ? AS + (int64_t)min(m0 + srow, M - 1) * G : WS + (int64_t)min(n0 + srow, N - 1) * G;
   };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *(v4i *)(&sA[buf][soff[i]]) = ra[i];
-      *(v4i *)(&sW[buf][soff[i]]) = rw[i];
-    }
+  rebase();
+  auto issue = [&]() {
+    const uint32_t so = (uint32_t)is_slot * (BM * BK);
+    dma16(pa0, ldsA + so);
+    dma16(pa1, ldsA + so + 1024);
+    dma16(pw0, ldsW + so);
+    dma16(pw1, ldsW + so + 1024);
     if (MODE == 0) {
 #pragma unroll
-      for (int g = 0; g < GPT; ++g) {
-        if (sc_a) sSA[buf][g][sc_r] = f16_to_f32(rs[g]);
-        else sSW[buf][g][sc_r] = f16_to_f32(rs[g]);
-      }
+      for (int g = 0; g < GPT; ++g) dma2(ps + g, ldsS + (uint32_t)(is_slot * GPT + g) * 1024);
+    }
+    pa0 += BK; pa1 += BK; pw0 += BK; pw1 += BK; ps += GPT;
+    is_slot = is_slot == NSLOT - 1 ? 0 : is_slot + 1;
+    if (++is_kt == KT) {
+      is_kt = 0;
+      if (++is_tile < t_end) rebase();
     }
   };
 
-  float acc[2][2][16];
+  // Operand fragments of group gi: 2 A tiles x MPG and 1 W tile x MPG (ds_read_b128 each)
+  struct Frags { v4i a[MPG][2]; v4i b[MPG]; uint32_t sa[2], sw; };
+  auto load_frags = [&](int slot, int gi, Frags &f) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int kk = 0; kk < MPG; ++kk) {
+      const int kc = (gi * MPG + kk) * 2 + half;
+      f.b[kk] = *(const v4i *)(&sW[slot][swz(wn * 32 + l32, kc)]);
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int i = 0; i < 2; ++i)
+        f.a[kk][i] = *(const v4i *)(&sA[slot][swz(wm * 64 + i * 32 + l32, kc)]);
+    }
+    if (MODE == 0) {
+      const uint32_t *ss = sS[slot][gi];
+      f.sw = ss[128 + wn * 32 + l32];
+      f.sa[0] = ss[wm * 64 + l32];
+      f.sa[1] = ss[wm * 64 + 32 + l32];
+    }
+  };
+  // int32 partials of the two 32x32 tiles
+  auto mfma_group = [&](const Frags &f, v16i (&p)[2]) {
+    p[0] = (v16i){};
+    p[1] = (v16i){};
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    for (int kk = 0; kk < MPG; ++kk)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        p[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[kk][i], f.b[kk], p[i], 0, 0, 0);
+  };
+  // s[i] = sa (x) sw for the two tiles: an fp16 MFMA whose only non-zero k slot is 0
+  // (lanes 32-63 carry k = 4..7 and supply zeros), so every product is exact in fp32
+  auto scale_group = [&](const Frags &f, v16f (&s)[2]) {
+    const _Float16 zero = (_Float16)0.0f;
+    const _Float16 swv = half ? zero : __builtin_bit_cast(_Float16, (uint16_t)f.sw);
+    const v4h bs = {swv, zero, zero, zero};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const _Float16 sav = half ? zero : __builtin_bit_cast(_Float16, (uint16_t)f.sa[i]);
+      const v4h as = {sav, zero, zero, zero};
+      s[i] = __builtin_amdgcn_mfma_f32_32x32x8f16(as, bs, (v16f){}, 0, 0, 0);
+    }
+  };
 
-  gload(0);
-  lstore(0);
-  __syncthreads();
-
-  const int half = lane >> 5, l32 = lane & 31;
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) gload(kt + 1);
+  v16f acc[2];
+  acc[0] = (v16f){};
+  acc[1] = (v16f){};
+  auto epilogue = [&](const v16i (&p)[2], const v16f (&s)[2]) {
 #pragma unroll
-    for (int gi = 0; gi < GPT; ++gi) {
-      v16i p[2][2];
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][e] = fmaf((float)p[i][e], s[i][e], acc[i][e]);
+  };
+  // Stores the finished tile: full tiles without per-element bounds checks, edge tiles
+  // masked.
+  auto store_tile = [&](int q) -> bool {
+    const int t = t_begin + q / KT;
+    const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
+    const int col = n0 + wn * 32 + l32;
+    const bool full = m0 + BM <= M && n0 + BN <= N;
+    if (full) {
+      const float b = BIAS ? bias[col] : 0.0f;
+      const int64_t base = (int64_t)(m0 + wm * 64 + half * 4) * N + col;
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) p[i][j] = (v16i){};
-#pragma unroll
-      for (int kk = 0; kk < MPG; ++kk) {
-        const int kc = (gi * MPG + kk) * 2 + half;
-        v4i a[2], b[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int row = wm * 64 + i * 32 + l32;
-          a[i] = *(const v4i *)(&sA[cur][swz(row, kc)]);
+        for (int e = 0; e < 16; ++e) {
+          float v = acc[i][e];
+          if (BIAS) v = v + b;
+          store_out<OUT>(Y, base + (int64_t)(i * 32 + (e >> 2) * 8 + (e & 3)) * N, v);
         }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int col = wn * 64 + j * 32 + l32;
-          b[j] = *(const v4i *)(&sW[cur][swz(col, kc)]);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            p[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], p[i][j], 0, 0, 0);
-      }
-      if (MODE == 0) {
-        float sw[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) sw[j] = sSW[cur][gi][wn * 64 + j * 32 + l32];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float4 sa4 =
-                *(const float4 *)(&sSA[cur][gi][wm * 64 + i * 32 + q * 8 + half * 4]);
-            const float sa[4] = {sa4.x, sa4.y, sa4.z, sa4.w};
-#pragma unroll
-            for (int e4 = 0; e4 < 4; ++e4)
-#pragma unroll
-              for (int j = 0; j < 2; ++j) {
-                const int e = q * 4 + e4;
-                acc[i][j][e] = fmaf((float)p[i][j][e], sa[e4] * sw[j], acc[i][j][e]);
-              }
-          }
-      } else {
-        const int g = kt * GPT + gi;
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              const int row = m0 + wm * 64 + i * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
-              const int col = n0 + wn * 64 + j * 32 + l32;
-              if (row < M && col < N)
-                partials[((int64_t)g * M + row) * N + col] = p[i][j][e];
-            }
-      }
-    }
-    if (kt + 1 < KT) lstore(cur ^ 1);
-    __syncthreads();
-  }
-
-  if (MODE == 0) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + wn * 64 + j * 32 + l32;
-      if (col >= N) continue;
+    } else if (col < N) {
       const float b = BIAS ? bias[col] : 0.0f;
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int row = m0 + wm * 64 + i * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
-          if (row >= M) continue;
-          float v = acc[i][j][e];
-          if (BIAS) v = v + b;
-          store_out<OUT>(Y, (int64_t)row * N + col, v);
+          if (row < M) {
+            float v = acc[i][e];
+            if (BIAS) v = v + b;
+            store_out<OUT>(Y, (int64_t)row * N + col, v);
+          }
         }
     }
+    acc[0] = (v16f){};
+    acc[1] = (v16f){};
+    return full;
+  };
+  auto store_partials = [&](int q, int gi, const v16i (&p)[2]) {
+    const int t = t_begin + q / KT, g = (q % KT) * GPT + gi;
+    const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
+    const int col = n0 + wn * 32 + l32;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = m0 + wm * 64 + i * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
+        if (row < M && col < N) partials[((int64_t)g * M + row) * N + col] = p[i][e];
+      }
+  };
+
+  // One K step (half of a super-step); (pc, sc) receive this step's group, (pp, sp)
+  // hold the previous one, whose VALU epilogue is interleaved with this step's MFMAs.
+  auto half_step = [&](int q, v16i (&pc)[2], v16f (&sc)[2], v16i (&pp)[2], v16f (&sp)[2]) {
+    const int kt = q % KT;
+    const int slot = q % NSLOT;
+    if (MODE == 1) {
+#pragma unroll
+      for (int gi = 0; gi < GPT; ++gi) {
+        Frags f;
+        load_frags(slot, gi, f);
+        mfma_group(f, pc);
+        store_partials(q, gi, pc);
+      }
+      return;
+    }
+    if constexpr (GPT == 1) {
+      // sp is zero at a tile's first step, so the previous-group epilogue is unconditional
+      Frags f;
+      load_frags(slot, 0, f);
+      mfma_group(f, pc);
+      scale_group(f, sc);
+      epilogue(pp, sp);
+      __builtin_amdgcn_sched_group_barrier(0x100, 15, 0);  // DS reads: fragments + scales
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {                         // 8 int8 MFMAs, VALU between
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+      }
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {                         // 2 fp16 outer products
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+      }
+      if (kt == KT - 1) {
+        epilogue(pc, sc);
+        store_tile(q);
+        sc[0] = (v16f){};   // the next step (a new tile) adds cvt(pc) * 0
+        sc[1] = (v16f){};
+      }
+    } else {
+#pragma unroll
+      for (int gi = 0; gi < GPT; ++gi) {
+        Frags f;
+        load_frags(slot, gi, f);
+        mfma_group(f, pc);
+        scale_group(f, sc);
+        epilogue(pc, sc);
+      }
+      if (kt == KT - 1) store_tile(q);
+    }
+  };
+
+  // Super-step: K steps q0 and q0+1 behind one barrier. Each wave first waits for all
+  // of its outstanding vector-memory ops (the DMA of these two stages, issued one
+  // super-step earlier, and any tile stores), then the barrier makes every wave's DMA
+  // visible and guarantees the slots of the previous super-step are no longer read;
+  // the next two stages are then prefetched into those slots.
+  issue();
+  if (total > 1) issue();
+  v16i p0[2], p1[2];
+  v16f s0[2], s1[2];
+  p0[0] = p0[1] = p1[0] = p1[1] = (v16i){};
+  s0[0] = s0[1] = s1[0] = s1[1] = (v16f){};
+  for (int q = 0; q < total; q += 2) {
+    KSD_WAIT_VM(0);
+    wg_barrier();
+    if (q + 2 < total) issue();
+    if (q + 3 < total) issue();
+    half_step(q, p0, s0, p1, s1);
+    if (q + 1 < total) half_step(q + 1, p1, s1, p0, s0);
   }
 }
 
-template <int GROUP, int OUT, bool BIAS>
-static void launch_gemm(const int8_t *a, const uint16_t *as, const int8_t *w,
-                        const uint16_t *ws, int M, int N, int K, const float *bias, void *y,
-                        hipStream_t st) {
+// one workgroup per CU; the CU count is a device constant, cached per device
+static int cu_count() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    __atomic_store_n(&cached[dev], n, __ATOMIC_RELAXED);
+  }
+  return n;
+}
+
+template <int GROUP, int OUT, bool BIAS, int MODE>
+static void launch(const int8_t *a, const uint16_t *as, const int8_t *w, const uint16_t *ws,
+                   int M, int N, int K, const float *bias, void *y, int32_t *partials,
+                   hipStream_t st) {
   const int tn = (N + BN - 1) / BN, tm = (M + BM - 1) / BM;
-  gemm_nt_kernel<GROUP, OUT, BIAS, 0><<<dim3(tm * tn), dim3(256), 0, st>>>(
-      a, as, w, ws, M, N, K, tn, bias, y, nullptr);
+  const int ntiles = tm * tn;
+  const int grid = min(ntiles, cu_count());
+  gemm_nt_kernel<GROUP, OUT, BIAS, MODE><<<dim3(grid), dim3(NTHREADS), 0, st>>>(
+      a, as, w, ws, M, N, K, tn, ntiles, bias, y, partials);
 }
 
 template <int GROUP, int OUT>
-static void launch_gemm_b(const int8_t *a, const uint16_t *as, const int8_t *w,
-                          const uint16_t *ws, int M, int N, int K, const float *bias, void *y,
-                          hipStream_t st) {
-  if (bias) launch_gemm<GROUP, OUT, true>(a, as, w, ws, M, N, K, bias, y, st);
-  else launch_gemm<GROUP, OUT, false>(a, as, w, ws, M, N, K, bias, y, st);
+static void launch_b(const int8_t *a, const uint16_t *as, const int8_t *w, const uint16_t *ws,
+                     int M, int N, int K, const float *bias, void *y, hipStream_t st) {
+  if (bias) launch<GROUP, OUT, true, 0>(a, as, w, ws, M, N, K, bias, y, nullptr, st);
+  else launch<GROUP, OUT, false, 0>(a, as, w, ws, M, N, K, bias, y, nullptr, st);
 }
 
 template <int GROUP>
-static int launch_gemm_o(const int8_t *a, const uint16_t *as, const int8_t *w,
-                         const uint16_t *ws, int M, int N, int K, const float *bias, void *y,
-                         int y_dtype, hipStream_t st) {
+static int launch_o(const int8_t *a, const uint16_t *as, const int8_t *w, const uint16_t *ws,
+                    int M, int N, int K, const float *bias, void *y, int y_dtype,
+                    hipStream_t st) {
   switch (y_dtype) {
-    case KSD_F32: launch_gemm_b<GROUP, KSD_F32>(a, as, w, ws, M, N, K, bias, y, st); break;
-    case KSD_BF16: launch_gemm_b<GROUP, KSD_BF16>(a, as, w, ws, M, N, K, bias, y, st); break;
-    case KSD_F16: launch_gemm_b<GROUP, KSD_F16>(a, as, w, ws, M, N, K, bias, y, st); break;
-    case KSD_F16_SAT: launch_gemm_b<GROUP, KSD_F16_SAT>(a, as, w, ws, M, N, K, bias, y, st); break;
+    case KSD_F32: launch_b<GROUP, KSD_F32>(a, as, w, ws, M, N, K, bias, y, st); break;
+    case KSD_BF16: launch_b<GROUP, KSD_BF16>(a, as, w, ws, M, N, K, bias, y, st); break;
+    case KSD_F16: launch_b<GROUP, KSD_F16>(a, as, w, ws, M, N, K, bias, y, st); break;
+    case KSD_F16_SAT: launch_b<GROUP, KSD_F16_SAT>(a, as, w, ws, M, N, K, bias, y, st); break;
     default: return fail(KSD_ETYPE, "w8a8_gemm: unsupported output dtype %d", y_dtype);
   }
   return check_launch("w8a8_gemm_nt");
@@ -261,9 +385,9 @@ extern "C" int ksd_w8a8_gemm_nt(const int8_t *a, const uint16_t *a_scales, const
   if (M == 0 || N == 0 || K == 0) return KSD_OK;
   hipStream_t st = (hipStream_t)stream;
   switch (group) {
-    case 32: return launch_gemm_o<32>(a, a_scales, w, w_scales, (int)M, (int)N, (int)K, bias, y, y_dtype, st);
-    case 64: return launch_gemm_o<64>(a, a_scales, w, w_scales, (int)M, (int)N, (int)K, bias, y, y_dtype, st);
-    default: return launch_gemm_o<128>(a, a_scales, w, w_scales, (int)M, (int)N, (int)K, bias, y, y_dtype, st);
+    case 32: return launch_o<32>(a, a_scales, w, w_scales, (int)M, (int)N, (int)K, bias, y, y_dtype, st);
+    case 64: return launch_o<64>(a, a_scales, w, w_scales, (int)M, (int)N, (int)K, bias, y, y_dtype, st);
+    default: return launch_o<128>(a, a_scales, w, w_scales, (int)M, (int)N, (int)K, bias, y, y_dtype, st);
   }
 }
 
@@ -274,12 +398,10 @@ extern "C" int ksd_w8a8_group_partials(const int8_t *a, const int8_t *w, int64_t
   if (rc != KSD_OK) return rc;
   if (M == 0 || N == 0 || K == 0) return KSD_OK;
   hipStream_t st = (hipStream_t)stream;
-  const int tn = (int)((N + BN - 1) / BN), tm = (int)((M + BM - 1) / BM);
-  const dim3 grid(tm * tn), block(256);
   switch (group) {
-    case 32: gemm_nt_kernel<32, KSD_F32, false, 1><<<grid, block, 0, st>>>(a, nullptr, w, nullptr, (int)M, (int)N, (int)K, tn, nullptr, nullptr, partials); break;
-    case 64: gemm_nt_kernel<64, KSD_F32, false, 1><<<grid, block, 0, st>>>(a, nullptr, w, nullptr, (int)M, (int)N, (int)K, tn, nullptr, nullptr, partials); break;
-    default: gemm_nt_kernel<128, KSD_F32, false, 1><<<grid, block, 0, st>>>(a, nullptr, w, nullptr, (int)M, (int)N, (int)K, tn, nullptr, nullptr, partials); break;
+    case 32: launch<32, KSD_F32, false, 1>(a, nullptr, w, nullptr, (int)M, (int)N, (int)K, nullptr, nullptr, partials, st); break;
+    case 64: launch<64, KSD_F32, false, 1>(a, nullptr, w, nullptr, (int)M, (int)N, (int)K, nullptr, nullptr, partials, st); break;
+    default: launch<128, KSD_F32, false, 1>(a, nullptr, w, nullptr, (int)M, (int)N, (int)K, nullptr, nullptr, partials, st); break;
   }
   return check_launch("w8a8_group_partials");
 }

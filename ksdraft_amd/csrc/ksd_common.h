@@ -44,11 +44,18 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 constexpr float kScaleMin = 5.9604644775390625e-08f;  // 2**-24, quant.py:22
 constexpr float kScaleMax = 65504.0f;                 // quant.py:23
 
+// Materialise v as an fp32 register value. Without this the backend may fuse the op
+// that produced v with the narrowing to fp16 (e.g. fma + cvt -> v_fma_mixlo_f16), which
+// rounds once instead of twice (fp32, then fp16) and differs on fp16 ties.
+__device__ __forceinline__ float opaque(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
 __device__ __forceinline__ float f16_round(float v) {  // fp32 -> fp16 -> fp32
-  return (float)(_Float16)v;
+  return (float)(_Float16)opaque(v);
 }
 __device__ __forceinline__ uint16_t f16_bits(float v) {
-  return __builtin_bit_cast(uint16_t, (_Float16)v);
+  return __builtin_bit_cast(uint16_t, (_Float16)opaque(v));
 }
 __device__ __forceinline__ float f16_to_f32(uint16_t b) {
   return (float)__builtin_bit_cast(_Float16, b);
@@ -106,7 +113,7 @@ template <> __device__ __forceinline__ void store_out<KSD_F16>(void *y, int64_t 
 }
 // fp16 then clamp(+-65504): ks3_int8.py:242 `.to(FP16).clamp(-65504., 65504.)`.
 template <> __device__ __forceinline__ void store_out<KSD_F16_SAT>(void *y, int64_t idx, float v) {
-  _Float16 h = (_Float16)v;
+  _Float16 h = (_Float16)opaque(v);
   float hf = (float)h;
   if (hf > kScaleMax) h = (_Float16)kScaleMax;
   if (hf < -kScaleMax) h = (_Float16)(-kScaleMax);

@@ -78,11 +78,12 @@ def test_epilogue_bias_and_output_dtypes():
     ta = _gpu(aq, as_, wq, ws)
     exp = torch.from_numpy(og.gemm_ordered(aq, as_, wq, ws, bias=bias.numpy()))
     y32 = kg.w8a8_gemm_out(*ta, bias=bias.to(DEV)).cpu()
-    assert torch.equal(y32, exp)
+    torch.testing.assert_close(y32, exp, rtol=0, atol=0)
     ybf = kg.w8a8_gemm_out(*ta, bias=bias.to(DEV), out_dtype=torch.bfloat16).cpu()
-    assert torch.equal(ybf, exp.to(torch.bfloat16))
+    torch.testing.assert_close(ybf, exp.to(torch.bfloat16), rtol=0, atol=0)
     y16 = kg.w8a8_gemm_out(*ta, out_dtype=torch.float16).cpu()
-    assert torch.equal(y16, torch.from_numpy(og.gemm_ordered(aq, as_, wq, ws)).half())
+    torch.testing.assert_close(y16, torch.from_numpy(og.gemm_ordered(aq, as_, wq, ws)).half(),
+                               rtol=0, atol=0)
 
 
 def test_fp16_saturating_output():
@@ -127,3 +128,24 @@ def test_config2_forward_sampled_rows():
     assert np.array_equal(y.cpu().numpy()[rows], exp)
     p = kg.w8a8_group_partials(xq[:128], wq).cpu().numpy()
     assert np.array_equal(p[:, :8], og.group_partials(hq[:8], hwq))
+
+
+@pytest.mark.parametrize("mag", [1e-4, 3e-7])
+def test_subnormal_fp16_scales(mag):
+    """Inputs this small give fp16-subnormal group scales (amax/127 < 6.1e-5)."""
+    g = torch.Generator().manual_seed(21)
+    a = torch.randn(96, 384, generator=g) * mag
+    w = torch.randn(160, 384, generator=g) * mag
+    aq, as_ = oq.quantize_last_dim(a.numpy())
+    wq, ws = oq.quantize_last_dim(w.numpy())
+    assert (np.abs(as_.astype(np.float32)) < 6.1e-5).all()
+    y = kg.w8a8_gemm(*_gpu(aq, as_, wq, ws)).cpu().numpy()
+    assert np.array_equal(y, og.gemm_ordered(aq, as_, wq, ws))
+
+
+def test_many_tiles_persistent_chunks():
+    """More tiles than CUs and an odd K-step count per tile (KT=5)."""
+    aq, as_, wq, ws = _operands(23, 2304, 640, 1920)
+    y = kg.w8a8_gemm(*_gpu(aq, as_, wq, ws)).cpu().numpy()
+    rows = np.arange(0, 2304, 37)
+    assert np.array_equal(y[rows], og.gemm_ordered(aq, as_, wq, ws, rows=rows))
