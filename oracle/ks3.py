@@ -1,0 +1,199 @@
+"""numpy restatement of the KS3 int8 cell (test infrastructure only).
+
+Follows reference ksdraft/kernels/ks3_int8.py:
+  * make_tanh_lut                  :50-54
+  * _round_div127                  :57-66
+  * _lut_index                     :69-72
+  * pack_spine / warp scalars      :87-92, 139-146, 158-165
+  * _spine_features, 'int8' mode   :205-234  (rank 1)
+  * _project (coords)              :238-260
+  * _KS3Int8Train.backward geometry VJP :354-401
+
+Every fp16 op of the reference is a torch fp16 tensor op: the operation is evaluated in
+fp32 ("opmath") with Python scalars converted to fp32, then rounded to fp16. `h()`
+below applies exactly that rounding. tanh is evaluated in float64 and rounded through
+fp32, i.e. a correctly rounded fp32 tanh, then to fp16.
+
+Pinned by: tests/golden/ks3_int8_golden.npz, written by tests/golden/make_ks3_golden.py
+from the reference's own CPU path (bit-exact spine features and VJP coordinate
+gradient given identical GEMM outputs); the LUT against an mpmath-free closed form
+check (float64 tanh, tie distance); _round_div127 by brute force over integer ranges
+(tests/test_oracle_ks3.py).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .quant import dequantize_last_dim, quantize_last_dim
+
+TANH_DOMAIN = 3.2
+f32 = np.float32
+f16 = np.float16
+
+
+def h(x):
+    """Round (an fp32 evaluation) to fp16 and return it as fp32 values."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def tanh32(x):
+    """Correctly rounded fp32 tanh of fp32 inputs (float64 evaluation)."""
+    return np.tanh(np.asarray(x, np.float64)).astype(np.float32)
+
+
+def make_tanh_lut():
+    """ks3_int8.py:50-54: round(tanh(i * (3.2/127)) * 127) for i in [-128, 127]."""
+    idx = np.arange(-128, 128, dtype=np.float32)
+    arg = (idx * f32(TANH_DOMAIN / 127.0)).astype(np.float32)
+    v = (tanh32(arg) * f32(127.0)).astype(np.float32)
+    return np.clip(np.rint(v), -127, 127).astype(np.int8)
+
+
+def round_div127(v):
+    """ks3_int8.py:57-66: trunc(v/127) with a +-1 correction for |remainder| > 63."""
+    v = np.asarray(v, np.int64)
+    q = np.trunc(v / 127.0).astype(np.int64)
+    # exact integer trunc division (the float path above is exact for |v| < 2^52; make it exact anyway)
+    q = np.where(v >= 0, v // 127, -((-v) // 127))
+    r = v - q * 127
+    return q + np.where(r > 63, 1, np.where(r < -63, -1, 0))
+
+
+def lut_index(x16):
+    """ks3_int8.py:69-72 on fp16 values (given as fp32)."""
+    c = np.clip(np.asarray(x16, np.float32), f32(-TANH_DOMAIN), f32(TANH_DOMAIN))
+    c = h(c)  # clamp result is an fp16 tensor
+    s = h(c * f32(127.0 / TANH_DOMAIN))
+    return np.rint(s).astype(np.int64)
+
+
+def warp_scalars(warp_scale_codes, warp_scale_scales, warp_shift_codes, warp_shift_scales):
+    """ks3_int8.py:158-165 in the fp16 domain: dequantize (fp32, exact) then fp16."""
+    sc = h(dequantize_last_dim(warp_scale_codes, warp_scale_scales, 128).reshape(-1))
+    sh = h(dequantize_last_dim(warp_shift_codes, warp_shift_scales, 128).reshape(-1))
+    return sc, sh
+
+
+def spine_features_int8(coords, spine_codes, spine_scale, scale16, shift16, lut):
+    """ks3_int8.py:205-234, rank 1. coords (M, F) fp32 holding fp16 values;
+    spine_codes (F, 6) int8; spine_scale (F,) fp16; scale16/shift16 (F,) fp16-valued.
+    Returns h (M, F) fp32."""
+    x = np.asarray(coords, np.float32)
+    lut = np.asarray(lut, np.int64)
+    c = np.asarray(spine_codes, np.int64)
+    c0, c1, c2, c3, c4, c5 = (c[:, k][None, :] for k in range(6))
+    ps16 = np.asarray(spine_scale, np.float16).astype(np.float32)[None, :]
+    sc = np.asarray(scale16, np.float32)[None, :]
+    sh = np.asarray(shift16, np.float32)[None, :]
+
+    ti = lut_index(h(x * f32(0.25)))
+    tq = lut[np.clip(ti + 128, 0, 255)]
+    tq16 = h(tq.astype(np.float32))
+    warp = h(sc * h(h(tq16 * f32(4.0 / 127.0)) + sh))
+    zi = lut_index(warp)
+    zq = lut[np.clip(zi + 128, 0, 255)]
+
+    a = 2 * c0 - 2 * c1 + c2 + c3
+    b = -3 * c0 + 3 * c1 - 2 * c2 - c3
+    poly = a * 64
+    poly = round_div127(poly * tq * 4) + b * 64
+    poly = round_div127(poly * tq * 4) + c2 * 64
+    poly = round_div127(poly * tq * 4) + c0 * 64
+    warped = 4 * c5 * 64
+    warped = round_div127(warped * zq) + 2 * c4 * 64
+    warped = round_div127(warped * zq) - 3 * c5 * 64
+    warped = round_div127(warped * zq) - c4 * 64
+    s = poly + warped
+    tdiv = np.where(s >= 0, s // 64, -((-s) // 64))
+    hv = (x + h(h(tdiv.astype(np.float32)) * ps16)).astype(np.float32)
+    hv = np.maximum(hv, f32(0.0))
+    pre = h(np.clip((np.abs(hv) / f32(127.0)).astype(np.float32), f32(2.0 ** -24), f32(65504.0)))
+    hq = np.clip(np.rint((hv / pre).astype(np.float32)), -127, 127)
+    hq = np.maximum(hq, 0)
+    hq16 = h(hq.astype(np.float32))
+    return (h(hq16 * hq16) * (pre * pre).astype(np.float32)).astype(np.float32)
+
+
+def coords_from_gemm(y32):
+    """ks3_int8.py:241-242: fp32 GEMM output -> fp16, clamped to +-65504, back to fp32."""
+    y = np.asarray(y32, np.float32).astype(np.float16)
+    return np.clip(y.astype(np.float32), -65504.0, 65504.0).astype(np.float32)
+
+
+def spine_params(spine_codes, spine_scale, warp_scale_codes, warp_scale_scales,
+                 warp_shift_codes, warp_shift_scales):
+    """The fp16 coefficients of the VJP: c_k = fp16(code * scale) (ks3_int8.py:355-362)."""
+    call = np.asarray(spine_codes, np.float32) * np.asarray(spine_scale, np.float16).astype(np.float32)[:, None]
+    coef = h(call)  # (F, 6)
+    sc, sh = warp_scalars(warp_scale_codes, warp_scale_scales, warp_shift_codes, warp_shift_scales)
+    return coef, sc, sh
+
+
+def vjp(value16, coords, coef, scale16, shift16, warp_scale_raw, warp_shift_raw):
+    """Geometry VJP of ks3_int8.py:354-401 (rank 1), every op rounded to fp16.
+
+    Returns dc (M, F) fp32 holding fp16 values, and the fp32 column sums
+    (d0..d5, dscale_t, dshift_t) before their final fp16 rounding, plus dcoeff (F,6),
+    dscale (F,), dshift (F,) fp16-valued as the reference returns them."""
+    v = np.asarray(value16, np.float32)
+    x16 = h(coords)
+    c0, c1, c2, c3, c4, c5 = (coef[:, k][None, :] for k in range(6))
+    sc = np.asarray(scale16, np.float32)[None, :]
+    sh = np.asarray(shift16, np.float32)[None, :]
+
+    t = h(f32(4.0) * h(tanh32(h(x16 * f32(0.25)))))
+    z = h(tanh32(h(sc * h(t + sh))))
+    cubic = h(h(h(h(2 * c0) - h(2 * c1)) + c2) + c3)
+    quad = h(h(h(h(-3 * c0) + h(3 * c1)) - h(2 * c2)) - c3)
+    spine = h(h(h(h(h(h(cubic * t) + quad) * t) + c2) * t) + c0)
+    warped = h(h(h(h(h(h(h(h(4 * c5) * z) + h(2 * c4)) * z) - h(3 * c5)) * z) - c4))
+    dpre = h(h(v * f32(2.0)) * np.maximum(h(h(x16 + spine) + warped), f32(0.0)))
+    dpoly = h(h(h(h(3 * cubic) * t) + h(2 * quad)) * t)
+    dpoly = h(dpoly + c2)
+    dwarp = h(h(h(h(h(12 * c5) * z) + h(4 * c4)) * z) - h(3 * c5))
+    dz = h(dwarp * h(f32(1.0) - h(z * z)))
+    dmean = h(h(dpre * h(dpoly + h(dz * sc))) * h(f32(1.0) - h(h(t * t) * f32(0.0625))))
+
+    t2 = h(t * t)
+    t3 = h(t2 * t)
+    z2 = h(z * z)
+    z3 = h(z2 * z)
+    terms = [
+        h(dpre * h(h(h(2 * t3) - h(3 * t2)) + f32(1.0))),
+        h(dpre * h(h(-2 * t3) + h(3 * t2))),
+        h(dpre * h(h(t3 - h(2 * t2)) + t)),
+        h(dpre * h(t3 - t2)),
+        h(dpre * h(h(2 * z2) - f32(1.0))),
+        h(dpre * h(h(4 * z3) - h(3 * z))),
+        h(h(dpre * dz) * h(t + sh)),
+        h(h(dpre * dz) * sc),
+    ]
+    sums = np.stack([tm.astype(np.float64).sum(0) for tm in terms])  # (8, F)
+    d = h(sums.astype(np.float32))
+    dcoeff = d[:6].T.copy()
+    dscale_t = d[6]
+    dshift_t = h(d[7] * f32(0.5))
+    sig = (1.0 / (1.0 + np.exp(-np.asarray(warp_scale_raw, np.float64)))).astype(np.float32)
+    th = tanh32(np.asarray(warp_shift_raw, np.float32))
+    dscale = h(dscale_t * sig)
+    dshift = h(dshift_t * (f32(1.0) - (th * th).astype(np.float32)))
+    dc = h(v + dmean)
+    return dc, sums.astype(np.float32), dcoeff, dscale, dshift
+
+
+def pack_masters(master_down, master_up, master_coefficients, master_raw_scale,
+                 master_raw_shift, group=128):
+    """_repack_masters (ks3_int8.py:262-277): every tensor of the cell from its masters."""
+    dq, ds = quantize_last_dim(master_down, group)
+    uq, us = quantize_last_dim(master_up, group)
+    sq, ss = quantize_last_dim(np.asarray(master_coefficients, np.float32).reshape(-1, 6), group)
+    ss = ss.reshape(-1)
+    raw_s = np.asarray(master_raw_scale, np.float64)
+    scale_t = (np.log1p(np.exp(-np.abs(raw_s))) + np.maximum(raw_s, 0)).astype(np.float32) + f32(1e-4)
+    shift_t = (f32(0.5) * tanh32(np.asarray(master_raw_shift, np.float32))).astype(np.float32)
+    wsc, wss = quantize_last_dim(scale_t.reshape(-1, 1), group)
+    whc, whs = quantize_last_dim(shift_t.reshape(-1, 1), group)
+    return dict(down_codes=dq, down_scales=ds, up_codes=uq, up_scales=us, spine_codes=sq,
+                spine_scale=ss, warp_scale_codes=wsc, warp_scale_scales=wss,
+                warp_shift_codes=whc, warp_shift_scales=whs)
