@@ -112,6 +112,84 @@ int ksd_w8a8_gemm_nt(const int8_t *a, const uint16_t *a_scales, const int8_t *w,
 int ksd_w8a8_group_partials(const int8_t *a, const int8_t *w, int64_t M, int64_t N,
                             int64_t K, int group, int32_t *partials, void *stream);
 
+/*
+ * K6 (+ the requantization that follows it) — KS3 int8-mode spine features, rank 1, of
+ * the composed contract: _spine_features 'int8' (reference ksdraft/kernels/ks3_int8.py:205-234)
+ * on the coordinates of _project (:241-242), then quantize_last_dim(h, group) (:309, :330).
+ *   coords            (M, F) fp16: fp16(GEMM(x, down)) clamped to +-65504 (ksd_w8a8_gemm_nt
+ *                     with KSD_F16_SAT writes exactly this)
+ *   spine_codes       (F, 6) int8, spine_scale (F,) fp16            (pack_spine, :87-92)
+ *   warp_scale, warp_shift (F,) fp16: _warp_scalars(FP16), i.e. fp16(dequantize) of the
+ *                     one-element warp groups                       (:158-165)
+ *   tanh_lut          (256,) int8, 4-byte aligned                   (make_tanh_lut, :50-54)
+ *   h                 NULL or (M, F) fp32: the features (_spine_features' return value)
+ *   h_codes, h_scales NULL, or (M, F) int8 and (M, ceil(F/group)) fp16: quantize_last_dim(h)
+ */
+int ksd_ks3_spine_fwd(const uint16_t *coords, int64_t M, int64_t F, const int8_t *spine_codes,
+                      const uint16_t *spine_scale, const uint16_t *warp_scale,
+                      const uint16_t *warp_shift, const int8_t *tanh_lut, int group, float *h,
+                      int8_t *h_codes, uint16_t *h_scales, void *stream);
+
+/*
+ * K8 — the spine + requantization stage of project_fused / _fused_gemm_spine, 'int8' mode
+ * (reference ksdraft/kernels/ks3_triton.py:47-75, 137-156 and 159-195), applied to the
+ * fp32 down-projection accumulator. This is the reference's GPU-eval contract, which
+ * differs from the composed one (fp32 coordinates, fp32 LUT index, no truncation, pre-ReLU
+ * group pre-scale, exact squares, a second per-group requantization).
+ *   acc        (M, F) fp32: w8a8_gemm(xq, xs, down_codes, down_scales)
+ *   spine/warp buffers and tanh_lut as for ksd_ks3_spine_fwd
+ *   h_codes (M, F) int8, h_scales (M, ceil(F/group)) fp16
+ */
+int ksd_ks3_spine_fused(const float *acc, int64_t M, int64_t F, const int8_t *spine_codes,
+                        const uint16_t *spine_scale, const uint16_t *warp_scale,
+                        const uint16_t *warp_shift, const int8_t *tanh_lut, int group,
+                        int8_t *h_codes, uint16_t *h_scales, void *stream);
+
+/*
+ * Number of row blocks (the first dim of the partials workspace) ksd_ks3_vjp uses for M
+ * rows: ceil(M / 128). Fixes the order of the column reductions.
+ */
+int ksd_ks3_vjp_row_blocks(int64_t M, int64_t *n_row_blocks);
+
+/*
+ * K10 steps 2-4 — the fp16 geometry VJP of _KS3Int8Train.backward, rank 1
+ * (reference ksdraft/kernels/ks3_int8.py:354-401), with dc emitted directly as the two
+ * int8 operands of the backward GEMMs.
+ *   value      (M, F) fp16: fp16(GEMM(quant(g), quant(dequant(up)^T)))  (:345-352)
+ *   coords     (M, F) fp16, as saved by the forward
+ *   spine_codes, spine_scale, warp_scale, warp_shift as for ksd_ks3_spine_fwd;
+ *              c_k = fp16(code_k * spine_scale)                           (:355-362)
+ *   dc         NULL or (M, F) fp16: value + dmean                        (:398-401)
+ *   dc_codes, dc_scales    NULL or (M, F) int8, (M, ceil(F/group)) fp16:
+ *                          quantize_last_dim(dc, group)                   (:410)
+ *   dct_codes, dct_scales  NULL or (F, M) int8, (F, ceil(M/group)) fp16:
+ *                          quantize_last_dim(dc.t(), group)               (:417)
+ *   partials   (n_row_blocks, 8, F) fp32 workspace: per-block column sums of the eight
+ *              reduction terms d0..d5, dscale_t, 2*dshift_t (:379-388)
+ */
+int ksd_ks3_vjp(const uint16_t *value, const uint16_t *coords, int64_t M, int64_t F,
+                const int8_t *spine_codes, const uint16_t *spine_scale, const uint16_t *warp_scale,
+                const uint16_t *warp_shift, int group,
+                uint16_t *dc, int8_t *dc_codes, uint16_t *dc_scales, int8_t *dct_codes,
+                uint16_t *dct_scales, float *partials, int64_t n_row_blocks, void *stream);
+
+/*
+ * K10 step 3 — reduce the partials of ksd_ks3_vjp in fixed block order and apply the
+ * reference's fp16 roundings and STE chain (reference ksdraft/kernels/ks3_int8.py:379-395).
+ *   warp_scale_raw, warp_shift_raw (F,) fp32 master parameters
+ *   sums    NULL or (8, F) fp32: the column sums before fp16 rounding
+ *   dcoeff  (F, 6) fp16; dscale, dshift (F,) fp16
+ */
+int ksd_ks3_vjp_finalize(const float *partials, int64_t n_row_blocks, int64_t F,
+                         const float *warp_scale_raw, const float *warp_shift_raw, float *sums,
+                         uint16_t *dcoeff, uint16_t *dscale, uint16_t *dshift, void *stream);
+
+/*
+ * Test-only export: fp16 tanh of n fp16 values through the table the VJP reads,
+ * i.e. torch.tanh on an fp16 tensor (reference ksdraft/kernels/ks3_int8.py:365-366).
+ */
+int ksd_ks3_tanh16(const uint16_t *x, int64_t n, uint16_t *y, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

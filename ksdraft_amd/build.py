@@ -9,11 +9,15 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libksdraft_amd.so")
-SOURCES = ["quant.hip", "gemm.hip"]
+SOURCES = ["quant.hip", "gemm.hip", "ks3.hip"]
+OBJDIR = os.path.join(HERE, "_build")
+# generated at build time (git-ignored): fp16 tanh table for the KS3 kernels
+TANH_INC = os.path.join(CSRC, "tanh16_table.inc")
 
 ARCH = "gfx950"
 
@@ -37,16 +41,31 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, *srcs]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         # hipcc's host pass warns about the device-only target feature; only errors fail
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-8000:]}")
+
+
+def build(verbose: bool = False) -> str:
+    sys.path.insert(0, CSRC)
+    try:
+        import gen_tanh16
+    finally:
+        sys.path.pop(0)
+    gen_tanh16.write(TANH_INC)
+    os.makedirs(OBJDIR, exist_ok=True)
+    objs = [os.path.join(OBJDIR, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    cmds = [[hipcc(), *flags, "-c", "-o", o, os.path.join(CSRC, s)]
+            for s, o in zip(SOURCES, objs)]
+    with ThreadPoolExecutor(len(cmds)) as ex:
+        list(ex.map(lambda c: _run(c, verbose), cmds))
+    tmp = LIB + ".tmp"
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB)
     return LIB
 

@@ -85,19 +85,32 @@ template <> struct Elem<KSD_F16> {
   __device__ __forceinline__ static float load(const T *p) { return f16_to_f32(*p); }
 };
 
+// NaN semantics follow torch's quantize_last_dim on the CPU: amax propagates NaN, the
+// NaN then passes through clamp, its fp16 scale is stored as 0x7fff, and the NaN codes
+// convert to 0 (tests/test_oracle_quant.py pins this against torch).
+
+// max of two magnitudes (sign bits clear) that propagates NaN: for non-negative floats
+// the IEEE order is the integer order of the bit patterns, and NaNs sort above inf.
+__device__ __forceinline__ float amax2(float a, float b) {
+  return __builtin_bit_cast(float, max(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)));
+}
+
 // GS scale of a group from its amax: clamp(amax/127, 2^-24, 65504) rounded through
 // fp16 (quant.py:48-49; ks3_triton.py:33-35).
 __device__ __forceinline__ float group_scale(float amax) {
   float s = amax / 127.0f;
-  s = fminf(fmaxf(s, kScaleMin), kScaleMax);
+  s = s != s ? s : fminf(fmaxf(s, kScaleMin), kScaleMax);
   return f16_round(s);
 }
 
-// clamp(round_half_even(v), -127, 127) as an int code (quant.py:50).
+// fp16 bits of a group scale (0x7fff for NaN, torch's fp16 conversion of that NaN).
+__device__ __forceinline__ uint16_t scale_bits(float s) { return s != s ? 0x7fff : f16_bits(s); }
+
+// clamp(round_half_even(v), -127, 127) as an int code (quant.py:50); NaN -> 0.
 __device__ __forceinline__ int8_t code_of(float v) {
   float r = rintf(v);
   r = fminf(fmaxf(r, -127.0f), 127.0f);
-  return (int8_t)(int)r;
+  return v != v ? (int8_t)0 : (int8_t)(int)r;
 }
 
 // Store one fp32 value as the output element type.

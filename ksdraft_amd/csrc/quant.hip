@@ -49,9 +49,9 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(
 
   float amax = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  for (int i = 0; i < 8; ++i) amax = amax2(amax, fabsf(v[i]));
 #pragma unroll
-  for (int off = LPG / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  for (int off = LPG / 2; off > 0; off >>= 1) amax = amax2(amax, __shfl_xor(amax, off));
   const float s = group_scale(amax);
 
   int8_t q[8];
@@ -74,7 +74,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(
     for (int i = 0; i < 8; ++i)
       if (k0 + i < K) cr[k0 + i] = q[i];
   }
-  if (sub == 0) scales[row * ngroups + grp] = f16_bits(s);
+  if (sub == 0) scales[row * ngroups + grp] = scale_bits(s);
 }
 
 // ----------------------------------------------------------------------------------
@@ -132,14 +132,14 @@ __global__ __launch_bounds__(256) void quant_T_kernel(Loader ld, int64_t R, int6
     const int r = rq + 4 * i;
     const float v = (cok && r0 + r < R) ? ld(r0 + r, c0 + c) : 0.0f;
     tile[r][c] = v;
-    m = fmaxf(m, fabsf(v));
+    m = amax2(m, fabsf(v));
   }
   cmax[rq][c] = m;
   __syncthreads();
-  const float amax = fmaxf(fmaxf(cmax[0][c], cmax[1][c]), fmaxf(cmax[2][c], cmax[3][c]));
+  const float amax = amax2(amax2(cmax[0][c], cmax[1][c]), amax2(cmax[2][c], cmax[3][c]));
   const float s = group_scale(amax);
   if (!cok) return;
-  if (rq == 0) scales[(c0 + c) * ngr + br] = f16_bits(s);
+  if (rq == 0) scales[(c0 + c) * ngr + br] = scale_bits(s);
 
   constexpr int RPT = G / 4;  // rows (output bytes) per thread
   int8_t q[RPT];
@@ -255,7 +255,7 @@ extern "C" int ksd_requant_transpose(const int8_t *codes, const uint16_t *scales
   return launch_quant_T(ld, R, C, group, out_codes, out_scales, (hipStream_t)stream);
 }
 
-extern "C" int ksd_abi_version(void) { return 1; }
+extern "C" int ksd_abi_version(void) { return 2; }
 
 extern "C" int ksd_last_error(char *buf, size_t len) {
   if (buf == nullptr || len == 0) return KSD_EINVAL;

@@ -8,6 +8,8 @@ Follows reference ksdraft/kernels/ks3_int8.py:
   * _spine_features, 'int8' mode   :205-234  (rank 1)
   * _project (coords)              :238-260
   * _KS3Int8Train.backward geometry VJP :354-401
+and reference ksdraft/kernels/ks3_triton.py:
+  * the fused (project_fused) spine + requant contract, 'int8' mode :47-75, 137-156
 
 Every fp16 op of the reference is a torch fp16 tensor op: the operation is evaluated in
 fp32 ("opmath") with Python scalars converted to fp32, then rounded to fp16. `h()`
@@ -19,6 +21,12 @@ from the reference's own CPU path (bit-exact spine features and VJP coordinate
 gradient given identical GEMM outputs); the LUT against an mpmath-free closed form
 check (float64 tanh, tie distance); _round_div127 by brute force over integer ranges
 (tests/test_oracle_ks3.py).
+
+spine_fused_int8 (the project_fused contract) is parity unpinned at the bit level: the
+reference computes it in a Triton kernel that cannot run here, and Triton's fp16 scalar
+promotion and fp32 division are not fixed by its source. It is pinned only by the
+reference's own tolerance against the composed path (rel < 0.05 on the cell output,
+tests/test_ks3_int8.py:82-84), checked on the golden cell.
 """
 
 from __future__ import annotations
@@ -109,7 +117,9 @@ def spine_features_int8(coords, spine_codes, spine_scale, scale16, shift16, lut)
     hv = (x + h(h(tdiv.astype(np.float32)) * ps16)).astype(np.float32)
     hv = np.maximum(hv, f32(0.0))
     pre = h(np.clip((np.abs(hv) / f32(127.0)).astype(np.float32), f32(2.0 ** -24), f32(65504.0)))
-    hq = np.clip(np.rint((hv / pre).astype(np.float32)), -127, 127)
+    q = (hv / pre).astype(np.float32)
+    # torch: NaN -> int32 is INT_MIN, which clamp(min=0) turns into 0
+    hq = np.where(np.isnan(q), 0.0, np.clip(np.rint(np.where(np.isnan(q), 0.0, q)), -127, 127))
     hq = np.maximum(hq, 0)
     hq16 = h(hq.astype(np.float32))
     return (h(hq16 * hq16) * (pre * pre).astype(np.float32)).astype(np.float32)
@@ -197,3 +207,56 @@ def pack_masters(master_down, master_up, master_coefficients, master_raw_scale,
     return dict(down_codes=dq, down_scales=ds, up_codes=uq, up_scales=us, spine_codes=sq,
                 spine_scale=ss, warp_scale_codes=wsc, warp_scale_scales=wss,
                 warp_shift_codes=whc, warp_shift_scales=whs)
+
+
+def spine_fused_int8(acc32, spine_codes, spine_scale, scale16, shift16, lut, group=128):
+    """ks3_triton.py:47-75 (NL == 2) + 137-156 on the fp32 down-GEMM accumulator (M, F).
+
+    Returns (h_codes int8 (M, F), h_scales fp16 (M, ceil(F/group)))."""
+    x = np.clip(np.asarray(acc32, np.float32), f32(-65504.0), f32(65504.0))
+    M, Fn = x.shape
+    lut = np.asarray(lut, np.int64)
+    c = np.asarray(spine_codes, np.int64).reshape(Fn, 6)
+    c0, c1, c2, c3, c4, c5 = (c[:, k][None, :] for k in range(6))
+    ps = np.asarray(spine_scale, np.float16).astype(np.float32).reshape(Fn)[None, :]
+    sc = np.asarray(scale16, np.float32).reshape(Fn)[None, :]
+    sh = np.asarray(shift16, np.float32).reshape(Fn)[None, :]
+    k = f32(127.0 / TANH_DOMAIN)
+
+    def idx32(v):
+        v = np.clip(np.asarray(v, np.float32), f32(-TANH_DOMAIN), f32(TANH_DOMAIN))
+        return np.rint((v * k).astype(np.float32)).astype(np.int64)
+
+    tq = lut[np.clip(idx32((x * f32(0.25)).astype(np.float32)) + 128, 0, 255)]
+    warp = h(sc * h(h(tq.astype(np.float32) * f32(4.0 / 127.0)) + sh))
+    zq = lut[np.clip(idx32(warp) + 128, 0, 255)]
+    a = 2 * c0 - 2 * c1 + c2 + c3
+    b = -3 * c0 + 3 * c1 - 2 * c2 - c3
+    poly = a * 64
+    poly = round_div127(poly * tq * 4) + b * 64
+    poly = round_div127(poly * tq * 4) + c2 * 64
+    poly = round_div127(poly * tq * 4) + c0 * 64
+    warped = 4 * c5 * 64
+    warped = round_div127(warped * zq) + 2 * c4 * 64
+    warped = round_div127(warped * zq) - 3 * c5 * 64
+    warped = round_div127(warped * zq) - c4 * 64
+    hv = (x + ((poly + warped).astype(np.float32) * (ps / f32(64.0))).astype(np.float32)).astype(np.float32)
+
+    ng = -(-Fn // group)
+    pad = ng * group - Fn
+
+    def group_max(v):
+        vp = np.pad(np.abs(v), ((0, 0), (0, pad)))
+        return vp.reshape(M, ng, group).max(-1)
+
+    def half_scale(m):
+        return h(np.clip((m / f32(127.0)).astype(np.float32), f32(2.0 ** -24), f32(65504.0)))
+
+    pre = np.repeat(half_scale(group_max(hv)), group, axis=1)[:, :Fn]
+    hq = np.clip(np.rint((hv / pre).astype(np.float32)), -127, 127)
+    hq = np.maximum(hq, 0)
+    h2 = ((hq * hq).astype(np.float32) * (pre * pre).astype(np.float32)).astype(np.float32)
+    hs = half_scale(group_max(h2))
+    s_full = np.repeat(hs, group, axis=1)[:, :Fn]
+    q = np.clip(np.rint((h2 / s_full).astype(np.float32)), -127, 127).astype(np.int8)
+    return q, hs.astype(np.float16)

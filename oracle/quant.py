@@ -48,9 +48,14 @@ def quantize_last_dim(x, group: int = GROUP_SIZE, noise=None, dither: float = 0.
         n = np.asarray(noise, dtype=np.float32).reshape(q.shape)
         nz = ((n - np.float32(0.5)).astype(np.float32) * np.float32(2.0 * dither)).astype(np.float32)
         q = (q + nz).astype(np.float32)
-    codes = np.clip(np.rint(q), -127.0, 127.0).astype(np.int8)
+    # NaN groups (torch: amax and clamp propagate NaN, NaN -> int8 gives 0, and the fp16
+    # NaN scale is 0x7fff); pinned against torch in tests/test_oracle_quant.py
+    nan = np.isnan(q)
+    codes = np.where(nan, 0.0, np.clip(np.rint(np.where(nan, 0.0, q)), -127.0, 127.0)).astype(np.int8)
     codes = codes.reshape(lead + (Kp,))[..., :K]
-    return np.ascontiguousarray(codes), scale.astype(np.float16)
+    s16 = scale.astype(np.float16)
+    s16.view(np.uint16)[np.isnan(s16)] = 0x7fff
+    return np.ascontiguousarray(codes), s16
 
 
 def dequantize_last_dim(codes, scales, group: int | None = None):

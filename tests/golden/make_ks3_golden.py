@@ -83,7 +83,8 @@ def main(ref_root: str) -> None:
                 "value": rec["gemm_out"][2].to(torch.float16).numpy(),  # backward GEMM 1 -> fp16
                 "dc": bq[2].numpy(),                        # 3rd backward quantize input
                 "dx": x.grad.numpy(),
-                "ddown": q.master_down.grad.half().numpy(),   # fp16 handoffs (finite)
+                "ddown": q.master_down.grad.half().numpy(),   # fp16 view (inf where the
+                                                              # reference handed off fp32)
                 "dup": q.master_up.grad.half().numpy(),
                 "dcoeff": q.master_coefficients.grad.float().numpy(),
                 "dscale": q.master_raw_scale.grad.float().numpy(),

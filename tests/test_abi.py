@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_channel():
     lib = _lib.load()
-    assert lib.ksd_abi_version() == 1
+    assert lib.ksd_abi_version() == 2
     rc = lib.ksd_quantize_lastdim(None, 0, 4, 128, 128, 48, None, None, None, 0.0, None)
     assert rc == 1
     buf = ctypes.create_string_buffer(256)
@@ -58,6 +58,28 @@ def test_validation_paths_without_gpu():
     assert lib.ksd_requant_transpose(None, None, 4, 4, 128, 24, None, None, None) == 1
     with pytest.raises(ValueError):
         _lib.call("ksd_w8a8_gemm_nt", None, None, None, None, 4, 4, 100, 128, None, None, 0, None)
+
+
+def test_ks3_validation_paths_without_gpu():
+    lib = _lib.load()
+    nrb = ctypes.c_int64(-1)
+    assert lib.ksd_ks3_vjp_row_blocks(300, ctypes.byref(nrb)) == 0 and nrb.value == 3
+    assert lib.ksd_ks3_vjp_row_blocks(0, ctypes.byref(nrb)) == 0 and nrb.value == 0
+    # bad group; null inputs; partials sized for the wrong block count
+    assert lib.ksd_ks3_spine_fwd(None, 4, 4, None, None, None, None, None, 48,
+                                 None, None, None, None) == 1
+    assert lib.ksd_ks3_spine_fwd(None, 4, 4, None, None, None, None, None, 128,
+                                 None, None, None, None) == 1
+    assert lib.ksd_ks3_spine_fused(None, 4, 4, None, None, None, None, None, 128,
+                                   None, None, None) == 1
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    assert lib.ksd_ks3_vjp(p, p, 300, 8, p, p, p, p, 128, None, None, None, None, None,
+                           p, 2, None) == 1
+    buf = ctypes.create_string_buffer(256)
+    lib.ksd_last_error(buf, 256)
+    assert b"row blocks" in buf.value
+    assert lib.ksd_ks3_vjp_finalize(None, 1, 8, None, None, None, None, None, None, None) == 1
+    assert lib.ksd_ks3_tanh16(None, 4, None, None) == 1
 
 
 def test_single_hip_runtime_in_process():

@@ -80,3 +80,50 @@ def test_pack_masters_reproduces_cell_buffers(gold):
     assert np.array_equal(packed["spine_scale"], gold["spine_scale"])
     for k in ("warp_scale_codes", "warp_scale_scales", "warp_shift_codes", "warp_shift_scales"):
         assert np.array_equal(packed[k], gold[k]), k
+
+
+@pytest.mark.parametrize("case", ["std1", "std8"])
+def test_fused_contract_within_reference_tolerance_of_composed(gold, case):
+    """The project_fused contract against the reference's composed output on the golden
+    cell: rel < 0.05, the reference's own bar (tests/test_ks3_int8.py:82-84)."""
+    from oracle import gemm as og
+    from oracle import quant as oq
+    packed = ok.pack_masters(gold["master_down"], gold["master_up"],
+                             gold["master_coefficients"], gold["master_raw_scale"],
+                             gold["master_raw_shift"])
+    sc, sh = ok.warp_scalars(gold["warp_scale_codes"], gold["warp_scale_scales"],
+                             gold["warp_shift_codes"], gold["warp_shift_scales"])
+    xq, xs = oq.quantize_last_dim(gold[f"{case}/x"])
+    acc = og.gemm_ordered(xq, xs, packed["down_codes"], packed["down_scales"])
+    # the composed contract's coordinates are fp16(acc); the reference's CPU GEMM sums in
+    # another order, so they agree to fp16 rounding
+    np.testing.assert_allclose(ok.coords_from_gemm(acc), gold[f"{case}/coords"], rtol=1e-3,
+                               atol=1e-3)
+    hq, hs = ok.spine_fused_int8(acc, gold["spine_codes"], gold["spine_scale"], sc, sh,
+                                 ok.make_tanh_lut())
+    y = og.gemm_ordered(hq, hs, packed["up_codes"], packed["up_scales"])
+    ref = gold[f"{case}/y"]
+    rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    assert rel < 0.05, rel
+
+
+def test_tanh_table_is_torch_fp16_tanh():
+    """The VJP's fp16 tanh table (ksdraft_amd/csrc/gen_tanh16.py) equals the oracle's
+    definition and torch.tanh on fp16 CPU tensors (the reference's op) for every
+    non-negative finite fp16 input; below 2**-6 tanh rounds to its argument."""
+    import importlib.util
+    import torch
+    path = os.path.join(os.path.dirname(os.path.dirname(__file__)), "ksdraft_amd", "csrc",
+                        "gen_tanh16.py")
+    spec = importlib.util.spec_from_file_location("gen_tanh16", path)
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    tab = gen.table()
+    bits = np.arange(0, 0x7c00, dtype=np.uint16)
+    x = bits.view(np.float16)
+    want = ok.h(ok.tanh32(x.astype(np.float32))).astype(np.float16).view(np.uint16)
+    got = tab[np.minimum(bits, gen.LIMIT)]
+    assert np.array_equal(got, want)
+    t = torch.tanh(torch.from_numpy(x.copy())).numpy().view(np.uint16)
+    assert np.array_equal(got, t)
+    assert np.array_equal(tab[:0x2400], bits[:0x2400])

@@ -114,3 +114,23 @@ def test_requant_transpose_is_quant_of_dequant_transpose():
     for r in range(0, 96, 7):
         ec, es = exact_quantize_group(real[r], 128)
         assert np.array_equal(tq[r], ec) and np.array_equal(ts[r], es)
+
+
+def test_nonfinite_groups_follow_torch():
+    """quant.py:47-51 run by torch on the CPU: a NaN in a group gives a NaN scale (fp16
+    bits 0x7fff) and zero codes; inf gives scale 65504 and +-127 at the inf."""
+    import torch
+    x = np.zeros((3, 256), np.float32)
+    x[0, 3] = np.nan
+    x[0, 200] = 5.0
+    x[1, 7] = np.inf
+    x[1, 8] = 2.0
+    x[2, 130] = -np.inf
+    codes, scales = oq.quantize_last_dim(x)
+    t = torch.from_numpy(x)
+    amax = t.reshape(3, 2, 128).abs().amax(-1, keepdim=True)
+    s = (amax / 127.0).clamp(2.0 ** -24, 65504.0).to(torch.float16).float()
+    tc = torch.clamp(torch.round(t.reshape(3, 2, 128) / s), -127.0, 127.0).to(torch.int8)
+    assert np.array_equal(codes, tc.reshape(3, 256).numpy())
+    assert np.array_equal(scales.view(np.uint16), s.to(torch.float16).reshape(3, 2).numpy().view(np.uint16))
+    assert scales.view(np.uint16)[0, 0] == 0x7fff and codes[1, 7] == 127 and codes[2, 130] == -127
