@@ -54,6 +54,7 @@ def parse():
     p.add_argument("--kernel-reps", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument("--no-ks3", action="store_true", help="skip the KS3 kernel report")
     p.add_argument("--pmc-probe", action="store_true",
                    help="for rocprofv3 --pmc runs: a 256 MiB device copy (counter "
                         "calibration), then 3 launches of each GEMM of the step; no timing")
@@ -156,6 +157,58 @@ def kernel_times(x, w, dy, reps):
         if nbytes is None:
             ent["tops"] = round(GEMM_OPS / (us * 1e-6) / 1e12, 1)
         else:
+            ent["GBps"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+            ent["hbm_frac"] = round(nbytes / (us * 1e-6) / PEAK_HBM, 3)
+        res[name] = ent
+    return res
+
+
+def ks3_kernel_times(dev, reps):
+    """The KS3 cell's kernels at BASELINE config 4's shape (M = 8192 tokens, d = 1536,
+    F = 5888 charts): average launch time and HBM rate against the algorithmic bytes.
+    Synthetic inputs: coordinates ~N(0, 0.8) (x ~N(0,1) through down ~N(0,0.02)),
+    value ~N(0, 1e-2), reference inits for the cell (coefficients ~N(0,0.05), raw_scale
+    0.75, raw_shift 0; model/ks3.py:85-88)."""
+    from ksdraft_amd.kernels import ks3_int8 as K
+    Mk, d, Fc, G = 8192, 1536, 5888, 128
+    g = torch.Generator().manual_seed(0)
+    coeffs = (torch.randn(Fc, 6, generator=g) * 0.05).to(dev)
+    raw_scale = torch.full((Fc,), 0.75, device=dev)
+    raw_shift = torch.zeros(Fc, device=dev)
+    coords16 = (torch.randn(Mk, Fc, generator=g) * 0.8).to(dev).half()
+    acc32 = coords16.float()
+    value16 = (torch.randn(Mk, Fc, generator=g) * 1e-2).to(dev).half()
+    x = torch.randn(Mk, d, generator=g).to(dev)
+    down = (torch.randn(Fc, d, generator=g) * 0.02).to(dev)
+    sq, ss = K.pack_spine(coeffs, G)
+    sc16 = (torch.nn.functional.softplus(raw_scale) + 1e-4).half()
+    sh16 = (0.5 * torch.tanh(raw_shift)).half()
+    lut = K.make_tanh_lut(dev)
+    xq, xs = quantize_last_dim(x)
+    dq, ds = quantize_last_dim(down)
+    MF = Mk * Fc
+    stages = {
+        "gemm_down_f16sat": (lambda: w8a8_gemm_out(xq, xs, dq, ds, fp16_saturate=True), None),
+        "ks3_spine_fwd": (lambda: K.spine_int8(coords16, sq, ss, sc16, sh16, lut, G),
+                          2 * MF + MF + 2 * MF // G),
+        "ks3_spine_fused": (lambda: K.spine_fused_int8(acc32, sq, ss, sc16, sh16, lut, G),
+                            4 * MF + MF + 2 * MF // G),
+        "ks3_vjp": (lambda: K.ks3_vjp(value16, coords16, sq, ss, sc16, sh16, raw_scale,
+                                      raw_shift, G),
+                    2 * MF + 2 * MF + MF + MF + 2 * 2 * MF // G + 2 * 8 * Fc * 4 * (Mk // 128)),
+    }
+    res = {}
+    for name, (fn, nbytes) in stages.items():
+        def rep(fn=fn):
+            for _ in range(reps):
+                fn()
+        _, _, ms = time_graph(rep, 3, warm=1)
+        us = ms * 1e3 / reps
+        ent = {"us": round(us, 3)}
+        if nbytes is None:
+            ent["tops"] = round(2 * Mk * Fc * d / (us * 1e-6) / 1e12, 1)
+        else:
+            ent["bytes"] = nbytes
             ent["GBps"] = round(nbytes / (us * 1e-6) / 1e9, 1)
             ent["hbm_frac"] = round(nbytes / (us * 1e-6) / PEAK_HBM, 3)
         res[name] = ent
@@ -291,6 +344,7 @@ def main():
         "eager_wall_ms_per_step": round(eager_wall_ms, 4),
         "draft_train_step_tok_s": None,
         "kernels": kern,
+        "ks3_c4_kernels": None if args.no_ks3 else ks3_kernel_times(dev, args.kernel_reps),
         "roofline": {
             "kernel": "gemm_nt_kernel<128,f32> (fwd, dX, dW launches averaged)",
             "bound": "mfma",

@@ -131,11 +131,17 @@ def coords_from_gemm(y32):
     return np.clip(y.astype(np.float32), -65504.0, 65504.0).astype(np.float32)
 
 
+def spine_coefficients(spine_codes, spine_scale):
+    """The fp16 coefficients of the VJP: c_k = fp16(code * scale) (ks3_int8.py:355-362)."""
+    call = (np.asarray(spine_codes, np.float32).reshape(-1, 6) *
+            np.asarray(spine_scale, np.float16).astype(np.float32).reshape(-1)[:, None])
+    return h(call)  # (F, 6)
+
+
 def spine_params(spine_codes, spine_scale, warp_scale_codes, warp_scale_scales,
                  warp_shift_codes, warp_shift_scales):
-    """The fp16 coefficients of the VJP: c_k = fp16(code * scale) (ks3_int8.py:355-362)."""
-    call = np.asarray(spine_codes, np.float32) * np.asarray(spine_scale, np.float16).astype(np.float32)[:, None]
-    coef = h(call)  # (F, 6)
+    """spine_coefficients plus the fp16 warp scalars."""
+    coef = spine_coefficients(spine_codes, spine_scale)
     sc, sh = warp_scalars(warp_scale_codes, warp_scale_scales, warp_shift_codes, warp_shift_scales)
     return coef, sc, sh
 
