@@ -41,6 +41,10 @@ def lib() -> ctypes.CDLL:
         _lib.ksd_oracle_partials.restype = None
         _lib.ksd_oracle_gemm_ordered.argtypes = [P, P, P, P, I64, I64, I64, I, P, P, I64, P]
         _lib.ksd_oracle_gemm_ordered.restype = None
+        _lib.ksd_oracle_rosa_match.argtypes = [P, P, P, I64, I64, I, P, P, P]
+        _lib.ksd_oracle_rosa_match.restype = None
+        _lib.ksd_oracle_rosa_credits.argtypes = [P, P, P, P, I64, I64, I, P]
+        _lib.ksd_oracle_rosa_credits.restype = None
     return _lib
 
 

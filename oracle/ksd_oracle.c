@@ -9,6 +9,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* exact fp16 -> fp32 decode (every fp16 value, subnormals included, is an fp32) */
@@ -82,4 +83,73 @@ void ksd_oracle_gemm_ordered(const int8_t *a, const uint16_t *as, const int8_t *
       if (bias) acc = acc + bias[n];
       y[r * N + n] = acc;
     }
+}
+
+/* ------------------------------------------------------------------ Rosa
+ * Longest-suffix match of reference ksdraft/model/rosa.py:40-98, by brute force over
+ * every pair (t, j < t): L(t, j) = min(common suffix length of q[0..t] and k[0..j],
+ * j + 1, lmax). The decision at t is the latest j with the largest L >= 1; sign is +1 when
+ * v[j + 1] is set, else -1; -1 when no j has L >= 1. Bits are uint8 {0,1}, (streams, T).
+ * match_j / match_len (optional) receive j* (-1 if none) and L*. */
+static void rosa_match_stream(const uint8_t *q, const uint8_t *k, const uint8_t *v, int64_t T,
+                              int lmax, float *sign, int32_t *mj, int32_t *ml) {
+  for (int64_t t = 0; t < T; ++t) {
+    int64_t best_j = -1;
+    int best_l = 0;
+    for (int64_t j = t - 1; j >= 0; --j) {
+      int cap = (int)(j + 1 < lmax ? j + 1 : lmax);
+      if (cap <= best_l) continue; /* cannot beat (and ties lose to a later j) */
+      int l = 0;
+      while (l < cap && q[t - l] == k[j - l]) ++l;
+      if (l > best_l) {
+        best_l = l;
+        best_j = j;
+      }
+    }
+    if (sign) sign[t] = (best_l >= 1 && v[best_j + 1]) ? 1.0f : -1.0f;
+    if (mj) mj[t] = best_l >= 1 ? (int32_t)best_j : -1;
+    if (ml) ml[t] = best_l;
+  }
+}
+
+void ksd_oracle_rosa_match(const uint8_t *q, const uint8_t *k, const uint8_t *v,
+                           int64_t n_streams, int64_t T, int lmax, float *sign,
+                           int32_t *match_j, int32_t *match_len) {
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t s = 0; s < n_streams; ++s)
+    rosa_match_stream(q + s * T, k + s * T, v + s * T, T, lmax, sign ? sign + s * T : 0,
+                      match_j ? match_j + s * T : 0, match_len ? match_len + s * T : 0);
+}
+
+/* First-order single-bit credits of reference ksdraft/kernels/rosa_credit_gpu.py:28-51,
+ * by definition: for every bit of q, k and v, flip it, redo the whole match and sum
+ * (sign' - sign) * grad_sign over t (in double). credits: (n_streams, 3, T). */
+void ksd_oracle_rosa_credits(const uint8_t *q, const uint8_t *k, const uint8_t *v,
+                             const float *grad_sign, int64_t n_streams, int64_t T, int lmax,
+                             double *credits) {
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t s = 0; s < n_streams; ++s) {
+    uint8_t *b[3];
+    float *base = (float *)malloc(sizeof(float) * T);
+    float *pert = (float *)malloc(sizeof(float) * T);
+    for (int w = 0; w < 3; ++w) b[w] = (uint8_t *)malloc(T);
+    memcpy(b[0], q + s * T, T);
+    memcpy(b[1], k + s * T, T);
+    memcpy(b[2], v + s * T, T);
+    const float *g = grad_sign + s * T;
+    rosa_match_stream(b[0], b[1], b[2], T, lmax, base, 0, 0);
+    for (int w = 0; w < 3; ++w) {
+      for (int64_t p = 0; p < T; ++p) {
+        b[w][p] ^= 1;
+        rosa_match_stream(b[0], b[1], b[2], T, lmax, pert, 0, 0);
+        b[w][p] ^= 1;
+        double c = 0.0;
+        for (int64_t t = 0; t < T; ++t) c += (double)(pert[t] - base[t]) * (double)g[t];
+        credits[(s * 3 + w) * T + p] = c;
+      }
+    }
+    for (int w = 0; w < 3; ++w) free(b[w]);
+    free(base);
+    free(pert);
+  }
 }
