@@ -190,6 +190,80 @@ int ksd_ks3_vjp_finalize(const float *partials, int64_t n_row_blocks, int64_t F,
  */
 int ksd_ks3_tanh16(const uint16_t *x, int64_t n, uint16_t *y, void *stream);
 
+/*
+ * R1 — RosaMixer._shifted fused with the quantization of each projection input
+ * (reference ksdraft/model/rosa.py:128-133, then Int8Linear's quantize_last_dim,
+ * ksdraft/kernels/linear.py:69): for every token row r = (b, t) and feature i,
+ *     m_in = prev + (x - prev) * sig_m,  prev = x[b, t-1] (0 at t = 0),
+ * with x - prev rounded to x's dtype and the rest in fp32, then quantized per group.
+ *   x        (B, T, d) of type x_dtype (KSD_F32, KSD_BF16, KSD_F16), dense
+ *   sig_q/k/v (d,) fp32: torch.sigmoid(time_mix_q/k/v)
+ *   *_codes  (B*T, d) int8; *_scales (B*T, ceil(d/group)) fp16
+ */
+int ksd_rosa_shift_quant(const void *x, int x_dtype, int64_t B, int64_t T, int64_t d,
+                         const float *sig_q, const float *sig_k, const float *sig_v, int group,
+                         int8_t *q_codes, uint16_t *q_scales, int8_t *k_codes, uint16_t *k_scales,
+                         int8_t *v_codes, uint16_t *v_scales, void *stream);
+
+/*
+ * The (x > 0) symbol bits of Rosa projections (reference ksdraft/model/rosa.py:156-158,
+ * ksdraft/kernels/rosa_credit_gpu.py:68-70), packed per stream along T.
+ *   x     (B, T, S) of type x_dtype, dense
+ *   bits  (B, S, ceil(T/32)) uint32: bit b of word w is position 32w + b
+ */
+int ksd_rosa_pack_bits(const void *x, int x_dtype, int64_t B, int64_t T, int64_t S,
+                       uint32_t *bits, void *stream);
+
+/*
+ * R2 — _match_payload_sign (reference ksdraft/model/rosa.py:40-98) on packed bits: for
+ * each stream and position t the latest endpoint j < t of the longest common suffix of
+ * q[..t] and k[..j], lengths capped at min(j + 1, lmax); sign = v[j + 1] ? +1 : -1, or -1
+ * when nothing matches.
+ *   q/k/v_bits  (n_streams, ceil(T/32)) uint32 as from ksd_rosa_pack_bits
+ *   lmax        the reference's max_match_len rule, resolved by the caller (<= 63)
+ *   sign        (n_streams, T) int8 in {-1, +1}
+ *   match_j     NULL or (n_streams, T) int32 endpoint (-1 when nothing matches)
+ *   T <= 65536.
+ */
+int ksd_rosa_match(const uint32_t *q_bits, const uint32_t *k_bits, const uint32_t *v_bits,
+                   int64_t n_streams, int64_t T, int lmax, int8_t *sign, int32_t *match_j,
+                   void *stream);
+
+/*
+ * R4 forward output — payload[s] * sign, transposed from (B, S, T) to (B, T, S)
+ * (reference ksdraft/kernels/rosa_credit_gpu.py:75).
+ *   out (B, T, S) of type out_dtype (KSD_F32, KSD_BF16, KSD_F16)
+ */
+int ksd_rosa_hard(const int8_t *sign, const float *payload, int64_t B, int64_t T, int64_t S,
+                  void *out, int out_dtype, void *stream);
+
+/*
+ * R5 — exact first-order single-bit counterfactual credits of HardRosaGPU.backward
+ * (reference ksdraft/kernels/rosa_credit_gpu.py:28-51, 78-104): for every q, k and v bit
+ * of every stream, sum over positions t of (sign after flipping that bit - sign) * g(t),
+ * g = grad[b, t, s] * payload[s]. No length guard: any T up to 65535.
+ *   q/k/v_bits  (B*S, ceil(T/32)) uint32 from ksd_rosa_pack_bits
+ *   match_j     (B*S, T) int32 endpoints from ksd_rosa_match
+ *   grad        (B, T, S) fp32 upstream gradient of the hard output
+ *   credits     (B*S, 3, T) fp32, zeroed by the caller; accumulated with atomics, so the
+ *               summation order (not the flip decisions) varies between runs
+ */
+int ksd_rosa_credits(const uint32_t *q_bits, const uint32_t *k_bits, const uint32_t *v_bits,
+                     const int32_t *match_j, const float *grad, const float *payload, int64_t B,
+                     int64_t T, int64_t S, int lmax, float *credits, void *stream);
+
+/*
+ * R5 projection-space gradients (reference ksdraft/kernels/rosa_credit_gpu.py:99-111):
+ * g_x = credit * (1 - 2 * bit) * sigmoid(x) * (1 - sigmoid(x)) in x's dtype, and
+ * d payload[s] = sum over (b, t) of grad * sign (fixed order).
+ *   q/k/v   (B, T, S) pre-bit projections of type dtype; grad (B, T, S) fp32
+ *   sign    (B, S, T) int8 from ksd_rosa_match
+ *   gq/gk/gv (B, T, S) of type dtype; gpayload (S,) fp32
+ */
+int ksd_rosa_credit_grads(const float *credits, const void *q, const void *k, const void *v,
+                          int dtype, const float *grad, const int8_t *sign, int64_t B, int64_t T,
+                          int64_t S, void *gq, void *gk, void *gv, float *gpayload, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,611 @@
+// Rosa mixer step kernels for gfx950 (reference ksdraft/model/rosa.py,
+// ksdraft/kernels/rosa_credit_gpu.py).
+//
+//   rosa_shift_quant_kernel  RosaMixer._shifted (rosa.py:128-133) fused with the
+//                            quantize_last_dim of each Int8Linear input: one pass over x
+//                            emits the int8 codes + fp16 scales of q_in, k_in and v_in.
+//   rosa_pack_kernel         (x > 0) bits of (B, T, S) projections, packed per stream
+//                            along T into 32-bit words (bit b of word w = position 32w+b).
+//   rosa_match_kernel        _match_payload_sign (rosa.py:40-98): per position t the
+//                            latest endpoint j < t of the longest common suffix of
+//                            q[..t] and k[..j], capped at min(j+1, lmax).
+//   rosa_hard_kernel         payload[s] * sign, transposed back to (B, T, S).
+//
+// The match is a bit-sliced walk over lengths. For a fixed t let A_L be the set of start
+// positions j' whose key window k[j'..j'+L-1] equals q[t-L+1..t]; then
+//     A_1 = { j' <= t-1 : k[j'] == q[t] },   A_{L+1}(j') = A_L(j'+1) & (k[j'] == q[t-L]),
+// one funnel shift and two bitwise ops per 32 candidates per length. A candidate j = j'+L-1
+// survives to length L exactly when its (capped) common suffix is >= L, so the last
+// non-empty length is the best length and its highest surviving j the latest endpoint.
+// Candidates are walked in chunks of kCH words; each chunk carries two words of halo to
+// its left so every chain j'..j'+61 of its own candidates lies inside the chunk.
+#include "ksd_common.h"
+
+namespace ksd {
+
+// ---------------------------------------------------------------- shift + quantize
+template <int DT>
+__device__ __forceinline__ float round_to_dt(float v);
+template <> __device__ __forceinline__ float round_to_dt<KSD_F32>(float v) { return v; }
+template <> __device__ __forceinline__ float round_to_dt<KSD_BF16>(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+template <> __device__ __forceinline__ float round_to_dt<KSD_F16>(float v) { return f16_round(v); }
+
+// One row (token) per G/8-lane group set; a lane owns 8 consecutive features.
+// q_in = prev + (x - prev) * sigmoid(mix): x - prev is an op in x's dtype (rounded to it),
+// the rest is fp32 (torch promotes the bf16/fp16 tensor against the fp32 sigmoid).
+template <int DT, int G>
+__global__ void __launch_bounds__(256) rosa_shift_quant_kernel(
+    const void *__restrict__ x, int64_t rows, int64_t T, int64_t d,
+    const float *__restrict__ sig_q, const float *__restrict__ sig_k, const float *__restrict__ sig_v,
+    int8_t *__restrict__ cq, uint16_t *__restrict__ sq, int8_t *__restrict__ ck,
+    uint16_t *__restrict__ sk, int8_t *__restrict__ cv, uint16_t *__restrict__ sv, int64_t ngroups) {
+  using E = Elem<DT>;
+  constexpr int LPG = G / 8;
+  const int64_t lanes_per_row = ngroups * LPG;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gid / lanes_per_row;
+  const int64_t k0 = (gid % lanes_per_row) * 8;
+  const bool active = row < rows;
+  const int64_t t = active ? row % T : 0;
+  const typename E::T *xr = (const typename E::T *)x + (active ? row : 0) * d;
+  float xv[8], pv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bool ok = active && k0 + i < d;
+    xv[i] = ok ? E::load(xr + k0 + i) : 0.0f;
+    pv[i] = ok && t > 0 ? E::load(xr - d + k0 + i) : 0.0f;
+  }
+  const float *sigs[3] = {sig_q, sig_k, sig_v};
+  int8_t *codes[3] = {cq, ck, cv};
+  uint16_t *scales[3] = {sq, sk, sv};
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    float v[8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float sg = active && k0 + i < d ? sigs[m][k0 + i] : 0.0f;
+      const float diff = round_to_dt<DT>(xv[i] - pv[i]);
+      v[i] = pv[i] + diff * sg;
+      amax = amax2(amax, fabsf(v[i]));
+    }
+#pragma unroll
+    for (int off = LPG / 2; off > 0; off >>= 1) amax = amax2(amax, __shfl_xor(amax, off));
+    const float s = group_scale(amax);
+    if (!active) continue;
+    int8_t *cr = codes[m] + row * d;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (k0 + i < d) cr[k0 + i] = code_of(v[i] / s);
+    if ((gid % LPG) == 0) scales[m][row * ngroups + k0 / G] = scale_bits(s);
+  }
+}
+
+// ---------------------------------------------------------------- bit packing
+// (B, T, S) -> words (B, S, W): one thread per (stream s, word w).
+template <int DT>
+__global__ void __launch_bounds__(256) rosa_pack_kernel(const void *__restrict__ x, int64_t T,
+                                                        int64_t S, int64_t W,
+                                                        uint32_t *__restrict__ bits) {
+  using E = Elem<DT>;
+  const int64_t s = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t w = blockIdx.y, b = blockIdx.z;
+  if (s >= S) return;
+  const typename E::T *xb = (const typename E::T *)x + b * T * S;
+  uint32_t word = 0;
+#pragma unroll 8
+  for (int i = 0; i < 32; ++i) {
+    const int64_t t = w * 32 + i;
+    if (t < T && E::load(xb + t * S + s) > 0.0f) word |= 1u << i;
+  }
+  bits[(b * S + s) * W + w] = word;
+}
+
+// ---------------------------------------------------------------- match
+constexpr int kCH = 8;  // candidate words per chunk
+
+// 64 q bits ending at t in memory order: bit 63 = q[t], bit 63-i = q[t-i] (0 before 0).
+__device__ __forceinline__ uint64_t q_window(const uint32_t *qw, int t) {
+  const int w = t >> 5, b = t & 31;
+  const uint64_t hi = qw[w], mid = w >= 1 ? qw[w - 1] : 0u, lo = w >= 2 ? qw[w - 2] : 0u;
+  const uint64_t m64 = (hi << 32) | mid;
+  return (m64 << (31 - b)) | (b == 31 ? 0ull : (lo >> (b + 1)));
+}
+
+// Best (length, endpoint) for position t >= 1. Returns length (0 = no match), sets *jout.
+__device__ int match_one(const uint32_t *qw, const uint32_t *kw_all, int W, int t, int lmax,
+                         int *jout) {
+  const uint64_t qwin = q_window(qw, t);
+  const int nw = (t - 1) / 32 + 1;  // words holding candidates j in [0, t-1]
+  int best_l = 0, best_j = -1;
+  for (int w0 = ((nw - 1) / kCH) * kCH; w0 >= 0; w0 -= kCH) {
+    if (min(lmax, 32 * (w0 + kCH)) <= best_l) break;  // cannot beat a later endpoint
+    uint32_t kw[kCH + 2], A[kCH + 2];
+    const uint32_t nq0 = ((qwin >> 63) & 1) ? 0u : ~0u;  // k ^ nq == (k == q bit)
+    uint32_t any = 0;
+#pragma unroll
+    for (int c = 0; c < kCH + 2; ++c) {
+      const int w = w0 - 2 + c;
+      kw[c] = (w >= 0 && w < W) ? kw_all[w] : 0u;
+      uint32_t valid = 0u;  // candidates 0 <= j' <= t-1
+      if (w >= 0) {
+        const int hi = t - 1 - 32 * w;  // last valid bit in this word
+        valid = hi >= 31 ? ~0u : (hi < 0 ? 0u : (2u << hi) - 1u);
+      }
+      A[c] = (kw[c] ^ nq0) & valid;
+      any |= A[c];
+    }
+    if (!any) continue;
+    int L = 1;
+    while (L < lmax) {
+      const uint32_t nq = ((qwin >> (63 - L)) & 1) ? 0u : ~0u;  // q[t - L]
+      uint32_t nx[kCH + 2];
+      uint32_t a2 = 0;
+#pragma unroll
+      for (int c = 0; c < kCH + 2; ++c) {
+        const uint32_t right = c + 1 < kCH + 2 ? A[c + 1] : 0u;
+        const uint32_t shifted = (A[c] >> 1) | (right << 31);  // A_L(j' + 1)
+        nx[c] = shifted & (kw[c] ^ nq) & (w0 - 2 + c >= 0 ? ~0u : 0u);
+        a2 |= nx[c];
+      }
+      if (!a2) break;
+#pragma unroll
+      for (int c = 0; c < kCH + 2; ++c) A[c] = nx[c];
+      ++L;
+    }
+    // survivors at length L: report the highest j = j' + L - 1 inside this chunk's range
+    const int jlo = 32 * w0, jhi = 32 * (w0 + kCH);  // [jlo, jhi)
+    int found = -1;
+#pragma unroll
+    for (int c = kCH + 1; c >= 0; --c) {
+      if (found >= 0 || A[c] == 0u) continue;
+      const int base = 32 * (w0 - 2 + c) + L - 1;  // j of bit 0
+      // keep bits whose j lies in [jlo, jhi)
+      uint32_t m = A[c];
+      const int lo_bit = jlo - base, hi_bit = jhi - base;  // allowed bit range [lo_bit, hi_bit)
+      if (hi_bit <= 0 || lo_bit >= 32) continue;
+      if (lo_bit > 0) m &= ~0u << lo_bit;
+      if (hi_bit < 32) m &= (1u << hi_bit) - 1u;
+      if (m) found = base + 31 - __clz(m);
+    }
+    if (found >= 0 && (L > best_l || (L == best_l && found > best_j))) {
+      best_l = L;
+      best_j = found;
+    }
+  }
+  *jout = best_j;
+  return best_l;
+}
+
+// One block per stream. sign (streams, T) int8 +-1; match_j (streams, T) int32 or NULL.
+__global__ void __launch_bounds__(256) rosa_match_kernel(const uint32_t *__restrict__ qb,
+                                                         const uint32_t *__restrict__ kb,
+                                                         const uint32_t *__restrict__ vb, int T,
+                                                         int W, int lmax, int8_t *__restrict__ sign,
+                                                         int32_t *__restrict__ match_j) {
+  extern __shared__ uint32_t sm[];
+  uint32_t *qw = sm, *kw = sm + W, *vw = sm + 2 * W;
+  const int64_t s = blockIdx.x;
+  for (int i = threadIdx.x; i < W; i += 256) {
+    qw[i] = qb[s * W + i];
+    kw[i] = kb[s * W + i];
+    vw[i] = vb[s * W + i];
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < T; t += 256) {
+    int j = -1, L = 0;
+    if (t >= 1 && lmax >= 1) L = match_one(qw, kw, W, t, lmax, &j);
+    int8_t sg = -1;
+    if (L >= 1) sg = ((vw[(j + 1) >> 5] >> ((j + 1) & 31)) & 1u) ? 1 : -1;
+    sign[s * T + t] = sg;
+    if (match_j) match_j[s * T + t] = L >= 1 ? j : -1;
+  }
+}
+
+// (B, S, T) int8 sign -> (B, T, S) payload[s] * sign in the output dtype, via a 64x64 tile.
+template <int DT>
+__global__ void __launch_bounds__(256) rosa_hard_kernel(const int8_t *__restrict__ sign,
+                                                        const float *__restrict__ payload,
+                                                        int64_t T, int64_t S, void *__restrict__ out) {
+  __shared__ int8_t tile[64][65];
+  const int64_t b = blockIdx.z;
+  const int64_t t0 = (int64_t)blockIdx.x * 64, s0 = (int64_t)blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {  // rows = streams, coalesced along t
+    const int64_t s = s0 + r, t = t0 + tx;
+    tile[r][tx] = (s < S && t < T) ? sign[(b * S + s) * T + t] : 0;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {  // rows = positions, coalesced along s
+    const int64_t t = t0 + r, s = s0 + tx;
+    if (t < T && s < S) store_out<DT>(out, (b * T + t) * S + s, payload[s] * (float)tile[tx][r]);
+  }
+}
+
+
+}  // namespace ksd
+
+using namespace ksd;
+
+extern "C" int ksd_rosa_shift_quant(const void *x, int x_dtype, int64_t B, int64_t T, int64_t d,
+                                    const float *sig_q, const float *sig_k, const float *sig_v,
+                                    int group, int8_t *q_codes, uint16_t *q_scales, int8_t *k_codes,
+                                    uint16_t *k_scales, int8_t *v_codes, uint16_t *v_scales,
+                                    void *stream) {
+  if (B < 0 || T < 0 || d < 0) return fail(KSD_EINVAL, "rosa_shift_quant: negative shape");
+  if (!valid_group(group)) return fail(KSD_EINVAL, "rosa_shift_quant: group must be 32, 64 or 128");
+  if (x_dtype != KSD_F32 && x_dtype != KSD_BF16 && x_dtype != KSD_F16)
+    return fail(KSD_ETYPE, "rosa_shift_quant: x must be float32, bfloat16 or float16");
+  const int64_t rows = B * T;
+  if (rows == 0 || d == 0) return KSD_OK;
+  if (!x || !sig_q || !sig_k || !sig_v || !q_codes || !q_scales || !k_codes || !k_scales ||
+      !v_codes || !v_scales)
+    return fail(KSD_EINVAL, "rosa_shift_quant: null pointer");
+  const int64_t ng = cdiv(d, group);
+  const int64_t threads = rows * ng * (group / 8);
+  const int64_t blocks = cdiv(threads, 256);
+  if (blocks > 0x7fffffff) return fail(KSD_EINVAL, "rosa_shift_quant: too large");
+  hipStream_t st = (hipStream_t)stream;
+#define KSD_SQ(DT, G)                                                                            \
+  hipLaunchKernelGGL((rosa_shift_quant_kernel<DT, G>), dim3((unsigned)blocks), dim3(256), 0, st, x, \
+                     rows, T, d, sig_q, sig_k, sig_v, q_codes, q_scales, k_codes, k_scales, v_codes, \
+                     v_scales, ng)
+#define KSD_SQ_G(DT) \
+  switch (group) { case 32: KSD_SQ(DT, 32); break; case 64: KSD_SQ(DT, 64); break; default: KSD_SQ(DT, 128); }
+  switch (x_dtype) {
+    case KSD_F32: KSD_SQ_G(KSD_F32); break;
+    case KSD_BF16: KSD_SQ_G(KSD_BF16); break;
+    default: KSD_SQ_G(KSD_F16); break;
+  }
+#undef KSD_SQ_G
+#undef KSD_SQ
+  return check_launch("rosa_shift_quant");
+}
+
+extern "C" int ksd_rosa_pack_bits(const void *x, int x_dtype, int64_t B, int64_t T, int64_t S,
+                                  uint32_t *bits, void *stream) {
+  if (B < 0 || T < 0 || S < 0) return fail(KSD_EINVAL, "rosa_pack_bits: negative shape");
+  if (x_dtype != KSD_F32 && x_dtype != KSD_BF16 && x_dtype != KSD_F16)
+    return fail(KSD_ETYPE, "rosa_pack_bits: x must be float32, bfloat16 or float16");
+  if (B == 0 || T == 0 || S == 0) return KSD_OK;
+  if (!x || !bits) return fail(KSD_EINVAL, "rosa_pack_bits: null pointer");
+  const int64_t W = cdiv(T, 32);
+  if (W > 65535 || B > 65535) return fail(KSD_EINVAL, "rosa_pack_bits: T or B too large");
+  dim3 grid((unsigned)cdiv(S, 256), (unsigned)W, (unsigned)B);
+  hipStream_t st = (hipStream_t)stream;
+  switch (x_dtype) {
+    case KSD_F32: hipLaunchKernelGGL(rosa_pack_kernel<KSD_F32>, grid, dim3(256), 0, st, x, T, S, W, bits); break;
+    case KSD_BF16: hipLaunchKernelGGL(rosa_pack_kernel<KSD_BF16>, grid, dim3(256), 0, st, x, T, S, W, bits); break;
+    default: hipLaunchKernelGGL(rosa_pack_kernel<KSD_F16>, grid, dim3(256), 0, st, x, T, S, W, bits); break;
+  }
+  return check_launch("rosa_pack_bits");
+}
+
+extern "C" int ksd_rosa_match(const uint32_t *q_bits, const uint32_t *k_bits, const uint32_t *v_bits,
+                              int64_t n_streams, int64_t T, int lmax, int8_t *sign, int32_t *match_j,
+                              void *stream) {
+  if (n_streams < 0 || T < 0) return fail(KSD_EINVAL, "rosa_match: negative shape");
+  if (lmax < 0 || lmax > 63) return fail(KSD_EINVAL, "rosa_match: lmax must be in [0, 63]");
+  if (T > (1 << 16)) return fail(KSD_EINVAL, "rosa_match: T above 65536 is not supported");
+  if (n_streams == 0 || T == 0) return KSD_OK;
+  if (!q_bits || !k_bits || !v_bits || !sign) return fail(KSD_EINVAL, "rosa_match: null pointer");
+  if (n_streams > 0x7fffffff) return fail(KSD_EINVAL, "rosa_match: too many streams");
+  const int W = (int)cdiv(T, 32);
+  hipLaunchKernelGGL(rosa_match_kernel, dim3((unsigned)n_streams), dim3(256), 3 * W * sizeof(uint32_t),
+                     (hipStream_t)stream, q_bits, k_bits, v_bits, (int)T, W, lmax, sign, match_j);
+  return check_launch("rosa_match");
+}
+
+extern "C" int ksd_rosa_hard(const int8_t *sign, const float *payload, int64_t B, int64_t T, int64_t S,
+                             void *out, int out_dtype, void *stream) {
+  if (B < 0 || T < 0 || S < 0) return fail(KSD_EINVAL, "rosa_hard: negative shape");
+  if (out_dtype != KSD_F32 && out_dtype != KSD_BF16 && out_dtype != KSD_F16)
+    return fail(KSD_ETYPE, "rosa_hard: out must be float32, bfloat16 or float16");
+  if (B == 0 || T == 0 || S == 0) return KSD_OK;
+  if (!sign || !payload || !out) return fail(KSD_EINVAL, "rosa_hard: null pointer");
+  if (B > 65535 || cdiv(S, 64) > 65535) return fail(KSD_EINVAL, "rosa_hard: B or S too large");
+  dim3 grid((unsigned)cdiv(T, 64), (unsigned)cdiv(S, 64), (unsigned)B);
+  hipStream_t st = (hipStream_t)stream;
+  switch (out_dtype) {
+    case KSD_F32: hipLaunchKernelGGL(rosa_hard_kernel<KSD_F32>, grid, dim3(256), 0, st, sign, payload, T, S, out); break;
+    case KSD_BF16: hipLaunchKernelGGL(rosa_hard_kernel<KSD_BF16>, grid, dim3(256), 0, st, sign, payload, T, S, out); break;
+    default: hipLaunchKernelGGL(rosa_hard_kernel<KSD_F16>, grid, dim3(256), 0, st, sign, payload, T, S, out); break;
+  }
+  return check_launch("rosa_hard");
+}
+
+namespace ksd {
+
+// ---------------------------------------------------------------- exact credits (R5)
+// First-order single-bit credits of rosa_credit_gpu.py:28-51 without re-matching per flip.
+// For one stream and position t every candidate j < t has a common-suffix length c_j
+// (uncapped, <= 64) and cap_j = min(j + 1, lmax); its key is (min(c_j, cap_j), j) and the
+// best key decides the sign. Flipping one bit changes candidate lengths in a known way:
+//   q[t - i]: c_j < i unchanged; c_j > i -> i; c_j == i -> c_j + 1 + e_j (e_j = the match
+//             run after the first mismatch). The new best is the max of the best key with
+//             c_j < i (prefix over length buckets), the latest j with c_j > i at length i,
+//             and the best extension with c_j == i (per-bucket max).
+//   k[p]:     only candidates j in [p, p + lmax) see it, at bit i = j - p: i < c_j truncates
+//             to i, i == c_j extends. A truncated key never exceeds the best key, so the sign
+//             can change only through (a) an extension beating the best, or (b) a flip inside
+//             the best candidate's matched run; (b) is at most lmax flips per t, resolved
+//             exactly by a window rescan plus the best keys outside the window.
+//   v[p]:     the sign at every t whose endpoint is p - 1 flips (closed form).
+// Contributions (sign' - sign) * g(t), g = grad * payload, are added with fp32 atomics.
+
+constexpr int kTopK = 4;
+
+__device__ __forceinline__ int clz64(uint64_t x) { return x ? __clzll((long long)x) : 64; }
+__device__ __forceinline__ int getbit(const uint32_t *w, int pos) { return (w[pos >> 5] >> (pos & 31)) & 1; }
+
+// key = (length << 16) | (j + 1); length 0 reads as "no match" for the sign.
+__device__ __forceinline__ uint32_t mkkey(int len, int j) { return ((uint32_t)len << 16) | (uint32_t)(j + 1); }
+__device__ __forceinline__ int key_len(uint32_t k) { return (int)(k >> 16); }
+__device__ __forceinline__ int key_j(uint32_t k) { return (int)(k & 0xffffu) - 1; }
+
+__device__ __forceinline__ float sign_of(uint32_t key, const uint32_t *vw) {
+  return key_len(key) >= 1 && getbit(vw, key_j(key) + 1) ? 1.0f : -1.0f;
+}
+
+// Key of candidate j when k[p] is flipped.
+__device__ __forceinline__ uint32_t key_under_kflip(uint64_t qwin, const uint32_t *kw, int j, int p,
+                                                    int lmax) {
+  const uint64_t x = qwin ^ q_window(kw, j);
+  const int c = clz64(x);
+  const int cap = min(j + 1, lmax);
+  const int d = j - p;
+  if (d >= 0 && d < min(c, cap)) return mkkey(d, j);  // truncated
+  if (d >= 0 && d == c && c < cap) {                   // extended
+    const int e = clz64(x << (c + 1));
+    return mkkey(min(c + 1 + e, cap), j);
+  }
+  return mkkey(min(c, cap), j);
+}
+
+__device__ __forceinline__ bool touched_by(int j, int c, int lmax, int p) {
+  const int cap = min(j + 1, lmax);
+  const int d = j - p;
+  return d >= 0 && (d < min(c, cap) || (d == c && c < cap));
+}
+
+// Block = 64 positions of one stream (grid: n_streams x ceil(T/64)).
+// grad (B, T, S) fp32 (d loss / d hard); payload (S,); match_j (n_streams, T) from the
+// forward; cred (n_streams, 3, T) fp32, zeroed by the caller.
+__global__ void __launch_bounds__(64) rosa_credits_kernel(
+    const uint32_t *__restrict__ qb, const uint32_t *__restrict__ kb, const uint32_t *__restrict__ vb,
+    const int32_t *__restrict__ match_j, const float *__restrict__ grad, const float *__restrict__ payload,
+    int64_t S, int T, int W, int lmax, float *__restrict__ cred) {
+  extern __shared__ uint32_t sm[];
+  uint32_t *qw = sm, *kw = sm + W, *vw = sm + 2 * W;
+  uint32_t *Mb = sm + 3 * W + threadIdx.x * 128;  // per-lane length buckets
+  uint32_t *Nb = Mb + 64;
+  const int64_t stream = blockIdx.x;
+  const int64_t b = stream / S, s = stream % S;
+  for (int i = threadIdx.x; i < W; i += 64) {
+    qw[i] = qb[stream * W + i];
+    kw[i] = kb[stream * W + i];
+    vw[i] = vb[stream * W + i];
+  }
+  __syncthreads();
+  const int t = blockIdx.y * 64 + threadIdx.x;
+  if (t >= T || t == 0) return;
+  const float g = grad[(b * T + t) * S + s] * payload[s];
+  if (g == 0.0f) return;
+  float *cq = cred + stream * 3 * T, *ck = cq + T, *cv = cq + 2 * T;
+
+  const uint64_t qwin = q_window(qw, t);
+  const int jstar = match_j[stream * T + t];
+  uint32_t best = 0u;
+  int cstar = 0, capstar = 0;
+  if (jstar >= 0) {
+    cstar = clz64(qwin ^ q_window(kw, jstar));
+    capstar = min(jstar + 1, lmax);
+    best = mkkey(min(cstar, capstar), jstar);
+  }
+  const float sgn = sign_of(best, vw);
+  const int Lstar = key_len(best);
+  // k flips inside the best candidate's matched run, resolved in (b)
+  const int trunc_lo = jstar >= 0 ? jstar - min(cstar, capstar) + 1 : 1;
+  const int trunc_hi = jstar;
+
+  for (int c = 0; c < 64; ++c) Mb[c] = Nb[c] = 0u;
+  uint32_t tk[kTopK] = {0u, 0u, 0u, 0u};
+  int tc[kTopK] = {0, 0, 0, 0};
+  int n_matching = 0;
+
+  uint64_t kwin = 0;  // 64 k bits ending at j, bit 63 = k[j]
+  for (int w = 0; w * 32 < t; ++w) {
+    const uint32_t kword = kw[w];
+    const int jn = min(32, t - w * 32);
+    for (int bb = 0; bb < jn; ++bb) {
+      const int j = w * 32 + bb;
+      kwin = (kwin >> 1) | ((uint64_t)((kword >> bb) & 1u) << 63);
+      const uint64_t x = qwin ^ kwin;
+      const int c = clz64(x);
+      const int cap = min(j + 1, lmax);
+      const int m = min(c, cap);
+      const uint32_t key = mkkey(m, j);
+      const int cb = min(c, 63);
+      if (key > Mb[cb]) Mb[cb] = key;
+      if (m >= 1) {
+        ++n_matching;
+        if (key > tk[kTopK - 1]) {  // the kTopK best keys, with their c (sorted network)
+          uint32_t kk = key;
+          int cc = c;
+#pragma unroll
+          for (int r = 0; r < kTopK; ++r) {
+            if (kk > tk[r]) {
+              const uint32_t tkk = tk[r];
+              const int tcc = tc[r];
+              tk[r] = kk;
+              tc[r] = cc;
+              kk = tkk;
+              cc = tcc;
+            }
+          }
+        }
+      }
+      // key of j when the q bit at its first mismatch flips (unchanged if that bit is
+      // beyond its cap)
+      uint32_t nkey = key;
+      if (c < cap) {
+        const int e = clz64(x << (c + 1));
+        nkey = mkkey(min(c + 1 + e, cap), j);
+        // (a) flipping k[j - c] lifts j above the best: the flip's new best is the largest
+        // extension among the candidates whose first mismatch is at that same k bit
+        const int p = j - c;
+        if (nkey > best && !(p >= trunc_lo && p <= trunc_hi)) {
+          uint32_t mx = 0u;
+          const int jend = min(p + lmax - 1, t - 1);
+          for (int j2 = p; j2 <= jend; ++j2) {
+            const uint64_t x2 = qwin ^ q_window(kw, j2);
+            const int c2 = clz64(x2);
+            const int cap2 = min(j2 + 1, lmax);
+            if (c2 == j2 - p && c2 < cap2) {
+              const int e2 = clz64(x2 << (c2 + 1));
+              mx = max(mx, mkkey(min(c2 + 1 + e2, cap2), j2));
+            }
+          }
+          if (mx == nkey) {  // emitted once, by the flip's best candidate
+            const float s2 = sign_of(nkey, vw);
+            if (s2 != sgn) atomicAdd(ck + p, (s2 - sgn) * g);
+          }
+        }
+      }
+      if (nkey > Nb[cb]) Nb[cb] = nkey;
+    }
+  }
+
+  // v: the endpoint's successor bit
+  if (Lstar >= 1) atomicAdd(cv + jstar + 1, -2.0f * sgn * g);
+
+  // q: flips of q[t - i] for i in [0, min(L*, lmax - 1)]; larger i changes no candidate
+  const int imax = min(min(Lstar, lmax - 1), t);
+  {
+    int sj = -1;  // latest j over buckets c > i
+    for (int c = imax + 2; c < 64; ++c)
+      if (Mb[c]) sj = max(sj, key_j(Mb[c]));
+    for (int i = imax; i >= 0; --i) {
+      if (Mb[i + 1]) sj = max(sj, key_j(Mb[i + 1]));
+      uint32_t g23 = Nb[i];  // extensions of the candidates with c == i
+      if (sj >= 0) g23 = max(g23, mkkey(min(i, min(sj + 1, lmax)), sj));
+      Nb[i] = g23;
+    }
+    uint32_t g1 = 0u;  // best key with c < i
+    for (int i = 0; i <= imax; ++i) {
+      if (i >= 1) g1 = max(g1, Mb[i - 1]);
+      const float s2 = sign_of(max(g1, Nb[i]), vw);
+      if (s2 != sgn) atomicAdd(cq + (t - i), (s2 - sgn) * g);
+    }
+  }
+
+  // (b) k flips inside the best candidate's run: the exact new best of each
+  if (jstar >= 0) {
+    for (int p = trunc_lo; p <= trunc_hi; ++p) {
+      uint32_t nb = 0u;
+      bool outside_known = n_matching <= kTopK;  // the list then holds every matching key
+      bool found = false;
+#pragma unroll
+      for (int r = 0; r < kTopK; ++r) {
+        if (!found && tk[r] != 0u && !touched_by(key_j(tk[r]), tc[r], lmax, p)) {
+          nb = tk[r];
+          found = true;
+        }
+      }
+      outside_known = outside_known || found;
+      if (outside_known) {
+        const int jend = min(p + lmax - 1, t - 1);
+        for (int j2 = p; j2 <= jend; ++j2) nb = max(nb, key_under_kflip(qwin, kw, j2, p, lmax));
+      } else {  // every listed key is touched: rescan all candidates
+        nb = 0u;
+        for (int j2 = 0; j2 < t; ++j2) nb = max(nb, key_under_kflip(qwin, kw, j2, p, lmax));
+      }
+      const float s2 = sign_of(nb, vw);
+      if (s2 != sgn) atomicAdd(ck + p, (s2 - sgn) * g);
+    }
+  }
+}
+
+// d loss / d payload = sum over (b, t) of grad * sign (rosa_credit_gpu.py:110), and the
+// Bernoulli map of the credits to projection space (:99-111): one thread per (b, t, s).
+template <int DT>
+__global__ void __launch_bounds__(256) rosa_credit_grad_kernel(
+    const float *__restrict__ cred, const void *__restrict__ q, const void *__restrict__ k,
+    const void *__restrict__ v, int64_t B, int64_t T, int64_t S, void *__restrict__ gq,
+    void *__restrict__ gk, void *__restrict__ gv) {
+  using E = Elem<DT>;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (b, t, s) flattened
+  if (idx >= B * T * S) return;
+  const int64_t s = idx % S, t = (idx / S) % T, b = idx / (S * T);
+  const float *c = cred + (b * S + s) * 3 * T + t;
+  const void *pre[3] = {q, k, v};
+  void *out[3] = {gq, gk, gv};
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    const float x = E::load((const typename E::T *)pre[m] + idx);
+    const float bit = x > 0.0f ? 1.0f : 0.0f;
+    const float delta = round_to_dt<DT>(c[m * T] * (1.0f - 2.0f * bit));
+    const float sg = 1.0f / (1.0f + expf(-x));
+    const float bern = round_to_dt<DT>(sg * (1.0f - sg));
+    store_out<DT>(out[m], idx, delta * bern);
+  }
+}
+
+// One thread per stream s: sum over b, t in a fixed order.
+__global__ void __launch_bounds__(256) rosa_payload_grad_kernel(const float *__restrict__ grad,
+                                                                const int8_t *__restrict__ sign,
+                                                                int64_t B, int64_t T, int64_t S,
+                                                                float *__restrict__ gp) {
+  const int64_t s = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (s >= S) return;
+  float acc = 0.0f;
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t t = 0; t < T; ++t) acc += grad[(b * T + t) * S + s] * (float)sign[(b * S + s) * T + t];
+  gp[s] = acc;
+}
+
+}  // namespace ksd
+
+using namespace ksd;
+
+extern "C" int ksd_rosa_credits(const uint32_t *q_bits, const uint32_t *k_bits, const uint32_t *v_bits,
+                                const int32_t *match_j, const float *grad, const float *payload,
+                                int64_t B, int64_t T, int64_t S, int lmax, float *credits,
+                                void *stream) {
+  if (B < 0 || T < 0 || S < 0) return fail(KSD_EINVAL, "rosa_credits: negative shape");
+  if (lmax < 0 || lmax > 63) return fail(KSD_EINVAL, "rosa_credits: lmax must be in [0, 63]");
+  if (T > 65535) return fail(KSD_EINVAL, "rosa_credits: T above 65535 is not supported");
+  if (B == 0 || T == 0 || S == 0 || lmax == 0) return KSD_OK;
+  if (!q_bits || !k_bits || !v_bits || !match_j || !grad || !payload || !credits)
+    return fail(KSD_EINVAL, "rosa_credits: null pointer");
+  const int W = (int)cdiv(T, 32);
+  const size_t lds = (3 * (size_t)W + 64 * 128) * sizeof(uint32_t);
+  if (lds > 160 * 1024) return fail(KSD_EINVAL, "rosa_credits: T too large for LDS");
+  dim3 grid((unsigned)(B * S), (unsigned)cdiv(T, 64));
+  hipLaunchKernelGGL(rosa_credits_kernel, grid, dim3(64), lds, (hipStream_t)stream, q_bits, k_bits,
+                     v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits);
+  return check_launch("rosa_credits");
+}
+
+extern "C" int ksd_rosa_credit_grads(const float *credits, const void *q, const void *k, const void *v,
+                                     int dtype, const float *grad, const int8_t *sign, int64_t B,
+                                     int64_t T, int64_t S, void *gq, void *gk, void *gv, float *gpayload,
+                                     void *stream) {
+  if (B < 0 || T < 0 || S < 0) return fail(KSD_EINVAL, "rosa_credit_grads: negative shape");
+  if (dtype != KSD_F32 && dtype != KSD_BF16 && dtype != KSD_F16)
+    return fail(KSD_ETYPE, "rosa_credit_grads: q/k/v must be float32, bfloat16 or float16");
+  if (B == 0 || T == 0 || S == 0) return KSD_OK;
+  if (!credits || !q || !k || !v || !grad || !sign || !gq || !gk || !gv || !gpayload)
+    return fail(KSD_EINVAL, "rosa_credit_grads: null pointer");
+  const int64_t n = B * T * S;
+  hipStream_t st = (hipStream_t)stream;
+  dim3 grid((unsigned)cdiv(n, 256));
+  switch (dtype) {
+    case KSD_F32: hipLaunchKernelGGL(rosa_credit_grad_kernel<KSD_F32>, grid, dim3(256), 0, st, credits, q, k, v, B, T, S, gq, gk, gv); break;
+    case KSD_BF16: hipLaunchKernelGGL(rosa_credit_grad_kernel<KSD_BF16>, grid, dim3(256), 0, st, credits, q, k, v, B, T, S, gq, gk, gv); break;
+    default: hipLaunchKernelGGL(rosa_credit_grad_kernel<KSD_F16>, grid, dim3(256), 0, st, credits, q, k, v, B, T, S, gq, gk, gv); break;
+  }
+  hipLaunchKernelGGL(rosa_payload_grad_kernel, dim3((unsigned)cdiv(S, 256)), dim3(256), 0, st, grad, sign,
+                     B, T, S, gpayload);
+  return check_launch("rosa_credit_grads");
+}

@@ -105,11 +105,27 @@ def sigmoid32(x):
     return (1.0 / (1.0 + np.exp(-np.asarray(x, np.float64)))).astype(np.float32)
 
 
-def shifted(x, time_mix):
-    """rosa.py:128-133 for fp32 x (B, T, d): prev + (x - prev) * sigmoid(mix), fp32 ops."""
+def _bf16_round(a):
+    """fp32 -> bf16 (round to nearest even) -> fp32."""
+    u = np.asarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return u.astype(np.uint32).view(np.float32)
+
+
+def shifted(x, sig, dtype="float32"):
+    """rosa.py:128-133: prev + (x - prev) * sig, sig = sigmoid(time_mix) as fp32.
+
+    x (B, T, d) holds values of `dtype` ("float32", "bfloat16", "float16"): x - prev is a
+    tensor op in that dtype (fp32 then rounded), the rest fp32 (type promotion against the
+    fp32 sigmoid)."""
     x = np.asarray(x, np.float32)
     prev = np.concatenate([np.zeros_like(x[:, :1]), x[:, :-1]], 1)
-    return (prev + ((x - prev).astype(np.float32) * sigmoid32(time_mix)).astype(np.float32)).astype(np.float32)
+    diff = (x - prev).astype(np.float32)
+    if dtype == "bfloat16":
+        diff = _bf16_round(diff)
+    elif dtype == "float16":
+        diff = diff.astype(np.float16).astype(np.float32)
+    return (prev + (diff * np.asarray(sig, np.float32)).astype(np.float32)).astype(np.float32)
 
 
 def bits_of(x):

@@ -1,0 +1,194 @@
+"""GPU parity: the Rosa mixer step kernels against the oracle (oracle/rosa.py).
+
+Bars: packed bits, match signs and endpoints bit-exact (pair brute force in C), including
+T = 2048 and streams whose matches pass the 62-bit cap; the fused time shift + quantize
+bit-exact against quantize_last_dim of the oracle's shift (same fp32 sigmoid values); the
+credits' flip decisions exact and their fp32 sums within 1e-5 relative (the reference's
+own sum order is torch's), the projection gradients after the Bernoulli map likewise.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from ksdraft_amd.kernels import rosa as R
+from ksdraft_amd.kernels.rosa_credit_gpu import HardRosaGPU
+from ksdraft_amd.model.rosa import RosaMixer, _match_payload_sign
+from oracle import quant as oq
+from oracle import rosa as orr
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _g(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _streams(rng, n, T):
+    """Random streams of varied density plus constant / periodic ones (long matches)."""
+    rows = [np.zeros(T), np.ones(T), np.arange(T) % 2, (np.arange(T) // 5) % 2]
+    while len(rows) < n:
+        rows.append(rng.uniform(size=T) < rng.uniform(0.1, 0.9))
+    return np.stack(rows[:n]).astype(np.uint8)
+
+
+def _bits_to_proj(bits, rng):
+    """(n, T) bits -> signed projection values whose (x > 0) bits are `bits`."""
+    mag = rng.uniform(0.1, 2.0, bits.shape).astype(np.float32)
+    return np.where(bits > 0, mag, -mag).astype(np.float32)
+
+
+@pytest.mark.parametrize("T", [2, 5, 33, 63, 64, 100, 300])
+def test_match_vs_pair_bruteforce(T):
+    rng = np.random.default_rng(T)
+    n = 24
+    q = _streams(rng, n, T)
+    k = np.concatenate([q[:6], _streams(rng, n - 6, T)])
+    v = _streams(rng, n, T)[::-1].copy()
+    proj = [_bits_to_proj(b, rng).T[None] for b in (q, k, v)]  # (1, T, n)
+    packed = [R.pack_bits(_g(p)) for p in proj]
+    sign, mj = R.match_packed(*(p.reshape(n, -1) for p in packed), T, want_j=True)
+    es, ej, _ = orr.match(q, k, v)
+    assert np.array_equal(sign.cpu().numpy().astype(np.float32), es)
+    assert np.array_equal(mj.cpu().numpy(), ej)
+
+
+def test_match_t2048_sampled_streams():
+    rng = np.random.default_rng(2048)
+    n, T = 12, 2048
+    q = _streams(rng, n, T)
+    k = np.concatenate([q[:4], _streams(rng, n - 4, T)])
+    v = _streams(rng, n, T)
+    proj = [_bits_to_proj(b, rng).T[None] for b in (q, k, v)]
+    packed = [R.pack_bits(_g(p)) for p in proj]
+    sign, mj = R.match_packed(*(p.reshape(n, -1) for p in packed), T, want_j=True)
+    es, ej, el = orr.match(q, k, v)
+    assert (el == 62).any()
+    assert np.array_equal(sign.cpu().numpy().astype(np.float32), es)
+    assert np.array_equal(mj.cpu().numpy(), ej)
+
+
+def test_pack_bits_dtypes():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((2, 70, 37)).astype(np.float32)
+    x[0, 3, 4] = 0.0
+    x[1, 5, 6] = -0.0
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        xt = _g(x).to(dt)
+        words = R.pack_bits(xt).cpu().numpy().view(np.uint32)
+        bits = orr.bits_of(xt.float().cpu().numpy()).transpose(0, 2, 1)  # (B, S, T)
+        for t in range(70):
+            got = (words[..., t // 32] >> (t % 32)) & 1
+            assert np.array_equal(got, bits[..., t]), (dt, t)
+
+
+def test_match_payload_sign_api_kats():
+    q, k, v = [[0, 1, 1, 1]], [[1, 0, 1, 1]], [[1, 0, 0, 1]]
+    got = _match_payload_sign(_g(np.array(q, np.int8)), _g(np.array(k, np.int8)),
+                              _g(np.array(v, np.int8)))
+    assert got.cpu().tolist() == [[-1.0, -1.0, -1.0, 1.0]]
+    got = _match_payload_sign(*(_g(np.array(a, np.int8)) for a in ([[1, 1, 1]], [[0, 0, 0]], [[1, 1, 1]])))
+    assert got.cpu().tolist() == [[-1.0, -1.0, -1.0]]
+    rng = np.random.default_rng(4)
+    q, k, v = (rng.integers(0, 2, (3, 5, 40)).astype(np.int8) for _ in range(3))
+    got = _match_payload_sign(_g(q), _g(k), _g(v), max_match_len=6).cpu().numpy()
+    assert np.array_equal(got, orr.match_payload_sign_loops(q, k, v, 6))
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+def test_shift_quantize(dtype):
+    rng = np.random.default_rng(9)
+    B, T, d = 2, 33, 320
+    x = rng.standard_normal((B, T, d)).astype(np.float32) * 2
+    tdt = getattr(torch, dtype)
+    xt = _g(x).to(tdt)
+    mixes = [_g(rng.standard_normal(d).astype(np.float32)) for _ in range(3)]
+    sigs = [torch.sigmoid(m) for m in mixes]
+    out = R.shift_quantize(xt, *sigs, group=128)
+    xv = xt.float().cpu().numpy()
+    for (codes, scales), sg in zip(out, sigs):
+        lerp = orr.shifted(xv, sg.cpu().numpy(), dtype).reshape(B * T, d)
+        ec, es = oq.quantize_last_dim(lerp)
+        assert np.array_equal(codes.cpu().numpy(), ec)
+        assert np.array_equal(scales.cpu().numpy(), es)
+
+
+def _hard_case(seed, B, T, S):
+    rng = np.random.default_rng(seed)
+    q, k, v = (rng.standard_normal((B, T, S)).astype(np.float32) * 2 for _ in range(3))
+    # a few streams with long matches: constant and copied patterns
+    q[:, :, 0] = 1.0
+    k[:, :, 0] = 1.0
+    k[:, :, 1] = q[:, :, 1]
+    payload = (np.abs(rng.standard_normal(S)) + 0.5).astype(np.float32)
+    g = rng.standard_normal((B, T, S)).astype(np.float32)
+    return q, k, v, payload, g
+
+
+@pytest.mark.parametrize("B,T,S", [(2, 16, 8), (1, 63, 6), (2, 70, 5), (1, 150, 4)])
+def test_hard_rosa_forward_backward(B, T, S):
+    q, k, v, payload, g = _hard_case(T, B, T, S)
+    tq, tk, tv, tp = (_g(a).requires_grad_(True) for a in (q, k, v, payload))
+    y = HardRosaGPU.apply(tq, tk, tv, tp)
+    y.backward(_g(g))
+    ey, _ = orr.hard_rosa_forward(q, k, v, payload)
+    assert torch.equal(y.detach().cpu(), torch.from_numpy(ey))
+    egq, egk, egv, egp = orr.hard_rosa_backward(q, k, v, payload, g)
+    for got, exp in ((tq.grad, egq), (tk.grad, egk), (tv.grad, egv), (tp.grad, egp)):
+        got = got.cpu().numpy()
+        scale = np.abs(exp).max() + 1e-30
+        np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * scale)
+        assert np.array_equal(got == 0, exp == 0)  # the same flips change the sign
+
+
+def test_credits_t2048_sampled_flips():
+    """At T = 2048 the oracle checks sampled flips by re-matching each flipped stream."""
+    rng = np.random.default_rng(77)
+    B, T, S = 1, 2048, 3
+    q, k, v, payload, g = _hard_case(77, B, T, S)
+    tq, tk, tv = (_g(a).requires_grad_(True) for a in (q, k, v))
+    y = HardRosaGPU.apply(tq, tk, tv, _g(payload))
+    y.backward(_g(g))
+    bits = [orr.bits_of(a[0].T) for a in (q, k, v)]  # (S, T)
+    base, _, _ = orr.match(*bits)
+    gsign = (g[0].T * payload[:, None]).astype(np.float64)
+    for which, grad in ((0, tq.grad), (1, tk.grad), (2, tv.grad)):
+        pre = (q, k, v)[which][0].T
+        sig = orr.sigmoid32(pre)
+        bern = (sig * (np.float32(1) - sig)).astype(np.float32)
+        gg = grad[0].T.cpu().numpy()  # (S, T)
+        for s in range(S):
+            for p in rng.choice(T, 12, replace=False):
+                fl = [b[s:s + 1].copy() for b in bits]
+                fl[which][0, p] ^= 1
+                sp, _, _ = orr.match(*fl)
+                cred = float(((sp[0] - base[s]) * gsign[s]).sum())
+                exp = np.float32(cred * (1.0 - 2.0 * bits[which][s, p])) * bern[s, p]
+                assert abs(gg[s, p] - exp) <= 1e-5 * max(1.0, abs(exp)), (which, s, p, gg[s, p], exp)
+
+
+def test_rosa_mixer_eval_and_training():
+    torch.manual_seed(0)
+    m = RosaMixer(64, 16).to(DEV)
+    with torch.no_grad():
+        m.out_proj.weight.normal_(0, 0.05)
+    x = torch.randn(2, 24, 64, device=DEV)
+    m.eval()
+    y = m(x)
+    q_in, k_in, v_in = m._shifted(x)
+    with torch.no_grad():
+        bits = [orr.bits_of(p(i).cpu().numpy()).transpose(0, 2, 1).reshape(-1, 24)
+                for p, i in ((m.q_proj, q_in), (m.k_proj, k_in), (m.v_proj, v_in))]
+    sign, _, _ = orr.match(*bits)
+    hard = (m.payload.detach().cpu().numpy()[None, :, None] * sign.reshape(2, 16, 24)).transpose(0, 2, 1)
+    exp = m.out_proj(torch.from_numpy(np.ascontiguousarray(hard)).to(DEV))
+    torch.testing.assert_close(y, exp, rtol=1e-5, atol=1e-6)
+    y.square().mean().backward()
+    assert m.payload.grad is not None and m.q_proj.weight.grad is None
+    m.zero_grad()
+    m.train()
+    m(x).square().mean().backward()
+    for name in ("payload", "q_proj.weight", "k_proj.weight", "v_proj.weight", "time_mix_q"):
+        p = dict(m.named_parameters())[name]
+        assert p.grad is not None and torch.isfinite(p.grad).all(), name
