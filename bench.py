@@ -55,6 +55,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-ks3", action="store_true", help="skip the KS3 kernel report")
+    p.add_argument("--no-rosa", action="store_true", help="skip the Rosa kernel report")
     p.add_argument("--pmc-probe", action="store_true",
                    help="for rocprofv3 --pmc runs: a 256 MiB device copy (counter "
                         "calibration), then 3 launches of each GEMM of the step; no timing")
@@ -215,6 +216,73 @@ def ks3_kernel_times(dev, reps):
     return res
 
 
+def rosa_kernel_times(dev, reps):
+    """The Rosa mixer step's kernels at BASELINE config 4's shape (B = 4, T = 2048,
+    d = 1536, S = 512 streams). x ~N(0,1) bf16; projections ~N(0,1) (their signs are the
+    symbol bits); time mixes 0 and payload 1 (model/rosa.py:117-123 inits); upstream
+    gradient ~N(0,1). The match and the credits are integer-VALU work over the
+    B*S*T*(T-1)/2 = 4.29e9 (t, j) pairs, reported as pairs/s."""
+    from ksdraft_amd.kernels import rosa as R
+    from ksdraft_amd.kernels.rosa_credit_gpu import HardRosaGPU
+    Bq, T, d, S = 4, 2048, 1536, 512
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(Bq, T, d, generator=g).to(dev).to(torch.bfloat16)
+    sig = torch.full((d,), 0.5, device=dev)
+    q, k, v = (torch.randn(Bq, T, S, generator=g).to(dev) for _ in range(3))
+    payload = torch.ones(S, device=dev)
+    gout = torch.randn(Bq, T, S, generator=g).to(dev)
+    bits = [R.pack_bits(t) for t in (q, k, v)]
+    flat = [b.reshape(Bq * S, -1) for b in bits]
+    sign, mj = R.match_packed(*flat, T, want_j=True)
+    pairs = Bq * S * T * (T - 1) // 2
+    from ksdraft_amd import _lib
+    cred = torch.zeros(Bq * S, 3, T, device=dev)
+    part = torch.empty(Bq * S, device=dev)
+
+    def credits():
+        _lib.call("ksd_rosa_credits", flat[0].data_ptr(), flat[1].data_ptr(), flat[2].data_ptr(),
+                  mj.data_ptr(), gout.data_ptr(), payload.data_ptr(), Bq, T, S, 62,
+                  cred.data_ptr(), part.data_ptr(), _lib.stream_ptr(dev))
+
+    BTd, BTS = Bq * T * d, Bq * T * S
+    stages = {
+        "rosa_shift_quant": (lambda: R.shift_quantize(x, sig, sig, sig), 2 * BTd + 3 * (BTd + 2 * BTd // 128), None),
+        "rosa_pack_bits_x3": (lambda: [R.pack_bits(t) for t in (q, k, v)], 3 * (4 * BTS + BTS // 8), None),
+        "rosa_match": (lambda: R.match_packed(*flat, T, want_j=True), None, pairs),
+        "rosa_hard_out": (lambda: R.hard_out(sign.reshape(Bq, S, T), payload), BTS + 4 * BTS, None),
+        "rosa_credits": (credits, None, pairs),
+    }
+    res = {}
+    for name, (fn, nbytes, npairs) in stages.items():
+        r = reps if npairs is None else max(1, reps // 4)
+
+        def rep(fn=fn, r=r):
+            for _ in range(r):
+                fn()
+        _, _, ms = time_graph(rep, 3, warm=1)
+        us = ms * 1e3 / r
+        ent = {"us": round(us, 3)}
+        if nbytes is not None:
+            ent["bytes"] = nbytes
+            ent["GBps"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+            ent["hbm_frac"] = round(nbytes / (us * 1e-6) / PEAK_HBM, 3)
+        else:
+            ent["pairs"] = npairs
+            ent["Gpairs_per_s"] = round(npairs / (us * 1e-6) / 1e9, 1)
+        res[name] = ent
+    # the autograd path end to end (forward + exact-credit backward)
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+    for _ in range(2):  # allocator warm-up
+        HardRosaGPU.apply(qg, kg, vg, payload).backward(gout)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        HardRosaGPU.apply(qg, kg, vg, payload).backward(gout)
+    torch.cuda.synchronize()
+    res["hard_rosa_fwd_bwd_ms"] = round((time.perf_counter() - t0) * 1e3 / 3, 3)
+    return res
+
+
 def cpu_baseline(x, w, dy, budget_s):
     """The oracle's restatement of the reference CPU path (quantize in numpy; GEMMs as
     dequantize + fp32 BLAS matmul, reference ksdraft/kernels/gemm.py:76-82), timed on
@@ -345,6 +413,7 @@ def main():
         "draft_train_step_tok_s": None,
         "kernels": kern,
         "ks3_c4_kernels": None if args.no_ks3 else ks3_kernel_times(dev, args.kernel_reps),
+        "rosa_c4_kernels": None if args.no_rosa else rosa_kernel_times(dev, args.kernel_reps),
         "roofline": {
             "kernel": "gemm_nt_kernel<128,f32> (fwd, dX, dW launches averaged)",
             "bound": "mfma",

@@ -247,22 +247,24 @@ int ksd_rosa_hard(const int8_t *sign, const float *payload, int64_t B, int64_t T
  *   grad        (B, T, S) fp32 upstream gradient of the hard output
  *   credits     (B*S, 3, T) fp32, zeroed by the caller; accumulated with atomics, so the
  *               summation order (not the flip decisions) varies between runs
+ *   payload_partial (B*S,) fp32: sum over t of grad * sign per stream (fixed order)
  */
 int ksd_rosa_credits(const uint32_t *q_bits, const uint32_t *k_bits, const uint32_t *v_bits,
                      const int32_t *match_j, const float *grad, const float *payload, int64_t B,
-                     int64_t T, int64_t S, int lmax, float *credits, void *stream);
+                     int64_t T, int64_t S, int lmax, float *credits, float *payload_partial,
+                     void *stream);
 
 /*
  * R5 projection-space gradients (reference ksdraft/kernels/rosa_credit_gpu.py:99-111):
  * g_x = credit * (1 - 2 * bit) * sigmoid(x) * (1 - sigmoid(x)) in x's dtype, and
- * d payload[s] = sum over (b, t) of grad * sign (fixed order).
- *   q/k/v   (B, T, S) pre-bit projections of type dtype; grad (B, T, S) fp32
- *   sign    (B, S, T) int8 from ksd_rosa_match
+ * d payload[s] = sum over b of payload_partial[b, s] (fixed order).
+ *   q/k/v   (B, T, S) pre-bit projections of type dtype
+ *   payload_partial (B*S,) fp32 from ksd_rosa_credits
  *   gq/gk/gv (B, T, S) of type dtype; gpayload (S,) fp32
  */
 int ksd_rosa_credit_grads(const float *credits, const void *q, const void *k, const void *v,
-                          int dtype, const float *grad, const int8_t *sign, int64_t B, int64_t T,
-                          int64_t S, void *gq, void *gk, void *gv, float *gpayload, void *stream);
+                          int dtype, const float *payload_partial, int64_t B, int64_t T, int64_t S,
+                          void *gq, void *gk, void *gv, float *gpayload, void *stream);
 
 #ifdef __cplusplus
 }

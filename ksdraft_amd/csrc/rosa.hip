@@ -327,13 +327,14 @@ namespace ksd {
 //             and the best extension with c_j == i (per-bucket max).
 //   k[p]:     only candidates j in [p, p + lmax) see it, at bit i = j - p: i < c_j truncates
 //             to i, i == c_j extends. A truncated key never exceeds the best key, so the sign
-//             can change only through (a) an extension beating the best, or (b) a flip inside
-//             the best candidate's matched run; (b) is at most lmax flips per t, resolved
-//             exactly by a window rescan plus the best keys outside the window.
+//             can change only through (a) an extension beating the best (every candidate
+//             that beats it under flip p is such an extension, so the flip's new best is the
+//             largest one), or (b) a flip inside the best candidate's matched run: at most
+//             lmax flips per t, each resolved from the candidates within 62 of j* (kept in
+//             LDS) and the best key farther away (unchanged by the flip).
 //   v[p]:     the sign at every t whose endpoint is p - 1 flips (closed form).
 // Contributions (sign' - sign) * g(t), g = grad * payload, are added with fp32 atomics.
 
-constexpr int kTopK = 4;
 
 __device__ __forceinline__ int clz64(uint64_t x) { return x ? __clzll((long long)x) : 64; }
 __device__ __forceinline__ int getbit(const uint32_t *w, int pos) { return (w[pos >> 5] >> (pos & 31)) & 1; }
@@ -347,183 +348,208 @@ __device__ __forceinline__ float sign_of(uint32_t key, const uint32_t *vw) {
   return key_len(key) >= 1 && getbit(vw, key_j(key) + 1) ? 1.0f : -1.0f;
 }
 
-// Key of candidate j when k[p] is flipped.
-__device__ __forceinline__ uint32_t key_under_kflip(uint64_t qwin, const uint32_t *kw, int j, int p,
-                                                    int lmax) {
-  const uint64_t x = qwin ^ q_window(kw, j);
-  const int c = clz64(x);
-  const int cap = min(j + 1, lmax);
-  const int d = j - p;
-  if (d >= 0 && d < min(c, cap)) return mkkey(d, j);  // truncated
-  if (d >= 0 && d == c && c < cap) {                   // extended
-    const int e = clz64(x << (c + 1));
-    return mkkey(min(c + 1 + e, cap), j);
-  }
-  return mkkey(min(c, cap), j);
+// Block = one stream, 4 waves; wave w handles positions t = w, w + 4, ... and its 64 lanes
+// split the candidates j. Per-wave LDS tables for the current t:
+//   Mw[64]   best key per common-suffix bucket c (c >= 63 pooled)
+//   Nw[64]   best key per bucket after flipping the q bit at the first mismatch
+//   Rk[128]  k-extension events, slot p mod 128: the best lifted key of flip k[p]
+//   Cn/En[128]  c_j and e_j (uint8) of the candidates j in [j* - 63, j* + 64)
+constexpr int kNear = 128;
+constexpr int kCredWaves = 4;
+constexpr int kCredWave32 = 64 + 64 + 128 + 2 * kNear / 4 + 2 * kNear;  // uint32 words per wave
+
+__device__ __forceinline__ uint32_t ext_key(int c, int e, int cap, int j) {
+  return mkkey(min(c + 1 + e, cap), j);
 }
 
-__device__ __forceinline__ bool touched_by(int j, int c, int lmax, int p) {
-  const int cap = min(j + 1, lmax);
-  const int d = j - p;
-  return d >= 0 && (d < min(c, cap) || (d == c && c < cap));
-}
-
-// Block = 64 positions of one stream (grid: n_streams x ceil(T/64)).
-// grad (B, T, S) fp32 (d loss / d hard); payload (S,); match_j (n_streams, T) from the
-// forward; cred (n_streams, 3, T) fp32, zeroed by the caller.
-__global__ void __launch_bounds__(64) rosa_credits_kernel(
+__global__ void __launch_bounds__(256) rosa_credits_kernel(
     const uint32_t *__restrict__ qb, const uint32_t *__restrict__ kb, const uint32_t *__restrict__ vb,
     const int32_t *__restrict__ match_j, const float *__restrict__ grad, const float *__restrict__ payload,
-    int64_t S, int T, int W, int lmax, float *__restrict__ cred) {
+    int64_t S, int T, int W, int lmax, float *__restrict__ cred, float *__restrict__ gp_partial) {
   extern __shared__ uint32_t sm[];
   uint32_t *qw = sm, *kw = sm + W, *vw = sm + 2 * W;
-  uint32_t *Mb = sm + 3 * W + threadIdx.x * 128;  // per-lane length buckets
-  uint32_t *Nb = Mb + 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint32_t *Mw = sm + 3 * W + wave * kCredWave32;
+  uint32_t *Nw = Mw + 64, *Rk = Mw + 128;
+  uint8_t *Cn = (uint8_t *)(Mw + 256), *En = Cn + kNear;
+  uint32_t *Pref = Mw + 256 + kNear / 2, *Suf = Pref + kNear;  // near-key prefix/suffix max
   const int64_t stream = blockIdx.x;
   const int64_t b = stream / S, s = stream % S;
-  for (int i = threadIdx.x; i < W; i += 64) {
+  for (int i = threadIdx.x; i < W; i += 256) {
     qw[i] = qb[stream * W + i];
     kw[i] = kb[stream * W + i];
     vw[i] = vb[stream * W + i];
   }
   __syncthreads();
-  const int t = blockIdx.y * 64 + threadIdx.x;
-  if (t >= T || t == 0) return;
-  const float g = grad[(b * T + t) * S + s] * payload[s];
-  if (g == 0.0f) return;
   float *cq = cred + stream * 3 * T, *ck = cq + T, *cv = cq + 2 * T;
+  const float pay = payload[s];
+  float gsum = 0.0f;  // this wave's share of sum_t grad * sign (d loss / d payload)
+  __shared__ float gps[kCredWaves];
 
-  const uint64_t qwin = q_window(qw, t);
-  const int jstar = match_j[stream * T + t];
-  uint32_t best = 0u;
-  int cstar = 0, capstar = 0;
-  if (jstar >= 0) {
-    cstar = clz64(qwin ^ q_window(kw, jstar));
-    capstar = min(jstar + 1, lmax);
-    best = mkkey(min(cstar, capstar), jstar);
-  }
-  const float sgn = sign_of(best, vw);
-  const int Lstar = key_len(best);
-  // k flips inside the best candidate's matched run, resolved in (b)
-  const int trunc_lo = jstar >= 0 ? jstar - min(cstar, capstar) + 1 : 1;
-  const int trunc_hi = jstar;
+  for (int t = wave; t < T; t += kCredWaves) {  // wave-uniform
+    const float gr = grad[(b * T + t) * S + s];
+    const int jstar = match_j[stream * T + t];
+    const uint64_t qwin = q_window(qw, t);
+    uint32_t best = 0u;
+    int cstar = 0, capstar = 0;
+    if (jstar >= 0) {
+      cstar = clz64(qwin ^ q_window(kw, jstar));
+      capstar = min(jstar + 1, lmax);
+      best = mkkey(min(cstar, capstar), jstar);
+    }
+    const float sgn = sign_of(best, vw);
+    gsum += gr * sgn;
+    const float g = gr * pay;
+    if (t == 0 || g == 0.0f || lmax < 1) continue;
+    const int Lstar = key_len(best);
+    // k flips inside the best candidate's matched run, resolved in (b)
+    const int trunc_lo = jstar >= 0 ? jstar - min(cstar, capstar) + 1 : 1;
+    const int trunc_hi = jstar;
+    const int near0 = jstar - 63;  // Cn/En hold j in [near0, near0 + kNear)
 
-  for (int c = 0; c < 64; ++c) Mb[c] = Nb[c] = 0u;
-  uint32_t tk[kTopK] = {0u, 0u, 0u, 0u};
-  int tc[kTopK] = {0, 0, 0, 0};
-  int n_matching = 0;
+    Mw[lane] = Nw[lane] = 0u;
+    Rk[lane] = Rk[lane + 64] = 0u;
+    uint32_t farbest = 0u;  // best key among j outside [j* - 62, j* + 62] (this lane's j)
+    int emit_hi = t - 1;    // k positions above emit_hi are done
 
-  uint64_t kwin = 0;  // 64 k bits ending at j, bit 63 = k[j]
-  for (int w = 0; w * 32 < t; ++w) {
-    const uint32_t kword = kw[w];
-    const int jn = min(32, t - w * 32);
-    for (int bb = 0; bb < jn; ++bb) {
-      const int j = w * 32 + bb;
-      kwin = (kwin >> 1) | ((uint64_t)((kword >> bb) & 1u) << 63);
-      const uint64_t x = qwin ^ kwin;
-      const int c = clz64(x);
-      const int cap = min(j + 1, lmax);
-      const int m = min(c, cap);
-      const uint32_t key = mkkey(m, j);
-      const int cb = min(c, 63);
-      if (key > Mb[cb]) Mb[cb] = key;
-      if (m >= 1) {
-        ++n_matching;
-        if (key > tk[kTopK - 1]) {  // the kTopK best keys, with their c (sorted network)
-          uint32_t kk = key;
-          int cc = c;
-#pragma unroll
-          for (int r = 0; r < kTopK; ++r) {
-            if (kk > tk[r]) {
-              const uint32_t tkk = tk[r];
-              const int tcc = tc[r];
-              tk[r] = kk;
-              tc[r] = cc;
-              kk = tkk;
-              cc = tcc;
-            }
-          }
+    // candidates from the latest down: a bucket's best key is its latest j, so the
+    // bucket tables are written only when a key beats the stored one
+    for (int j0 = ((t - 1) / 64) * 64; j0 >= 0; j0 -= 64) {
+      const int j = j0 + lane;
+      if (j < t) {
+        const uint64_t x = qwin ^ q_window(kw, j);
+        const int c = clz64(x);
+        const int cap = min(j + 1, lmax);
+        const uint32_t key = mkkey(min(c, cap), j);
+        const int cb = min(c, 63);
+        if (key > Mw[cb]) atomicMax(Mw + cb, key);
+        const int r = j - near0;
+        if (r < 1 || r > 125) farbest = max(farbest, key);
+        uint32_t nkey = key;  // after flipping the q bit at j's first mismatch
+        int e = 0;
+        if (c < cap) {
+          e = clz64(x << (c + 1));
+          nkey = ext_key(c, e, cap, j);
+          // (a) flipping k[j - c] extends j past the best
+          const int p = j - c;
+          if (nkey > best && !(p >= trunc_lo && p <= trunc_hi)) atomicMax(Rk + (p & 127), nkey);
+        }
+        if (nkey > Nw[cb]) atomicMax(Nw + cb, nkey);
+        if (r >= 0 && r < kNear) {
+          Cn[r] = (uint8_t)c;
+          En[r] = (uint8_t)e;
         }
       }
-      // key of j when the q bit at its first mismatch flips (unchanged if that bit is
-      // beyond its cap)
-      uint32_t nkey = key;
-      if (c < cap) {
-        const int e = clz64(x << (c + 1));
-        nkey = mkkey(min(c + 1 + e, cap), j);
-        // (a) flipping k[j - c] lifts j above the best: the flip's new best is the largest
-        // extension among the candidates whose first mismatch is at that same k bit
-        const int p = j - c;
-        if (nkey > best && !(p >= trunc_lo && p <= trunc_hi)) {
-          uint32_t mx = 0u;
-          const int jend = min(p + lmax - 1, t - 1);
-          for (int j2 = p; j2 <= jend; ++j2) {
-            const uint64_t x2 = qwin ^ q_window(kw, j2);
-            const int c2 = clz64(x2);
-            const int cap2 = min(j2 + 1, lmax);
-            if (c2 == j2 - p && c2 < cap2) {
-              const int e2 = clz64(x2 << (c2 + 1));
-              mx = max(mx, mkkey(min(c2 + 1 + e2, cap2), j2));
-            }
-          }
-          if (mx == nkey) {  // emitted once, by the flip's best candidate
-            const float s2 = sign_of(nkey, vw);
+      // events of p come from j in [p, p + 61]: every p >= j0 is now complete
+      {
+        const int p = j0 + lane;
+        if (p <= emit_hi) {
+          const uint32_t v = Rk[p & 127];
+          if (v) {
+            Rk[p & 127] = 0u;
+            const float s2 = sign_of(v, vw);
             if (s2 != sgn) atomicAdd(ck + p, (s2 - sgn) * g);
           }
         }
       }
-      if (nkey > Nb[cb]) Nb[cb] = nkey;
+      emit_hi = j0 - 1;
     }
-  }
-
-  // v: the endpoint's successor bit
-  if (Lstar >= 1) atomicAdd(cv + jstar + 1, -2.0f * sgn * g);
-
-  // q: flips of q[t - i] for i in [0, min(L*, lmax - 1)]; larger i changes no candidate
-  const int imax = min(min(Lstar, lmax - 1), t);
-  {
-    int sj = -1;  // latest j over buckets c > i
-    for (int c = imax + 2; c < 64; ++c)
-      if (Mb[c]) sj = max(sj, key_j(Mb[c]));
-    for (int i = imax; i >= 0; --i) {
-      if (Mb[i + 1]) sj = max(sj, key_j(Mb[i + 1]));
-      uint32_t g23 = Nb[i];  // extensions of the candidates with c == i
-      if (sj >= 0) g23 = max(g23, mkkey(min(i, min(sj + 1, lmax)), sj));
-      Nb[i] = g23;
-    }
-    uint32_t g1 = 0u;  // best key with c < i
-    for (int i = 0; i <= imax; ++i) {
-      if (i >= 1) g1 = max(g1, Mb[i - 1]);
-      const float s2 = sign_of(max(g1, Nb[i]), vw);
-      if (s2 != sgn) atomicAdd(cq + (t - i), (s2 - sgn) * g);
-    }
-  }
-
-  // (b) k flips inside the best candidate's run: the exact new best of each
-  if (jstar >= 0) {
-    for (int p = trunc_lo; p <= trunc_hi; ++p) {
-      uint32_t nb = 0u;
-      bool outside_known = n_matching <= kTopK;  // the list then holds every matching key
-      bool found = false;
 #pragma unroll
-      for (int r = 0; r < kTopK; ++r) {
-        if (!found && tk[r] != 0u && !touched_by(key_j(tk[r]), tc[r], lmax, p)) {
-          nb = tk[r];
-          found = true;
+    for (int o = 32; o > 0; o >>= 1) farbest = max(farbest, (uint32_t)__shfl_xor((int)farbest, o));
+
+    // v: the endpoint's successor bit
+    if (lane == 0 && Lstar >= 1) atomicAdd(cv + jstar + 1, -2.0f * sgn * g);
+
+    // q: flip of q[t - i], one lane per i in [0, min(L*, lmax - 1)]. Lane c holds bucket c;
+    // g1 = max key over buckets < i (exclusive prefix scan), sj = latest j over buckets > i
+    // (exclusive suffix scan).
+    {
+      const uint32_t mk = Mw[lane];
+      uint32_t pre = mk;
+      int suf = mk ? key_j(mk) : -1;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t a = (uint32_t)__shfl_up((int)pre, d);
+        const int bsj = __shfl_down(suf, d);
+        if (lane >= d) pre = max(pre, a);
+        if (lane + d < 64) suf = max(suf, bsj);
+      }
+      const uint32_t g1 = lane >= 1 ? (uint32_t)__shfl_up((int)pre, 1) : 0u;  // buckets < lane
+      const int sj = __shfl_down(suf, 1);                                      // buckets > lane
+      const int imax = min(min(Lstar, lmax - 1), t);
+      if (lane <= imax) {
+        const int i = lane;
+        uint32_t nb = max(g1, Nw[i]);  // Nw[i]: the candidates with c == i, bit flipped
+        if (lane < 63 && sj >= 0) nb = max(nb, mkkey(min(i, min(sj + 1, lmax)), sj));
+        const float s2 = sign_of(nb, vw);
+        if (s2 != sgn) atomicAdd(cq + (t - i), (s2 - sgn) * g);
+      }
+    }
+
+    // (b) k flips inside the best candidate's run, one lane per flip. Flip p touches only
+    // candidates j with j - c_j <= p <= j, all within 62 of j*; keys farther away are
+    // unchanged (farbest), and near keys outside [p, p + cmax] through prefix / suffix
+    // maxima of the unchanged near keys.
+    if (jstar >= 0) {
+      const int jlo = max(0, jstar - 62), jhi = min(t - 1, jstar + 62);
+      // unchanged near keys, two per lane (r = 2 * lane, 2 * lane + 1), and their max c
+      uint32_t kr[2];
+      int cmax = 0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = 2 * lane + h;
+        const int j2 = near0 + r;
+        kr[h] = 0u;
+        if (j2 >= jlo && j2 <= jhi) {
+          const int c2 = Cn[r];
+          kr[h] = mkkey(min(c2, min(j2 + 1, lmax)), j2);
+          cmax = max(cmax, c2);
         }
       }
-      outside_known = outside_known || found;
-      if (outside_known) {
-        const int jend = min(p + lmax - 1, t - 1);
-        for (int j2 = p; j2 <= jend; ++j2) nb = max(nb, key_under_kflip(qwin, kw, j2, p, lmax));
-      } else {  // every listed key is touched: rescan all candidates
-        nb = 0u;
-        for (int j2 = 0; j2 < t; ++j2) nb = max(nb, key_under_kflip(qwin, kw, j2, p, lmax));
+      uint32_t pre = max(kr[0], kr[1]), suf = pre;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t a = (uint32_t)__shfl_up((int)pre, d);
+        const uint32_t bb = (uint32_t)__shfl_down((int)suf, d);
+        const int cm = __shfl_xor(cmax, d);
+        if (lane >= d) pre = max(pre, a);
+        if (lane + d < 64) suf = max(suf, bb);
+        cmax = max(cmax, cm);
       }
-      const float s2 = sign_of(nb, vw);
-      if (s2 != sgn) atomicAdd(ck + p, (s2 - sgn) * g);
+      // inclusive prefix / suffix max per near index r
+      const uint32_t pre_prev = lane >= 1 ? (uint32_t)__shfl_up((int)pre, 1) : 0u;
+      const uint32_t suf_next = lane < 63 ? (uint32_t)__shfl_down((int)suf, 1) : 0u;
+      Pref[2 * lane] = max(pre_prev, kr[0]);
+      Pref[2 * lane + 1] = pre;
+      Suf[2 * lane] = suf;
+      Suf[2 * lane + 1] = max(suf_next, kr[1]);
+      const int p = trunc_lo + lane;
+      if (p <= trunc_hi) {
+        uint32_t nb = farbest;
+        const int rl = p - 1 - near0;          // near keys left of the flip
+        if (p - 1 >= jlo) nb = max(nb, Pref[rl]);
+        const int jend = min(jhi, p + cmax);   // candidates that can reach k[p]
+        if (jend + 1 <= jhi) nb = max(nb, Suf[jend + 1 - near0]);
+        for (int j2 = p; j2 <= jend; ++j2) {
+          const int r = j2 - near0;
+          const int c2 = Cn[r], e2 = En[r];
+          const int cap2 = min(j2 + 1, lmax);
+          const int d = j2 - p;
+          uint32_t k2;
+          if (d < min(c2, cap2)) k2 = mkkey(d, j2);
+          else if (d == c2 && c2 < cap2) k2 = ext_key(c2, e2, cap2, j2);
+          else k2 = mkkey(min(c2, cap2), j2);
+          nb = max(nb, k2);
+        }
+        const float s2 = sign_of(nb, vw);
+        if (s2 != sgn) atomicAdd(ck + p, (s2 - sgn) * g);
+      }
     }
   }
+  if (lane == 0) gps[wave] = gsum;
+  __syncthreads();
+  if (threadIdx.x == 0) gp_partial[stream] = ((gps[0] + gps[1]) + gps[2]) + gps[3];
 }
 
 // d loss / d payload = sum over (b, t) of grad * sign (rosa_credit_gpu.py:110), and the
@@ -551,16 +577,14 @@ __global__ void __launch_bounds__(256) rosa_credit_grad_kernel(
   }
 }
 
-// One thread per stream s: sum over b, t in a fixed order.
-__global__ void __launch_bounds__(256) rosa_payload_grad_kernel(const float *__restrict__ grad,
-                                                                const int8_t *__restrict__ sign,
-                                                                int64_t B, int64_t T, int64_t S,
+// d payload[s] = sum over b of the per-stream partials, in a fixed order.
+__global__ void __launch_bounds__(256) rosa_payload_grad_kernel(const float *__restrict__ partial,
+                                                                int64_t B, int64_t S,
                                                                 float *__restrict__ gp) {
   const int64_t s = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (s >= S) return;
   float acc = 0.0f;
-  for (int64_t b = 0; b < B; ++b)
-    for (int64_t t = 0; t < T; ++t) acc += grad[(b * T + t) * S + s] * (float)sign[(b * S + s) * T + t];
+  for (int64_t b = 0; b < B; ++b) acc += partial[b * S + s];
   gp[s] = acc;
 }
 
@@ -571,31 +595,32 @@ using namespace ksd;
 extern "C" int ksd_rosa_credits(const uint32_t *q_bits, const uint32_t *k_bits, const uint32_t *v_bits,
                                 const int32_t *match_j, const float *grad, const float *payload,
                                 int64_t B, int64_t T, int64_t S, int lmax, float *credits,
-                                void *stream) {
+                                float *payload_partial, void *stream) {
   if (B < 0 || T < 0 || S < 0) return fail(KSD_EINVAL, "rosa_credits: negative shape");
   if (lmax < 0 || lmax > 63) return fail(KSD_EINVAL, "rosa_credits: lmax must be in [0, 63]");
   if (T > 65535) return fail(KSD_EINVAL, "rosa_credits: T above 65535 is not supported");
-  if (B == 0 || T == 0 || S == 0 || lmax == 0) return KSD_OK;
-  if (!q_bits || !k_bits || !v_bits || !match_j || !grad || !payload || !credits)
+  if (B == 0 || T == 0 || S == 0) return KSD_OK;
+  if (!q_bits || !k_bits || !v_bits || !match_j || !grad || !payload || !credits || !payload_partial)
     return fail(KSD_EINVAL, "rosa_credits: null pointer");
   const int W = (int)cdiv(T, 32);
-  const size_t lds = (3 * (size_t)W + 64 * 128) * sizeof(uint32_t);
-  if (lds > 160 * 1024) return fail(KSD_EINVAL, "rosa_credits: T too large for LDS");
-  dim3 grid((unsigned)(B * S), (unsigned)cdiv(T, 64));
-  hipLaunchKernelGGL(rosa_credits_kernel, grid, dim3(64), lds, (hipStream_t)stream, q_bits, k_bits,
-                     v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits);
+  const size_t lds = (3 * (size_t)W + kCredWaves * (size_t)kCredWave32) * sizeof(uint32_t);
+  if (lds > 64 * 1024) return fail(KSD_EINVAL, "rosa_credits: T too large for LDS");
+  if (B * S > 0x7fffffff) return fail(KSD_EINVAL, "rosa_credits: too many streams");
+  hipLaunchKernelGGL(rosa_credits_kernel, dim3((unsigned)(B * S)), dim3(256), lds, (hipStream_t)stream,
+                     q_bits, k_bits, v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits,
+                     payload_partial);
   return check_launch("rosa_credits");
 }
 
 extern "C" int ksd_rosa_credit_grads(const float *credits, const void *q, const void *k, const void *v,
-                                     int dtype, const float *grad, const int8_t *sign, int64_t B,
-                                     int64_t T, int64_t S, void *gq, void *gk, void *gv, float *gpayload,
+                                     int dtype, const float *payload_partial, int64_t B, int64_t T,
+                                     int64_t S, void *gq, void *gk, void *gv, float *gpayload,
                                      void *stream) {
   if (B < 0 || T < 0 || S < 0) return fail(KSD_EINVAL, "rosa_credit_grads: negative shape");
   if (dtype != KSD_F32 && dtype != KSD_BF16 && dtype != KSD_F16)
     return fail(KSD_ETYPE, "rosa_credit_grads: q/k/v must be float32, bfloat16 or float16");
   if (B == 0 || T == 0 || S == 0) return KSD_OK;
-  if (!credits || !q || !k || !v || !grad || !sign || !gq || !gk || !gv || !gpayload)
+  if (!credits || !q || !k || !v || !payload_partial || !gq || !gk || !gv || !gpayload)
     return fail(KSD_EINVAL, "rosa_credit_grads: null pointer");
   const int64_t n = B * T * S;
   hipStream_t st = (hipStream_t)stream;
@@ -605,7 +630,7 @@ extern "C" int ksd_rosa_credit_grads(const float *credits, const void *q, const 
     case KSD_BF16: hipLaunchKernelGGL(rosa_credit_grad_kernel<KSD_BF16>, grid, dim3(256), 0, st, credits, q, k, v, B, T, S, gq, gk, gv); break;
     default: hipLaunchKernelGGL(rosa_credit_grad_kernel<KSD_F16>, grid, dim3(256), 0, st, credits, q, k, v, B, T, S, gq, gk, gv); break;
   }
-  hipLaunchKernelGGL(rosa_payload_grad_kernel, dim3((unsigned)cdiv(S, 256)), dim3(256), 0, st, grad, sign,
-                     B, T, S, gpayload);
+  hipLaunchKernelGGL(rosa_payload_grad_kernel, dim3((unsigned)cdiv(S, 256)), dim3(256), 0, st,
+                     payload_partial, B, S, gpayload);
   return check_launch("rosa_credit_grads");
 }

@@ -43,14 +43,16 @@ class HardRosaGPU(torch.autograd.Function):
         p32 = payload.detach().float().contiguous()
         lmax = R.resolve_max_match_len(T)
         cred = torch.zeros((B * S, 3, T), dtype=torch.float32, device=dev)
+        part = torch.empty((B * S,), dtype=torch.float32, device=dev)
         st = _lib.stream_ptr(dev)
         _lib.call("ksd_rosa_credits", qb.data_ptr(), kb.data_ptr(), vb.data_ptr(), mj.data_ptr(),
-                  grad.data_ptr(), p32.data_ptr(), B, T, S, lmax, cred.data_ptr(), st)
+                  grad.data_ptr(), p32.data_ptr(), B, T, S, lmax, cred.data_ptr(),
+                  part.data_ptr(), st)
         dt = q.dtype if q.dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
         qc, kc, vc = (t.detach().to(dt).contiguous() for t in (q, k, v))
         gq, gk, gv = (torch.empty((B, T, S), dtype=dt, device=dev) for _ in range(3))
         gp = torch.empty((S,), dtype=torch.float32, device=dev)
         _lib.call("ksd_rosa_credit_grads", cred.data_ptr(), qc.data_ptr(), kc.data_ptr(),
-                  vc.data_ptr(), _lib.dtype_code(dt), grad.data_ptr(), sign.data_ptr(), B, T, S,
+                  vc.data_ptr(), _lib.dtype_code(dt), part.data_ptr(), B, T, S,
                   gq.data_ptr(), gk.data_ptr(), gv.data_ptr(), gp.data_ptr(), st)
         return gq.to(q.dtype), gk.to(k.dtype), gv.to(v.dtype), gp.to(payload.dtype)
