@@ -55,15 +55,17 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(
   const float s = group_scale(amax);
 
   int8_t q[8];
+  if (noise != nullptr) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float c = v[i] / s;
-    if (noise != nullptr && active) {
+    for (int i = 0; i < 8; ++i) {
       // stages.py:44-47: codes + (rand - 0.5) * (2*dither), fp32 ops, separately rounded
-      const float r = noise[row * ngroups * G + k0 + i];
-      c = c + (r - 0.5f) * dither2;
+      float c = v[i] / s;
+      if (active) c = c + (noise[row * ngroups * G + k0 + i] - 0.5f) * dither2;
+      q[i] = code_of(c);
     }
-    q[i] = code_of(c);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = code_of(v[i] / s);
   }
   if (!active) return;
   int8_t *cr = codes + row * K;
@@ -91,65 +93,111 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(
 }
 
 // ----------------------------------------------------------------------------------
-// Transposed quantization: codes (C, R) = quantize along R of x (R, C). A block owns one
-// G-row group by 64 columns; the tile goes through LDS so both the loads (along C) and
-// the code stores (along R) are contiguous.
-struct LoadF32 {
-  const float *x; int64_t C;
-  __device__ float operator()(int64_t r, int64_t c) const { return x[r * C + c]; }
-};
-struct LoadBF16 {
-  const uint16_t *x; int64_t C;
-  __device__ float operator()(int64_t r, int64_t c) const { return bf16_to_f32(x[r * C + c]); }
-};
-struct LoadF16 {
-  const uint16_t *x; int64_t C;
-  __device__ float operator()(int64_t r, int64_t c) const { return f16_to_f32(x[r * C + c]); }
-};
-// dequantized codes: float(code) * float(scale) (the exact product of quant.py:66)
-struct LoadDequant {
-  const int8_t *q; const uint16_t *s; int64_t C; int64_t nsc; int gin;
-  __device__ float operator()(int64_t r, int64_t c) const {
-    return (float)q[r * C + c] * f16_to_f32(s[r * nsc + c / gin]);
-  }
-};
+// Transposed quantization: codes (C, R) = quantize along R of x (R, C); with an int8 source
+// the values are dequantized first (requant: float(code) * float(scale), exact).
+//
+// A 256-thread block owns one G-row group by 64 columns. Loads are 16 bytes per lane along
+// C (a wave covers whole 64-column row segments); the tile goes to LDS transposed (column
+// pitch G + 1 floats: the transposing writes hit distinct banks); then 4 lanes per column
+// reduce the group amax with two shuffles and each stores G/4 contiguous codes, so an
+// output row receives G contiguous bytes from 4 adjacent lanes.
+enum { SRC_F32 = 0, SRC_BF16 = 1, SRC_F16 = 2, SRC_I8 = 3 };
 
-template <class Loader, int G>
-__global__ __launch_bounds__(256) void quant_T_kernel(Loader ld, int64_t R, int64_t C,
-                                                      int64_t nbc, int64_t ngr,
-                                                      int8_t *__restrict__ codes,
-                                                      uint16_t *__restrict__ scales) {
-  __shared__ float tile[G][65];
-  __shared__ float cmax[4][64];
+template <int SRC, int G>
+__global__ __launch_bounds__(256) void quant_T_kernel(
+    const void *__restrict__ xv, const uint16_t *__restrict__ in_scales, int64_t nsc_in,
+    int gin, int64_t R, int64_t C, int64_t nbc, int64_t ngr, int8_t *__restrict__ codes,
+    uint16_t *__restrict__ scales, bool rows_vec) {
+  constexpr int PITCH = G + 1;
+  __shared__ float tile[64 * PITCH];
+  const int tid = threadIdx.x;
   const int64_t bc = blockIdx.x % nbc, br = blockIdx.x / nbc;
   const int64_t r0 = br * G, c0 = bc * 64;
-  const int c = threadIdx.x & 63, rq = threadIdx.x >> 6;
-  const bool cok = c0 + c < C;
 
-  float m = 0.0f;
-#pragma unroll 4
-  for (int i = 0; i < G / 4; ++i) {
-    const int r = rq + 4 * i;
-    const float v = (cok && r0 + r < R) ? ld(r0 + r, c0 + c) : 0.0f;
-    tile[r][c] = v;
-    m = amax2(m, fabsf(v));
+  // ---- load: EPV elements per 16-byte vector, LPR lanes per 64-column row segment
+  constexpr int EPV = SRC == SRC_F32 ? 4 : SRC == SRC_I8 ? 16 : 8;
+  constexpr int LPR = 64 / EPV, RPP = 256 / LPR;  // rows per pass
+  const int tx = tid % LPR, ty = tid / LPR;
+  const int64_t cb = c0 + tx * EPV;  // first column of this lane's vector
+  constexpr int NP = G >= RPP ? G / RPP : 1;  // passes (with RPP > G, rows ty >= G idle)
+  const bool ty_ok = ty < G;
+  float v[NP][EPV];
+  if (rows_vec && r0 + G <= R && c0 + 64 <= C && ty_ok) {
+    // interior tile: every load a 16-byte vector, all issued before any LDS write
+#pragma unroll
+    for (int pass = 0; pass < NP; ++pass) {
+      const int64_t gr = r0 + ty + pass * RPP;
+      if constexpr (SRC == SRC_F32) {
+        const float4 a = *(const float4 *)((const float *)xv + gr * C + cb);
+        v[pass][0] = a.x; v[pass][1] = a.y; v[pass][2] = a.z; v[pass][3] = a.w;
+      } else if constexpr (SRC == SRC_I8) {
+        const int4 a = *(const int4 *)((const int8_t *)xv + gr * C + cb);
+        const float sc = f16_to_f32(in_scales[gr * nsc_in + cb / gin]);
+        const int w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[pass][i] = (float)(int8_t)(w[i >> 2] >> ((i & 3) * 8)) * sc;
+      } else {
+        const uint4 a = *(const uint4 *)((const uint16_t *)xv + gr * C + cb);
+        const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint16_t h = (uint16_t)(w[i >> 1] >> ((i & 1) * 16));
+          v[pass][i] = SRC == SRC_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+        }
+      }
+    }
+  } else {
+    // ragged or unaligned tile: element loads, zeros outside the tensor
+#pragma unroll
+    for (int pass = 0; pass < NP; ++pass) {
+      const int64_t gr = r0 + ty + pass * RPP;
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) {
+        const int64_t gc = cb + i;
+        float x = 0.0f;
+        if (ty_ok && gr < R && gc < C) {
+          if constexpr (SRC == SRC_F32) x = ((const float *)xv)[gr * C + gc];
+          else if constexpr (SRC == SRC_BF16) x = bf16_to_f32(((const uint16_t *)xv)[gr * C + gc]);
+          else if constexpr (SRC == SRC_F16) x = f16_to_f32(((const uint16_t *)xv)[gr * C + gc]);
+          else x = (float)((const int8_t *)xv)[gr * C + gc] * f16_to_f32(in_scales[gr * nsc_in + gc / gin]);
+        }
+        v[pass][i] = x;
+      }
+    }
   }
-  cmax[rq][c] = m;
+  if (ty_ok) {
+#pragma unroll
+    for (int pass = 0; pass < NP; ++pass)
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) tile[(tx * EPV + i) * PITCH + ty + pass * RPP] = v[pass][i];
+  }
   __syncthreads();
-  const float amax = amax2(amax2(cmax[0][c], cmax[1][c]), amax2(cmax[2][c], cmax[3][c]));
-  const float s = group_scale(amax);
-  if (!cok) return;
-  if (rq == 0) scales[(c0 + c) * ngr + br] = scale_bits(s);
 
-  constexpr int RPT = G / 4;  // rows (output bytes) per thread
+  // ---- column c = tid / 4, rows [part * G/4, +G/4)
+  constexpr int RPT = G / 4;
+  const int c = tid >> 2, part = tid & 3;
+  const float *col = tile + c * PITCH + part * RPT;
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) m = amax2(m, fabsf(col[j]));
+  m = amax2(m, __shfl_xor(m, 1));
+  m = amax2(m, __shfl_xor(m, 2));
+  const float s = group_scale(m);
+  const int64_t gc = c0 + c;
+  if (gc >= C) return;
+  if (part == 0) scales[gc * ngr + br] = scale_bits(s);
   int8_t q[RPT];
 #pragma unroll
-  for (int j = 0; j < RPT; ++j) q[j] = code_of(tile[rq * RPT + j][c] / s);
-  int8_t *dst = codes + (c0 + c) * R + r0 + rq * RPT;
-  const int64_t rbase = r0 + rq * RPT;
-  if (rbase + RPT <= R && (((uintptr_t)dst) & 7) == 0) {
+  for (int j = 0; j < RPT; ++j) q[j] = code_of(col[j] / s);
+  int8_t *dst = codes + gc * R + r0 + part * RPT;
+  const int64_t rbase = r0 + part * RPT;
+  if (rbase + RPT <= R && (((uintptr_t)dst) % (RPT < 16 ? RPT : 16)) == 0) {
+    if constexpr (RPT == 8) {
+      *(uint2 *)dst = *(const uint2 *)q;
+    } else {
 #pragma unroll
-    for (int j = 0; j < RPT; j += 8) *(uint2 *)(dst + j) = *(const uint2 *)(q + j);
+      for (int j = 0; j < RPT; j += 16) *(uint4 *)(dst + j) = *(const uint4 *)(q + j);
+    }
   } else {
 #pragma unroll
     for (int j = 0; j < RPT; ++j)
@@ -157,16 +205,21 @@ __global__ __launch_bounds__(256) void quant_T_kernel(Loader ld, int64_t R, int6
   }
 }
 
-template <class Loader>
-static int launch_quant_T(Loader ld, int64_t R, int64_t C, int group, int8_t *codes,
-                          uint16_t *scales, hipStream_t st) {
+template <int SRC>
+static int launch_quant_T(const void *x, const uint16_t *in_scales, int64_t nsc_in, int gin,
+                          int64_t R, int64_t C, int group, int8_t *codes, uint16_t *scales,
+                          hipStream_t st) {
   const int64_t nbc = cdiv(C, 64), ngr = cdiv(R, group);
   const int64_t blocks = nbc * ngr;
   if (blocks > 0x7fffffffLL) return fail(KSD_EINVAL, "quantize_transpose: tensor too large");
+  const dim3 g((unsigned)blocks), b(256);
+  // 16-byte vector loads need an aligned base and a row pitch that is a multiple of 16 B
+  const int esz = SRC == SRC_F32 ? 4 : SRC == SRC_I8 ? 1 : 2;
+  const bool rv = ((uintptr_t)x) % 16 == 0 && (C * esz) % 16 == 0;
   switch (group) {
-    case 32: quant_T_kernel<Loader, 32><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(ld, R, C, nbc, ngr, codes, scales); break;
-    case 64: quant_T_kernel<Loader, 64><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(ld, R, C, nbc, ngr, codes, scales); break;
-    default: quant_T_kernel<Loader, 128><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(ld, R, C, nbc, ngr, codes, scales); break;
+    case 32: quant_T_kernel<SRC, 32><<<g, b, 0, st>>>(x, in_scales, nsc_in, gin, R, C, nbc, ngr, codes, scales, rv); break;
+    case 64: quant_T_kernel<SRC, 64><<<g, b, 0, st>>>(x, in_scales, nsc_in, gin, R, C, nbc, ngr, codes, scales, rv); break;
+    default: quant_T_kernel<SRC, 128><<<g, b, 0, st>>>(x, in_scales, nsc_in, gin, R, C, nbc, ngr, codes, scales, rv); break;
   }
   return check_launch("quantize_transpose");
 }
@@ -238,9 +291,9 @@ extern "C" int ksd_quantize_transpose(const void *x, int x_dtype, int64_t R, int
   if (R == 0 || C == 0) return KSD_OK;
   hipStream_t st = (hipStream_t)stream;
   switch (x_dtype) {
-    case KSD_F32: return launch_quant_T(LoadF32{(const float *)x, C}, R, C, group, codes, scales, st);
-    case KSD_BF16: return launch_quant_T(LoadBF16{(const uint16_t *)x, C}, R, C, group, codes, scales, st);
-    case KSD_F16: return launch_quant_T(LoadF16{(const uint16_t *)x, C}, R, C, group, codes, scales, st);
+    case KSD_F32: return launch_quant_T<SRC_F32>(x, nullptr, 0, 1, R, C, group, codes, scales, st);
+    case KSD_BF16: return launch_quant_T<SRC_BF16>(x, nullptr, 0, 1, R, C, group, codes, scales, st);
+    case KSD_F16: return launch_quant_T<SRC_F16>(x, nullptr, 0, 1, R, C, group, codes, scales, st);
     default: return fail(KSD_ETYPE, "quantize expects float32, bfloat16 or float16 input");
   }
 }
@@ -251,8 +304,8 @@ extern "C" int ksd_requant_transpose(const int8_t *codes, const uint16_t *scales
   if (!valid_group(group) || !valid_group(group_in))
     return fail(KSD_EINVAL, "group must be 32, 64 or 128");
   if (R == 0 || C == 0) return KSD_OK;
-  LoadDequant ld{codes, scales, C, cdiv(C, group_in), group_in};
-  return launch_quant_T(ld, R, C, group, out_codes, out_scales, (hipStream_t)stream);
+  return launch_quant_T<SRC_I8>(codes, scales, cdiv(C, group_in), group_in, R, C, group, out_codes,
+                                out_scales, (hipStream_t)stream);
 }
 
 extern "C" int ksd_abi_version(void) { return 2; }

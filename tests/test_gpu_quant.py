@@ -104,3 +104,35 @@ def test_requant_transpose_matches_oracle(R, C, group_in, group):
     eq, es = oq.requant_transpose(wq, ws, group_in, group)
     assert np.array_equal(tq.cpu().numpy(), eq)
     assert np.array_equal(ts.cpu().numpy(), es)
+
+
+@pytest.mark.parametrize("group", [32, 128])
+def test_quantize_transpose_adversarial_rounding(group):
+    """Half-integer quotients and their fp32 neighbours, grouped along R (transposed)."""
+    x = _adversarial_rows(np.random.default_rng(7 + group), group).T.copy()  # (2*group, rows)
+    codes, scales = kq.quantize_transpose(torch.from_numpy(x).to(DEV), group)
+    ec, es = oq.quantize_transpose(x, group)
+    assert np.array_equal(codes.cpu().numpy(), ec)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint16), es.view(np.uint16))
+
+
+@pytest.mark.parametrize("group", [32, 128])
+def test_requant_transpose_rounding_ties(group):
+    """Rows whose input scale is half the group's output scale give half-integer quotients
+    (odd codes), the exact ties of the requantization; neighbouring scales give near-ties."""
+    rng = np.random.default_rng(31 + group)
+    R, C = 2 * group, 64
+    S = np.float16(0.0078125)
+    codes = rng.integers(-127, 128, (R, C)).astype(np.int8)
+    codes[::group, :] = 127  # each column group's amax row: 127 * S, so the new scale is S
+    scales = np.empty((R, 1), np.float16)
+    scales[:, 0] = np.float16(S / np.float16(2))
+    scales[::group, 0] = S
+    scales[1::4, 0] = np.nextafter(np.float16(S / np.float16(2)), np.float16(1))
+    scales[2::4, 0] = np.nextafter(np.float16(S / np.float16(2)), np.float16(0))
+    scales[::group, 0] = S
+    tq, ts = kq.requant_transpose(torch.from_numpy(codes).to(DEV), torch.from_numpy(scales).to(DEV),
+                                  C, group)
+    eq, es = oq.requant_transpose(codes, scales, C, group)
+    assert np.array_equal(tq.cpu().numpy(), eq)
+    assert np.array_equal(ts.cpu().numpy().view(np.uint16), es.view(np.uint16))
