@@ -397,15 +397,6 @@ __device__ __forceinline__ h2 hmax2(h2 a, h2 b) {
                                                           __builtin_bit_cast(u16x2, b)));
 }
 
-// Raw buffer resources: a lane whose offset lies at or past num_records reads zeros and
-// its stores are dropped, which masks ragged rows and columns without branches.
-constexpr int kBufFlags = 0x00020000;
-constexpr uint32_t kOob = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0,
-                                           (int)min(bytes, (int64_t)0x7fffffff), kBufFlags);
-}
 // The rows [row0, row0 + n) of a row-major tensor, clipped at M: rows past M read zeros
 // and drop stores. row0 is wave-uniform, so the descriptor lives in SGPRs.
 template <typename T>

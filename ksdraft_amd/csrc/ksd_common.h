@@ -63,12 +63,52 @@ __device__ __forceinline__ float f16_to_f32(uint16_t b) {
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __builtin_bit_cast(float, (uint32_t)b << 16);
 }
-// fp32 -> bf16 round-to-nearest-even (NaN kept quiet), torch's conversion.
+// fp32 -> bf16 round-to-nearest-even (NaN kept quiet), torch's conversion; branch-free.
 __device__ __forceinline__ uint16_t f32_to_bf16(float v) {
-  uint32_t u = __builtin_bit_cast(uint32_t, v);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (uint16_t)(v != v ? (u >> 16) | 0x40u : r);
+}
+// fp32 -> bf16 -> fp32 (round-to-nearest-even; a NaN stays a NaN).
+__device__ __forceinline__ float bf16_round(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const float r = __builtin_bit_cast(float, (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
+  return v != v ? v : r;
+}
+
+// Two fp32 values through bf16 and back with one v_cvt_pk_bf16_f32 (round-to-nearest-even,
+// denormals kept under the kernels' fp32 denormal mode; a NaN stays a NaN).
+__device__ __forceinline__ void bf16_round2(float &a, float &b) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const f32x2 r = __builtin_convertvector(__builtin_convertvector((f32x2){a, b}, bf16x2), f32x2);
+  a = r.x;
+  b = r.y;
+}
+
+// NaN-propagating max of |v[0..n)| as fp32 (v_maximum3_f32 with abs modifiers); the result
+// has its sign bit clear, so its u32 pattern orders like the magnitude, NaN above inf.
+template <int N>
+__device__ __forceinline__ float abs_max(const float *v) {
+  float m = fabsf(v[0]);
+#pragma unroll
+  for (int i = 1; i + 1 < N; i += 2)
+    m = __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(fabsf(v[i]), fabsf(v[i + 1])));
+  if constexpr (N % 2 == 0) m = __builtin_elementwise_maximum(m, fabsf(v[N - 1]));
+  return fabsf(m);
+}
+
+// Max of the u32 patterns over aligned groups of L lanes (L = 1, 2, 4, 8 or 16), every
+// lane of a group getting the result: DPP quad permutes for the pairs and quads, then
+// the half-row and row mirrors, which pair each quad (each half-row) with the other one.
+template <int L>
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
+  static_assert(L == 1 || L == 2 || L == 4 || L == 8 || L == 16, "group of 1..16 lanes");
+  if constexpr (L >= 2) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  if constexpr (L >= 4) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  if constexpr (L >= 8) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+  if constexpr (L >= 16) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+  return v;
 }
 
 template <int DT> struct Elem;
@@ -111,6 +151,81 @@ __device__ __forceinline__ int8_t code_of(float v) {
   float r = rintf(v);
   r = fminf(fmaxf(r, -127.0f), 127.0f);
   return v != v ? (int8_t)0 : (int8_t)(int)r;
+}
+
+// code_of(x[j] / s) for NV values of one group, s being that group's scale from the
+// NaN-propagating amax over values that include these x (so s is NaN exactly when one of
+// them is, and then every code is 0, as x / NaN is). Otherwise s lies in [2^-24, 65504]
+// and a reciprocal multiply replaces the correctly rounded division: r = rcp(s) is within
+// 1 ulp of 1/s, so p = x * r is within 2^-22 relative of the real quotient, which is less
+// than 2^-15 absolute wherever |p| <= 128 (beyond that both sides clamp to +-127). rint(p)
+// therefore equals rint(x / s) unless p lies within 2^-15 of a half-integer (half-integers
+// below 2^22 are fp32 values, so the rounded division cannot cross one either). A lane
+// with any p within 2^-12 of a half-integer recomputes its NV codes with the division.
+template <int NV>
+__device__ __forceinline__ void codes_rcp(const float *x, float s, int8_t *q) {
+  if (s != s) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) q[j] = 0;
+    return;
+  }
+  const float r = __builtin_amdgcn_rcpf(s);
+  bool near_tie = false;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const float p = x[j] * r;
+    const float t = rintf(p);
+    near_tie |= fabsf(fabsf(p - t) - 0.5f) < 0x1p-12f;
+    q[j] = (int8_t)(int)fminf(fmaxf(t, -127.0f), 127.0f);   // t is integral or +-inf
+  }
+  if (near_tie) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) q[j] = code_of(x[j] / s);
+  }
+}
+
+// The codes of codes_rcp<NV> (NV a multiple of 4) packed four to a word, little-endian.
+// Rounding and clamping go through one add: for |c| <= 127, c + 1.5 * 2^23 rounds c to
+// the nearest integer (ties to even) and leaves it, two's complement, in the low byte of
+// the sum's bit pattern; v_perm_b32 then gathers four low bytes. Clamping before the
+// rounding equals clamping after it, +-127 being integers.
+template <int NV>
+__device__ __forceinline__ void codes_rcp_packed(const float *x, float s, uint32_t *w) {
+  static_assert(NV % 4 == 0, "whole words");
+  if (s != s) {
+#pragma unroll
+    for (int k = 0; k < NV / 4; ++k) w[k] = 0;
+    return;
+  }
+  constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
+  const float r = __builtin_amdgcn_rcpf(s);
+  float near = 1.0f;
+  uint32_t f[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const float c = __builtin_amdgcn_fmed3f(x[j] * r, -127.0f, 127.0f);
+    const float m = c + kMagic;
+    near = fminf(near, fabsf(fabsf(c - (m - kMagic)) - 0.5f));
+    f[j] = __builtin_bit_cast(uint32_t, m);
+  }
+  if (near < 0x1p-12f) {  // some quotient within 2^-12 of a half-integer: divide
+#pragma unroll
+    for (int j = 0; j < NV; ++j) f[j] = (uint8_t)code_of(x[j] / s);
+  }
+#pragma unroll
+  for (int k = 0; k < NV / 4; ++k)
+    w[k] = __builtin_amdgcn_perm(f[4 * k + 1], f[4 * k], 0x0c0c0400u) |
+           __builtin_amdgcn_perm(f[4 * k + 3], f[4 * k + 2], 0x04000c0cu);
+}
+
+// Raw buffer resources: a lane whose offset lies at or past num_records reads zeros and
+// its stores are dropped, which masks ragged rows and columns without branches.
+constexpr int kBufFlags = 0x00020000;
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0,
+                                           (int)min(bytes, (int64_t)0x7fffffff), kBufFlags);
 }
 
 // Store one fp32 value as the output element type.

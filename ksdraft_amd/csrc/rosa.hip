@@ -27,57 +27,161 @@ namespace ksd {
 template <int DT>
 __device__ __forceinline__ float round_to_dt(float v);
 template <> __device__ __forceinline__ float round_to_dt<KSD_F32>(float v) { return v; }
-template <> __device__ __forceinline__ float round_to_dt<KSD_BF16>(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+template <> __device__ __forceinline__ float round_to_dt<KSD_BF16>(float v) { return bf16_round(v); }
 template <> __device__ __forceinline__ float round_to_dt<KSD_F16>(float v) { return f16_round(v); }
 
-// One row (token) per G/8-lane group set; a lane owns 8 consecutive features.
-// q_in = prev + (x - prev) * sigmoid(mix): x - prev is an op in x's dtype (rounded to it),
-// the rest is fp32 (torch promotes the bf16/fp16 tensor against the fp32 sigmoid).
-template <int DT, int G>
-__global__ void __launch_bounds__(256) rosa_shift_quant_kernel(
-    const void *__restrict__ x, int64_t rows, int64_t T, int64_t d,
-    const float *__restrict__ sig_q, const float *__restrict__ sig_k, const float *__restrict__ sig_v,
-    int8_t *__restrict__ cq, uint16_t *__restrict__ sq, int8_t *__restrict__ ck,
-    uint16_t *__restrict__ sk, int8_t *__restrict__ cv, uint16_t *__restrict__ sv, int64_t ngroups) {
-  using E = Elem<DT>;
-  constexpr int LPG = G / 8;
-  const int64_t lanes_per_row = ngroups * LPG;
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t row = gid / lanes_per_row;
-  const int64_t k0 = (gid % lanes_per_row) * 8;
-  const bool active = row < rows;
-  const int64_t t = active ? row % T : 0;
-  const typename E::T *xr = (const typename E::T *)x + (active ? row : 0) * d;
-  float xv[8], pv[8];
+// Load 8 consecutive features of a row as fp32 (k0 + 8 <= d on the vector path).
+template <int DT, bool VEC>
+__device__ __forceinline__ void load8(const typename Elem<DT>::T *p, int k0, int d, bool ok, float *v) {
+  if (VEC && ok) {
+    if constexpr (DT == KSD_F32) {
+      const float4 a = *(const float4 *)(p + k0), b = *(const float4 *)(p + k0 + 4);
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+      const uint4 a = *(const uint4 *)(p + k0);
+      const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint16_t lo = (uint16_t)(w[i] & 0xffffu), hi = (uint16_t)(w[i] >> 16);
+        v[2 * i] = Elem<DT>::load(&lo);
+        v[2 * i + 1] = Elem<DT>::load(&hi);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = ok && k0 + i < d ? Elem<DT>::load(p + k0 + i) : 0.0f;
+  }
+}
+
+// 8 consecutive features as raw bits: two 16-byte vectors for fp32, one for 16-bit types.
+template <int DT> struct Raw8 { uint4 a, b; };
+template <int DT>
+__device__ __forceinline__ Raw8<DT> load_raw8(const typename Elem<DT>::T *p) {
+  Raw8<DT> r;
+  r.a = *(const uint4 *)p;
+  if constexpr (DT == KSD_F32) r.b = *(const uint4 *)(p + 4);
+  return r;
+}
+template <int DT>
+__device__ __forceinline__ void cvt_raw8(const Raw8<DT> &r, bool ok, float *v) {
+  const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const bool ok = active && k0 + i < d;
-    xv[i] = ok ? E::load(xr + k0 + i) : 0.0f;
-    pv[i] = ok && t > 0 ? E::load(xr - d + k0 + i) : 0.0f;
+    float f;
+    if constexpr (DT == KSD_F32) {
+      f = __builtin_bit_cast(float, w[i]);
+    } else {
+      const uint16_t h = (uint16_t)(i & 1 ? w[i / 2] >> 16 : w[i / 2] & 0xffffu);
+      f = Elem<DT>::load(&h);
+    }
+    v[i] = ok ? f : 0.0f;
   }
-  const float *sigs[3] = {sig_q, sig_k, sig_v};
+}
+
+// Block = 4 waves x 64 lanes; a wave walks RT consecutive rows (tokens) and a lane owns 8
+// consecutive features, so a group is G/8 adjacent lanes of one wave (grid.y walks the row
+// in 512-feature slices). Each row is read once: it is the next row's previous token, and
+// the row after it is loaded (unconditionally, from a clamped valid address) while the
+// current one is encoded. q_in = prev + (x - prev) * sigmoid(mix): x - prev is an op in
+// x's dtype (rounded to it), the rest is fp32 (torch promotes the bf16/fp16 tensor against
+// the fp32 sigmoid). VEC: d % 8 == 0 and every row, sigmoid and code row 16/8-byte aligned.
+template <int DT, int G, bool VEC, int RT>
+__global__ void __launch_bounds__(256) rosa_shift_quant_kernel(
+    const void *__restrict__ x, int rows, int T, int d,
+    const float *__restrict__ sig_q, const float *__restrict__ sig_k, const float *__restrict__ sig_v,
+    int8_t *__restrict__ cq, uint16_t *__restrict__ sq, int8_t *__restrict__ ck,
+    uint16_t *__restrict__ sk, int8_t *__restrict__ cv, uint16_t *__restrict__ sv, int ngroups) {
+  using E = Elem<DT>;
+  constexpr int LPG = G / 8;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = ((int)blockIdx.x * 4 + wave) * RT;
+  if (row0 >= rows) return;                                   // wave-uniform
+  const int k0 = ((int)blockIdx.y * 64 + (int)(threadIdx.x & 63)) * 8;
+  const bool kok = k0 < d;
+  const int kc = kok ? k0 : 0;                                // a valid column for every lane
+  float sg[3][8];
+  const typename E::T *xb = (const typename E::T *)x + kc;
+  if constexpr (VEC) {
+    cvt_raw8<KSD_F32>(load_raw8<KSD_F32>(sig_q + kc), kok, sg[0]);
+    cvt_raw8<KSD_F32>(load_raw8<KSD_F32>(sig_k + kc), kok, sg[1]);
+    cvt_raw8<KSD_F32>(load_raw8<KSD_F32>(sig_v + kc), kok, sg[2]);
+  } else {
+    load8<KSD_F32, false>(sig_q, k0, d, kok, sg[0]);
+    load8<KSD_F32, false>(sig_k, k0, d, kok, sg[1]);
+    load8<KSD_F32, false>(sig_v, k0, d, kok, sg[2]);
+  }
   int8_t *codes[3] = {cq, ck, cv};
   uint16_t *scales[3] = {sq, sk, sv};
+  int t = row0 % T;
+  float xv[8], pv[8];
+  Raw8<DT> rn;
+  if constexpr (VEC) {
+    Raw8<DT> rp = load_raw8<DT>(xb + (int64_t)(row0 > 0 ? row0 - 1 : 0) * d);
+    rn = load_raw8<DT>(xb + (int64_t)row0 * d);
+    cvt_raw8<DT>(rp, kok && t > 0, pv);
+  } else {
+    const typename E::T *xr = (const typename E::T *)x + (int64_t)row0 * d;
+    load8<DT, false>(xr - d, k0, d, kok && t > 0, pv);
+  }
 #pragma unroll
-  for (int m = 0; m < 3; ++m) {
-    float v[8];
-    float amax = 0.0f;
+  for (int i = 0; i < RT; ++i) {
+    const int row = row0 + i;
+    if (row >= rows) break;                                   // wave-uniform
+    if constexpr (VEC) {
+      cvt_raw8<DT>(rn, kok, xv);
+      if (i + 1 < RT) rn = load_raw8<DT>(xb + (int64_t)min(row + 1, rows - 1) * d);
+    } else {
+      load8<DT, false>((const typename E::T *)x + (int64_t)row * d, k0, d, kok, xv);
+    }
+    if (t == 0) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float sg = active && k0 + i < d ? sigs[m][k0 + i] : 0.0f;
-      const float diff = round_to_dt<DT>(xv[i] - pv[i]);
-      v[i] = pv[i] + diff * sg;
-      amax = amax2(amax, fabsf(v[i]));
+      for (int e = 0; e < 8; ++e) pv[e] = 0.0f;
+    }
+    float diff[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) diff[e] = xv[e] - pv[e];
+    if constexpr (DT == KSD_BF16) {
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) bf16_round2(diff[e], diff[e + 1]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) diff[e] = round_to_dt<DT>(diff[e]);
     }
 #pragma unroll
-    for (int off = LPG / 2; off > 0; off >>= 1) amax = amax2(amax, __shfl_xor(amax, off));
-    const float s = group_scale(amax);
-    if (!active) continue;
-    int8_t *cr = codes[m] + row * d;
+    for (int m = 0; m < 3; ++m) {
+      float v[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (k0 + i < d) cr[k0 + i] = code_of(v[i] / s);
-    if ((gid % LPG) == 0) scales[m][row * ngroups + k0 / G] = scale_bits(s);
+      for (int e = 0; e < 8; ++e) v[e] = pv[e] + diff[e] * sg[m][e];
+      const uint32_t am = __builtin_bit_cast(uint32_t, abs_max<8>(v));
+      const float s = group_scale(__builtin_bit_cast(float, group_max_u32<LPG>(am)));
+      if constexpr (VEC) {
+        // stores without branches: a lane past d (or not leading its group, for the
+        // scale) gets an offset past num_records, and the buffer unit drops its store
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        u32x2 q;
+        uint32_t qw[2];
+        codes_rcp_packed<8>(v, s, qw);
+        q.x = qw[0];
+        q.y = qw[1];
+        const auto rc = rsrc(codes[m] + (int64_t)row * d, d);
+        __builtin_amdgcn_raw_buffer_store_b64(q, rc, kok ? (uint32_t)k0 : kOob, 0, 0);
+        const auto rs = rsrc(scales[m] + (int64_t)row * ngroups, 2 * (int64_t)ngroups);
+        const bool lead = kok && (k0 / 8) % LPG == 0;
+        __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rs, lead ? (uint32_t)(k0 / G) * 2 : kOob, 0, 0);
+      } else if (kok) {
+        int8_t q[8];
+        codes_rcp<8>(v, s, q);
+        int8_t *cr = codes[m] + (int64_t)row * d;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (k0 + e < d) cr[k0 + e] = q[e];
+        if ((k0 / 8) % LPG == 0) scales[m][(int64_t)row * ngroups + k0 / G] = scale_bits(s);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pv[e] = xv[e];
+    t = t + 1 == T ? 0 : t + 1;
   }
 }
 
@@ -242,22 +346,30 @@ extern "C" int ksd_rosa_shift_quant(const void *x, int x_dtype, int64_t B, int64
       !v_codes || !v_scales)
     return fail(KSD_EINVAL, "rosa_shift_quant: null pointer");
   const int64_t ng = cdiv(d, group);
-  const int64_t threads = rows * ng * (group / 8);
-  const int64_t blocks = cdiv(threads, 256);
-  if (blocks > 0x7fffffff) return fail(KSD_EINVAL, "rosa_shift_quant: too large");
+  if (rows > 0x7fffffff - 64 || d > (1 << 28) || T > 0x7fffffff)
+    return fail(KSD_EINVAL, "rosa_shift_quant: too large");
+  const size_t esz = x_dtype == KSD_F32 ? 4 : 2;
+  auto al = [](const void *p, size_t a) { return ((uintptr_t)p % a) == 0; };
+  const bool vec = d % 8 == 0 && al(x, 16) && (d * esz) % 16 == 0 && al(sig_q, 16) && al(sig_k, 16) &&
+                   al(sig_v, 16) && al(q_codes, 8) && al(k_codes, 8) && al(v_codes, 8);
+  constexpr int RT = 4;
+  const dim3 grid((unsigned)cdiv(rows, 4 * RT), (unsigned)cdiv(d, 512));
   hipStream_t st = (hipStream_t)stream;
-#define KSD_SQ(DT, G)                                                                            \
-  hipLaunchKernelGGL((rosa_shift_quant_kernel<DT, G>), dim3((unsigned)blocks), dim3(256), 0, st, x, \
-                     rows, T, d, sig_q, sig_k, sig_v, q_codes, q_scales, k_codes, k_scales, v_codes, \
-                     v_scales, ng)
+#define KSD_SQ(DT, G, V)                                                                         \
+  hipLaunchKernelGGL((rosa_shift_quant_kernel<DT, G, V, RT>), grid, dim3(256), 0, st, x, (int)rows,   \
+                     (int)T, (int)d, sig_q, sig_k, sig_v, q_codes, q_scales, k_codes, k_scales,   \
+                     v_codes, v_scales, (int)ng)
+#define KSD_SQ_V(DT, G) \
+  if (vec) KSD_SQ(DT, G, true); else KSD_SQ(DT, G, false)
 #define KSD_SQ_G(DT) \
-  switch (group) { case 32: KSD_SQ(DT, 32); break; case 64: KSD_SQ(DT, 64); break; default: KSD_SQ(DT, 128); }
+  switch (group) { case 32: KSD_SQ_V(DT, 32); break; case 64: KSD_SQ_V(DT, 64); break; default: KSD_SQ_V(DT, 128); }
   switch (x_dtype) {
     case KSD_F32: KSD_SQ_G(KSD_F32); break;
     case KSD_BF16: KSD_SQ_G(KSD_BF16); break;
     default: KSD_SQ_G(KSD_F16); break;
   }
 #undef KSD_SQ_G
+#undef KSD_SQ_V
 #undef KSD_SQ
   return check_launch("rosa_shift_quant");
 }

@@ -97,21 +97,39 @@ def test_match_payload_sign_api_kats():
 
 
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
-def test_shift_quantize(dtype):
-    rng = np.random.default_rng(9)
-    B, T, d = 2, 33, 320
+@pytest.mark.parametrize("B,T,d,group", [(2, 33, 320, 128), (1, 17, 301, 128), (3, 5, 1536, 64),
+                                         (2, 9, 72, 32), (1, 1, 8, 128)])
+def test_shift_quantize(dtype, B, T, d, group):
+    rng = np.random.default_rng(9 + d)
     x = rng.standard_normal((B, T, d)).astype(np.float32) * 2
     tdt = getattr(torch, dtype)
     xt = _g(x).to(tdt)
     mixes = [_g(rng.standard_normal(d).astype(np.float32)) for _ in range(3)]
     sigs = [torch.sigmoid(m) for m in mixes]
-    out = R.shift_quantize(xt, *sigs, group=128)
+    out = R.shift_quantize(xt, *sigs, group=group)
     xv = xt.float().cpu().numpy()
     for (codes, scales), sg in zip(out, sigs):
         lerp = orr.shifted(xv, sg.cpu().numpy(), dtype).reshape(B * T, d)
-        ec, es = oq.quantize_last_dim(lerp)
+        ec, es = oq.quantize_last_dim(lerp, group)
         assert np.array_equal(codes.cpu().numpy(), ec)
         assert np.array_equal(scales.cpu().numpy(), es)
+
+
+@pytest.mark.parametrize("group", [32, 128])
+def test_shift_quantize_adversarial_rounding(group):
+    """Quotients on and next to half-integers (the codes' rounding ties) through the fused
+    shift: with T = 1 the previous token is zero, so q_in = x * sigmoid, and sigmoid values
+    1 and 0.5 keep every quotient of the quantize-time rows exactly where it was."""
+    from tests.test_oracle_quant import _adversarial_rows
+    x = _adversarial_rows(np.random.default_rng(7 + group), group)
+    n, d = x.shape
+    sigs = [torch.full((d,), v, dtype=torch.float32, device=DEV) for v in (1.0, 0.5, 1.0)]
+    out = R.shift_quantize(_g(x.reshape(n, 1, d)), *sigs, group=group)
+    for (codes, scales), sg in zip(out, sigs):
+        lerp = orr.shifted(x.reshape(n, 1, d), sg.cpu().numpy(), "float32").reshape(n, d)
+        ec, es = oq.quantize_last_dim(lerp, group)
+        assert np.array_equal(codes.cpu().numpy(), ec)
+        assert np.array_equal(scales.cpu().numpy().view(np.uint16), es.view(np.uint16))
 
 
 def _hard_case(seed, B, T, S):
