@@ -157,11 +157,12 @@ __device__ __forceinline__ int8_t code_of(float v) {
 // NaN-propagating amax over values that include these x (so s is NaN exactly when one of
 // them is, and then every code is 0, as x / NaN is). Otherwise s lies in [2^-24, 65504]
 // and a reciprocal multiply replaces the correctly rounded division: r = rcp(s) is within
-// 1 ulp of 1/s, so p = x * r is within 2^-22 relative of the real quotient, which is less
-// than 2^-15 absolute wherever |p| <= 128 (beyond that both sides clamp to +-127). rint(p)
-// therefore equals rint(x / s) unless p lies within 2^-15 of a half-integer (half-integers
-// below 2^22 are fp32 values, so the rounded division cannot cross one either). A lane
-// with any p within 2^-12 of a half-integer recomputes its NV codes with the division.
+// 1 ulp of 1/s, so p = x * r is within 1.5 * 2^-23 relative of the real quotient, which is
+// below 1.5 * 2^-16 absolute wherever |p| <= 128 (beyond that both sides clamp to +-127).
+// rint(p) therefore equals rint(x / s) unless p lies within 2^-15 of a half-integer
+// (half-integers below 2^22 are fp32 values, so the rounded division cannot cross one
+// either). A lane with any p within 2^-14 of a half-integer recomputes its NV codes with
+// the division.
 template <int NV>
 __device__ __forceinline__ void codes_rcp(const float *x, float s, int8_t *q) {
   if (s != s) {
@@ -175,7 +176,7 @@ __device__ __forceinline__ void codes_rcp(const float *x, float s, int8_t *q) {
   for (int j = 0; j < NV; ++j) {
     const float p = x[j] * r;
     const float t = rintf(p);
-    near_tie |= fabsf(fabsf(p - t) - 0.5f) < 0x1p-12f;
+    near_tie |= fabsf(fabsf(p - t) - 0.5f) < 0x1p-14f;
     q[j] = (int8_t)(int)fminf(fmaxf(t, -127.0f), 127.0f);   // t is integral or +-inf
   }
   if (near_tie) {
@@ -184,11 +185,20 @@ __device__ __forceinline__ void codes_rcp(const float *x, float s, int8_t *q) {
   }
 }
 
-// The codes of codes_rcp<NV> (NV a multiple of 4) packed four to a word, little-endian.
-// Rounding and clamping go through one add: for |c| <= 127, c + 1.5 * 2^23 rounds c to
-// the nearest integer (ties to even) and leaves it, two's complement, in the low byte of
-// the sum's bit pattern; v_perm_b32 then gathers four low bytes. Clamping before the
-// rounding equals clamping after it, +-127 being integers.
+// code_of(x[j] / s) for NV values of one group (NV a multiple of 4), packed four to a word,
+// little-endian. s is that group's scale from the NaN-propagating amax over values that
+// include these x: it is NaN exactly when one of them is, and then every code is 0 (as
+// x / NaN is). Otherwise s lies in [2^-24, 65504] and a reciprocal multiply replaces the
+// correctly rounded division. r = rcp(s) is within 1 ulp of 1/s, so p = x * r is within
+// 1.5 * 2^-23 relative of the real quotient: below 1.5 * 2^-16 absolute wherever |p| <= 128
+// (beyond that both sides clamp to +-127), and the rounded quotient is within 2^-18 of the
+// real one. rint(p) therefore equals rint(x / s) unless p lies within 2^-15 of a
+// half-integer; an 8-code chunk holding any p within 2^-14 of one is recomputed with the
+// division (the branch is rarely taken by a whole wave, so it stays cheap on average).
+// Rounding and clamping go through one add: for |c| <= 127, c + 1.5 * 2^23 rounds c to the
+// nearest integer (ties to even) and leaves it, two's complement, in the low byte of the
+// sum's bit pattern; v_perm_b32 then gathers four low bytes. Clamping before the rounding
+// equals clamping after it, +-127 being integers.
 template <int NV>
 __device__ __forceinline__ void codes_rcp_packed(const float *x, float s, uint32_t *w) {
   static_assert(NV % 4 == 0, "whole words");
@@ -198,19 +208,23 @@ __device__ __forceinline__ void codes_rcp_packed(const float *x, float s, uint32
     return;
   }
   constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
+  constexpr int CH = NV < 8 ? NV : 8;
   const float r = __builtin_amdgcn_rcpf(s);
-  float near = 1.0f;
   uint32_t f[NV];
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const float c = __builtin_amdgcn_fmed3f(x[j] * r, -127.0f, 127.0f);
-    const float m = c + kMagic;
-    near = fminf(near, fabsf(fabsf(c - (m - kMagic)) - 0.5f));
-    f[j] = __builtin_bit_cast(uint32_t, m);
-  }
-  if (near < 0x1p-12f) {  // some quotient within 2^-12 of a half-integer: divide
+  for (int c0 = 0; c0 < NV; c0 += CH) {
+    float near = 1.0f;
 #pragma unroll
-    for (int j = 0; j < NV; ++j) f[j] = (uint8_t)code_of(x[j] / s);
+    for (int j = c0; j < c0 + CH; ++j) {
+      const float c = __builtin_amdgcn_fmed3f(x[j] * r, -127.0f, 127.0f);
+      const float m = c + kMagic;
+      near = fminf(near, fabsf(fabsf(c - (m - kMagic)) - 0.5f));
+      f[j] = __builtin_bit_cast(uint32_t, m);
+    }
+    if (near < 0x1p-14f) {
+#pragma unroll
+      for (int j = c0; j < c0 + CH; ++j) f[j] = (uint8_t)code_of(x[j] / s);
+    }
   }
 #pragma unroll
   for (int k = 0; k < NV / 4; ++k)
@@ -226,6 +240,31 @@ constexpr uint32_t kOob = 0x80000000u;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0,
                                            (int)min(bytes, (int64_t)0x7fffffff), kBufFlags);
+}
+
+// 8 consecutive elements as raw bits: two 16-byte vectors for fp32, one for 16-bit types.
+template <int DT> struct Raw8 { uint4 a, b; };
+template <int DT>
+__device__ __forceinline__ Raw8<DT> load_raw8(const typename Elem<DT>::T *p) {
+  Raw8<DT> r;
+  r.a = *(const uint4 *)p;
+  if constexpr (DT == KSD_F32) r.b = *(const uint4 *)(p + 4);
+  return r;
+}
+template <int DT>
+__device__ __forceinline__ void cvt_raw8(const Raw8<DT> &r, bool ok, float *v) {
+  const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float f;
+    if constexpr (DT == KSD_F32) {
+      f = __builtin_bit_cast(float, w[i]);
+    } else {
+      const uint16_t h = (uint16_t)(i & 1 ? w[i / 2] >> 16 : w[i / 2] & 0xffffu);
+      f = Elem<DT>::load(&h);
+    }
+    v[i] = ok ? f : 0.0f;
+  }
 }
 
 // Store one fp32 value as the output element type.

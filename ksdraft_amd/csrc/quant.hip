@@ -79,6 +79,48 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(
   if (sub == 0) scales[row * ngroups + grp] = scale_bits(s);
 }
 
+// Row-wise quantization, aligned rows without dither: block = 4 waves; a wave walks RT
+// consecutive rows, a lane owns 8 consecutive elements (grid.y walks a row in 512-element
+// slices, so a group is G/8 adjacent lanes of one wave). The next row is loaded from a
+// clamped valid address while the current one is encoded; stores go through buffer
+// resources, lanes past K (or not leading their group, for the scale) getting an offset
+// past num_records, so no store sits in a branch and no wait covers the stores.
+// Requires K % 8 == 0, 16-byte aligned rows and 8-byte aligned code rows.
+template <int DT, int G, int RT>
+__global__ __launch_bounds__(256) void quant_rows_fast_kernel(
+    const void *__restrict__ xv, int64_t rows, int K, int64_t stride, int ngroups,
+    int8_t *__restrict__ codes, uint16_t *__restrict__ scales) {
+  using T = typename Elem<DT>::T;
+  constexpr int LPG = G / 8;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * RT;
+  if (row0 >= rows) return;                                   // wave-uniform
+  const int k0 = ((int)blockIdx.y * 64 + (int)(threadIdx.x & 63)) * 8;
+  const bool kok = k0 < K;
+  const T *xb = (const T *)xv + (kok ? k0 : 0);
+  const bool lead = kok && (k0 / 8) % LPG == 0;
+  Raw8<DT> rn = load_raw8<DT>(xb + row0 * stride);
+#pragma unroll
+  for (int i = 0; i < RT; ++i) {
+    const int64_t row = row0 + i;
+    if (row >= rows) break;                                   // wave-uniform
+    float v[8];
+    cvt_raw8<DT>(rn, kok, v);
+    if (i + 1 < RT) rn = load_raw8<DT>(xb + min(row + 1, rows - 1) * stride);
+    const uint32_t am = __builtin_bit_cast(uint32_t, abs_max<8>(v));
+    const float s = group_scale(__builtin_bit_cast(float, group_max_u32<LPG>(am)));
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    uint32_t qw[2];
+    codes_rcp_packed<8>(v, s, qw);
+    u32x2 q;
+    q.x = qw[0];
+    q.y = qw[1];
+    __builtin_amdgcn_raw_buffer_store_b64(q, rsrc(codes + row * K, K), kok ? (uint32_t)k0 : kOob, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsrc(scales + row * ngroups, 2 * (int64_t)ngroups),
+                                          lead ? (uint32_t)(k0 / G) * 2 : kOob, 0, 0);
+  }
+}
+
 // ----------------------------------------------------------------------------------
 // Dequantization: out = float(code) * float(scale), exact in fp32 (quant.py:66).
 __global__ __launch_bounds__(256) void dequant_rows_kernel(
@@ -97,8 +139,8 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(
 // the values are dequantized first (requant: float(code) * float(scale), exact).
 //
 // A 256-thread block owns one G-row group by 64 columns. Loads are 16 bytes per lane along
-// C (a wave covers whole 64-column row segments); the tile goes to LDS transposed (column
-// pitch G + 1 floats: the transposing writes hit distinct banks); then 4 lanes per column
+// C (a wave covers whole 64-column row segments); the tile goes to LDS transposed (a skewed
+// column layout keeps writes and reads free of bank conflicts); then 4 lanes per column
 // reduce the group amax with two shuffles and each stores G/4 contiguous codes, so an
 // output row receives G contiguous bytes from 4 adjacent lanes.
 enum { SRC_F32 = 0, SRC_BF16 = 1, SRC_F16 = 2, SRC_I8 = 3 };
@@ -108,8 +150,14 @@ __global__ __launch_bounds__(256) void quant_T_kernel(
     const void *__restrict__ xv, const uint16_t *__restrict__ in_scales, int64_t nsc_in,
     int gin, int64_t R, int64_t C, int64_t nbc, int64_t ngr, int8_t *__restrict__ codes,
     uint16_t *__restrict__ scales, bool rows_vec) {
-  constexpr int PITCH = G + 1;
+  // LDS column layout: column c at c * PITCH, row r at + r + SKEW(r). For G = 128 the
+  // pitch is 145 (17 mod 64 banks) and rows >= 64 are shifted by 16: the transposing
+  // writes (a wave covers 4..16 rows of 16..4 column quads) and the group reads (lanes =
+  // 16 columns x 4 quarter-groups of 32 rows) both hit 64 distinct banks. For G <= 64 the
+  // pitch is G + 1 with no shift (the quarter-groups are then 16 rows or fewer apart).
+  constexpr int PITCH = G == 128 ? 145 : G + 1;
   __shared__ float tile[64 * PITCH];
+  auto lds_at = [](int c, int r) { return c * PITCH + r + (G == 128 && r >= 64 ? 16 : 0); };
   const int tid = threadIdx.x;
   const int64_t bc = blockIdx.x % nbc, br = blockIdx.x / nbc;
   const int64_t r0 = br * G, c0 = bc * 64;
@@ -169,39 +217,36 @@ __global__ __launch_bounds__(256) void quant_T_kernel(
 #pragma unroll
     for (int pass = 0; pass < NP; ++pass)
 #pragma unroll
-      for (int i = 0; i < EPV; ++i) tile[(tx * EPV + i) * PITCH + ty + pass * RPP] = v[pass][i];
+      for (int i = 0; i < EPV; ++i) tile[lds_at(tx * EPV + i, ty + pass * RPP)] = v[pass][i];
   }
   __syncthreads();
 
   // ---- column c = tid / 4, rows [part * G/4, +G/4)
   constexpr int RPT = G / 4;
   const int c = tid >> 2, part = tid & 3;
-  const float *col = tile + c * PITCH + part * RPT;
-  float m = 0.0f;
+  float col[RPT];
 #pragma unroll
-  for (int j = 0; j < RPT; ++j) m = amax2(m, fabsf(col[j]));
-  m = amax2(m, __shfl_xor(m, 1));
-  m = amax2(m, __shfl_xor(m, 2));
-  const float s = group_scale(m);
+  for (int j = 0; j < RPT; ++j) col[j] = tile[lds_at(c, part * RPT + j)];
+  const uint32_t am = __builtin_bit_cast(uint32_t, abs_max<RPT>(col));
+  const float s = group_scale(__builtin_bit_cast(float, group_max_u32<4>(am)));
   const int64_t gc = c0 + c;
   if (gc >= C) return;
   if (part == 0) scales[gc * ngr + br] = scale_bits(s);
-  int8_t q[RPT];
-#pragma unroll
-  for (int j = 0; j < RPT; ++j) q[j] = code_of(col[j] / s);
+  uint32_t w[RPT / 4];
+  codes_rcp_packed<RPT>(col, s, w);
   int8_t *dst = codes + gc * R + r0 + part * RPT;
   const int64_t rbase = r0 + part * RPT;
   if (rbase + RPT <= R && (((uintptr_t)dst) % (RPT < 16 ? RPT : 16)) == 0) {
     if constexpr (RPT == 8) {
-      *(uint2 *)dst = *(const uint2 *)q;
+      *(uint2 *)dst = make_uint2(w[0], w[1]);
     } else {
 #pragma unroll
-      for (int j = 0; j < RPT; j += 16) *(uint4 *)(dst + j) = *(const uint4 *)(q + j);
+      for (int j = 0; j < RPT / 4; j += 4) *(uint4 *)(dst + 4 * j) = make_uint4(w[j], w[j + 1], w[j + 2], w[j + 3]);
     }
   } else {
 #pragma unroll
     for (int j = 0; j < RPT; ++j)
-      if (rbase + j < R) dst[j] = q[j];
+      if (rbase + j < R) dst[j] = (int8_t)(w[j / 4] >> (8 * (j % 4)));
   }
 }
 
@@ -229,6 +274,18 @@ static void launch_rows(const void *x, int64_t rows, int64_t K, int64_t stride,
                         int8_t *codes, uint16_t *scales, const float *noise, float d2,
                         bool vec, hipStream_t st) {
   const int64_t ng = cdiv(K, G);
+  if (vec && noise == nullptr && K <= (1 << 24)) {
+    // four rows per wave where that still gives every CU several blocks
+    const unsigned gy = (unsigned)cdiv(K, 512);
+    if (cdiv(rows, 16) * gy >= 1024) {
+      const dim3 grid((unsigned)cdiv(rows, 16), gy);
+      quant_rows_fast_kernel<DT, G, 4><<<grid, 256, 0, st>>>(x, rows, (int)K, stride, (int)ng, codes, scales);
+    } else {
+      const dim3 grid((unsigned)cdiv(rows, 4), gy);
+      quant_rows_fast_kernel<DT, G, 1><<<grid, 256, 0, st>>>(x, rows, (int)K, stride, (int)ng, codes, scales);
+    }
+    return;
+  }
   const int64_t lanes = rows * ng * (G / 8);
   const unsigned blocks = (unsigned)cdiv(lanes, 256);
   if (vec)

@@ -54,31 +54,6 @@ __device__ __forceinline__ void load8(const typename Elem<DT>::T *p, int k0, int
   }
 }
 
-// 8 consecutive features as raw bits: two 16-byte vectors for fp32, one for 16-bit types.
-template <int DT> struct Raw8 { uint4 a, b; };
-template <int DT>
-__device__ __forceinline__ Raw8<DT> load_raw8(const typename Elem<DT>::T *p) {
-  Raw8<DT> r;
-  r.a = *(const uint4 *)p;
-  if constexpr (DT == KSD_F32) r.b = *(const uint4 *)(p + 4);
-  return r;
-}
-template <int DT>
-__device__ __forceinline__ void cvt_raw8(const Raw8<DT> &r, bool ok, float *v) {
-  const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float f;
-    if constexpr (DT == KSD_F32) {
-      f = __builtin_bit_cast(float, w[i]);
-    } else {
-      const uint16_t h = (uint16_t)(i & 1 ? w[i / 2] >> 16 : w[i / 2] & 0xffffu);
-      f = Elem<DT>::load(&h);
-    }
-    v[i] = ok ? f : 0.0f;
-  }
-}
-
 // Block = 4 waves x 64 lanes; a wave walks RT consecutive rows (tokens) and a lane owns 8
 // consecutive features, so a group is G/8 adjacent lanes of one wave (grid.y walks the row
 // in 512-feature slices). Each row is read once: it is the next row's previous token, and
