@@ -326,12 +326,12 @@ def cpu_baseline(x, w, dy, budget_s):
 
 
 def traffic_from_profiles():
-    path = os.path.join(ROOT, "profiles", "gemm_nt_c2_pmc.json")
+    path = os.path.join(ROOT, "profiles", "gemm_g128_c2_pmc.json")
     if not os.path.exists(path):
         return None, None
     with open(path) as f:
         d = json.load(f)
-    return d.get("traffic_bytes_per_launch"), "profiles/gemm_nt_c2_pmc.json"
+    return d.get("traffic_bytes_per_launch"), "profiles/gemm_g128_c2_pmc.json"
 
 
 def main():
@@ -415,7 +415,7 @@ def main():
         "ks3_c4_kernels": None if args.no_ks3 else ks3_kernel_times(dev, args.kernel_reps),
         "rosa_c4_kernels": None if args.no_rosa else rosa_kernel_times(dev, args.kernel_reps),
         "roofline": {
-            "kernel": "gemm_nt_kernel<128,f32> (fwd, dX, dW launches averaged)",
+            "kernel": "ksd::g128::gemm_g128_kernel<f32> (fwd, dX, dW launches averaged)",
             "bound": "mfma",
             "achieved": round(achieved / 1e12, 1),
             "peak": PEAK_INT8 / 1e12,
