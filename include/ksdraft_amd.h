@@ -124,11 +124,14 @@ int ksd_w8a8_group_partials(const int8_t *a, const int8_t *w, int64_t M, int64_t
  *   tanh_lut          (256,) int8, 4-byte aligned                   (make_tanh_lut, :50-54)
  *   h                 NULL or (M, F) fp32: the features (_spine_features' return value)
  *   h_codes, h_scales NULL, or (M, F) int8 and (M, ceil(F/group)) fp16: quantize_last_dim(h)
+ *   table             workspace, (F, 256) fp16, 16-byte aligned, overwritten: the per-chart
+ *                     spine increment for each of the 256 LUT indices (it depends on the
+ *                     chart's spine and warp parameters only)
  */
 int ksd_ks3_spine_fwd(const uint16_t *coords, int64_t M, int64_t F, const int8_t *spine_codes,
                       const uint16_t *spine_scale, const uint16_t *warp_scale,
                       const uint16_t *warp_shift, const int8_t *tanh_lut, int group, float *h,
-                      int8_t *h_codes, uint16_t *h_scales, void *stream);
+                      int8_t *h_codes, uint16_t *h_scales, uint16_t *table, void *stream);
 
 /*
  * K8 — the spine + requantization stage of project_fused / _fused_gemm_spine, 'int8' mode
@@ -139,11 +142,12 @@ int ksd_ks3_spine_fwd(const uint16_t *coords, int64_t M, int64_t F, const int8_t
  *   acc        (M, F) fp32: w8a8_gemm(xq, xs, down_codes, down_scales)
  *   spine/warp buffers and tanh_lut as for ksd_ks3_spine_fwd
  *   h_codes (M, F) int8, h_scales (M, ceil(F/group)) fp16
+ *   table      workspace, (F, 256) fp32, 16-byte aligned, overwritten (per-chart increments)
  */
 int ksd_ks3_spine_fused(const float *acc, int64_t M, int64_t F, const int8_t *spine_codes,
                         const uint16_t *spine_scale, const uint16_t *warp_scale,
                         const uint16_t *warp_shift, const int8_t *tanh_lut, int group,
-                        int8_t *h_codes, uint16_t *h_scales, void *stream);
+                        int8_t *h_codes, uint16_t *h_scales, float *table, void *stream);
 
 /*
  * Number of row blocks (the first dim of the partials workspace) ksd_ks3_vjp uses for M

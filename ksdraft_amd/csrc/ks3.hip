@@ -84,14 +84,19 @@ __device__ __forceinline__ SpineCol load_spine_col(const int8_t *codes, const ui
   return c;
 }
 
-// One feature of _spine_features 'int8' mode, rank 1 (mean == x). Returns the fp32
-// ReLU^2 feature fp16(hq*hq) * pre^2.
-__device__ __forceinline__ float spine_feature(float x, const SpineCol &c, const int8_t *lut) {
-  int ti = lut_index(f16_round(x * 0.25f));
-  int tq = lut_at(lut, ti);
+// The chart part of _spine_features 'int8' mode, rank 1 (ks3_int8.py:209-225), and of the
+// fused kernel's spine (ks3_triton.py:52-70): for the LUT index ti of a coordinate, tq =
+// LUT[ti], the warp w(tq) and zq = LUT[index(w)], then the two integer Horner sums. Every
+// step depends on the chart and ti alone, so the kernels tabulate it per chart over the 256
+// indices: the composed contract as its fp16 increment fp16(fp16(trunc(sum / 64)) * ps)
+// (:226-227), the fused one as its fp32 increment sum * (ps / 64) (ks3_triton.py:70).
+template <bool FUSED>
+__device__ __forceinline__ int spine_sum(int ti, const SpineCol &c, const int8_t *lut) {
+  const int tq = lut_at(lut, ti);
   float w = f16_round(f16_round((float)tq * kTq16Step) + c.sh);
   w = f16_round(c.sc * w);
-  int zq = lut_at(lut, lut_index(w));
+  const int zq = lut_at(lut, FUSED ? (int)rintf(fminf(fmaxf(w, -kLutDomain), kLutDomain) * kLutScale)
+                                   : lut_index(w));
   int poly = c.a64;
   poly = round_div127(poly * tq * 4) + c.b64;
   poly = round_div127(poly * tq * 4) + c.c2_64;
@@ -100,90 +105,264 @@ __device__ __forceinline__ float spine_feature(float x, const SpineCol &c, const
   wp = round_div127(wp * zq) + c.c4x2_64;
   wp = round_div127(wp * zq) - c.c5x3_64;
   wp = round_div127(wp * zq) - c.c4_64;
-  int td = (poly + wp) / 64;  // torch.div(..., rounding_mode="trunc")
-  float h = x + f16_round(f16_round((float)td) * c.ps);
-  h = h < 0.0f ? 0.0f : h;  // relu
-  float pre = group_scale(fabsf(h));  // amax over the rank dim (one element), ks3_int8.py:230-231
-  float q = fminf(fmaxf(rintf(h / pre), -127.0f), 127.0f);
-  q = fmaxf(q, 0.0f);
-  return f16_round(q * q) * (pre * pre);
+  return poly + wp;
 }
 
-// Block: 256 threads = 8 rows x 32 lanes; a lane owns 4 consecutive columns of a
-// 128-column segment (blockIdx.x). Rows [blockIdx.y * kSpineRows, +kSpineRows).
-constexpr int kSpineRows = 64;
-
-template <int G, bool VEC>
-__global__ void __launch_bounds__(256) ks3_spine_kernel(
-    const uint16_t *__restrict__ coords, int64_t M, int64_t F,
+// Table builder: block = one chart, thread = LUT index ti + 128 (0..255). Composed: fp16
+// bits of the increment; fused: fp32 bits.
+template <bool FUSED>
+__global__ void __launch_bounds__(256) ks3_spine_table_kernel(
     const int8_t *__restrict__ spine_codes, const uint16_t *__restrict__ spine_scale,
     const uint16_t *__restrict__ sc16, const uint16_t *__restrict__ sh16,
-    const int8_t *__restrict__ tanh_lut, float *__restrict__ h_out,
-    int8_t *__restrict__ hq, uint16_t *__restrict__ hs, int64_t n_groups) {
+    const int8_t *__restrict__ tanh_lut, void *__restrict__ table) {
   __shared__ int8_t lut[256];
   if (threadIdx.x < 64) ((uint32_t *)lut)[threadIdx.x] = ((const uint32_t *)tanh_lut)[threadIdx.x];
-  const int lane = threadIdx.x & 31;
-  const int rsub = threadIdx.x >> 5;
-  const int64_t col0 = (int64_t)blockIdx.x * 128 + lane * 4;
-  SpineCol cc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    cc[j] = load_spine_col(spine_codes, spine_scale, sc16, sh16, col0 + j, col0 + j < F);
   __syncthreads();
-
-  const int64_t row_end = min(M, (int64_t)(blockIdx.y + 1) * kSpineRows);
-  for (int64_t row = (int64_t)blockIdx.y * kSpineRows + rsub; row < row_end; row += 8) {
-    float x[4];
-    const uint16_t *src = coords + row * F + col0;
-    if (VEC && col0 + 3 < F) {
-      uint2 u = *(const uint2 *)src;
-      x[0] = f16_to_f32((uint16_t)u.x);
-      x[1] = f16_to_f32((uint16_t)(u.x >> 16));
-      x[2] = f16_to_f32((uint16_t)u.y);
-      x[3] = f16_to_f32((uint16_t)(u.y >> 16));
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = col0 + j < F ? f16_to_f32(src[j]) : 0.0f;
-    }
-    float h[4];
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      h[j] = col0 + j < F ? spine_feature(x[j], cc[j], lut) : 0.0f;
-      amax = amax2(amax, fabsf(h[j]));
-    }
-    if (h_out) {
-      float *dst = h_out + row * F + col0;
-      if (VEC && col0 + 3 < F) {
-        *(float4 *)dst = make_float4(h[0], h[1], h[2], h[3]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (col0 + j < F) dst[j] = h[j];
-      }
-    }
-    if (hq) {
-      // quantize_last_dim(h, G): one group = G/4 lanes
-#pragma unroll
-      for (int o = 1; o < G / 4; o <<= 1) amax = amax2(amax, __shfl_xor(amax, o, 32));
-      const float s = group_scale(amax);
-      int8_t q[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) q[j] = code_of(h[j] / s);
-      int8_t *dst = hq + row * F + col0;
-      if (VEC && col0 + 3 < F) {
-        *(uint32_t *)dst = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) |
-                           ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (col0 + j < F) dst[j] = q[j];
-      }
-      if ((lane & (G / 4 - 1)) == 0 && col0 < F) hs[row * n_groups + col0 / G] = scale_bits(s);
-    }
+  const int64_t f = blockIdx.x;
+  const SpineCol c = load_spine_col(spine_codes, spine_scale, sc16, sh16, f, true);
+  const int sum = spine_sum<FUSED>((int)threadIdx.x - 128, c, lut);
+  if constexpr (FUSED) {
+    ((float *)table)[f * 256 + threadIdx.x] = (float)sum * (c.ps / 64.0f);
+  } else {
+    const int td = sum / 64;  // torch.div(..., rounding_mode="trunc")
+    ((uint16_t *)table)[f * 256 + threadIdx.x] = f16_bits(f16_round((float)td) * c.ps);
   }
 }
 
+// _lut_index of an fp16 coordinate x (ks3_int8.py:69-72, composed contract). x / 4 is
+// exact in fp16 unless |x| < 2^-12, where either way the index is 0, so the fp16 rounding
+// of x * 0.25 is skipped; clamping an fp16 value to the fp16 bounds +-fp16(3.2) equals
+// torch's clamp to +-3.2 followed by the fp16 rounding.
+__device__ __forceinline__ int lut_index_x(float x) {
+  constexpr float kDom16 = 3.19921875f;  // fp16(3.2)
+  const float c = __builtin_amdgcn_fmed3f(x * 0.25f, -kDom16, kDom16);
+  return (int)rintf(f16_round(c * kLutScale));
+}
+// _lut_index_f32 of the fused kernel (ks3_triton.py:56): fp32 throughout.
+__device__ __forceinline__ int lut_index_f32(float v) {
+  return (int)rintf(__builtin_amdgcn_fmed3f(v, -kLutDomain, kLutDomain) * kLutScale);
+}
+
+// rint(h / pre) clamped to [0, 127] for the rank-1 ReLU^2 codes (ks3_int8.py:232): the
+// reciprocal multiply of codes_rcp (within 2^-15 of the quotient for |p| <= 128), the
+// IEEE division when p lies within 2^-14 of a half-integer. NaN gives 0 as fmax/fmin do.
+__device__ __forceinline__ float relu2_code(float h, float pre) {
+  const float p = h * __builtin_amdgcn_rcpf(pre);
+  float t = rintf(p);
+  if (fabsf(fabsf(p - t) - 0.5f) < 0x1p-14f) t = rintf(h / pre);
+  return fmaxf(fminf(fmaxf(t, -127.0f), 127.0f), 0.0f);
+}
+
+// Max over the 32 lanes of each half-wave (u32 patterns): DPP within 16-lane rows, then
+// a ds_swizzle exchange of lanes i and i ^ 16.
+__device__ __forceinline__ uint32_t group_max32_u32(uint32_t v) {
+  v = group_max_u32<16>(v);
+  return max(v, (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401f));
+}
+template <int L>
+__device__ __forceinline__ uint32_t lane_group_max(uint32_t v) {
+  if constexpr (L == 32) return group_max32_u32(v);
+  else return group_max_u32<L>(v);
+}
+
+// Spine kernels: block = 512 threads = 16 rows x 32 lanes; a lane owns 4 consecutive
+// charts of the block's 128-chart segment (blockIdx.x), so a G-chart group is G/4 lanes of
+// one half-wave. Rows [blockIdx.y * kSpineRows, +kSpineRows), 2 per lane per iteration
+// with both rows' loads issued first. The segment's increment table (128 charts x 256
+// indices) is staged in LDS with a pitch of 129 words (fp16 table) / 257 words (fp32):
+// lanes reading the same index of different charts then fall in different banks.
+constexpr int kSpineRows = 512;
+constexpr int kSpineThreads = 512;
+
+template <bool FUSED>
+struct SpineTab {
+  static constexpr int kPitch = FUSED ? 257 : 129;  // 32-bit words per chart
+  __device__ static void stage(uint32_t *tab, const void *table, int64_t c0, int64_t F) {
+    constexpr int WPC = FUSED ? 256 : 128;           // words per chart in global memory
+    const uint32_t *src = (const uint32_t *)table;
+    for (int i = threadIdx.x; i < 128 * WPC / 4; i += kSpineThreads) {
+      const int ch = i / (WPC / 4), w4 = i % (WPC / 4);
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (c0 + ch < F) v = *(const uint4 *)(src + (c0 + ch) * WPC + w4 * 4);
+      uint32_t *d = tab + ch * kPitch + w4 * 4;
+      d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+    }
+  }
+  __device__ static float inc(const uint32_t *tab, int ch, int idx) {
+    if constexpr (FUSED) return __builtin_bit_cast(float, tab[ch * kPitch + idx]);
+    else return f16_to_f32(((const uint16_t *)tab)[ch * (2 * kPitch) + idx]);
+  }
+};
+
+// LUT byte offsets (2 * (ti + 128)) of two fp16 coordinates packed in a word, on packed
+// fp16 (the composed contract's _lut_index, ks3_int8.py:69-72): x * 0.25 (exact, and where
+// it is not, |x| < 2^-12, the index is 0 either way), the clamp to +-fp16(3.2) (equal to
+// torch's fp32 clamp followed by fp16 rounding), the fp16 product with 127/3.2 (exact in
+// fp32, so rounding once to fp16 equals torch's two roundings), then + 1.5 * 2^10, which
+// rounds to an integer (ties to even) and leaves 0x6600 + ti in the bits (|ti| <= 127).
+__device__ __forceinline__ void lut_offsets2(uint32_t xw, uint32_t &o0, uint32_t &o1) {
+  const h2 kQ = {(_Float16)0.25f, (_Float16)0.25f};
+  const h2 kLo = {(_Float16)-3.19921875f, (_Float16)-3.19921875f};
+  const h2 kHi = {(_Float16)3.19921875f, (_Float16)3.19921875f};
+  const h2 kS = {(_Float16)39.6875f, (_Float16)39.6875f};
+  const h2 kM = {(_Float16)1536.0f, (_Float16)1536.0f};
+  h2 c = __builtin_bit_cast(h2, xw) * kQ;
+  c = __builtin_elementwise_min(__builtin_elementwise_max(c, kLo), kHi);
+  const uint32_t b = __builtin_bit_cast(uint32_t, c * kS + kM);
+  o0 = ((b & 0xffffu) - 0x6580u) * 2u;
+  o1 = ((b >> 16) - 0x6580u) * 2u;
+}
+
+// fp16(clamp(h / 127, 2^-24, 65504)) for a finite or NaN h >= 0 (group_scale of one
+// element: the div127 correction needs no infinity guard, and the clamp propagates NaN).
+__device__ __forceinline__ float scale_of_finite(float h) {
+  constexpr float r = 1.0f / 127.0f;
+  const float q0 = h * r;
+  const float q = fmaf(fmaf(-q0, 127.0f, h), r, q0);
+  return f16_round(__builtin_elementwise_minimum(__builtin_elementwise_maximum(q, kScaleMin), kScaleMax));
+}
+
+// Composed contract (ks3_int8.py:205-234 + quantize_last_dim(h, G)): x is the fp16
+// coordinate; h = relu(x + inc[ti]); the rank-1 ReLU^2 requantization pre = fp16 scale of
+// |h|, code q = rint(h / pre) in [0, 127], feature fp16(q * q) * pre^2; then the feature's
+// per-group quantization. Per iteration a lane takes 2 rows x 4 charts in phases (loads,
+// LUT offsets, the 8 table reads, the arithmetic), with one fallback branch for the rare
+// near-tie ReLU^2 codes; codes and scales leave through buffer stores whose offsets for
+// rows past the block's end or charts past F lie past num_records.
+template <int G, bool VEC>
+__global__ void __launch_bounds__(kSpineThreads) ks3_spine_kernel(
+    const uint16_t *__restrict__ coords, int64_t M, int64_t F, const void *__restrict__ table,
+    float *__restrict__ h_out, int8_t *__restrict__ hq, uint16_t *__restrict__ hs, int64_t n_groups) {
+  using Tab = SpineTab<false>;
+  __shared__ uint32_t tab[128 * Tab::kPitch];
+  const int64_t c0 = (int64_t)blockIdx.x * 128;
+  Tab::stage(tab, table, c0, F);
+  __syncthreads();
+  const int lane = threadIdx.x & 31;
+  const int rsub = threadIdx.x >> 5;
+  const int64_t col0 = c0 + lane * 4;
+  const bool cok = col0 < F;
+  const bool seg_full = c0 + 128 <= F;             // block-uniform: no chart past F
+  const int64_t colc = cok ? col0 : 0;             // a valid column for every lane
+  const uint32_t tab_lane = (uint32_t)(uintptr_t)(tab) + (uint32_t)(lane * 4) * (4 * Tab::kPitch);
+  const int64_t row_end = min(M, (int64_t)(blockIdx.y + 1) * kSpineRows);
+  const int64_t rfirst = (int64_t)blockIdx.y * kSpineRows + rsub;
+  // the two rows (r0, r0 + 16) of an iteration as packed fp16 words: 4 charts each
+  auto raw2 = [&](int64_t r0, uint2 (&w)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint16_t *src = coords + min(r0 + 16 * u, M - 1) * F + colc;
+      if (VEC) {
+        w[u] = *(const uint2 *)src;
+      } else {
+        uint32_t e[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) e[j] = col0 + j < F ? src[j] : 0u;
+        w[u] = make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16));
+      }
+    }
+  };
+  auto body = [&](int64_t r0, const uint2 (&w)[2]) __attribute__((always_inline)) {
+    uint32_t off[2][4];
+    float x[2][4], inc[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      lut_offsets2(w[u].x, off[u][0], off[u][1]);
+      lut_offsets2(w[u].y, off[u][2], off[u][3]);
+      x[u][0] = f16_to_f32((uint16_t)w[u].x);
+      x[u][1] = f16_to_f32((uint16_t)(w[u].x >> 16));
+      x[u][2] = f16_to_f32((uint16_t)w[u].y);
+      x[u][3] = f16_to_f32((uint16_t)(w[u].y >> 16));
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        typedef __attribute__((address_space(3))) const uint16_t lds_u16;
+        inc[u][j] = f16_to_f32(*(lds_u16 *)(uintptr_t)(tab_lane + j * (4 * Tab::kPitch) + off[u][j]));
+      }
+    float v[2][4], pre[2][4], h[2][4];
+    float near = 1.0f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // relu (NaN-propagating max; -0 becomes +0, which leaves every output unchanged)
+        const float t = __builtin_elementwise_maximum(x[u][j] + inc[u][j], 0.0f);
+        v[u][j] = t;
+        pre[u][j] = scale_of_finite(t);  // amax over the rank dim (one element), :230-231
+        const float p = t * __builtin_amdgcn_rcpf(pre[u][j]);
+        const float r = rintf(p);
+        near = fminf(near, fabsf(fabsf(p - r) - 0.5f));
+        h[u][j] = r;
+      }
+    if (near < 0x1p-14f) {  // some quotient within 2^-14 of a half-integer: divide
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) h[u][j] = rintf(v[u][j] / pre[u][j]);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // q = clamp(rint(h / pre), 0, 127); a NaN q leaves the feature NaN via pre
+        const float q = __builtin_amdgcn_fmed3f(h[u][j], 0.0f, 127.0f);
+        const float f = f16_round(q * q) * (pre[u][j] * pre[u][j]);
+        h[u][j] = seg_full || (VEC ? cok : col0 + j < F) ? f : 0.0f;
+      }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int64_t row = r0 + 16 * u;
+      const bool rok = row < row_end;
+      if (h_out && rok) {
+        float *dst = h_out + row * F + col0;
+        if (VEC && cok) {
+          *(float4 *)dst = make_float4(h[u][0], h[u][1], h[u][2], h[u][3]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (col0 + j < F) dst[j] = h[u][j];
+        }
+      }
+      if (hq) {
+        // quantize_last_dim(h, G): one group = G/4 lanes of a half-wave
+        const uint32_t am = lane_group_max<G / 4>(__builtin_bit_cast(uint32_t, abs_max<4>(h[u])));
+        const float s = group_scale(__builtin_bit_cast(float, am));
+        uint32_t wq;
+        codes_rcp_packed<4>(h[u], s, &wq);
+        const int64_t rowc = rok ? row : 0;
+        const bool lead = rok && cok && (lane & (G / 4 - 1)) == 0;
+        __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsrc(hs + rowc * n_groups, 2 * n_groups),
+                                              lead ? (uint32_t)(col0 / G) * 2 : kOob, 0, 0);
+        if (VEC) {
+          __builtin_amdgcn_raw_buffer_store_b32(wq, rsrc(hq + rowc * F, F),
+                                                rok && cok ? (uint32_t)col0 : kOob, 0, 0);
+        } else if (rok) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (col0 + j < F) hq[row * F + col0 + j] = (int8_t)(wq >> (8 * j));
+        }
+      }
+    }
+  };
+  // two row pairs in flight: the pair after next is loaded (from clamped valid rows) before
+  // this pair's arithmetic, into the buffer the previous pair just released; a fixed trip
+  // count, rows past the block's end only having their stores masked
+  uint2 wa[2], wb[2];
+  raw2(rfirst, wa);
+  raw2(rfirst + 32, wb);
+#pragma unroll 1
+  for (int it = 0; it < kSpineRows / 64; ++it) {
+    const int64_t r0 = rfirst + 64 * it;
+    const uint2 ca[2] = {wa[0], wa[1]};
+    raw2(r0 + 64, wa);
+    body(r0, ca);
+    const uint2 cb[2] = {wb[0], wb[1]};
+    raw2(r0 + 96, wb);
+    body(r0 + 32, cb);
+  }
+}
 
 // The fused-kernel contract of project_fused / _fused_gemm_spine, 'int8' mode
 // (ks3_triton.py:47-75, 137-156). It differs from the composed one: x is the fp32 GEMM
@@ -191,89 +370,71 @@ __global__ void __launch_bounds__(256) ks3_spine_kernel(
 // fp32; the Horner sum is scaled by ps/64 in fp32 without truncation; the ReLU^2 pre-scale
 // is the amax of |h| (before ReLU) over the row's G-chart group; the squared codes are
 // exact; and the result is requantized per group a second time.
-__device__ __forceinline__ int lut_index_f32(float v) {
-  return (int)rintf(fminf(fmaxf(v, -kLutDomain), kLutDomain) * kLutScale);
-}
-
-__device__ __forceinline__ float spine_fused_h(float x, const SpineCol &c, const int8_t *lut) {
-  int tq = lut_at(lut, lut_index_f32(x * 0.25f));
-  float w = f16_round(f16_round((float)tq * kTq16Step) + c.sh);
-  w = f16_round(c.sc * w);
-  int zq = lut_at(lut, lut_index_f32(w));
-  int poly = c.a64;
-  poly = round_div127(poly * tq * 4) + c.b64;
-  poly = round_div127(poly * tq * 4) + c.c2_64;
-  poly = round_div127(poly * tq * 4) + c.c0_64;
-  int wp = c.c5x4_64;
-  wp = round_div127(wp * zq) + c.c4x2_64;
-  wp = round_div127(wp * zq) - c.c5x3_64;
-  wp = round_div127(wp * zq) - c.c4_64;
-  return x + (float)(poly + wp) * (c.ps / 64.0f);
-}
-
 template <int G, bool VEC>
-__global__ void __launch_bounds__(256) ks3_spine_fused_kernel(
-    const float *__restrict__ acc, int64_t M, int64_t F,
-    const int8_t *__restrict__ spine_codes, const uint16_t *__restrict__ spine_scale,
-    const uint16_t *__restrict__ sc16, const uint16_t *__restrict__ sh16,
-    const int8_t *__restrict__ tanh_lut, int8_t *__restrict__ hq, uint16_t *__restrict__ hs,
-    int64_t n_groups) {
-  __shared__ int8_t lut[256];
-  if (threadIdx.x < 64) ((uint32_t *)lut)[threadIdx.x] = ((const uint32_t *)tanh_lut)[threadIdx.x];
+__global__ void __launch_bounds__(kSpineThreads) ks3_spine_fused_kernel(
+    const float *__restrict__ acc, int64_t M, int64_t F, const void *__restrict__ table,
+    int8_t *__restrict__ hq, uint16_t *__restrict__ hs, int64_t n_groups) {
+  using Tab = SpineTab<true>;
+  __shared__ uint32_t tab[128 * Tab::kPitch];
+  const int64_t c0 = (int64_t)blockIdx.x * 128;
+  Tab::stage(tab, table, c0, F);
+  __syncthreads();
   const int lane = threadIdx.x & 31;
   const int rsub = threadIdx.x >> 5;
-  const int64_t col0 = (int64_t)blockIdx.x * 128 + lane * 4;
-  SpineCol cc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    cc[j] = load_spine_col(spine_codes, spine_scale, sc16, sh16, col0 + j, col0 + j < F);
-  __syncthreads();
-
+  const int64_t col0 = c0 + lane * 4;
+  const bool full = VEC && col0 + 3 < F;
   const int64_t row_end = min(M, (int64_t)(blockIdx.y + 1) * kSpineRows);
-  for (int64_t row = (int64_t)blockIdx.y * kSpineRows + rsub; row < row_end; row += 8) {
-    float x[4];
-    const float *src = acc + row * F + col0;
-    if (VEC && col0 + 3 < F) {
-      float4 u = *(const float4 *)src;
-      x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
-    } else {
+  for (int64_t r0 = (int64_t)blockIdx.y * kSpineRows + rsub; r0 < row_end; r0 += 32) {
+    float x[2][4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = col0 + j < F ? src[j] : 0.0f;
-    }
-    float h[4];
-    float amax = 0.0f;
+    for (int u = 0; u < 2; ++u) {
+      const float *src = acc + min(r0 + 16 * u, M - 1) * F + col0;
+      if (full) {
+        const float4 v = *(const float4 *)src;
+        x[u][0] = v.x; x[u][1] = v.y; x[u][2] = v.z; x[u][3] = v.w;
+      } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float xc = fminf(fmaxf(x[j], -kScaleMax), kScaleMax);
-      h[j] = col0 + j < F ? spine_fused_h(xc, cc[j], lut) : 0.0f;
-      amax = amax2(amax, fabsf(h[j]));
+        for (int j = 0; j < 4; ++j) x[u][j] = col0 + j < F ? src[j] : 0.0f;
+      }
     }
 #pragma unroll
-    for (int o = 1; o < G / 4; o <<= 1) amax = amax2(amax, __shfl_xor(amax, o, 32));
-    const float pre = group_scale(amax);
-    float hmax = 0.0f;
+    for (int u = 0; u < 2; ++u) {
+      const int64_t row = r0 + 16 * u;
+      const bool rok = row < row_end;
+      float h[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float q = fmaxf(fminf(fmaxf(rintf(h[j] / pre), -127.0f), 127.0f), 0.0f);
-      h[j] = (q * q) * (pre * pre);
-      hmax = amax2(hmax, fabsf(h[j]));
+      for (int j = 0; j < 4; ++j) {
+        const float xc = __builtin_amdgcn_fmed3f(x[u][j], -kScaleMax, kScaleMax);
+        const int idx = min(max(lut_index_f32(xc * 0.25f) + 128, 0), 255);
+        h[j] = col0 + j < F ? xc + Tab::inc(tab, lane * 4 + j, idx) : 0.0f;
+      }
+      const uint32_t am = lane_group_max<G / 4>(__builtin_bit_cast(uint32_t, abs_max<4>(h)));
+      const float pre = group_scale(__builtin_bit_cast(float, am));
+      const float rp = __builtin_amdgcn_rcpf(pre);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float p = h[j] * rp;
+        float t = rintf(p);
+        if (fabsf(fabsf(p - t) - 0.5f) < 0x1p-14f) t = rintf(h[j] / pre);
+        const float q = fmaxf(fminf(fmaxf(t, -127.0f), 127.0f), 0.0f);
+        h[j] = (q * q) * (pre * pre);
+      }
+      const uint32_t hm = lane_group_max<G / 4>(__builtin_bit_cast(uint32_t, abs_max<4>(h)));
+      const float s = group_scale(__builtin_bit_cast(float, hm));
+      uint32_t w;
+      codes_rcp_packed<4>(h, s, &w);
+      if (rok) {
+        int8_t *dst = hq + row * F + col0;
+        if (full) {
+          *(uint32_t *)dst = w;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (col0 + j < F) dst[j] = (int8_t)(w >> (8 * j));
+        }
+        if ((lane & (G / 4 - 1)) == 0 && col0 < F) hs[row * n_groups + col0 / G] = scale_bits(s);
+      }
     }
-#pragma unroll
-    for (int o = 1; o < G / 4; o <<= 1) hmax = amax2(hmax, __shfl_xor(hmax, o, 32));
-    const float s = group_scale(hmax);
-    int8_t q[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) q[j] = code_of(h[j] / s);
-    int8_t *dst = hq + row * F + col0;
-    if (VEC && col0 + 3 < F) {
-      *(uint32_t *)dst = (uint32_t)(uint8_t)q[0] | ((uint32_t)(uint8_t)q[1] << 8) |
-                         ((uint32_t)(uint8_t)q[2] << 16) | ((uint32_t)(uint8_t)q[3] << 24);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (col0 + j < F) dst[j] = q[j];
-    }
-    if ((lane & (G / 4 - 1)) == 0 && col0 < F) hs[row * n_groups + col0 / G] = scale_bits(s);
   }
 }
 
@@ -599,30 +760,40 @@ __global__ void __launch_bounds__(256) ks3_vjp_kernel(
 }
 
 // Fixed-order sum of the per-block partials, then the reference's fp16 roundings and the
-// STE chain to the raw warp parameters (ks3_int8.py:379-395).
+// STE chain to the raw warp parameters (ks3_int8.py:379-395). One thread per (reduction k,
+// chart f): eight interleaved accumulators (row block b goes to accumulator b mod 8), added
+// pairwise at the end, so the order depends on the row-block count only, not on the device.
 __global__ void ks3_vjp_finalize_kernel(const float *__restrict__ partials, int64_t nrb, int64_t F,
                                         const float *__restrict__ raw_scale,
                                         const float *__restrict__ raw_shift, float *__restrict__ sums,
                                         uint16_t *__restrict__ dcoeff, uint16_t *__restrict__ dscale,
                                         uint16_t *__restrict__ dshift) {
   const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int k = blockIdx.y;
   if (f >= F) return;
-  float s[8];
+  const float *p = partials + (int64_t)k * F + f;
+  const int64_t step = 8 * F;
+  float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  int64_t b = 0;
+  for (; b + 8 <= nrb; b += 8) {
+    float v[8];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    float a = 0.0f;
-    for (int64_t b = 0; b < nrb; ++b) a += partials[(b * 8 + k) * F + f];
-    s[k] = a;
-    if (sums) sums[k * F + f] = a;
+    for (int j = 0; j < 8; ++j) v[j] = p[(b + j) * step];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] += v[j];
   }
-#pragma unroll
-  for (int k = 0; k < 6; ++k) dcoeff[f * 6 + k] = f16_bits(s[k]);
-  const float dscale_t = f16_round(s[6]);
-  const float dshift_t = f16_round(f16_round(s[7]) * 0.5f);
-  const float sig = 1.0f / (1.0f + expf(-raw_scale[f]));
-  const float th = tanhf(raw_shift[f]);
-  dscale[f] = f16_bits(dscale_t * sig);
-  dshift[f] = f16_bits(dshift_t * (1.0f - th * th));
+  for (int j = 0; b < nrb; ++b, ++j) acc[j] += p[b * step];
+  const float a = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  if (sums) sums[k * F + f] = a;
+  if (k < 6) {
+    dcoeff[f * 6 + k] = f16_bits(a);
+  } else if (k == 6) {
+    const float sig = 1.0f / (1.0f + expf(-raw_scale[f]));
+    dscale[f] = f16_bits(f16_round(a) * sig);
+  } else {
+    const float th = tanhf(raw_shift[f]);
+    dshift[f] = f16_bits(f16_round(f16_round(a) * 0.5f) * (1.0f - th * th));
+  }
 }
 
 // fp16 tanh through the same table (test export).
@@ -639,28 +810,24 @@ __global__ void ks3_tanh16_kernel(const uint16_t *__restrict__ x, int64_t n, uin
 // ---------------------------------------------------------------- launchers
 template <int G>
 static void launch_spine(bool vec, dim3 grid, hipStream_t st, const uint16_t *coords, int64_t M,
-                         int64_t F, const int8_t *sc, const uint16_t *ss, const uint16_t *w16,
-                         const uint16_t *h16, const int8_t *lut, float *h, int8_t *hq, uint16_t *hs,
-                         int64_t ng) {
+                         int64_t F, const void *table, float *h, int8_t *hq, uint16_t *hs, int64_t ng) {
   if (vec)
-    hipLaunchKernelGGL((ks3_spine_kernel<G, true>), grid, dim3(256), 0, st, coords, M, F, sc, ss,
-                       w16, h16, lut, h, hq, hs, ng);
+    hipLaunchKernelGGL((ks3_spine_kernel<G, true>), grid, dim3(kSpineThreads), 0, st, coords, M, F,
+                       table, h, hq, hs, ng);
   else
-    hipLaunchKernelGGL((ks3_spine_kernel<G, false>), grid, dim3(256), 0, st, coords, M, F, sc, ss,
-                       w16, h16, lut, h, hq, hs, ng);
+    hipLaunchKernelGGL((ks3_spine_kernel<G, false>), grid, dim3(kSpineThreads), 0, st, coords, M, F,
+                       table, h, hq, hs, ng);
 }
 
 template <int G>
 static void launch_fused(bool vec, dim3 grid, hipStream_t st, const float *acc, int64_t M,
-                         int64_t F, const int8_t *sc, const uint16_t *ss, const uint16_t *w16,
-                         const uint16_t *h16, const int8_t *lut, int8_t *hq, uint16_t *hs,
-                         int64_t ng) {
+                         int64_t F, const void *table, int8_t *hq, uint16_t *hs, int64_t ng) {
   if (vec)
-    hipLaunchKernelGGL((ks3_spine_fused_kernel<G, true>), grid, dim3(256), 0, st, acc, M, F, sc,
-                       ss, w16, h16, lut, hq, hs, ng);
+    hipLaunchKernelGGL((ks3_spine_fused_kernel<G, true>), grid, dim3(kSpineThreads), 0, st, acc, M,
+                       F, table, hq, hs, ng);
   else
-    hipLaunchKernelGGL((ks3_spine_fused_kernel<G, false>), grid, dim3(256), 0, st, acc, M, F, sc,
-                       ss, w16, h16, lut, hq, hs, ng);
+    hipLaunchKernelGGL((ks3_spine_fused_kernel<G, false>), grid, dim3(kSpineThreads), 0, st, acc,
+                       M, F, table, hq, hs, ng);
 }
 
 static int64_t vjp_row_blocks(int64_t M) { return cdiv(M, kVjpTile); }
@@ -671,11 +838,15 @@ using namespace ksd;
 
 static int spine_checks(const char *who, const void *in, int64_t M, int64_t F, const int8_t *spine_codes,
                         const uint16_t *spine_scale, const uint16_t *warp_scale,
-                        const uint16_t *warp_shift, const int8_t *tanh_lut, int group) {
+                        const uint16_t *warp_shift, const int8_t *tanh_lut, int group,
+                        const void *table) {
   if (M < 0 || F < 0) return fail(KSD_EINVAL, "%s: negative shape (%lld, %lld)", who, (long long)M, (long long)F);
   if (!valid_group(group)) return fail(KSD_EINVAL, "%s: group must be 32, 64 or 128", who);
   if (!in || !spine_codes || !spine_scale || !warp_scale || !warp_shift || !tanh_lut)
     return fail(KSD_EINVAL, "%s: null input pointer", who);
+  if (!table || ((uintptr_t)table & 15) != 0)
+    return fail(KSD_EINVAL, "%s: table workspace must be a 16-byte aligned buffer", who);
+  if (F > (1LL << 31) / 256) return fail(KSD_EINVAL, "%s: F too large", who);
   if (((uintptr_t)tanh_lut & 3) != 0) return fail(KSD_EINVAL, "%s: tanh_lut must be 4-byte aligned", who);
   if (cdiv(M, kSpineRows) > 0x7fffffff) return fail(KSD_EINVAL, "%s: M too large", who);
   return KSD_OK;
@@ -685,9 +856,9 @@ extern "C" int ksd_ks3_spine_fwd(const uint16_t *coords, int64_t M, int64_t F,
                                  const int8_t *spine_codes, const uint16_t *spine_scale,
                                  const uint16_t *warp_scale, const uint16_t *warp_shift,
                                  const int8_t *tanh_lut, int group, float *h, int8_t *h_codes,
-                                 uint16_t *h_scales, void *stream) {
+                                 uint16_t *h_scales, uint16_t *table, void *stream) {
   int rc = spine_checks("ks3_spine_fwd", coords, M, F, spine_codes, spine_scale, warp_scale,
-                        warp_shift, tanh_lut, group);
+                        warp_shift, tanh_lut, group, table);
   if (rc) return rc;
   if ((h_codes == nullptr) != (h_scales == nullptr))
     return fail(KSD_EINVAL, "ks3_spine_fwd: h_codes and h_scales go together");
@@ -698,8 +869,9 @@ extern "C" int ksd_ks3_spine_fwd(const uint16_t *coords, int64_t M, int64_t F,
   const int64_t ng = cdiv(F, group);
   dim3 grid((unsigned)cdiv(F, 128), (unsigned)cdiv(M, kSpineRows));
   hipStream_t st = (hipStream_t)stream;
-#define KSD_SPINE_ARGS vec, grid, st, coords, M, F, spine_codes, spine_scale, warp_scale, warp_shift, \
-    tanh_lut, h, h_codes, h_scales, ng
+  hipLaunchKernelGGL(ks3_spine_table_kernel<false>, dim3((unsigned)F), dim3(256), 0, st, spine_codes,
+                     spine_scale, warp_scale, warp_shift, tanh_lut, (void *)table);
+#define KSD_SPINE_ARGS vec, grid, st, coords, M, F, table, h, h_codes, h_scales, ng
   switch (group) {
     case 32: launch_spine<32>(KSD_SPINE_ARGS); break;
     case 64: launch_spine<64>(KSD_SPINE_ARGS); break;
@@ -713,9 +885,9 @@ extern "C" int ksd_ks3_spine_fused(const float *acc, int64_t M, int64_t F,
                                    const int8_t *spine_codes, const uint16_t *spine_scale,
                                    const uint16_t *warp_scale, const uint16_t *warp_shift,
                                    const int8_t *tanh_lut, int group, int8_t *h_codes,
-                                   uint16_t *h_scales, void *stream) {
+                                   uint16_t *h_scales, float *table, void *stream) {
   int rc = spine_checks("ks3_spine_fused", acc, M, F, spine_codes, spine_scale, warp_scale,
-                        warp_shift, tanh_lut, group);
+                        warp_shift, tanh_lut, group, table);
   if (rc) return rc;
   if (!h_codes || !h_scales) return fail(KSD_EINVAL, "ks3_spine_fused: null output pointer");
   if (M == 0 || F == 0) return KSD_OK;
@@ -723,8 +895,9 @@ extern "C" int ksd_ks3_spine_fused(const float *acc, int64_t M, int64_t F,
   const int64_t ng = cdiv(F, group);
   dim3 grid((unsigned)cdiv(F, 128), (unsigned)cdiv(M, kSpineRows));
   hipStream_t st = (hipStream_t)stream;
-#define KSD_FUSED_ARGS vec, grid, st, acc, M, F, spine_codes, spine_scale, warp_scale, warp_shift, \
-    tanh_lut, h_codes, h_scales, ng
+  hipLaunchKernelGGL(ks3_spine_table_kernel<true>, dim3((unsigned)F), dim3(256), 0, st, spine_codes,
+                     spine_scale, warp_scale, warp_shift, tanh_lut, (void *)table);
+#define KSD_FUSED_ARGS vec, grid, st, acc, M, F, table, h_codes, h_scales, ng
   switch (group) {
     case 32: launch_fused<32>(KSD_FUSED_ARGS); break;
     case 64: launch_fused<64>(KSD_FUSED_ARGS); break;
@@ -789,7 +962,7 @@ extern "C" int ksd_ks3_vjp_finalize(const float *partials, int64_t n_row_blocks,
   if (!partials || !warp_scale_raw || !warp_shift_raw || !dcoeff || !dscale || !dshift)
     return fail(KSD_EINVAL, "ks3_vjp_finalize: null pointer");
   if (F == 0) return KSD_OK;
-  hipLaunchKernelGGL(ks3_vjp_finalize_kernel, dim3((unsigned)cdiv(F, 256)), dim3(256), 0,
+  hipLaunchKernelGGL(ks3_vjp_finalize_kernel, dim3((unsigned)cdiv(F, 256), 8), dim3(256), 0,
                      (hipStream_t)stream, partials, n_row_blocks, F, warp_scale_raw, warp_shift_raw,
                      sums, dcoeff, dscale, dshift);
   return check_launch("ks3_vjp_finalize");

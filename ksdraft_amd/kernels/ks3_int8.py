@@ -101,10 +101,11 @@ def spine_int8(coords16: torch.Tensor, spine_codes: torch.Tensor, spine_scale: t
     h = torch.empty((M, Fn), dtype=torch.float32, device=dev) if want_h else None
     hq = torch.empty((M, Fn), dtype=torch.int8, device=dev) if want_codes else None
     hs = (torch.empty((M, -(-Fn // group)), dtype=FP16, device=dev) if want_codes else None)
+    table = torch.empty((max(Fn, 1), 256), dtype=FP16, device=dev)   # per-chart increments
     _lib.call("ksd_ks3_spine_fwd", coords16.data_ptr(), M, Fn, sc.data_ptr(),
               _c(spine_scale.reshape(Fn)).data_ptr(), _c(warp_scale16.reshape(Fn)).data_ptr(),
               _c(warp_shift16.reshape(Fn)).data_ptr(), _c(tanh_lut).data_ptr(), group,
-              _lib.ptr(h), _lib.ptr(hq), _lib.ptr(hs), _lib.stream_ptr(dev))
+              _lib.ptr(h), _lib.ptr(hq), _lib.ptr(hs), table.data_ptr(), _lib.stream_ptr(dev))
     return h, hq, hs
 
 
@@ -120,10 +121,11 @@ def spine_fused_int8(acc: torch.Tensor, spine_codes: torch.Tensor, spine_scale: 
     acc = _c(acc)
     hq = torch.empty((M, Fn), dtype=torch.int8, device=dev)
     hs = torch.empty((M, -(-Fn // group)), dtype=FP16, device=dev)
+    table = torch.empty((max(Fn, 1), 256), dtype=torch.float32, device=dev)
     _lib.call("ksd_ks3_spine_fused", acc.data_ptr(), M, Fn, _c(spine_codes.reshape(Fn, 6)).data_ptr(),
               _c(spine_scale.reshape(Fn)).data_ptr(), _c(warp_scale16.reshape(Fn)).data_ptr(),
               _c(warp_shift16.reshape(Fn)).data_ptr(), _c(tanh_lut).data_ptr(), group,
-              hq.data_ptr(), hs.data_ptr(), _lib.stream_ptr(dev))
+              hq.data_ptr(), hs.data_ptr(), table.data_ptr(), _lib.stream_ptr(dev))
     return hq, hs
 
 

@@ -35,6 +35,8 @@ def lib() -> ctypes.CDLL:
             build()
         _lib = ctypes.CDLL(LIB)
         P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        _lib.ksd_check_div127.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
+        _lib.ksd_check_div127.restype = ctypes.c_uint64
         _lib.ksd_half_to_float.argtypes = [ctypes.c_uint16]
         _lib.ksd_half_to_float.restype = ctypes.c_float
         _lib.ksd_oracle_partials.argtypes = [P, P, I64, I64, I64, I, P]

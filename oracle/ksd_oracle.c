@@ -153,3 +153,24 @@ void ksd_oracle_rosa_credits(const uint8_t *q, const uint8_t *k, const uint8_t *
     free(pert);
   }
 }
+
+/* Checker of a device-code identity (test infrastructure): the number of fp32 bit patterns
+ * u in [lo, hi) for which the reciprocal division by 127 of the library's group scale,
+ *     q0 = x * RN(1/127),  q1 = fma(fma(-q0, 127, x), RN(1/127), q0)   (q0 if q1 is not finite)
+ * differs from the IEEE quotient x / 127. */
+uint64_t ksd_check_div127(uint32_t lo, uint32_t hi) {
+  const float r = 1.0f / 127.0f;
+  uint64_t bad = 0;
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+  for (int64_t i = (int64_t)lo; i < (int64_t)hi; ++i) {
+    const uint32_t u = (uint32_t)i;
+    float x;
+    memcpy(&x, &u, 4);
+    const float q0 = x * r;
+    float q1 = fmaf(fmaf(-q0, 127.0f, x), r, q0);
+    if (!isfinite(q1)) q1 = q0;
+    const float ref = x / 127.0f;
+    if (!(q1 == ref || (isnan(q1) && isnan(ref)))) ++bad;
+  }
+  return bad;
+}

@@ -67,11 +67,17 @@ def test_ks3_validation_paths_without_gpu():
     assert lib.ksd_ks3_vjp_row_blocks(0, ctypes.byref(nrb)) == 0 and nrb.value == 0
     # bad group; null inputs; partials sized for the wrong block count
     assert lib.ksd_ks3_spine_fwd(None, 4, 4, None, None, None, None, None, 48,
-                                 None, None, None, None) == 1
+                                 None, None, None, None, None) == 1
     assert lib.ksd_ks3_spine_fwd(None, 4, 4, None, None, None, None, None, 128,
-                                 None, None, None, None) == 1
+                                 None, None, None, None, None) == 1
     assert lib.ksd_ks3_spine_fused(None, 4, 4, None, None, None, None, None, 128,
-                                   None, None, None) == 1
+                                   None, None, None, None) == 1
+    # a table workspace that is missing or misaligned is rejected before any launch
+    q = ctypes.c_void_p(24)
+    assert lib.ksd_ks3_spine_fwd(q, 4, 4, q, q, q, q, ctypes.c_void_p(16), 128,
+                                 None, q, q, ctypes.c_void_p(8), None) == 1
+    lib.ksd_last_error(buf := ctypes.create_string_buffer(256), 256)
+    assert b"table" in buf.value
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     assert lib.ksd_ks3_vjp(p, p, 300, 8, p, p, p, p, 128, None, None, None, None, None,
                            p, 2, None) == 1
