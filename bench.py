@@ -196,7 +196,7 @@ def ks3_kernel_times(dev, reps):
                             4 * MF + MF + 2 * MF // G),
         "ks3_vjp": (lambda: K.ks3_vjp(value16, coords16, sq, ss, sc16, sh16, raw_scale,
                                       raw_shift, G),
-                    2 * MF + 2 * MF + MF + MF + 2 * 2 * MF // G + 2 * 8 * Fc * 4 * (Mk // 128)),
+                    2 * MF + 2 * MF + MF + MF + 2 * 2 * MF // G + 2 * 8 * Fc * 4 * (Mk // 512)),
     }
     res = {}
     for name, (fn, nbytes) in stages.items():

@@ -151,7 +151,7 @@ int ksd_ks3_spine_fused(const float *acc, int64_t M, int64_t F, const int8_t *sp
 
 /*
  * Number of row blocks (the first dim of the partials workspace) ksd_ks3_vjp uses for M
- * rows: ceil(M / 128). Fixes the order of the column reductions.
+ * rows: ceil(M / 512). Fixes the order of the column reductions.
  */
 int ksd_ks3_vjp_row_blocks(int64_t M, int64_t *n_row_blocks);
 

@@ -546,6 +546,67 @@ __device__ __forceinline__ h2 vjp_pair(h2 v, h2 x, const VjpCols &c, const uint1
   return v + dmean;
 }
 
+// vjp_pair over N rows in phases: the N first tanh lookups, then the N warp lookups, then
+// the arithmetic of each row, so the LDS reads of different rows overlap. Same op-by-op
+// fp16 arithmetic as vjp_pair.
+template <int N>
+__device__ __forceinline__ void vjp_rows(const h2 *v, const h2 *x, const VjpCols &c,
+                                         const uint16_t *tab, float (*acc)[2], h2 *dc) {
+  const h2 one = bc((_Float16)1.0f);
+  h2 t[N], tps[N], z[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) t[i] = tanh2(x[i] * bc((_Float16)0.25f), tab);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    t[i] = bc((_Float16)4.0f) * t[i];
+    tps[i] = t[i] + c.sh;
+    z[i] = tanh2(c.sc * tps[i], tab);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const h2 ti = t[i], zi = z[i];
+    h2 spine = c.cubic * ti + c.quad;
+    spine = spine * ti + c.c2;
+    spine = spine * ti + c.c0;
+    h2 warped = c.c5x4 * zi + c.c4x2;
+    warped = warped * zi - c.c5x3;
+    warped = warped * zi - c.c4;
+    h2 pre = x[i] + spine;
+    pre = pre + warped;
+    pre = pre < bc((_Float16)0.0f) ? bc((_Float16)0.0f) : pre;  // torch.relu: keeps -0 and NaN
+    const h2 dpre = (v[i] * bc((_Float16)2.0f)) * pre;
+    h2 dpoly = c.cubic3 * ti + c.quad2;
+    dpoly = dpoly * ti + c.c2;
+    h2 dwarp = c.c5x12 * zi + c.c4x4;
+    dwarp = dwarp * zi - c.c5x3;
+    const h2 z2 = zi * zi;
+    const h2 dz = dwarp * (one - z2);
+    const h2 t2 = ti * ti;
+    const h2 dmean = (dpre * (dpoly + dz * c.sc)) * (one - t2 * bc((_Float16)0.0625f));
+    const h2 t3 = t2 * ti;
+    const h2 z3 = z2 * zi;
+    const h2 t3x2 = bc((_Float16)2.0f) * t3;
+    const h2 t2x3 = bc((_Float16)3.0f) * t2;
+    const h2 dpdz = dpre * dz;
+    const h2 terms[8] = {
+        dpre * ((t3x2 - t2x3) + one),
+        dpre * (t2x3 - t3x2),
+        dpre * ((t3 - bc((_Float16)2.0f) * t2) + ti),
+        dpre * (t3 - t2),
+        dpre * (bc((_Float16)2.0f) * z2 - one),
+        dpre * (bc((_Float16)4.0f) * z3 - bc((_Float16)3.0f) * zi),
+        dpdz * tps[i],
+        dpdz * c.sc,
+    };
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      acc[k][0] = add_lo(acc[k][0], terms[k]);
+      acc[k][1] = add_hi(acc[k][1], terms[k]);
+    }
+    dc[i] = v[i] + dmean;
+  }
+}
+
 __device__ __forceinline__ h2 habs2(h2 a) {
   return __builtin_bit_cast(h2, __builtin_bit_cast(uint32_t, a) & 0x7fff7fffu);
 }
@@ -567,10 +628,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(T *base, int64_t row
   return rsrc(base + row0 * row_elems, rows * row_elems * (int64_t)sizeof(T));
 }
 
-// Block: 256 threads (4 waves) on the 128 x 128 tile (column tile blockIdx.x, row tile
-// blockIdx.y). Lane l owns columns 2l and 2l+1 of the 32 rows wave*32 + i; a register
-// holds one row at both columns. VEC: F is even, so a lane's two columns are both valid
-// or both past F.
+// Max of packed u16 pairs (fp16 magnitudes: the NaN-propagating order) over aligned groups
+// of L lanes (2..64): DPP within 16-lane rows, ds_swizzle across a half-wave, and the two
+// half-waves' lane 0 / lane 32 values for the whole wave (then wave-uniform).
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
+                                                                __builtin_bit_cast(u16x2, b)));
+}
+template <int L>
+__device__ __forceinline__ uint32_t group_max_pk16(uint32_t v) {
+  if constexpr (L >= 2) v = pk_max_u16(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  if constexpr (L >= 4) v = pk_max_u16(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  if constexpr (L >= 8) v = pk_max_u16(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+  if constexpr (L >= 16) v = pk_max_u16(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+  if constexpr (L >= 32) v = pk_max_u16(v, (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401f));
+  if constexpr (L >= 64)
+    v = pk_max_u16((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 32));
+  return v;
+}
+
+// Row tiles (128 rows) per VJP block: the tanh table is staged once per block and the
+// eight column sums are reduced once per block (one partial row per kVjpRowsPerBlock rows).
+constexpr int kVjpTilesPerBlock = 4;
+constexpr int kVjpRowsPerBlock = kVjpTile * kVjpTilesPerBlock;
+
+// Block: 256 threads (4 waves) on 128 columns (blockIdx.x) and kVjpTilesPerBlock row tiles
+// of 128 rows (blockIdx.y). In a tile, lane l owns columns 2l and 2l+1 of the 32 rows
+// wave*32 + i; a register holds one row at both columns. VEC: F is even, so a lane's two
+// columns are both valid or both past F.
 template <int G, bool VEC>
 __global__ void __launch_bounds__(256) ks3_vjp_kernel(
     const uint16_t *__restrict__ value, const uint16_t *__restrict__ coords, int64_t M, int64_t F,
@@ -578,12 +663,11 @@ __global__ void __launch_bounds__(256) ks3_vjp_kernel(
     const uint16_t *__restrict__ sc16, const uint16_t *__restrict__ sh16,
     uint16_t *__restrict__ dc_out, int8_t *__restrict__ dcq, uint16_t *__restrict__ dcs,
     int8_t *__restrict__ dctq, uint16_t *__restrict__ dcts, float *__restrict__ partials) {
-  __shared__ uint16_t tab[KSD_TANH16_LIMIT + 2];
+  __shared__ __attribute__((aligned(16))) uint32_t tabw[KSD_TANH16_WORDS];
   __shared__ uint32_t colmax[4][kVjpTile / 2];  // packed fp16 column maxima per wave
-  for (int i = threadIdx.x; i < (KSD_TANH16_LIMIT + 2) / 2; i += 256)
-    ((uint32_t *)tab)[i] = i * 2 + 1 <= KSD_TANH16_LIMIT
-                               ? (uint32_t)kTanh16[2 * i] | ((uint32_t)kTanh16[2 * i + 1] << 16)
-                               : (uint32_t)kTanh16[2 * i];
+  const uint16_t *tab = (const uint16_t *)tabw;
+  for (int i = threadIdx.x; i < KSD_TANH16_WORDS / 4; i += 256)
+    ((uint4 *)tabw)[i] = ((const uint4 *)kTanh16)[i];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t col0 = (int64_t)blockIdx.x * kVjpTile + lane * 2;
@@ -602,15 +686,16 @@ __global__ void __launch_bounds__(256) ks3_vjp_kernel(
   int8_t *dctq_b = dctq ? dctq + (int64_t)blockIdx.x * kVjpTile * M : nullptr;
   uint16_t *dcts_b = dcts ? dcts + (int64_t)blockIdx.x * kVjpTile * ngM : nullptr;
   const int64_t cols_here = min((int64_t)kVjpTile, F - (int64_t)blockIdx.x * kVjpTile);
+  const uint32_t rstride2 = (uint32_t)(F * 2);
   __syncthreads();
 
-  {
-    const int64_t tr0 = (int64_t)blockIdx.y * kVjpTile;  // first row of the tile
+  for (int tt = 0; tt < kVjpTilesPerBlock; ++tt) {
+    const int64_t tr0 = (int64_t)blockIdx.y * kVjpRowsPerBlock + (int64_t)tt * kVjpTile;
+    if (tr0 >= M) break;                                 // block-uniform
     const int r0 = wave * 32;                            // first tile row of this wave
     const int64_t grow0 = tr0 + r0;                      // global row of this wave's first row
     const auto rv = rows_rsrc(value, grow0, 32, M, F);
     const auto rx = rows_rsrc(coords, grow0, 32, M, F);
-    const uint32_t rstride2 = (uint32_t)(F * 2);
 
     h2 dc[32];
 #pragma unroll
@@ -631,9 +716,9 @@ __global__ void __launch_bounds__(256) ks3_vjp_kernel(
         }
       }
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
+      for (int q = 0; q < 16; q += 4) {
         __builtin_amdgcn_sched_barrier(0);
-        dc[half * 16 + i] = vjp_pair(va[i], xa[i], cc, tab, acc);
+        vjp_rows<4>(va + q, xa + q, cc, tab, acc, dc + half * 16 + q);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -657,7 +742,8 @@ __global__ void __launch_bounds__(256) ks3_vjp_kernel(
     }
 
     // quantize_last_dim(dc, G): groups of G columns per row (ks3_int8.py:410); a group is
-    // G/2 lanes. Two rows are reduced per packed register.
+    // G/2 lanes. Two rows are reduced per packed register; codes by reciprocal multiply
+    // (codes_rcp_packed's bound), the division redoing two rows with a near-tie quotient.
     if (dcq) {
       const bool writes_scale = (lane & (G / 2 - 1)) == 0 && ok0;
       const uint32_t soff = writes_scale ? (uint32_t)(col0 / G * 2) : kOob;
@@ -666,25 +752,42 @@ __global__ void __launch_bounds__(256) ks3_vjp_kernel(
 #pragma unroll
       for (int i = 0; i < 32; i += 2) {
         const h2 a0 = habs2(dc[i]), a1 = habs2(dc[i + 1]);
-        h2 m = hmax2((h2){a0[0], a1[0]}, (h2){a0[1], a1[1]});
+        const h2 m = __builtin_bit_cast(
+            h2, group_max_pk16<G / 2>(__builtin_bit_cast(uint32_t, hmax2((h2){a0[0], a1[0]}, (h2){a0[1], a1[1]}))));
+        float s[2], f[2][2];
+        uint32_t mg[2][2];
+        float near = 1.0f;
 #pragma unroll
-        for (int o = 1; o < G / 2; o <<= 1) {
-          uint32_t u = __shfl_xor(__builtin_bit_cast(uint32_t, m), o, 64);
-          m = hmax2(m, __builtin_bit_cast(h2, u));
+        for (int e = 0; e < 2; ++e) {
+          s[e] = group_scale((float)m[e]);
+          const float r = __builtin_amdgcn_rcpf(s[e]);
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            f[e][c] = (float)dc[i + e][c];
+            const float q = __builtin_amdgcn_fmed3f(f[e][c] * r, -127.0f, 127.0f);
+            const float mq = q + 12582912.0f;
+            near = fminf(near, fabsf(fabsf(q - (mq - 12582912.0f)) - 0.5f));
+            mg[e][c] = __builtin_bit_cast(uint32_t, mq);
+            if (s[e] != s[e]) mg[e][c] = 0;  // NaN group: zero codes
+          }
+        }
+        if (near < 0x1p-14f) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) mg[e][c] = (uint8_t)code_of(f[e][c] / s[e]);
         }
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const uint32_t ro = (uint32_t)((i + e) * F);
-          const float s = group_scale((float)m[e]);
-          const uint32_t q0 = (uint8_t)code_of((float)dc[i + e][0] / s);
-          const uint32_t q1 = (uint8_t)code_of((float)dc[i + e][1] / s);
+          const uint32_t q0 = mg[e][0] & 0xffu, q1 = mg[e][1] & 0xffu;
           if (VEC) {
             __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(q0 | (q1 << 8)), rq, voff1 + ro, 0, 0);
           } else {
             __builtin_amdgcn_raw_buffer_store_b8((uint8_t)q0, rq, voff1 + ro, 0, 0);
             __builtin_amdgcn_raw_buffer_store_b8((uint8_t)q1, rq, voff1b + ro, 0, 0);
           }
-          __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsc, soff + (uint32_t)((i + e) * ngF * 2), 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s[e]), rsc, soff + (uint32_t)((i + e) * ngF * 2), 0, 0);
         }
       }
     }
@@ -711,14 +814,11 @@ __global__ void __launch_bounds__(256) ks3_vjp_kernel(
         const float s = group_scale((float)m[e]);
         const bool colok = e ? ok1 : ok0;
         const int64_t lc = lane * 2 + e;  // column within the block
+        float col[32];
+#pragma unroll
+        for (int r = 0; r < 32; ++r) col[r] = (float)dc[r][e];
         uint32_t w[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          w[q] = 0;
-#pragma unroll
-          for (int b = 0; b < 4; ++b)
-            w[q] |= (uint32_t)(uint8_t)code_of((float)dc[q * 4 + b][e] / s) << (8 * b);
-        }
+        codes_rcp_packed<32>(col, s, w);
         if (grow0 + 32 <= M && (M & 15) == 0) {
           const uint32_t off = colok ? (uint32_t)(lc * M + grow0) : kOob;
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, make_uint4(w[0], w[1], w[2], w[3])),
@@ -740,7 +840,7 @@ __global__ void __launch_bounds__(256) ks3_vjp_kernel(
 
   // column partial sums of this block: the 4 waves hold the same columns
   __syncthreads();  // the table region is reused below
-  float *red = (float *)tab;  // [4 waves][8 terms][128 cols] = 16 KiB
+  float *red = (float *)tabw;  // [4 waves][8 terms][128 cols] = 16 KiB
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     red[(wave * 8 + k) * kVjpTile + lane * 2] = acc[k][0];
@@ -751,11 +851,11 @@ __global__ void __launch_bounds__(256) ks3_vjp_kernel(
     const int k = i / kVjpTile, c = i % kVjpTile;
     const int64_t col = (int64_t)blockIdx.x * kVjpTile + c;
     if (col >= F) continue;
-    float s = red[(0 * 8 + k) * kVjpTile + c];
-    s += red[(1 * 8 + k) * kVjpTile + c];
-    s += red[(2 * 8 + k) * kVjpTile + c];
-    s += red[(3 * 8 + k) * kVjpTile + c];
-    partials[((int64_t)blockIdx.y * 8 + k) * F + col] = s;
+    float sum = red[(0 * 8 + k) * kVjpTile + c];
+    sum += red[(1 * 8 + k) * kVjpTile + c];
+    sum += red[(2 * 8 + k) * kVjpTile + c];
+    sum += red[(3 * 8 + k) * kVjpTile + c];
+    partials[((int64_t)blockIdx.y * 8 + k) * F + col] = sum;
   }
 }
 
@@ -830,7 +930,7 @@ static void launch_fused(bool vec, dim3 grid, hipStream_t st, const float *acc, 
                        M, F, table, hq, hs, ng);
 }
 
-static int64_t vjp_row_blocks(int64_t M) { return cdiv(M, kVjpTile); }
+static int64_t vjp_row_blocks(int64_t M) { return cdiv(M, kVjpRowsPerBlock); }
 
 }  // namespace ksd
 

@@ -20,6 +20,8 @@ builds, model/block.py:32) in the 'int8' nonlinear mode, the reference default; 
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 from torch import nn
 import torch.nn.functional as F
@@ -145,7 +147,9 @@ def ks3_vjp(value16: torch.Tensor, coords16: torch.Tensor, spine_codes: torch.Te
     M, Fn = coords16.shape
     if value16.shape != (M, Fn):
         raise ValueError(f"value shape {tuple(value16.shape)} != coords shape {(M, Fn)}")
-    nrb = max(-(-M // 128), 0)
+    nrb_c = ctypes.c_int64(0)
+    _lib.call("ksd_ks3_vjp_row_blocks", M, ctypes.byref(nrb_c))
+    nrb = nrb_c.value
     f16 = dict(dtype=FP16, device=dev)
     out = {
         "dc": torch.empty((M, Fn), **f16) if want_dc else None,

@@ -63,7 +63,8 @@ def test_validation_paths_without_gpu():
 def test_ks3_validation_paths_without_gpu():
     lib = _lib.load()
     nrb = ctypes.c_int64(-1)
-    assert lib.ksd_ks3_vjp_row_blocks(300, ctypes.byref(nrb)) == 0 and nrb.value == 3
+    assert lib.ksd_ks3_vjp_row_blocks(300, ctypes.byref(nrb)) == 0 and nrb.value == 1
+    assert lib.ksd_ks3_vjp_row_blocks(1025, ctypes.byref(nrb)) == 0 and nrb.value == 3
     assert lib.ksd_ks3_vjp_row_blocks(0, ctypes.byref(nrb)) == 0 and nrb.value == 0
     # bad group; null inputs; partials sized for the wrong block count
     assert lib.ksd_ks3_spine_fwd(None, 4, 4, None, None, None, None, None, 48,
