@@ -56,6 +56,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-ks3", action="store_true", help="skip the KS3 kernel report")
     p.add_argument("--no-rosa", action="store_true", help="skip the Rosa kernel report")
+    p.add_argument("--no-c3", action="store_true", help="skip the config-3 LM-head report")
     p.add_argument("--pmc-probe", action="store_true",
                    help="for rocprofv3 --pmc runs: a 256 MiB device copy (counter "
                         "calibration), then 3 launches of each GEMM of the step; no timing")
@@ -213,6 +214,64 @@ def ks3_kernel_times(dev, reps):
             ent["GBps"] = round(nbytes / (us * 1e-6) / 1e9, 1)
             ent["hbm_frac"] = round(nbytes / (us * 1e-6) / PEAK_HBM, 3)
         res[name] = ent
+    return res
+
+
+def lmhead_c3_times(dev, reps):
+    """the LM-head / vocab projection as one W8A8 GS128 linear layer,
+    forward + dX + dW, M = 4096 tokens, K = 1536, N = 150144 (int8 W 230.6 MB, fp32 Y
+    2.46 GB). X ~N(0,1), W ~N(0,0.02) drawn by a seeded generator on the device (1 GB of
+    fp32 master weights), dY = softmax(Y) - onehot(t) with t uniform in [0, N). Each kernel
+    of the step is timed as a graph of back-to-back launches; GEMMs are reported in TOPS
+    against 2*M*N*K = 1.889e12 ops, quantizations in GB/s against their algorithmic bytes."""
+    M3, K3, N3 = 4096, 1536, 150144
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(M3, K3, device=dev, generator=g)
+    w = torch.randn(N3, K3, device=dev, generator=g) * 0.02
+    wq, ws = quantize_last_dim(w)
+    xq, xs = quantize_last_dim(x)
+    y = w8a8_gemm_out(xq, xs, wq, ws)
+    t = torch.randint(0, N3, (M3,), device=dev, generator=g)
+    dy = torch.softmax(y, dim=1)
+    dy[torch.arange(M3, device=dev), t] -= 1.0
+    del y
+    gq, gs = quantize_last_dim(dy)
+    wtq, wts = requant_transpose(wq, ws)
+    gtq, gts = quantize_transpose(dy)
+    xtq, xts = requant_transpose(xq, xs)
+    ops = 2 * M3 * N3 * K3
+    stages = {
+        "quantize_W": (lambda: quantize_last_dim(w), 4 * N3 * K3 + N3 * K3 + 2 * N3 * K3 // 128),
+        "quantize_X": (lambda: quantize_last_dim(x), 4 * M3 * K3 + M3 * K3 + 2 * M3 * K3 // 128),
+        "gemm_fwd": (lambda: w8a8_gemm_out(xq, xs, wq, ws), None),
+        "quantize_dY": (lambda: quantize_last_dim(dy), 4 * M3 * N3 + M3 * N3 + 2 * M3 * N3 // 128),
+        "requant_WT": (lambda: requant_transpose(wq, ws), 2 * (N3 * K3 + 2 * N3 * K3 // 128)),
+        "gemm_dX": (lambda: w8a8_gemm_out(gq, gs, wtq, wts), None),
+        "quantize_T_dY": (lambda: quantize_transpose(dy), 4 * M3 * N3 + M3 * N3 + 2 * M3 * N3 // 128),
+        "requant_XT": (lambda: requant_transpose(xq, xs), 2 * (M3 * K3 + 2 * M3 * K3 // 128)),
+        "gemm_dW": (lambda: w8a8_gemm_out(gtq, gts, xtq, xts), None),
+    }
+    res = {}
+    for name, (fn, nbytes) in stages.items():
+        def rep(fn=fn):
+            for _ in range(reps):
+                fn()
+        _, _, ms = time_graph(rep, 1, warm=1)
+        us = ms * 1e3 / reps
+        ent = {"us": round(us, 2)}
+        if nbytes is None:
+            ent["tops"] = round(ops / (us * 1e-6) / 1e12, 1)
+        else:
+            ent["GBps"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+            ent["hbm_frac"] = round(nbytes / (us * 1e-6) / PEAK_HBM, 3)
+        res[name] = ent
+        torch.cuda.empty_cache()
+    gemm_us = sum(res[k]["us"] for k in ("gemm_fwd", "gemm_dX", "gemm_dW"))
+    step_us = sum(v["us"] for v in res.values())
+    res["three_gemms_ms"] = round(gemm_us / 1e3, 3)
+    res["three_gemms_tops"] = round(3 * ops / (gemm_us * 1e-6) / 1e12, 1)
+    res["step_ms_sum_of_kernels"] = round(step_us / 1e3, 3)
+    res["step_tops_incl_quantize"] = round(3 * ops / (step_us * 1e-6) / 1e12, 1)
     return res
 
 
@@ -414,6 +473,7 @@ def main():
         "kernels": kern,
         "ks3_c4_kernels": None if args.no_ks3 else ks3_kernel_times(dev, args.kernel_reps),
         "rosa_c4_kernels": None if args.no_rosa else rosa_kernel_times(dev, args.kernel_reps),
+        "lmhead_c3": None if args.no_c3 else lmhead_c3_times(dev, 3),
         "roofline": {
             "kernel": "ksd::g128::gemm_g128_kernel<f32> (fwd, dX, dW launches averaged)",
             "bound": "mfma",
