@@ -6,10 +6,11 @@ forward + both backward GEMMs, M = 8192 tokens (batch 4 x seq 2048), K = N = 153
 X ~ N(0,1), W ~ N(0,0.02) fp32 master, dY ~ N(0,1e-2), all fp32, seeded (torch CPU
 generator, seed 0) and resident in HBM before timing.
 
-One step = exactly what the training path runs for this layer:
-    quantize W -> quantize X -> GEMM Y = X W^T (fp32 out)
-    quantize dY (along N) -> requant W^T -> GEMM dX = dY W
-    quantize dY^T (along M) -> requant X^T -> GEMM dW = dY^T X   (fp32)
+One step = exactly what the training path (W8A8LinearFunction) runs for this layer:
+    quantize W -> quantize X, and X^T requantized along M, in one pass (quantize_dual)
+      -> GEMM Y = X W^T (fp32 out)
+    quantize dY along N and along M in one pass (quantize_dual) -> requant W^T
+      -> GEMM dX = dY W -> GEMM dW = dY^T X   (fp32)
 value = algorithmic int8 ops of the three GEMMs (3 * 2*M*N*K) / step time, in TOPS.
 The step runs as a captured HIP graph (no host launch overhead; replays are checked
 bit-equal to the eager step); the eager step time is reported beside it.
@@ -34,9 +35,10 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from ksdraft_amd.kernels.linear import w8a8_linear_backward, w8a8_linear_forward  # noqa: E402
-from ksdraft_amd.kernels.quant import (quantize_last_dim, quantize_transpose,  # noqa: E402
-                                       requant_transpose)
+from ksdraft_amd.kernels.linear import (w8a8_linear_backward,  # noqa: E402
+                                        w8a8_linear_forward_train)
+from ksdraft_amd.kernels.quant import (quantize_dual, quantize_last_dim,  # noqa: E402
+                                       quantize_transpose, requant_transpose)
 from ksdraft_amd.kernels.gemm import w8a8_gemm_out  # noqa: E402
 
 METRIC = ("W8A8 GS128 GEMM TOPS fwd+bwd @d=1536 (% int8 peak); draft train-step tok/s")
@@ -97,8 +99,8 @@ def make_inputs(dev):
 
 def step(x, w, dy):
     wq, ws = quantize_last_dim(w)
-    y, xq, xs = w8a8_linear_forward(x, wq, ws, None, out_dtype=torch.float32)
-    dx, dw = w8a8_linear_backward(dy, xq, xs, wq, ws, dx_dtype=torch.float32)
+    y, xtq, xts = w8a8_linear_forward_train(x, wq, ws, None, out_dtype=torch.float32)
+    dx, dw = w8a8_linear_backward(dy, None, None, wq, ws, dx_dtype=torch.float32, xt=(xtq, xts))
     return y, dx, dw
 
 
@@ -139,14 +141,17 @@ def kernel_times(x, w, dy, reps):
     xtq, xts = requant_transpose(xq, xs)
     stages = {
         "quantize_W": (lambda: quantize_last_dim(w), 4 * N * K + N * K + 2 * N * K // 128),
-        "quantize_X": (lambda: quantize_last_dim(x), 4 * M * K + M * K + 2 * M * K // 128),
+        "quantize_X_dual": (lambda: quantize_dual(x, t_from_codes=True), 4 * M * K + 2 * (M * K + 2 * M * K // 128)),
         "gemm_fwd": (lambda: w8a8_gemm_out(xq, xs, wq, ws), None),
-        "quantize_dY": (lambda: quantize_last_dim(dy), 4 * M * N + M * N + 2 * M * N // 128),
+        "quantize_dY_dual": (lambda: quantize_dual(dy), 4 * M * N + 2 * (M * N + 2 * M * N // 128)),
         "requant_WT": (lambda: requant_transpose(wq, ws), 2 * (N * K + 2 * N * K // 128)),
         "gemm_dX": (lambda: w8a8_gemm_out(gq, gs, wtq, wts), None),
-        "quantize_T_dY": (lambda: quantize_transpose(dy), 4 * M * N + M * N + 2 * M * N // 128),
-        "requant_XT": (lambda: requant_transpose(xq, xs), 2 * (M * K + 2 * M * K // 128)),
         "gemm_dW": (lambda: w8a8_gemm_out(gtq, gts, xtq, xts), None),
+        # the single-layout kernels the dual ones replace in the step (for comparison)
+        "quantize_X": (lambda: quantize_last_dim(x), 4 * M * K + M * K + 2 * M * K // 128),
+        "requant_XT": (lambda: requant_transpose(xq, xs), 2 * (M * K + 2 * M * K // 128)),
+        "quantize_dY": (lambda: quantize_last_dim(dy), 4 * M * N + M * N + 2 * M * N // 128),
+        "quantize_T_dY": (lambda: quantize_transpose(dy), 4 * M * N + M * N + 2 * M * N // 128),
     }
     res = {}
     for name, (fn, nbytes) in stages.items():
@@ -242,13 +247,11 @@ def lmhead_c3_times(dev, reps):
     ops = 2 * M3 * N3 * K3
     stages = {
         "quantize_W": (lambda: quantize_last_dim(w), 4 * N3 * K3 + N3 * K3 + 2 * N3 * K3 // 128),
-        "quantize_X": (lambda: quantize_last_dim(x), 4 * M3 * K3 + M3 * K3 + 2 * M3 * K3 // 128),
+        "quantize_X_dual": (lambda: quantize_dual(x, t_from_codes=True), 4 * M3 * K3 + 2 * (M3 * K3 + 2 * M3 * K3 // 128)),
         "gemm_fwd": (lambda: w8a8_gemm_out(xq, xs, wq, ws), None),
-        "quantize_dY": (lambda: quantize_last_dim(dy), 4 * M3 * N3 + M3 * N3 + 2 * M3 * N3 // 128),
+        "quantize_dY_dual": (lambda: quantize_dual(dy), 4 * M3 * N3 + 2 * (M3 * N3 + 2 * M3 * N3 // 128)),
         "requant_WT": (lambda: requant_transpose(wq, ws), 2 * (N3 * K3 + 2 * N3 * K3 // 128)),
         "gemm_dX": (lambda: w8a8_gemm_out(gq, gs, wtq, wts), None),
-        "quantize_T_dY": (lambda: quantize_transpose(dy), 4 * M3 * N3 + M3 * N3 + 2 * M3 * N3 // 128),
-        "requant_XT": (lambda: requant_transpose(xq, xs), 2 * (M3 * K3 + 2 * M3 * K3 // 128)),
         "gemm_dW": (lambda: w8a8_gemm_out(gtq, gts, xtq, xts), None),
     }
     res = {}

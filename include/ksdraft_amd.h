@@ -90,6 +90,22 @@ int ksd_requant_transpose(const int8_t *codes, const uint16_t *scales, int64_t R
                           uint16_t *out_scales, void *stream);
 
 /*
+ * Both layouts of one tensor in one pass: the row codes quantize_last_dim(x, group) and
+ * the column codes quantize_last_dim(x.t(), group) (t_from_codes = 0: the dY and dY^T
+ * operands of the linear backward, reference ksdraft/kernels/ks3_int8.py:410, 418), or
+ * the column codes of the row-quantized values, quantize_last_dim(dequantize_last_dim(
+ * codes, scales).t(), group) (t_from_codes = 1: the X and X^T operands, :417-420).
+ * No reference counterpart as one call; the results equal those of ksd_quantize_lastdim
+ * followed by ksd_quantize_transpose or ksd_requant_transpose.
+ *   x       (R, C) of type x_dtype (KSD_F32, KSD_BF16, KSD_F16), dense
+ *   codes   (R, C) int8;  scales   (R, ceil(C/group)) fp16
+ *   codes_t (C, R) int8;  scales_t (C, ceil(R/group)) fp16
+ */
+int ksd_quantize_dual(const void *x, int x_dtype, int64_t R, int64_t C, int group,
+                      int t_from_codes, int8_t *codes, uint16_t *scales, int8_t *codes_t,
+                      uint16_t *scales_t, void *stream);
+
+/*
  * G1 / G2 — W8A8 GEMM, "NT" layout: Y = dequant(A) . dequant(W)^T with the ordered
  * per-group contract
  *     acc = 0;  for g in 0..K/group-1:  acc = fmaf(float(P_g), sa[m,g]*sw[n,g], acc)

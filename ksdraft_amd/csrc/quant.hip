@@ -250,6 +250,89 @@ __global__ __launch_bounds__(256) void quant_T_kernel(
   }
 }
 
+// ----------------------------------------------------------------------------------
+// Dual-layout quantization, G = 128: one pass over a 128 x 128 tile of x (R, C) emits the
+// row codes (quantize_last_dim(x), along C) and the column codes (along R) of either x
+// itself (quantize_last_dim(x.t())) or, T_FROM_CODES, the row-quantized values
+// dequantize(codes, scales) (the X^T recipe quant(dequant(quant(X))^T)). The rows are
+// quantized from registers (16 lanes per row, 8 elements each), the values then go to LDS
+// transposed in quant_T_kernel's conflict-free layout, and 4 lanes per column quantize the
+// columns. Requires C % 8 == 0 and 16-byte aligned rows; rows past R read as zeros and
+// are not stored.
+template <int DT, bool T_FROM_CODES>
+__global__ __launch_bounds__(512) void quant_dual_kernel(
+    const void *__restrict__ xv, int64_t R, int64_t C, int8_t *__restrict__ codes,
+    uint16_t *__restrict__ scales, int8_t *__restrict__ codes_t, uint16_t *__restrict__ scales_t) {
+  using T = typename Elem<DT>::T;
+  constexpr int G = 128, PITCH = 145;
+  __shared__ float tile[128 * PITCH];
+  auto lds_at = [](int c, int r) { return c * PITCH + r + (r >= 64 ? 16 : 0); };
+  const int tid = threadIdx.x;
+  const int64_t c0 = (int64_t)blockIdx.x * 128, r0 = (int64_t)blockIdx.y * 128;
+  const int64_t ngC = (C + G - 1) / G, ngR = (R + G - 1) / G;
+
+  // ---- rows: lane (rr, sub) takes rows r0 + 32 p + rr (p = 0..3), columns c0 + 8 sub .. + 8;
+  // the four rows' loads are issued before any arithmetic
+  const int rr = tid >> 4, sub = tid & 15;
+  const int64_t col = c0 + sub * 8;
+  const bool cok = col < C;
+  const T *xb = (const T *)xv + (cok ? col : 0);
+  Raw8<DT> raw[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) raw[p] = load_raw8<DT>(xb + min(r0 + 32 * p + rr, R - 1) * C);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int lr = 32 * p + rr;  // row within the tile
+    const int64_t row = r0 + lr;
+    const bool ok = cok && row < R;
+    float v[8];
+    cvt_raw8<DT>(raw[p], ok, v);
+    const uint32_t am = group_max_u32<16>(__builtin_bit_cast(uint32_t, abs_max<8>(v)));
+    const float s = group_scale(__builtin_bit_cast(float, am));
+    uint32_t w[2];
+    codes_rcp_packed<8>(v, s, w);
+    const int64_t rowc = row < R ? row : 0;
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 q;
+    q.x = w[0];
+    q.y = w[1];
+    __builtin_amdgcn_raw_buffer_store_b64(q, rsrc(codes + rowc * C, C), ok ? (uint32_t)col : kOob, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsrc(scales + rowc * ngC, 2 * ngC),
+                                          ok && sub == 0 ? (uint32_t)(col / G) * 2 : kOob, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float t = v[i];
+      if (T_FROM_CODES) t = (float)(int8_t)(w[i >> 2] >> (8 * (i & 3))) * s;  // dequantize (exact)
+      tile[lds_at(sub * 8 + i, lr)] = t;
+    }
+  }
+  __syncthreads();
+
+  // ---- columns: lane (c, part) takes column c, rows part * 32 .. + 32
+  constexpr int RPT = 32;
+  const int c = tid >> 2, part = tid & 3;
+  float colv[RPT];
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) colv[j] = tile[lds_at(c, part * RPT + j)];
+  const uint32_t am = group_max_u32<4>(__builtin_bit_cast(uint32_t, abs_max<RPT>(colv)));
+  const float s = group_scale(__builtin_bit_cast(float, am));
+  const int64_t gc = c0 + c;
+  if (gc >= C) return;
+  if (part == 0) scales_t[gc * ngR + blockIdx.y] = scale_bits(s);
+  uint32_t w[RPT / 4];
+  codes_rcp_packed<RPT>(colv, s, w);
+  int8_t *dst = codes_t + gc * R + r0 + part * RPT;
+  const int64_t rbase = r0 + part * RPT;
+  if (rbase + RPT <= R && (((uintptr_t)dst) & 15) == 0) {
+#pragma unroll
+    for (int j = 0; j < RPT / 4; j += 4) *(uint4 *)(dst + 4 * j) = make_uint4(w[j], w[j + 1], w[j + 2], w[j + 3]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < RPT; ++j)
+      if (rbase + j < R) dst[j] = (int8_t)(w[j / 4] >> (8 * (j % 4)));
+  }
+}
+
 template <int SRC>
 static int launch_quant_T(const void *x, const uint16_t *in_scales, int64_t nsc_in, int gin,
                           int64_t R, int64_t C, int group, int8_t *codes, uint16_t *scales,
@@ -363,6 +446,43 @@ extern "C" int ksd_requant_transpose(const int8_t *codes, const uint16_t *scales
   if (R == 0 || C == 0) return KSD_OK;
   return launch_quant_T<SRC_I8>(codes, scales, cdiv(C, group_in), group_in, R, C, group, out_codes,
                                 out_scales, (hipStream_t)stream);
+}
+
+extern "C" int ksd_quantize_dual(const void *x, int x_dtype, int64_t R, int64_t C, int group,
+                                 int t_from_codes, int8_t *codes, uint16_t *scales,
+                                 int8_t *codes_t, uint16_t *scales_t, void *stream) {
+  if (!valid_group(group)) return fail(KSD_EINVAL, "group must be 32, 64 or 128, got %d", group);
+  if (R < 0 || C < 0) return fail(KSD_EINVAL, "quantize_dual: negative shape");
+  if (x_dtype != KSD_F32 && x_dtype != KSD_BF16 && x_dtype != KSD_F16)
+    return fail(KSD_ETYPE, "quantize expects float32, bfloat16 or float16 input");
+  if (R == 0 || C == 0) return KSD_OK;
+  if (!x || !codes || !scales || !codes_t || !scales_t)
+    return fail(KSD_EINVAL, "quantize_dual: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  const int esz = x_dtype == KSD_F32 ? 4 : 2;
+  const bool fast = group == 128 && C % 8 == 0 && ((uintptr_t)x) % 16 == 0 && (C * esz) % 16 == 0 &&
+                    ((uintptr_t)codes) % 8 == 0 && cdiv(R, 128) <= 65535 && cdiv(C, 128) <= 0x7fffffff;
+  if (!fast) {
+    // the two single-layout kernels: row codes, then the transposed codes of x or of them
+    int rc = ksd_quantize_lastdim(x, x_dtype, R, C, C, group, codes, scales, nullptr, 0.0f, stream);
+    if (rc) return rc;
+    if (t_from_codes)
+      return launch_quant_T<SRC_I8>(codes, scales, cdiv(C, group), group, R, C, group, codes_t, scales_t, st);
+    return ksd_quantize_transpose(x, x_dtype, R, C, group, codes_t, scales_t, stream);
+  }
+  const dim3 grid((unsigned)cdiv(C, 128), (unsigned)cdiv(R, 128));
+#define KSD_DUAL(DT)                                                                                      \
+  if (t_from_codes)                                                                                       \
+    quant_dual_kernel<DT, true><<<grid, 512, 0, st>>>(x, R, C, codes, scales, codes_t, scales_t);         \
+  else                                                                                                    \
+    quant_dual_kernel<DT, false><<<grid, 512, 0, st>>>(x, R, C, codes, scales, codes_t, scales_t);
+  switch (x_dtype) {
+    case KSD_F32: KSD_DUAL(KSD_F32); break;
+    case KSD_BF16: KSD_DUAL(KSD_BF16); break;
+    default: KSD_DUAL(KSD_F16); break;
+  }
+#undef KSD_DUAL
+  return check_launch("quantize_dual");
 }
 
 extern "C" int ksd_abi_version(void) { return 2; }

@@ -22,7 +22,7 @@ import torch
 from torch import nn
 
 from .gemm import w8a8_gemm, w8a8_gemm_out
-from .quant import (GROUP_SIZE, dequantize_last_dim, quantize_last_dim,
+from .quant import (GROUP_SIZE, dequantize_last_dim, quantize_dual, quantize_last_dim,
                     quantize_last_dim_dithered, quantize_transpose, requant_transpose)
 
 
@@ -45,22 +45,45 @@ def w8a8_linear_forward(x2: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
     return y, xq, xs
 
 
-def w8a8_linear_backward(g: torch.Tensor, xq: torch.Tensor, xs: torch.Tensor,
+def w8a8_linear_forward_train(x2: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
+                              bias: torch.Tensor | None, group: int = GROUP_SIZE,
+                              out_dtype: torch.dtype | None = None):
+    """w8a8_linear_forward that also builds dW's activation operand in the same pass
+    over x: X^T requantized along the tokens from the row codes (the double-quant recipe
+    of ks3_int8.py:417-420, quantize_dual). The backward needs only that operand, not
+    the row codes. Returns (y, xtq (K, M), xts (K, ceil(M/group)))."""
+    xq, xs, xtq, xts = quantize_dual(x2, group, t_from_codes=True)
+    y = w8a8_gemm_out(xq, xs, wq, ws, group, bias=bias,
+                      out_dtype=_out_dtype(out_dtype or x2.dtype))
+    return y, xtq, xts
+
+
+def w8a8_linear_backward(g: torch.Tensor, xq: torch.Tensor | None, xs: torch.Tensor | None,
                          wq: torch.Tensor, ws: torch.Tensor, group: int = GROUP_SIZE,
                          dx_dtype: torch.dtype = torch.float32, need_dx: bool = True,
-                         need_dw: bool = True):
+                         need_dw: bool = True, xt: tuple | None = None):
     """INT8 backward GEMMs of the linear layer (recipe of ks3_int8.py:403-424).
 
-    g (M, N) upstream gradient; xq/xs the forward's activation codes; wq/ws the weight
-    codes. Returns (dx (M, K) in dx_dtype or None, dw (N, K) fp32 or None)."""
+    g (M, N) upstream gradient; xq/xs the forward's activation codes, or ``xt`` =
+    (xtq, xts) the already requantized X^T operand; wq/ws the weight codes. When both
+    gradients are needed, dY is quantized in both layouts in one pass (quantize_dual).
+    Returns (dx (M, K) in dx_dtype or None, dw (N, K) fp32 or None)."""
     dx = dw = None
+    gq = gs = gtq = gts = None
+    if need_dx and need_dw:
+        gq, gs, gtq, gts = quantize_dual(g, group)              # along N and along M
     if need_dx:
-        gq, gs = quantize_last_dim(g, group)                    # along N (per token)
+        if gq is None:
+            gq, gs = quantize_last_dim(g, group)                # along N (per token)
         wtq, wts = requant_transpose(wq, ws, group, group)      # W^T (K, N) along N
         dx = w8a8_gemm_out(gq, gs, wtq, wts, group, out_dtype=_out_dtype(dx_dtype))
     if need_dw:
-        gtq, gts = quantize_transpose(g, group)                 # dY^T (N, M) along M
-        xtq, xts = requant_transpose(xq, xs, group, group)      # X^T (K, M) along M
+        if gtq is None:
+            gtq, gts = quantize_transpose(g, group)             # dY^T (N, M) along M
+        if xt is not None:
+            xtq, xts = xt
+        else:
+            xtq, xts = requant_transpose(xq, xs, group, group)  # X^T (K, M) along M
         dw = w8a8_gemm(gtq, gts, xtq, xts, group)                # (N, K) fp32
     return dx, dw
 
@@ -72,8 +95,14 @@ class W8A8LinearFunction(torch.autograd.Function):
     def forward(ctx, x, weight, bias, wq, ws, group):
         K = x.shape[-1]
         N = wq.shape[0]
-        y, xq, xs = w8a8_linear_forward(x.reshape(-1, K), wq, ws, bias, group, x.dtype)
-        ctx.save_for_backward(xq, xs, wq, ws)
+        x2 = x.reshape(-1, K)
+        if ctx.needs_input_grad[1]:
+            # dW's operand X^T comes out of the same pass over x as the forward's codes
+            y, xtq, xts = w8a8_linear_forward_train(x2, wq, ws, bias, group, x.dtype)
+        else:
+            y, _, _ = w8a8_linear_forward(x2, wq, ws, bias, group, x.dtype)
+            xtq = xts = None
+        ctx.save_for_backward(xtq, xts, wq, ws)
         ctx.x_shape = x.shape
         ctx.x_dtype = x.dtype
         ctx.group = group
@@ -82,14 +111,15 @@ class W8A8LinearFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out):
-        xq, xs, wq, ws = ctx.saved_tensors
+        xtq, xts, wq, ws = ctx.saved_tensors
         N = wq.shape[0]
         g = grad_out.reshape(-1, N)
         if g.dtype not in _OUT_DTYPES:
             g = g.float()
         g = g.contiguous()
-        dx, dw = w8a8_linear_backward(g, xq, xs, wq, ws, ctx.group, ctx.x_dtype,
-                                      ctx.needs_input_grad[0], ctx.needs_input_grad[1])
+        dx, dw = w8a8_linear_backward(g, None, None, wq, ws, ctx.group, ctx.x_dtype,
+                                      ctx.needs_input_grad[0], ctx.needs_input_grad[1],
+                                      xt=(xtq, xts) if xtq is not None else None)
         if dx is not None:
             dx = dx.reshape(ctx.x_shape).to(ctx.x_dtype)
         db = None

@@ -136,3 +136,45 @@ def test_requant_transpose_rounding_ties(group):
     eq, es = oq.requant_transpose(codes, scales, C, group)
     assert np.array_equal(tq.cpu().numpy(), eq)
     assert np.array_equal(ts.cpu().numpy().view(np.uint16), es.view(np.uint16))
+
+
+@pytest.mark.parametrize("t_from_codes", [False, True])
+@pytest.mark.parametrize("shape,dtype,group", [
+    ((256, 384), torch.float32, 128),      # whole tiles (dual kernel)
+    ((300, 136), torch.float32, 128),      # ragged rows and columns (dual kernel)
+    ((129, 1024), torch.bfloat16, 128),
+    ((64, 200), torch.float16, 128),
+    ((100, 96), torch.float32, 64),        # other groups: the single-layout kernels
+    ((70, 13), torch.float32, 128),        # C % 8 != 0: the single-layout kernels
+])
+def test_quantize_dual_matches_oracle(shape, dtype, group, t_from_codes):
+    """quantize_dual = quantize_last_dim plus quantize_transpose (dY) or plus
+    requant_transpose of the row codes (X^T's double quantization), bit-exact."""
+    g = torch.Generator().manual_seed(hash((shape, group, t_from_codes)) % 2**31)
+    x_cpu = (torch.randn(*shape, generator=g) * 2).to(dtype)
+    c, s, ct, st = kq.quantize_dual(x_cpu.to(DEV), group, t_from_codes=t_from_codes)
+    xf = x_cpu.float().numpy()
+    ec, es = oq.quantize_last_dim(xf, group)
+    if t_from_codes:
+        ect, est = oq.requant_transpose(ec, es, group, group)
+    else:
+        ect, est = oq.quantize_transpose(xf, group)
+    assert np.array_equal(c.cpu().numpy(), ec)
+    assert np.array_equal(s.cpu().numpy().view(np.uint16), es.view(np.uint16))
+    assert np.array_equal(ct.cpu().numpy(), ect)
+    assert np.array_equal(st.cpu().numpy().view(np.uint16), est.view(np.uint16))
+
+
+@pytest.mark.parametrize("t_from_codes", [False, True])
+def test_quantize_dual_adversarial_rounding(t_from_codes):
+    """Quotients on and next to half-integers through both layouts of the dual kernel."""
+    x = _adversarial_rows(np.random.default_rng(5), 128)            # (rows, 256)
+    x = np.concatenate([x, x[::-1] * np.float32(0.5)], 0)            # more rows, two tiles
+    c, s, ct, st = kq.quantize_dual(torch.from_numpy(x).to(DEV), 128, t_from_codes=t_from_codes)
+    ec, es = oq.quantize_last_dim(x, 128)
+    ect, est = (oq.requant_transpose(ec, es, 128, 128) if t_from_codes
+                else oq.quantize_transpose(x, 128))
+    assert np.array_equal(c.cpu().numpy(), ec)
+    assert np.array_equal(s.cpu().numpy().view(np.uint16), es.view(np.uint16))
+    assert np.array_equal(ct.cpu().numpy(), ect)
+    assert np.array_equal(st.cpu().numpy().view(np.uint16), est.view(np.uint16))
