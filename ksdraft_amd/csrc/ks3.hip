@@ -369,7 +369,8 @@ __global__ void __launch_bounds__(kSpineThreads) ks3_spine_kernel(
 // accumulator clamped to +-65504 (no fp16 materialisation); LUT indices are computed in
 // fp32; the Horner sum is scaled by ps/64 in fp32 without truncation; the ReLU^2 pre-scale
 // is the amax of |h| (before ReLU) over the row's G-chart group; the squared codes are
-// exact; and the result is requantized per group a second time.
+// exact; and the result is requantized per group a second time. Same block layout, row
+// prefetch and phase order as ks3_spine_kernel.
 template <int G, bool VEC>
 __global__ void __launch_bounds__(kSpineThreads) ks3_spine_fused_kernel(
     const float *__restrict__ acc, int64_t M, int64_t F, const void *__restrict__ table,
@@ -382,59 +383,101 @@ __global__ void __launch_bounds__(kSpineThreads) ks3_spine_fused_kernel(
   const int lane = threadIdx.x & 31;
   const int rsub = threadIdx.x >> 5;
   const int64_t col0 = c0 + lane * 4;
-  const bool full = VEC && col0 + 3 < F;
+  const bool cok = col0 < F;
+  const bool seg_full = c0 + 128 <= F;
+  const int64_t colc = cok ? col0 : 0;
+  const uint32_t tab_lane = (uint32_t)(uintptr_t)(tab) + (uint32_t)(lane * 4) * (4 * Tab::kPitch);
   const int64_t row_end = min(M, (int64_t)(blockIdx.y + 1) * kSpineRows);
-  for (int64_t r0 = (int64_t)blockIdx.y * kSpineRows + rsub; r0 < row_end; r0 += 32) {
-    float x[2][4];
+  const int64_t rfirst = (int64_t)blockIdx.y * kSpineRows + rsub;
+  auto raw2 = [&](int64_t r0, float4 (&w)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const float *src = acc + min(r0 + 16 * u, M - 1) * F + col0;
-      if (full) {
-        const float4 v = *(const float4 *)src;
-        x[u][0] = v.x; x[u][1] = v.y; x[u][2] = v.z; x[u][3] = v.w;
+      const float *src = acc + min(r0 + 16 * u, M - 1) * F + colc;
+      if (VEC) {
+        w[u] = *(const float4 *)src;
       } else {
+        float e[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) x[u][j] = col0 + j < F ? src[j] : 0.0f;
+        for (int j = 0; j < 4; ++j) e[j] = col0 + j < F ? src[j] : 0.0f;
+        w[u] = make_float4(e[0], e[1], e[2], e[3]);
       }
     }
+  };
+  auto body = [&](int64_t r0, const float4 (&w)[2]) __attribute__((always_inline)) {
+    float xc[2][4], h[2][4];
+    uint32_t off[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const float xs[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xc[u][j] = fminf(fmaxf(xs[j], -kScaleMax), kScaleMax);  // as the reference clamp (a NaN -> -65504)
+        off[u][j] = (uint32_t)(min(max(lut_index_f32(xc[u][j] * 0.25f) + 128, 0), 255)) * 4u;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        typedef __attribute__((address_space(3))) const float lds_f32;
+        const float inc = *(lds_f32 *)(uintptr_t)(tab_lane + j * (4 * Tab::kPitch) + off[u][j]);
+        h[u][j] = seg_full || col0 + j < F ? xc[u][j] + inc : 0.0f;
+      }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int64_t row = r0 + 16 * u;
       const bool rok = row < row_end;
-      float h[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float xc = __builtin_amdgcn_fmed3f(x[u][j], -kScaleMax, kScaleMax);
-        const int idx = min(max(lut_index_f32(xc * 0.25f) + 128, 0), 255);
-        h[j] = col0 + j < F ? xc + Tab::inc(tab, lane * 4 + j, idx) : 0.0f;
-      }
-      const uint32_t am = lane_group_max<G / 4>(__builtin_bit_cast(uint32_t, abs_max<4>(h)));
+      const uint32_t am = lane_group_max<G / 4>(__builtin_bit_cast(uint32_t, abs_max<4>(h[u])));
       const float pre = group_scale(__builtin_bit_cast(float, am));
       const float rp = __builtin_amdgcn_rcpf(pre);
+      float t[4];
+      float near = 1.0f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float p = h[j] * rp;
-        float t = rintf(p);
-        if (fabsf(fabsf(p - t) - 0.5f) < 0x1p-14f) t = rintf(h[j] / pre);
-        const float q = fmaxf(fminf(fmaxf(t, -127.0f), 127.0f), 0.0f);
-        h[j] = (q * q) * (pre * pre);
+        const float p = h[u][j] * rp;
+        t[j] = rintf(p);
+        near = fminf(near, fabsf(fabsf(p - t[j]) - 0.5f));
       }
-      const uint32_t hm = lane_group_max<G / 4>(__builtin_bit_cast(uint32_t, abs_max<4>(h)));
-      const float s = group_scale(__builtin_bit_cast(float, hm));
-      uint32_t w;
-      codes_rcp_packed<4>(h, s, &w);
-      if (rok) {
-        int8_t *dst = hq + row * F + col0;
-        if (full) {
-          *(uint32_t *)dst = w;
-        } else {
+      if (near < 0x1p-14f) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (col0 + j < F) dst[j] = (int8_t)(w >> (8 * j));
-        }
-        if ((lane & (G / 4 - 1)) == 0 && col0 < F) hs[row * n_groups + col0 / G] = scale_bits(s);
+        for (int j = 0; j < 4; ++j) t[j] = rintf(h[u][j] / pre);
+      }
+      float f[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float q = __builtin_amdgcn_fmed3f(t[j], 0.0f, 127.0f);  // NaN q: NaN via pre
+        f[j] = (q * q) * (pre * pre);
+      }
+      const uint32_t hm = lane_group_max<G / 4>(__builtin_bit_cast(uint32_t, abs_max<4>(f)));
+      const float s = group_scale(__builtin_bit_cast(float, hm));
+      uint32_t wq;
+      codes_rcp_packed<4>(f, s, &wq);
+      const int64_t rowc = rok ? row : 0;
+      const bool lead = rok && cok && (lane & (G / 4 - 1)) == 0;
+      __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsrc(hs + rowc * n_groups, 2 * n_groups),
+                                            lead ? (uint32_t)(col0 / G) * 2 : kOob, 0, 0);
+      if (VEC) {
+        __builtin_amdgcn_raw_buffer_store_b32(wq, rsrc(hq + rowc * F, F),
+                                              rok && cok ? (uint32_t)col0 : kOob, 0, 0);
+      } else if (rok) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (col0 + j < F) hq[row * F + col0 + j] = (int8_t)(wq >> (8 * j));
       }
     }
+  };
+  float4 wa[2], wb[2];
+  raw2(rfirst, wa);
+  raw2(rfirst + 32, wb);
+#pragma unroll 1
+  for (int it = 0; it < kSpineRows / 64; ++it) {
+    const int64_t r0 = rfirst + 64 * it;
+    const float4 ca[2] = {wa[0], wa[1]};
+    raw2(r0 + 64, wa);
+    body(r0, ca);
+    const float4 cb[2] = {wb[0], wb[1]};
+    raw2(r0 + 96, wb);
+    body(r0 + 32, cb);
   }
 }
 
