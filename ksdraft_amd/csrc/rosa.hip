@@ -170,13 +170,15 @@ __global__ void __launch_bounds__(256) rosa_pack_kernel(const void *__restrict__
   const int64_t s = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t w = blockIdx.y, b = blockIdx.z;
   if (s >= S) return;
-  const typename E::T *xb = (const typename E::T *)x + b * T * S;
+  const typename E::T *xb = (const typename E::T *)x + b * T * S + s;
+  // all 32 loads first (rows past T clamped to a valid row and masked below)
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) v[i] = E::load(xb + min(w * 32 + i, T - 1) * S);
   uint32_t word = 0;
-#pragma unroll 8
-  for (int i = 0; i < 32; ++i) {
-    const int64_t t = w * 32 + i;
-    if (t < T && E::load(xb + t * S + s) > 0.0f) word |= 1u << i;
-  }
+#pragma unroll
+  for (int i = 0; i < 32; ++i)
+    if (w * 32 + i < T && v[i] > 0.0f) word |= 1u << i;
   bits[(b * S + s) * W + w] = word;
 }
 
