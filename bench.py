@@ -40,6 +40,7 @@ from ksdraft_amd.kernels.linear import (w8a8_linear_backward,  # noqa: E402
 from ksdraft_amd.kernels.quant import (quantize_dual, quantize_last_dim,  # noqa: E402
                                        quantize_transpose, requant_transpose)
 from ksdraft_amd.kernels.gemm import w8a8_gemm_out  # noqa: E402
+from ksdraft_amd.train import cross_entropy_grad_int8, cross_entropy_stats  # noqa: E402
 
 METRIC = ("W8A8 GS128 GEMM TOPS fwd+bwd @d=1536 (% int8 peak); draft train-step tok/s")
 PEAK_INT8 = 5.0e15   # MI355X dense int8 MFMA, ops/s
@@ -239,20 +240,27 @@ def lmhead_c3_times(dev, reps):
     t = torch.randint(0, N3, (M3,), device=dev, generator=g)
     dy = torch.softmax(y, dim=1)
     dy[torch.arange(M3, device=dev), t] -= 1.0
-    del y
     gq, gs = quantize_last_dim(dy)
     wtq, wts = requant_transpose(wq, ws)
     gtq, gts = quantize_transpose(dy)
     xtq, xts = requant_transpose(xq, xs)
     ops = 2 * M3 * N3 * K3
+    # the loss side: fused cross entropy on the logits (row statistics, then dY formed and
+    # quantized in both layouts without an fp32 dY)
+    _, rmax, rinv, n_rows = cross_entropy_stats(y, t, check_targets=False)
+    gsc = (torch.ones((), device=dev) / n_rows).reshape(1)
     stages = {
         "quantize_W": (lambda: quantize_last_dim(w), 4 * N3 * K3 + N3 * K3 + 2 * N3 * K3 // 128),
         "quantize_X_dual": (lambda: quantize_dual(x, t_from_codes=True), 4 * M3 * K3 + 2 * (M3 * K3 + 2 * M3 * K3 // 128)),
         "gemm_fwd": (lambda: w8a8_gemm_out(xq, xs, wq, ws), None),
-        "quantize_dY_dual": (lambda: quantize_dual(dy), 4 * M3 * N3 + 2 * (M3 * N3 + 2 * M3 * N3 // 128)),
+        "ce_row_stats": (lambda: cross_entropy_stats(y, t, check_targets=False), 4 * M3 * N3),
+        "ce_grad_int8_dual": (lambda: cross_entropy_grad_int8(y, t, rmax, rinv, gsc),
+                              4 * M3 * N3 + 2 * (M3 * N3 + 2 * M3 * N3 // 128)),
         "requant_WT": (lambda: requant_transpose(wq, ws), 2 * (N3 * K3 + 2 * N3 * K3 // 128)),
         "gemm_dX": (lambda: w8a8_gemm_out(gq, gs, wtq, wts), None),
         "gemm_dW": (lambda: w8a8_gemm_out(gtq, gts, xtq, xts), None),
+        # not part of the step: the unfused dual quantization of a dY computed beforehand
+        "cmp_quantize_dY_dual": (lambda: quantize_dual(dy), 4 * M3 * N3 + 2 * (M3 * N3 + 2 * M3 * N3 // 128)),
     }
     res = {}
     for name, (fn, nbytes) in stages.items():
@@ -270,7 +278,7 @@ def lmhead_c3_times(dev, reps):
         res[name] = ent
         torch.cuda.empty_cache()
     gemm_us = sum(res[k]["us"] for k in ("gemm_fwd", "gemm_dX", "gemm_dW"))
-    step_us = sum(v["us"] for v in res.values())
+    step_us = sum(v["us"] for k, v in res.items() if not k.startswith("cmp_"))
     res["three_gemms_ms"] = round(gemm_us / 1e3, 3)
     res["three_gemms_tops"] = round(3 * ops / (gemm_us * 1e-6) / 1e12, 1)
     res["step_ms_sum_of_kernels"] = round(step_us / 1e3, 3)

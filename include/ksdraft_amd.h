@@ -106,6 +106,39 @@ int ksd_quantize_dual(const void *x, int x_dtype, int64_t R, int64_t C, int grou
                       uint16_t *scales_t, void *stream);
 
 /*
+ * Cross entropy over the rows of fp32 logits (R, C) with class targets, the
+ * F.cross_entropy(logits, tgt) of reference ksdraft/train/__init__.py:77 (mean reduction,
+ * torch's default ignore_index semantics). Row statistics, one read of the logits:
+ *   row_max[r]     = max_c y[r, c]
+ *   row_inv_sum[r] = 1 / sum_c exp(y[r, c] - row_max[r])
+ *   row_loss[r]    = row_max[r] + log(1 / row_inv_sum[r]) - y[r, t_r], or 0 when t_r is
+ *                    ignore_index or outside [0, C) (the caller validates targets)
+ * The mean loss is sum(row_loss) / (number of counted rows), as torch computes it.
+ */
+int ksd_ce_row_stats(const float *logits, int64_t R, int64_t C, const int64_t *targets,
+                     int64_t ignore_index, float *row_max, float *row_inv_sum, float *row_loss,
+                     void *stream);
+
+/*
+ * The backward of that cross entropy, quantized straight into both int8 operand layouts of
+ * the LM head's int8 backward (dY for dX = dY.W, dY^T for dW = dY^T.X; the recipe of
+ * reference ksdraft/kernels/ks3_int8.py:403-424), without writing dY:
+ *   dY[r, c] = (exp(y[r, c] - row_max[r]) * row_inv_sum[r] - [c == t_r]) * grad_scale[0]
+ * for counted rows and 0 for ignored ones; grad_scale is a device fp32 scalar (d loss /
+ * d mean-CE divided by the counted-row count). codes/scales and codes_t/scales_t are
+ * exactly ksd_quantize_dual(dY, t_from_codes = 0) of these dY values. No reference
+ * counterpart as one call (the reference's autograd materialises dY in fp32).
+ *   group 128; dy_out (R, C) fp32 optional: when given, dY is also written there. Shapes
+ *   with C % 8 != 0 (or unaligned buffers) require dy_out, which then serves as the
+ *   staging buffer of the two-pass path.
+ */
+int ksd_ce_backward_quant_dual(const float *logits, int64_t R, int64_t C, const float *row_max,
+                               const float *row_inv_sum, const int64_t *targets,
+                               int64_t ignore_index, const float *grad_scale, int group,
+                               int8_t *codes, uint16_t *scales, int8_t *codes_t,
+                               uint16_t *scales_t, float *dy_out, void *stream);
+
+/*
  * G1 / G2 — W8A8 GEMM, "NT" layout: Y = dequant(A) . dequant(W)^T with the ordered
  * per-group contract
  *     acc = 0;  for g in 0..K/group-1:  acc = fmaf(float(P_g), sa[m,g]*sw[n,g], acc)

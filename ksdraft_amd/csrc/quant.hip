@@ -259,10 +259,24 @@ __global__ __launch_bounds__(256) void quant_T_kernel(
 // transposed in quant_T_kernel's conflict-free layout, and 4 lanes per column quantize the
 // columns. Requires C % 8 == 0 and 16-byte aligned rows; rows past R read as zeros and
 // are not stored.
-template <int DT, bool T_FROM_CODES>
+// Cross-entropy backward source of the dual kernel: x[r, c] is not read from memory but
+// formed from fp32 logits y and per-row softmax statistics,
+//   dY[r, c] = (exp(y[r, c] - max_r) / sum_r - [c == t_r]) * w_r,
+// with w_r = grad_scale for a row whose target is in range and not ignore_index, else 0.
+struct CeSrc {
+  const float *rmax, *rinv;  // max_r and 1 / sum_r (ce_row_stats_kernel)
+  const int64_t *tgt;
+  int64_t ignore;
+  const float *gscale;       // device scalar: d loss / d (mean CE), divided by the row count
+  float *dy;                 // optional fp32 copy of dY (R, C), nullptr when not wanted
+};
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <int DT, bool T_FROM_CODES, bool CE = false>
 __global__ __launch_bounds__(512) void quant_dual_kernel(
     const void *__restrict__ xv, int64_t R, int64_t C, int8_t *__restrict__ codes,
-    uint16_t *__restrict__ scales, int8_t *__restrict__ codes_t, uint16_t *__restrict__ scales_t) {
+    uint16_t *__restrict__ scales, int8_t *__restrict__ codes_t, uint16_t *__restrict__ scales_t,
+    CeSrc ce = CeSrc{}) {
   using T = typename Elem<DT>::T;
   constexpr int G = 128, PITCH = 145;
   __shared__ float tile[128 * PITCH];
@@ -287,6 +301,26 @@ __global__ __launch_bounds__(512) void quant_dual_kernel(
     const bool ok = cok && row < R;
     float v[8];
     cvt_raw8<DT>(raw[p], ok, v);
+    if constexpr (CE) {
+      const int64_t rs = row < R ? row : R - 1;
+      const int64_t t = ce.tgt[rs];
+      const bool live = ok && t != ce.ignore && t >= 0 && t < C;
+      const float m = ce.rmax[rs], inv = ce.rinv[rs], w = live ? *ce.gscale : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float e = __builtin_amdgcn_exp2f((v[i] - m) * kLog2e) * inv;
+        v[i] = live ? (e - (col + i == t ? 1.0f : 0.0f)) * w : 0.0f;
+      }
+      if (ce.dy) {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        const auto dr = rsrc(ce.dy + (row < R ? row : 0) * C, 4 * C);
+        const uint32_t off = ok ? (uint32_t)col * 4 : kOob;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{v[0], v[1], v[2], v[3]}), dr, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{v[4], v[5], v[6], v[7]}), dr,
+                                               ok ? off + 16 : kOob, 0, 0);
+      }
+    }
     const uint32_t am = group_max_u32<16>(__builtin_bit_cast(uint32_t, abs_max<8>(v)));
     const float s = group_scale(__builtin_bit_cast(float, am));
     uint32_t w[2];
@@ -331,6 +365,97 @@ __global__ __launch_bounds__(512) void quant_dual_kernel(
     for (int j = 0; j < RPT; ++j)
       if (rbase + j < R) dst[j] = (int8_t)(w[j / 4] >> (8 * (j % 4)));
   }
+}
+
+// ---------------------------------------------------------------- cross entropy
+// Online (max, sum of exp) of one row: the running pair (m, s) absorbs a chunk with maximum
+// cm as m' = max(m, cm), s' = s * 2^((m - m') log2 e) + sum 2^((y - m') log2 e). A chunk
+// or partner that is entirely -inf contributes nothing (and no inf - inf).
+__device__ __forceinline__ void ce_merge(float &m, float &s, float m2, float s2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;  // both empty
+  s = (m == -INFINITY ? 0.0f : s * __builtin_amdgcn_exp2f((m - mn) * kLog2e)) +
+      (m2 == -INFINITY ? 0.0f : s2 * __builtin_amdgcn_exp2f((m2 - mn) * kLog2e));
+  m = mn;
+}
+
+// One 256-thread block per row of fp32 logits (R, C): row max, 1 / (sum of exp(y - max))
+// and the row's cross-entropy term max + log(sum) - y[t] (0 for an ignored row). A NaN
+// anywhere in the row makes its sum NaN, as torch's softmax does.
+template <bool VEC>
+__global__ __launch_bounds__(256) void ce_row_stats_kernel(
+    const float *__restrict__ logits, int64_t C, const int64_t *__restrict__ tgt, int64_t ignore,
+    float *__restrict__ rmax, float *__restrict__ rinv, float *__restrict__ rloss) {
+  __shared__ float sm[2][4];
+  const int64_t row = blockIdx.x;
+  const float *y = logits + row * C;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float m = -INFINITY, s = 0.0f;
+  bool nan = false;
+  auto absorb = [&](const float *v, int n) __attribute__((always_inline)) {
+    float cm = -INFINITY;
+    for (int i = 0; i < n; ++i) {
+      cm = fmaxf(cm, v[i]);
+      nan |= v[i] != v[i];
+    }
+    float cs = 0.0f;
+    if (cm != -INFINITY)
+      for (int i = 0; i < n; ++i) cs += __builtin_amdgcn_exp2f((v[i] - cm) * kLog2e);
+    ce_merge(m, s, cm, cs);
+  };
+  if (VEC) {  // 16 consecutive elements per chunk (C % 16 == 0, 16-byte aligned rows)
+    const float4 *y4 = (const float4 *)y;
+    for (int64_t c = (int64_t)tid * 4; c < C / 4; c += 256 * 4) {
+      float v[16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 q = y4[c + j];
+        v[4 * j] = q.x;
+        v[4 * j + 1] = q.y;
+        v[4 * j + 2] = q.z;
+        v[4 * j + 3] = q.w;
+      }
+      absorb(v, 16);
+    }
+  } else {
+    for (int64_t c = tid; c < C; c += 256) {
+      const float v = y[c];
+      absorb(&v, 1);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
+    ce_merge(m, s, m2, s2);
+  }
+  nan = __any(nan);
+  if (lane == 0) {
+    sm[0][wave] = m;
+    sm[1][wave] = s;
+  }
+  __syncthreads();
+  if (tid != 0) return;
+  m = sm[0][0];
+  s = sm[1][0];
+  for (int w = 1; w < 4; ++w) ce_merge(m, s, sm[0][w], sm[1][w]);
+  if (nan) s = NAN;
+  rmax[row] = m;
+  rinv[row] = 1.0f / s;
+  const int64_t t = tgt[row];
+  const bool live = t != ignore && t >= 0 && t < C;
+  rloss[row] = live ? (m + logf(s)) - y[t] : 0.0f;
+}
+
+// dY of one element per thread (any shape): the fallback when the fused dual path does not
+// apply; the codes then come from the dual quantizer run on this dY.
+__global__ __launch_bounds__(256) void ce_dy_kernel(const float *__restrict__ logits, int64_t R, int64_t C,
+                                                    CeSrc ce) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= R * C) return;
+  const int64_t r = idx / C, c = idx % C, t = ce.tgt[r];
+  const bool live = t != ce.ignore && t >= 0 && t < C;
+  const float e = __builtin_amdgcn_exp2f((logits[idx] - ce.rmax[r]) * kLog2e) * ce.rinv[r];
+  ce.dy[idx] = live ? (e - (c == t ? 1.0f : 0.0f)) * *ce.gscale : 0.0f;
 }
 
 template <int SRC>
@@ -483,6 +608,58 @@ extern "C" int ksd_quantize_dual(const void *x, int x_dtype, int64_t R, int64_t 
   }
 #undef KSD_DUAL
   return check_launch("quantize_dual");
+}
+
+extern "C" int ksd_ce_row_stats(const float *logits, int64_t R, int64_t C, const int64_t *targets,
+                                int64_t ignore_index, float *row_max, float *row_inv_sum,
+                                float *row_loss, void *stream) {
+  if (R < 0 || C < 0) return fail(KSD_EINVAL, "ce_row_stats: negative shape");
+  if (R == 0) return KSD_OK;
+  if (C == 0) return fail(KSD_EINVAL, "ce_row_stats: no classes");
+  if (!logits || !targets || !row_max || !row_inv_sum || !row_loss)
+    return fail(KSD_EINVAL, "ce_row_stats: null pointer");
+  if (R > 0x7fffffffLL) return fail(KSD_EINVAL, "ce_row_stats: too many rows");
+  hipStream_t st = (hipStream_t)stream;
+  const bool vec = C % 16 == 0 && ((uintptr_t)logits) % 16 == 0;
+  if (vec)
+    ce_row_stats_kernel<true><<<(unsigned)R, 256, 0, st>>>(logits, C, targets, ignore_index, row_max,
+                                                          row_inv_sum, row_loss);
+  else
+    ce_row_stats_kernel<false><<<(unsigned)R, 256, 0, st>>>(logits, C, targets, ignore_index, row_max,
+                                                           row_inv_sum, row_loss);
+  return check_launch("ce_row_stats");
+}
+
+extern "C" int ksd_ce_backward_quant_dual(const float *logits, int64_t R, int64_t C,
+                                          const float *row_max, const float *row_inv_sum,
+                                          const int64_t *targets, int64_t ignore_index,
+                                          const float *grad_scale, int group, int8_t *codes,
+                                          uint16_t *scales, int8_t *codes_t, uint16_t *scales_t,
+                                          float *dy_out, void *stream) {
+  if (group != 128) return fail(KSD_EINVAL, "ce_backward_quant_dual: group must be 128, got %d", group);
+  if (R < 0 || C < 0) return fail(KSD_EINVAL, "ce_backward_quant_dual: negative shape");
+  if (R == 0 || C == 0) return KSD_OK;
+  if (!logits || !row_max || !row_inv_sum || !targets || !grad_scale || !codes || !scales || !codes_t ||
+      !scales_t)
+    return fail(KSD_EINVAL, "ce_backward_quant_dual: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  const CeSrc ce{row_max, row_inv_sum, targets, ignore_index, grad_scale, dy_out};
+  const bool fast = C % 8 == 0 && ((uintptr_t)logits) % 16 == 0 && ((uintptr_t)codes) % 8 == 0 &&
+                    (dy_out == nullptr || ((uintptr_t)dy_out) % 16 == 0) && cdiv(R, 128) <= 65535 &&
+                    cdiv(C, 128) <= 0x7fffffff;
+  if (fast) {
+    const dim3 grid((unsigned)cdiv(C, 128), (unsigned)cdiv(R, 128));
+    quant_dual_kernel<KSD_F32, false, true><<<grid, 512, 0, st>>>(logits, R, C, codes, scales, codes_t,
+                                                                  scales_t, ce);
+    return check_launch("ce_backward_quant_dual");
+  }
+  // other shapes: dY into dy_out (required here), then the dual quantizer on it
+  if (!dy_out) return fail(KSD_EINVAL, "ce_backward_quant_dual: this shape needs dy_out (R x C fp32)");
+  if (cdiv(R * C, 256) > 0x7fffffffLL) return fail(KSD_EINVAL, "ce_backward_quant_dual: tensor too large");
+  ce_dy_kernel<<<(unsigned)cdiv(R * C, 256), 256, 0, st>>>(logits, R, C, ce);
+  const int rc = check_launch("ce_backward_quant_dual (dY)");
+  if (rc) return rc;
+  return ksd_quantize_dual(dy_out, KSD_F32, R, C, group, 0, codes, scales, codes_t, scales_t, stream);
 }
 
 extern "C" int ksd_abi_version(void) { return 2; }

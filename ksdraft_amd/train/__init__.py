@@ -1,1 +1,138 @@
-"""Training-side helpers the INT8 kernels call (reference ksdraft/train)."""
+"""Training-side helpers the INT8 kernels call (reference ksdraft/train).
+
+Cross entropy over the LM head's logits, ``F.cross_entropy(logits, tgt)`` of reference
+ksdraft/train/__init__.py:77, with its gradient delivered straight as the two int8 operand
+layouts of the int8 head backward (dY per token along the vocabulary for dX = dY.W, dY^T
+per vocabulary row along the tokens for dW = dY^T.X; the recipe of
+ksdraft/kernels/ks3_int8.py:403-424). The fp32 dY is never written.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ..kernels.gemm import w8a8_gemm, w8a8_gemm_out
+from ..kernels.linear import w8a8_linear_forward_train
+from ..kernels.quant import GROUP_SIZE, SCALE_DTYPE, requant_transpose
+
+IGNORE_INDEX = -100  # torch.nn.functional.cross_entropy's default
+
+
+def _check_logits(logits: torch.Tensor, targets: torch.Tensor, ignore_index: int,
+                  check_targets: bool = True):
+    dev = _lib.require_gpu(logits, targets)
+    if logits.dim() != 2 or logits.dtype != torch.float32:
+        raise ValueError("cross entropy expects 2-D float32 logits (rows, classes)")
+    if targets.dim() != 1 or targets.shape[0] != logits.shape[0]:
+        raise ValueError(f"targets of shape {tuple(targets.shape)} do not match logits "
+                         f"{tuple(logits.shape)}")
+    if targets.dtype != torch.int64:
+        raise TypeError("targets must be int64 class indices")
+    if check_targets:  # torch raises for such targets too (a host sync)
+        C = logits.shape[1]
+        bad = ((targets < 0) & (targets != ignore_index)) | (targets >= C)
+        if bool(bad.any()):
+            t = int(targets[bad][0])
+            raise IndexError(f"Target {t} is out of bounds.")
+    return dev
+
+
+def cross_entropy_stats(logits: torch.Tensor, targets: torch.Tensor,
+                        ignore_index: int = IGNORE_INDEX, check_targets: bool = True):
+    """One read of the logits: (loss, row_max, row_inv_sum, n_counted).
+
+    loss is the mean over counted rows of log(sum exp(y)) - y[t] (a 0-d fp32 tensor, NaN
+    when no row counts, as torch gives); row_max / row_inv_sum feed the backward.
+    ``check_targets=False`` skips the range check and its host sync (for graph capture):
+    the kernels then treat an out-of-range target as an ignored row."""
+    dev = _check_logits(logits, targets, ignore_index, check_targets)
+    logits = logits.contiguous()
+    targets = targets.contiguous()
+    R, C = logits.shape
+    rmax = torch.empty(R, dtype=torch.float32, device=dev)
+    rinv = torch.empty(R, dtype=torch.float32, device=dev)
+    rloss = torch.empty(R, dtype=torch.float32, device=dev)
+    _lib.call("ksd_ce_row_stats", logits.data_ptr(), R, C, targets.data_ptr(), int(ignore_index),
+              rmax.data_ptr(), rinv.data_ptr(), rloss.data_ptr(), _lib.stream_ptr(dev))
+    n = (targets != ignore_index).sum().to(torch.float32)
+    return rloss.sum() / n, rmax, rinv, n
+
+
+def cross_entropy_grad_int8(logits: torch.Tensor, targets: torch.Tensor, row_max: torch.Tensor,
+                            row_inv_sum: torch.Tensor, grad_scale: torch.Tensor,
+                            ignore_index: int = IGNORE_INDEX, group: int = GROUP_SIZE,
+                            return_dy: bool = False):
+    """d(loss)/d(logits) = (softmax(y) - onehot(t)) * grad_scale, quantized in both layouts.
+
+    grad_scale: a 1-element fp32 device tensor (the upstream gradient over the number of
+    counted rows). Returns (codes (R, C), scales (R, C/group), codes_t (C, R), scales_t
+    (C, R/group)) and, with ``return_dy``, the fp32 dY the codes were made from."""
+    dev = _lib.require_gpu(logits, targets, row_max, row_inv_sum, grad_scale)
+    if group != GROUP_SIZE:
+        raise ValueError(f"the fused cross-entropy gradient supports group {GROUP_SIZE} only")
+    logits = logits.contiguous()
+    targets = targets.contiguous()
+    R, C = logits.shape
+    gsc = grad_scale.to(device=dev, dtype=torch.float32).reshape(1).contiguous()
+    codes = torch.empty((R, C), dtype=torch.int8, device=dev)
+    scales = torch.empty((R, -(-C // group)), dtype=SCALE_DTYPE, device=dev)
+    codes_t = torch.empty((C, R), dtype=torch.int8, device=dev)
+    scales_t = torch.empty((C, -(-R // group)), dtype=SCALE_DTYPE, device=dev)
+    # shapes off the fused path (C % 8 != 0) stage dY in an fp32 buffer
+    dy = torch.empty((R, C), dtype=torch.float32, device=dev) if (return_dy or C % 8) else None
+    _lib.call("ksd_ce_backward_quant_dual", logits.data_ptr(), R, C, row_max.data_ptr(),
+              row_inv_sum.data_ptr(), targets.data_ptr(), int(ignore_index), gsc.data_ptr(),
+              group, codes.data_ptr(), scales.data_ptr(), codes_t.data_ptr(), scales_t.data_ptr(),
+              0 if dy is None else dy.data_ptr(), _lib.stream_ptr(dev))
+    out = (codes, scales, codes_t, scales_t)
+    return (out, dy) if return_dy else out
+
+
+def cross_entropy_int8(logits: torch.Tensor, targets: torch.Tensor,
+                       ignore_index: int = IGNORE_INDEX, grad_output: float = 1.0,
+                       group: int = GROUP_SIZE, return_dy: bool = False):
+    """F.cross_entropy(logits, targets) and its int8 logits gradient in one call.
+
+    Returns (loss, (codes, scales, codes_t, scales_t)) [, dy]."""
+    loss, rmax, rinv, n = cross_entropy_stats(logits, targets, ignore_index)
+    gsc = torch.as_tensor(grad_output, dtype=torch.float32, device=logits.device) / n
+    res = cross_entropy_grad_int8(logits, targets, rmax, rinv, gsc, ignore_index, group, return_dy)
+    if return_dy:
+        ops, dy = res
+        return loss, ops, dy
+    return loss, res
+
+
+class LinearCrossEntropyInt8(torch.autograd.Function):
+    """loss = F.cross_entropy(W8A8(x, W), t) for the bias-free LM head of reference
+    ksdraft/model/draft.py:39, 82 with the loss of ksdraft/train/__init__.py:77.
+
+    Forward: the int8 head GEMM (fp32 logits) and the row statistics. Backward: the fused
+    cross-entropy gradient in both int8 layouts, then dX = dY.W and dW = dY^T.X on the int8
+    GEMMs. Returns fp32 gradients for x (in x's dtype) and the fp32 master weight."""
+
+    @staticmethod
+    def forward(ctx, x, weight, wq, ws, targets, ignore_index, group):
+        K = x.shape[-1]
+        x2 = x.reshape(-1, K)
+        y, xtq, xts = w8a8_linear_forward_train(x2, wq, ws, None, group, torch.float32)
+        loss, rmax, rinv, n = cross_entropy_stats(y, targets.reshape(-1), ignore_index)
+        ctx.save_for_backward(y, rmax, rinv, n, targets.reshape(-1), xtq, xts, wq, ws)
+        ctx.ignore_index, ctx.group, ctx.x_shape, ctx.x_dtype = ignore_index, group, x.shape, x.dtype
+        return loss
+
+    @staticmethod
+    def backward(ctx, grad_loss):
+        y, rmax, rinv, n, t, xtq, xts, wq, ws = ctx.saved_tensors
+        group = ctx.group
+        gsc = grad_loss.to(torch.float32).reshape(1) / n
+        gq, gs, gtq, gts = cross_entropy_grad_int8(y, t, rmax, rinv, gsc, ctx.ignore_index, group)
+        dx = dw = None
+        if ctx.needs_input_grad[0]:
+            wtq, wts = requant_transpose(wq, ws, group, group)
+            out = ctx.x_dtype if ctx.x_dtype in (torch.bfloat16, torch.float16) else torch.float32
+            dx = w8a8_gemm_out(gq, gs, wtq, wts, group, out_dtype=out).reshape(ctx.x_shape)
+        if ctx.needs_input_grad[1]:
+            dw = w8a8_gemm(gtq, gts, xtq, xts, group)
+        return dx, dw, None, None, None, None, None
