@@ -40,7 +40,7 @@ from ksdraft_amd.kernels.linear import (w8a8_linear_backward,  # noqa: E402
 from ksdraft_amd.kernels.quant import (quantize_dual, quantize_last_dim,  # noqa: E402
                                        quantize_transpose, requant_transpose)
 from ksdraft_amd.kernels.gemm import w8a8_gemm_out  # noqa: E402
-from ksdraft_amd.train import cross_entropy_grad_int8, cross_entropy_stats  # noqa: E402
+from ksdraft_amd.train import adamw_requant_, cross_entropy_grad_int8, cross_entropy_stats  # noqa: E402
 
 METRIC = ("W8A8 GS128 GEMM TOPS fwd+bwd @d=1536 (% int8 peak); draft train-step tok/s")
 PEAK_INT8 = 5.0e15   # MI355X dense int8 MFMA, ops/s
@@ -227,9 +227,12 @@ def lmhead_c3_times(dev, reps):
     """the LM-head / vocab projection as one W8A8 GS128 linear layer,
     forward + dX + dW, M = 4096 tokens, K = 1536, N = 150144 (int8 W 230.6 MB, fp32 Y
     2.46 GB). X ~N(0,1), W ~N(0,0.02) drawn by a seeded generator on the device (1 GB of
-    fp32 master weights), dY = softmax(Y) - onehot(t) with t uniform in [0, N). Each kernel
-    of the step is timed as a graph of back-to-back launches; GEMMs are reported in TOPS
-    against 2*M*N*K = 1.889e12 ops, quantizations in GB/s against their algorithmic bytes."""
+    fp32 master weights), targets t uniform in [0, N). The step is the head's training step:
+    the fused AdamW + int8 repack of W, the forward GEMM, the fused cross entropy (row
+    statistics, then dY quantized in both layouts), and the dX and dW GEMMs. Each kernel is
+    timed as a graph of back-to-back launches; GEMMs are reported in TOPS against
+    2*M*N*K = 1.889e12 ops, the rest in GB/s against their algorithmic bytes. Entries named
+    cmp_* are unfused alternatives, timed for comparison and not summed."""
     M3, K3, N3 = 4096, 1536, 150144
     g = torch.Generator(device=dev).manual_seed(0)
     x = torch.randn(M3, K3, device=dev, generator=g)
@@ -249,8 +252,22 @@ def lmhead_c3_times(dev, reps):
     # quantized in both layouts without an fp32 dY)
     _, rmax, rinv, n_rows = cross_entropy_stats(y, t, check_targets=False)
     gsc = (torch.ones((), device=dev) / n_rows).reshape(1)
+    # the optimizer side: AdamW on the fp32 master fused with its int8 repack (this replaces
+    # the forward's per-call weight quantization), and torch's AdamW + quantize to compare
+    wm = torch.zeros_like(w)
+    wv = torch.zeros_like(w)
+    wg = torch.randn(N3, K3, device=dev, generator=g) * 1e-3
+    tw = w.clone().requires_grad_(True)
+    tw.grad = wg.clone()
+    topt = torch.optim.AdamW([tw], lr=1e-3, weight_decay=0.01, capturable=True)
+
+    def torch_adamw_quantize():
+        topt.step()
+        return quantize_last_dim(tw.detach())
+
     stages = {
-        "quantize_W": (lambda: quantize_last_dim(w), 4 * N3 * K3 + N3 * K3 + 2 * N3 * K3 // 128),
+        "adamw_requant_W": (lambda: adamw_requant_(w, wg, wm, wv, 2, 1e-3, weight_decay=0.01),
+                            29 * N3 * K3 + 2 * N3 * K3 // 128),
         "quantize_X_dual": (lambda: quantize_dual(x, t_from_codes=True), 4 * M3 * K3 + 2 * (M3 * K3 + 2 * M3 * K3 // 128)),
         "gemm_fwd": (lambda: w8a8_gemm_out(xq, xs, wq, ws), None),
         "ce_row_stats": (lambda: cross_entropy_stats(y, t, check_targets=False), 4 * M3 * N3),
@@ -259,8 +276,12 @@ def lmhead_c3_times(dev, reps):
         "requant_WT": (lambda: requant_transpose(wq, ws), 2 * (N3 * K3 + 2 * N3 * K3 // 128)),
         "gemm_dX": (lambda: w8a8_gemm_out(gq, gs, wtq, wts), None),
         "gemm_dW": (lambda: w8a8_gemm_out(gtq, gts, xtq, xts), None),
-        # not part of the step: the unfused dual quantization of a dY computed beforehand
+        # not part of the step: the unfused dual quantization of a dY computed beforehand,
+        # the forward's weight quantization the fused optimizer makes unnecessary, and
+        # torch's AdamW step followed by that quantization
         "cmp_quantize_dY_dual": (lambda: quantize_dual(dy), 4 * M3 * N3 + 2 * (M3 * N3 + 2 * M3 * N3 // 128)),
+        "cmp_quantize_W": (lambda: quantize_last_dim(w), 4 * N3 * K3 + N3 * K3 + 2 * N3 * K3 // 128),
+        "cmp_torch_adamw_then_quantize_W": (torch_adamw_quantize, 29 * N3 * K3 + 2 * N3 * K3 // 128),
     }
     res = {}
     for name, (fn, nbytes) in stages.items():

@@ -139,6 +139,29 @@ int ksd_ce_backward_quant_dual(const float *logits, int64_t R, int64_t C, const 
                                uint16_t *scales_t, float *dy_out, void *stream);
 
 /*
+ * One torch.optim.AdamW step on fp32 masters with the int8 repack of the updated masters:
+ * the optimizer step of reference ksdraft/train/__init__.py:114-116, 166 (AdamW with
+ * decoupled weight decay after clip_grad_norm_) fused with the per-call weight quantization
+ * of ksdraft/kernels/linear.py:46-56 (and the master repack of ks3_int8.py:262-277).
+ * Elementwise, in the order of torch's single-tensor AdamW, each op one fp32 rounding:
+ *   g  = grad * clip_coef[0]          (when clip_coef is non-null: clip_grad_norm_'s mul_)
+ *   p  = param * decay                (decay = 1 - lr * weight_decay)
+ *   m  = m + one_minus_beta1 * (g - m)
+ *   v  = v * beta2 + (one_minus_beta2 * g) * g
+ *   p  = p + (-step_size) * (m / (sqrt(v) / bias_correction2_sqrt + eps))
+ * param, exp_avg, exp_avg_sq are updated in place; grad is read only. The scalars are
+ * torch's python-double values rounded to fp32: step_size = lr / (1 - beta1^step),
+ * bias_correction2_sqrt = (1 - beta2^step)^0.5. When codes/scales are non-null they
+ * receive quantize_last_dim(p) (rows, K) int8 / (rows, ceil(K/128)) fp16. group 128.
+ * No reference counterpart as one call.
+ */
+int ksd_adamw_requant(float *param, const float *grad, float *exp_avg, float *exp_avg_sq,
+                      int64_t rows, int64_t K, const float *clip_coef, float decay,
+                      float one_minus_beta1, float beta2, float one_minus_beta2, float eps,
+                      float step_size, float bias_correction2_sqrt, int group, int8_t *codes,
+                      uint16_t *scales, void *stream);
+
+/*
  * G1 / G2 — W8A8 GEMM, "NT" layout: Y = dequant(A) . dequant(W)^T with the ordered
  * per-group contract
  *     acc = 0;  for g in 0..K/group-1:  acc = fmaf(float(P_g), sa[m,g]*sw[n,g], acc)

@@ -458,6 +458,106 @@ __global__ __launch_bounds__(256) void ce_dy_kernel(const float *__restrict__ lo
   ce.dy[idx] = live ? (e - (c == t ? 1.0f : 0.0f)) * *ce.gscale : 0.0f;
 }
 
+// ---------------------------------------------------------------- AdamW + requant
+// One torch.optim.AdamW step (decoupled weight decay, amsgrad off; the order of
+// torch/optim/adam.py _single_tensor_adam, every op one fp32 rounding) on fp32 masters, and
+// the int8 codes of the updated masters by the quantize_last_dim contract. The host
+// passes torch's python-double scalars rounded to fp32.
+struct AdamArgs {
+  float decay;      // 1 - lr * weight_decay
+  float w1;         // 1 - beta1 (lerp weight, < 0.5)
+  float beta2, w2;  // beta2, 1 - beta2
+  float eps;
+  float step_size;  // lr / (1 - beta1^step)
+  float bc2_sqrt;   // (1 - beta2^step)^0.5
+};
+
+// A group of 128 consecutive elements of a row per 16 lanes, 8 per lane. VEC: K % 8 == 0
+// and 16-byte aligned buffers, so a lane's 8 elements are all in range or all out.
+template <bool VEC>
+__global__ __launch_bounds__(256) void adamw_requant_kernel(
+    float *__restrict__ p, const float *__restrict__ g, float *__restrict__ m, float *__restrict__ v,
+    int64_t rows, int64_t K, int64_t ng, const float *__restrict__ clip, AdamArgs a,
+    int8_t *__restrict__ codes, uint16_t *__restrict__ scales) {
+  const int64_t gid = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);  // (row, group): 16 lanes
+  if (gid >= rows * ng) return;                                      // uniform per 16 lanes
+  const int sub = threadIdx.x & 15;
+  const int64_t row = gid / ng, grp = gid % ng, col = grp * 128 + sub * 8;
+  const int64_t base = row * K + col;
+  float pv[8], gv[8], mv[8], vv[8];
+  bool ok[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ok[i] = col + i < K;
+  if (VEC) {
+    if (ok[0]) {
+      const float4 *pp = (const float4 *)(p + base), *gp = (const float4 *)(g + base);
+      const float4 *mp = (const float4 *)(m + base), *vp = (const float4 *)(v + base);
+      const float4 q[8] = {pp[0], pp[1], gp[0], gp[1], mp[0], mp[1], vp[0], vp[1]};
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        pv[4 * h] = q[h].x, pv[4 * h + 1] = q[h].y, pv[4 * h + 2] = q[h].z, pv[4 * h + 3] = q[h].w;
+        gv[4 * h] = q[2 + h].x, gv[4 * h + 1] = q[2 + h].y, gv[4 * h + 2] = q[2 + h].z, gv[4 * h + 3] = q[2 + h].w;
+        mv[4 * h] = q[4 + h].x, mv[4 * h + 1] = q[4 + h].y, mv[4 * h + 2] = q[4 + h].z, mv[4 * h + 3] = q[4 + h].w;
+        vv[4 * h] = q[6 + h].x, vv[4 * h + 1] = q[6 + h].y, vv[4 * h + 2] = q[6 + h].z, vv[4 * h + 3] = q[6 + h].w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pv[i] = gv[i] = mv[i] = vv[i] = 0.0f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pv[i] = ok[i] ? p[base + i] : 0.0f;
+      gv[i] = ok[i] ? g[base + i] : 0.0f;
+      mv[i] = ok[i] ? m[base + i] : 0.0f;
+      vv[i] = ok[i] ? v[base + i] : 0.0f;
+    }
+  }
+  const float c = clip ? *clip : 1.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float gi = clip ? gv[i] * c : gv[i];          // clip_grad_norm_: g.mul_(coef)
+    const float pd = pv[i] * a.decay;                    // param.mul_(1 - lr * wd)
+    mv[i] = mv[i] + a.w1 * (gi - mv[i]);                 // exp_avg.lerp_(g, 1 - beta1)
+    vv[i] = vv[i] * a.beta2 + (a.w2 * gi) * gi;          // exp_avg_sq.mul_(b2).addcmul_(g, g, 1 - b2)
+    const float den = sqrtf(vv[i]) / a.bc2_sqrt + a.eps;  // IEEE sqrt and division (build flags)
+    pv[i] = pd + (-a.step_size) * (mv[i] / den);         // param.addcdiv_(m, den, -step_size)
+    if (!ok[i]) pv[i] = 0.0f;
+  }
+  if (VEC) {
+    if (ok[0]) {
+      float4 *pp = (float4 *)(p + base), *mp = (float4 *)(m + base), *vp = (float4 *)(v + base);
+      pp[0] = make_float4(pv[0], pv[1], pv[2], pv[3]);
+      pp[1] = make_float4(pv[4], pv[5], pv[6], pv[7]);
+      mp[0] = make_float4(mv[0], mv[1], mv[2], mv[3]);
+      mp[1] = make_float4(mv[4], mv[5], mv[6], mv[7]);
+      vp[0] = make_float4(vv[0], vv[1], vv[2], vv[3]);
+      vp[1] = make_float4(vv[4], vv[5], vv[6], vv[7]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (ok[i]) {
+        p[base + i] = pv[i];
+        m[base + i] = mv[i];
+        v[base + i] = vv[i];
+      }
+  }
+  if (codes == nullptr) return;  // uniform
+  const uint32_t am = group_max_u32<16>(__builtin_bit_cast(uint32_t, abs_max<8>(pv)));
+  const float s = group_scale(__builtin_bit_cast(float, am));
+  uint32_t w[2];
+  codes_rcp_packed<8>(pv, s, w);
+  if (sub == 0) scales[row * ng + grp] = scale_bits(s);
+  if (VEC) {
+    if (ok[0]) *(uint2 *)(codes + base) = make_uint2(w[0], w[1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (ok[i]) codes[base + i] = (int8_t)(w[i >> 2] >> (8 * (i & 3)));
+  }
+}
+
 template <int SRC>
 static int launch_quant_T(const void *x, const uint16_t *in_scales, int64_t nsc_in, int gin,
                           int64_t R, int64_t C, int group, int8_t *codes, uint16_t *scales,
@@ -660,6 +760,34 @@ extern "C" int ksd_ce_backward_quant_dual(const float *logits, int64_t R, int64_
   const int rc = check_launch("ce_backward_quant_dual (dY)");
   if (rc) return rc;
   return ksd_quantize_dual(dy_out, KSD_F32, R, C, group, 0, codes, scales, codes_t, scales_t, stream);
+}
+
+extern "C" int ksd_adamw_requant(float *param, const float *grad, float *exp_avg, float *exp_avg_sq,
+                                 int64_t rows, int64_t K, const float *clip_coef, float decay,
+                                 float one_minus_beta1, float beta2, float one_minus_beta2, float eps,
+                                 float step_size, float bias_correction2_sqrt, int group, int8_t *codes,
+                                 uint16_t *scales, void *stream) {
+  if (group != 128) return fail(KSD_EINVAL, "adamw_requant: group must be 128, got %d", group);
+  if (rows < 0 || K < 0) return fail(KSD_EINVAL, "adamw_requant: negative shape");
+  if (rows == 0 || K == 0) return KSD_OK;
+  if (!param || !grad || !exp_avg || !exp_avg_sq) return fail(KSD_EINVAL, "adamw_requant: null pointer");
+  if ((codes == nullptr) != (scales == nullptr))
+    return fail(KSD_EINVAL, "adamw_requant: codes and scales go together");
+  const int64_t ng = cdiv(K, 128);
+  const int64_t blocks = cdiv(rows * ng, 16);
+  if (blocks > 0x7fffffffLL) return fail(KSD_EINVAL, "adamw_requant: tensor too large");
+  const AdamArgs a{decay, one_minus_beta1, beta2, one_minus_beta2, eps, step_size, bias_correction2_sqrt};
+  auto al = [](const void *q, uintptr_t n) { return ((uintptr_t)q) % n == 0; };
+  const bool vec = K % 8 == 0 && al(param, 16) && al(grad, 16) && al(exp_avg, 16) && al(exp_avg_sq, 16) &&
+                   (codes == nullptr || al(codes, 8));
+  hipStream_t st = (hipStream_t)stream;
+  if (vec)
+    adamw_requant_kernel<true><<<(unsigned)blocks, 256, 0, st>>>(param, grad, exp_avg, exp_avg_sq, rows, K, ng,
+                                                                 clip_coef, a, codes, scales);
+  else
+    adamw_requant_kernel<false><<<(unsigned)blocks, 256, 0, st>>>(param, grad, exp_avg, exp_avg_sq, rows, K, ng,
+                                                                  clip_coef, a, codes, scales);
+  return check_launch("adamw_requant");
 }
 
 extern "C" int ksd_abi_version(void) { return 2; }

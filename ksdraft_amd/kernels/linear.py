@@ -173,7 +173,15 @@ class Int8Linear(nn.Module):
         self._quantize_weight()
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        self._quantize_weight()  # live fp32 masters stay authoritative (linear.py:66)
+        # live fp32 masters stay authoritative (linear.py:66): the codes are rebuilt on every
+        # call, except when train.AdamWRequant wrote them in the same pass that last updated
+        # the master and the master has not changed since (same storage, same in-place
+        # version); dithered codes are redrawn every call
+        key = getattr(self, "_codes_key", None)
+        if (self.weight_codes is None or getattr(self, "_dither", 0.0) > 0 or key is None
+                or key != (self.weight.data_ptr(), self.weight._version)):
+            self._codes_key = None
+            self._quantize_weight()
         if torch.is_grad_enabled() and (self.weight.requires_grad or x.requires_grad):
             if self.ste_training:
                 return self.fake_quant_forward(x)

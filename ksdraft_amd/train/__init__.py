@@ -136,3 +136,90 @@ class LinearCrossEntropyInt8(torch.autograd.Function):
         if ctx.needs_input_grad[1]:
             dw = w8a8_gemm(gtq, gts, xtq, xts, group)
         return dx, dw, None, None, None, None, None
+
+
+def adamw_requant_(param: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor,
+                   exp_avg_sq: torch.Tensor, step: int, lr: float, betas=(0.9, 0.999),
+                   eps: float = 1e-8, weight_decay: float = 1e-2,
+                   clip_coef: torch.Tensor | None = None, quantize: bool = True,
+                   group: int = GROUP_SIZE):
+    """One torch.optim.AdamW step (decoupled weight decay, amsgrad off, step already
+    incremented to ``step``) on an fp32 master in place, fused with the int8 repack of the
+    updated master (quantize_last_dim along the last dim, as Int8Linear._quantize_weight of
+    reference ksdraft/kernels/linear.py:46-56 does on every call).
+
+    clip_coef: optional 1-element fp32 device tensor, the factor clip_grad_norm_ would
+    multiply the gradient by (the gradient itself is read, not rewritten). Returns (codes,
+    scales) of the updated master, or None when ``quantize`` is False."""
+    dev = _lib.require_gpu(param, grad, exp_avg, exp_avg_sq, clip_coef)
+    for name, t in (("param", param), ("grad", grad), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"adamw_requant_: {name} must be a contiguous float32 tensor")
+        if t.shape != param.shape:
+            raise ValueError(f"adamw_requant_: {name} shape {tuple(t.shape)} != {tuple(param.shape)}")
+    if group != GROUP_SIZE:
+        raise ValueError(f"adamw_requant_ supports group {GROUP_SIZE} only")
+    beta1, beta2 = betas
+    K = param.shape[-1] if param.dim() >= 1 else 1
+    rows = param.numel() // max(K, 1)
+    # torch's python-double scalars, rounded to fp32 by the kernel's arguments
+    bc1 = 1 - beta1 ** step
+    bc2 = 1 - beta2 ** step
+    codes = scales = None
+    if quantize:
+        codes = torch.empty(param.shape, dtype=torch.int8, device=dev)
+        scales = torch.empty((*param.shape[:-1], -(-K // group)), dtype=SCALE_DTYPE, device=dev)
+    cc = None if clip_coef is None else clip_coef.to(dtype=torch.float32).reshape(1).contiguous()
+    _lib.call("ksd_adamw_requant", param.data_ptr(), grad.data_ptr(), exp_avg.data_ptr(),
+              exp_avg_sq.data_ptr(), rows, K, 0 if cc is None else cc.data_ptr(),
+              1 - lr * weight_decay, 1 - beta1, beta2, 1 - beta2, eps, lr / bc1, bc2 ** 0.5,
+              group, 0 if codes is None else codes.data_ptr(),
+              0 if scales is None else scales.data_ptr(), _lib.stream_ptr(dev))
+    return None if codes is None else (codes, scales)
+
+
+class AdamWRequant(torch.optim.Optimizer):
+    """torch.optim.AdamW (the optimizer of reference ksdraft/train/__init__.py:114-116,
+    amsgrad off) whose step also repacks int8 weights.
+
+    Same hyper-parameters and per-parameter state ("step", "exp_avg", "exp_avg_sq") as
+    torch's AdamW. ``register_int8(module)`` attaches an Int8Linear-like module: after each
+    step its ``weight_codes`` / ``weight_scales`` hold quantize_last_dim of the updated
+    fp32 master, from the same pass over the weight. ``step(clip_coef=...)`` takes the
+    factor of clip_grad_norm_ as a device tensor instead of rescaling every gradient."""
+
+    def __init__(self, params, lr: float = 1e-3, betas=(0.9, 0.999), eps: float = 1e-8,
+                 weight_decay: float = 1e-2):
+        if lr < 0 or eps < 0 or weight_decay < 0 or not (0 <= betas[0] < 1 and 0 <= betas[1] < 1):
+            raise ValueError("invalid AdamW hyper-parameter")
+        super().__init__(params, dict(lr=lr, betas=tuple(betas), eps=eps, weight_decay=weight_decay))
+        self._int8 = {}
+
+    def register_int8(self, module) -> None:
+        self._int8[id(module.weight)] = module
+
+    @torch.no_grad()
+    def step(self, closure=None, clip_coef: torch.Tensor | None = None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        for group in self.param_groups:
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                st = self.state[p]
+                if not st:
+                    st["step"] = torch.tensor(0.0)
+                    st["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+                    st["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+                st["step"] += 1
+                mod = self._int8.get(id(p))
+                res = adamw_requant_(p, p.grad.contiguous(), st["exp_avg"], st["exp_avg_sq"],
+                                     int(st["step"].item()), group["lr"], group["betas"],
+                                     group["eps"], group["weight_decay"], clip_coef,
+                                     quantize=mod is not None)
+                if mod is not None:  # the codes now belong to the master as it is
+                    mod.weight_codes, mod.weight_scales = res
+                    mod._codes_key = (p.data_ptr(), p._version)
+        return loss

@@ -1,0 +1,88 @@
+"""GPU parity: the fused AdamW step + int8 repack (ksdraft_amd/train) against
+torch.optim.AdamW and the oracle quantizer.
+
+Bars:
+- Masters and both moments are TOL against torch.optim.AdamW, the reference's optimizer
+  (ksdraft/train/__init__.py:114-116, 166; its single-tensor update order), on the same
+  device in fp32: rtol 2e-6 with an absolute floor of 2e-6 of the tensor's largest
+  magnitude, after each of three steps. torch's elementwise kernels may contract a*b + c
+  into one rounding (its lerp does, judging by the results), and this build does not, so
+  moments that cancel to tiny values differ in their last bits.
+- The int8 codes and fp16 scales are bit-exact against oracle/quant.py's
+  quantize_last_dim of the kernel's own updated master.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from ksdraft_amd import train as T
+from ksdraft_amd.kernels import Int8Linear
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _codes_match(p, res):
+    codes, scales = (a.cpu().numpy() for a in res)
+    ec, es = oq.quantize_last_dim(p.detach().cpu().numpy(), 128)
+    assert np.array_equal(codes, ec)
+    assert np.array_equal(scales.view(np.uint16), es.view(np.uint16))
+
+
+@pytest.mark.parametrize("shape", [(256, 384), (130, 200), (1, 1536), (64, 1000), (7, 13)])
+@pytest.mark.parametrize("wd,clip", [(0.1, None), (0.0, 0.5)])
+def test_adamw_requant_matches_torch(shape, wd, clip):
+    g = torch.Generator().manual_seed(hash((shape, wd)) % 2**31)
+    p0 = (torch.randn(*shape, generator=g) * 0.02).to(DEV)
+    ref = p0.clone().requires_grad_(True)
+    opt = torch.optim.AdamW([ref], lr=3e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=wd,
+                            foreach=False)
+    p = p0.clone()
+    m = torch.zeros_like(p)
+    v = torch.zeros_like(p)
+    cc = None if clip is None else torch.tensor([clip], device=DEV)
+    for step in range(1, 4):
+        grad = (torch.randn(*shape, generator=g) * 0.01).to(DEV)
+        ref.grad = grad * clip if clip is not None else grad.clone()
+        opt.step()
+        res = T.adamw_requant_(p, grad, m, v, step, 3e-3, (0.9, 0.95), 1e-8, wd, clip_coef=cc)
+        torch.cuda.synchronize()
+        st = opt.state[ref]
+        for got, exp in ((p, ref.detach()), (m, st["exp_avg"]), (v, st["exp_avg_sq"])):
+            torch.testing.assert_close(got, exp, rtol=2e-6, atol=2e-6 * exp.abs().max().item())
+        _codes_match(p, res)
+
+
+def test_adamw_requant_optimizer_drives_int8linear():
+    """AdamWRequant on an Int8Linear: after the step the module's codes are those of the
+    updated master, and the next forward uses them without rebuilding them."""
+    torch.manual_seed(0)
+    lin = Int8Linear(256, 384).to(DEV)
+    with torch.no_grad():
+        lin.weight.normal_(0, 0.02)
+    lin_ref = Int8Linear(256, 384).to(DEV)
+    lin_ref.load_state_dict(lin.state_dict())
+    opt = T.AdamWRequant(lin.parameters(), lr=1e-3, weight_decay=0.01)
+    opt.register_int8(lin)
+    opt_ref = torch.optim.AdamW(lin_ref.parameters(), lr=1e-3, weight_decay=0.01, foreach=False)
+    x = torch.randn(64, 256, device=DEV)
+    for _ in range(2):
+        for mod, o in ((lin, opt), (lin_ref, opt_ref)):
+            o.zero_grad()
+            mod(x).square().mean().backward()
+            o.step()
+        _codes_match(lin.weight, (lin.weight_codes, lin.weight_scales))
+        codes = lin.weight_codes
+        y = lin(x)  # no requant: the optimizer's codes are current
+        assert lin.weight_codes is codes
+        torch.testing.assert_close(lin.weight, lin_ref.weight, rtol=2e-6,
+                                   atol=2e-6 * lin_ref.weight.abs().max().item())
+        torch.testing.assert_close(y, lin_ref(x), rtol=1e-3, atol=1e-4)
+    # a torch-side change of the master makes the next forward requantize
+    with torch.no_grad():
+        lin.weight.mul_(2.0)
+    lin(x)
+    assert lin.weight_codes is not codes
+    _codes_match(lin.weight, (lin.weight_codes, lin.weight_scales))
