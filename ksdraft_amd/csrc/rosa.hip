@@ -451,6 +451,74 @@ __device__ __forceinline__ uint32_t ext_key(int c, int e, int cap, int j) {
   return mkkey(min(c + 1 + e, cap), j);
 }
 
+// k flips inside the best candidate's matched run [trunc_lo, trunc_hi], one lane per flip.
+// Flip p touches only candidates j with j - c_j <= p <= j, all within 62 of j*; keys
+// farther away are unchanged (farbest), and near keys outside [p, p + cmax] enter through
+// prefix / suffix maxima of the unchanged near keys. Cn/En hold c_j and e_j of the
+// candidates j in [j* - 63, j* + 64); Pref/Suf are per-wave scratch of kNear words each.
+__device__ __forceinline__ void near_run_flips(int lane, int t, int lmax, int jstar, int trunc_lo,
+                                               int trunc_hi, uint32_t farbest, const uint8_t *Cn,
+                                               const uint8_t *En, uint32_t *Pref, uint32_t *Suf,
+                                               const uint32_t *vw, float sgn, float g, float *ck) {
+  const int near0 = jstar - 63;
+  const int jlo = max(0, jstar - 62), jhi = min(t - 1, jstar + 62);
+  // unchanged near keys, two per lane (r = 2 * lane, 2 * lane + 1), and their max c
+  uint32_t kr[2];
+  int cmax = 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int r = 2 * lane + h;
+    const int j2 = near0 + r;
+    kr[h] = 0u;
+    if (j2 >= jlo && j2 <= jhi) {
+      const int c2 = Cn[r];
+      kr[h] = mkkey(min(c2, min(j2 + 1, lmax)), j2);
+      cmax = max(cmax, c2);
+    }
+  }
+  uint32_t pre = max(kr[0], kr[1]), suf = pre;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t a = (uint32_t)__shfl_up((int)pre, d);
+    const uint32_t bb = (uint32_t)__shfl_down((int)suf, d);
+    const int cm = __shfl_xor(cmax, d);
+    if (lane >= d) pre = max(pre, a);
+    if (lane + d < 64) suf = max(suf, bb);
+    cmax = max(cmax, cm);
+  }
+  // inclusive prefix / suffix max per near index r. The shuffles run with every lane
+  // active: a cross-lane read from a lane masked off by a branch returns 0.
+  const uint32_t up1 = (uint32_t)__shfl_up((int)pre, 1);
+  const uint32_t down1 = (uint32_t)__shfl_down((int)suf, 1);
+  const uint32_t pre_prev = lane >= 1 ? up1 : 0u;
+  const uint32_t suf_next = lane < 63 ? down1 : 0u;
+  Pref[2 * lane] = max(pre_prev, kr[0]);
+  Pref[2 * lane + 1] = pre;
+  Suf[2 * lane] = suf;
+  Suf[2 * lane + 1] = max(suf_next, kr[1]);
+  const int p = trunc_lo + lane;
+  if (p <= trunc_hi) {
+    uint32_t nb = farbest;
+    const int rl = p - 1 - near0;          // near keys left of the flip
+    if (p - 1 >= jlo) nb = max(nb, Pref[rl]);
+    const int jend = min(jhi, p + cmax);   // candidates that can reach k[p]
+    if (jend + 1 <= jhi) nb = max(nb, Suf[jend + 1 - near0]);
+    for (int j2 = p; j2 <= jend; ++j2) {
+      const int r = j2 - near0;
+      const int c2 = Cn[r], e2 = En[r];
+      const int cap2 = min(j2 + 1, lmax);
+      const int d = j2 - p;
+      uint32_t k2;
+      if (d < min(c2, cap2)) k2 = mkkey(d, j2);
+      else if (d == c2 && c2 < cap2) k2 = ext_key(c2, e2, cap2, j2);
+      else k2 = mkkey(min(c2, cap2), j2);
+      nb = max(nb, k2);
+    }
+    const float s2 = sign_of(nb, vw);
+    if (s2 != sgn) atomicAdd(ck + p, (s2 - sgn) * g);
+  }
+}
+
 __global__ void __launch_bounds__(256) rosa_credits_kernel(
     const uint32_t *__restrict__ qb, const uint32_t *__restrict__ kb, const uint32_t *__restrict__ vb,
     const int32_t *__restrict__ match_j, const float *__restrict__ grad, const float *__restrict__ payload,
@@ -564,7 +632,8 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
         if (lane >= d) pre = max(pre, a);
         if (lane + d < 64) suf = max(suf, bsj);
       }
-      const uint32_t g1 = lane >= 1 ? (uint32_t)__shfl_up((int)pre, 1) : 0u;  // buckets < lane
+      const uint32_t up1 = (uint32_t)__shfl_up((int)pre, 1);  // all lanes active
+      const uint32_t g1 = lane >= 1 ? up1 : 0u;                 // buckets < lane
       const int sj = __shfl_down(suf, 1);                                      // buckets > lane
       const int imax = min(min(Lstar, lmax - 1), t);
       if (lane <= imax) {
@@ -576,64 +645,256 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
       }
     }
 
-    // (b) k flips inside the best candidate's run, one lane per flip. Flip p touches only
-    // candidates j with j - c_j <= p <= j, all within 62 of j*; keys farther away are
-    // unchanged (farbest), and near keys outside [p, p + cmax] through prefix / suffix
-    // maxima of the unchanged near keys.
+    // (b) k flips inside the best candidate's run
+    if (jstar >= 0)
+      near_run_flips(lane, t, lmax, jstar, trunc_lo, trunc_hi, farbest, Cn, En, Pref, Suf, vw, sgn, g, ck);
+  }
+  if (lane == 0) gps[wave] = gsum;
+  __syncthreads();
+  if (threadIdx.x == 0) gp_partial[stream] = ((gps[0] + gps[1]) + gps[2]) + gps[3];
+}
+
+// Bit-parallel credits for streams of up to 2048 positions (W <= 64 words). Same outputs as
+// rosa_credits_kernel. For position t, lane w of a wave holds word w of every candidate
+// set (bit b = candidate j = 32 w + b, j < t), and the levels L of the common-suffix chain
+// are processed a whole set at a time:
+//   D_L  = {j >= L : k[j - L] == q[t - L]}      (one alignbit of the lane's k words)
+//   A_L  = {j : the first L positions match}     A_0 = [0, t),  A_{L+1} = A_L & D_L
+//   O_L  = {j : exactly one mismatch in the first L positions, j >= L - 1}
+//          O_{L+1} = (O_L & D_L) | (A_L & ~D_L & {j >= L})
+// A_L holds the candidates whose key length (capped by min(j + 1, lmax)) is at least L.
+// O_L holds those whose "lifted" length is at least L: with the bit of their single
+// mismatch flipped they would match L positions.
+//  q flip at offset i (i <= min(L*, lmax - 1)): the new best is the longest lifted member
+//    of bucket i (the candidates whose first mismatch is at i), if the bucket has one
+//    within its cap; otherwise (i, latest j of A_i). The bucket maxima come from the
+//    members of O at the checkpoint levels L*, L* - 3 and L* - 6: a member with lifted
+//    length >= L lies in O_L. Each member gets its first mismatch c and lifted length from
+//    its 64-bit window. A bucket no checkpoint covers is resolved by its own chain.
+//  k flip at p outside the best run: the largest lifted key among the members j of
+//    O_{L*+1} u (O_{L*} & {j > j*}) with j - c_j = p (a per-p table), if any.
+//  k flip inside the best run, and v flips: as in rosa_credits_kernel.
+constexpr int kBpMaxT = 2048;
+constexpr int kBpWave32 = 64 + 64 + kBpMaxT + kNear / 2 + 2 * kNear;  // u32 words per wave
+
+__device__ __forceinline__ int set_maxbit(uint32_t word) {  // highest candidate of a wave set
+  const uint64_t bal = __ballot(word != 0u);
+  if (bal == 0) return -1;
+  const int hl = 63 - __clzll((long long)bal);
+  const uint32_t hw = (uint32_t)__shfl((int)word, hl);
+  return 32 * hl + 31 - __clz(hw);
+}
+
+__global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
+    const uint32_t *__restrict__ qb, const uint32_t *__restrict__ kb, const uint32_t *__restrict__ vb,
+    const int32_t *__restrict__ match_j, const float *__restrict__ grad, const float *__restrict__ payload,
+    int64_t S, int T, int W, int lmax, float *__restrict__ cred, float *__restrict__ gp_partial) {
+  __shared__ uint32_t qw[64], kw[64], vw[64];
+  __shared__ uint32_t wsm[kCredWaves][kBpWave32];
+  __shared__ float gps[kCredWaves];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint32_t *Nw = wsm[wave];                       // [64] best lifted key per bucket
+  int *lat = (int *)(Nw + 64);                    // [64] latest j of A_i
+  uint32_t *evt = Nw + 128;                       // [kBpMaxT] best lifted key per flip p
+  uint8_t *Cn = (uint8_t *)(evt + kBpMaxT), *En = Cn + kNear;
+  uint32_t *Pref = evt + kBpMaxT + kNear / 2, *Suf = Pref + kNear;
+  const int64_t stream = blockIdx.x;
+  const int64_t b = stream / S, s = stream % S;
+  for (int i = threadIdx.x; i < 64; i += 256) {
+    qw[i] = i < W ? qb[stream * W + i] : 0u;
+    kw[i] = i < W ? kb[stream * W + i] : 0u;
+    vw[i] = i < W ? vb[stream * W + i] : 0u;
+  }
+  for (int i = lane; i < 64 + kBpMaxT; i += 64) Nw[i < 64 ? i : 64 + i] = 0u;  // Nw and evt
+  __syncthreads();
+  // this lane's k words: word w and the two below it (zeros before position 0)
+  const uint32_t k0 = kw[lane], k1 = lane >= 1 ? kw[lane - 1] : 0u, k2 = lane >= 2 ? kw[lane - 2] : 0u;
+  const bool w0 = lane == 0, w1 = lane == 1;
+  float *cq = cred + stream * 3 * T, *ck = cq + T, *cv = cq + 2 * T;
+  const float pay = payload[s];
+  float gsum = 0.0f;
+  for (int t = wave; t < T; t += kCredWaves) {  // wave-uniform
+    const float gr = grad[(b * T + t) * S + s];
+    const int jstar = match_j[stream * T + t];
+    const uint64_t qwin = q_window(qw, t);
+    uint32_t best = 0u;
+    int cstar = 0, capstar = 0;
     if (jstar >= 0) {
-      const int jlo = max(0, jstar - 62), jhi = min(t - 1, jstar + 62);
-      // unchanged near keys, two per lane (r = 2 * lane, 2 * lane + 1), and their max c
-      uint32_t kr[2];
-      int cmax = 0;
+      cstar = clz64(qwin ^ q_window(kw, jstar));
+      capstar = min(jstar + 1, lmax);
+      best = mkkey(min(cstar, capstar), jstar);
+    }
+    const float sgn = sign_of(best, vw);
+    gsum += gr * sgn;
+    const float g = gr * pay;
+    if (t == 0 || g == 0.0f || lmax < 1) continue;
+    const int Ls = key_len(best);
+    if (lane == 0 && Ls >= 1) atomicAdd(cv + jstar + 1, -2.0f * sgn * g);  // v flips
+    const int imax = min(min(Ls, lmax - 1), t);
+    const int trunc_lo = jstar >= 0 ? jstar - min(cstar, capstar) + 1 : 1;
+    const int trunc_hi = jstar;
+
+    // masks of this lane's word: candidates j < t, and j outside [j* - 62, j* + 62]
+    const int tw = t >> 5;
+    const uint32_t valid = lane < tw ? ~0u : (lane == tw ? (1u << (t & 31)) - 1u : 0u);
+    uint32_t farm = ~0u;
+    if (jstar >= 0) {
+      const int lo = jstar - 62, hi = jstar + 62, w0b = 32 * lane;  // near range [lo, hi]
+      const int a = max(lo - w0b, 0), e = min(hi - w0b, 31);        // its bits in this word
+      if (a <= e) farm = ~(((e - a == 31) ? ~0u : ((2u << (e - a)) - 1u)) << a);
+    }
+    // D_L and its complement {j >= L : mismatch at L} for this lane
+    auto level = [&](int L, uint32_t &D, uint32_t &Dn) __attribute__((always_inline)) {
+      const uint32_t KL = L == 0 ? k0 : (L <= 32 ? __builtin_amdgcn_alignbit(k0, k1, 32 - L)
+                                                 : __builtin_amdgcn_alignbit(k1, k2, 64 - L));
+      const uint32_t p0 = L < 32 ? ~0u << L : 0u, p1 = L <= 32 ? ~0u : ~0u << (L - 32);
+      const uint32_t pos = w0 ? p0 : (w1 ? p1 : ~0u);
+      const bool qbit = (qwin >> (63 - L)) & 1ull;
+      D = (qbit ? KL : ~KL) & pos;
+      Dn = pos & ~D;
+    };
+
+    // ascending pass over the levels 0 .. min(lmax, L* + 1) - 1
+    uint32_t A = valid, O = 0u, O6 = 0u, O3 = 0u, Os = 0u, Os1 = 0u;
+    uint64_t hasext = 0;
+    uint32_t farw = 0u;
+    int farL = -1;
+    const int Lend = min(lmax, Ls + 1);
+    for (int L = 0; L < Lend; ++L) {
+      uint32_t D, Dn;
+      level(L, D, Dn);
+      if (L <= imax) {
+        if (__any((A & Dn) != 0u)) hasext |= 1ull << L;
+        if (L >= 1) {
+          const int lj = set_maxbit(A);
+          if (lane == 0) lat[L] = lj;
+        }
+      }
+      if (__any((A & farm) != 0u)) {
+        farw = A & farm;
+        farL = L;
+      }
+      const uint32_t An = A & D;
+      O = (O & D) | (A & Dn);
+      A = An;
+      const int L1 = L + 1;
+      if (L1 == Ls - 6) O6 = O;
+      if (L1 == Ls - 3) O3 = O;
+      if (L1 == Ls) Os = O;
+      if (L1 == Ls + 1) Os1 = O;
+    }
+    if (Lend == Ls && __any((A & farm) != 0u)) {  // L* = lmax: A_{L*} is still non-empty
+      farw = A & farm;
+      farL = Lend;
+    }
+
+    // members of a checkpoint set: bucket maxima, and (ev) the lifted keys per flip p
+    auto members = [&](uint32_t x, bool ev) __attribute__((always_inline)) {
+      while (__any(x != 0u)) {
+        if (x != 0u) {
+          const int bb = 31 - __clz(x);
+          x &= ~(1u << bb);
+          const int j = 32 * lane + bb;
+          const uint64_t hi = ((uint64_t)k0 << 32) | k1;
+          const uint64_t kwin = (hi << (31 - bb)) | (bb == 31 ? 0ull : ((uint64_t)k2 >> (bb + 1)));
+          const uint64_t xx = qwin ^ kwin;
+          const int c = clz64(xx);               // < cap for every member of O
+          const int e = clz64(xx << (c + 1));
+          const uint32_t key = ext_key(c, e, min(j + 1, lmax), j);
+          if (c <= imax) atomicMax(Nw + c, key);
+          const int p = j - c;
+          if (ev && key > best && !(p >= trunc_lo && p <= trunc_hi)) atomicMax(evt + p, key);
+        }
+      }
+    };
+    auto unresolved = [&]() __attribute__((always_inline)) -> uint64_t {
+      return __ballot(lane <= imax && ((hasext >> lane) & 1ull) && Nw[lane] == 0u);
+    };
+    members(Os | Os1, true);
+    uint64_t U = unresolved();
+    if (U && Ls - 3 >= 1) {
+      members(O3 & ~Os, false);
+      U = unresolved();
+      if (U && Ls - 6 >= 1) {
+        members(O6 & ~O3, false);
+        U = unresolved();
+      }
+    }
+    while (U) {  // buckets with every lifted length below the last checkpoint: own chain
+      const int i = __ffsll((long long)U) - 1;
+      U &= U - 1;
+      uint32_t Ai = valid, D, Dn;
+      for (int L = 0; L < i; ++L) {
+        level(L, D, Dn);
+        Ai &= D;
+      }
+      level(i, D, Dn);
+      uint32_t Tt = Ai & Dn;
+      int L = i + 1;
+      for (; L < lmax; ++L) {
+        level(L, D, Dn);
+        const uint32_t T2 = Tt & D;
+        if (!__any(T2 != 0u)) break;
+        Tt = T2;
+      }
+      const int jp = set_maxbit(Tt);
+      if (lane == 0) Nw[i] = mkkey(L, jp);
+    }
+
+    // q flips: one lane per offset i
+    if (lane <= imax) {
+      const int i = lane;
+      const uint32_t nb = ((hasext >> i) & 1ull) ? Nw[i] : (i >= 1 ? mkkey(i, lat[i]) : 0u);
+      const float s2 = sign_of(nb, vw);
+      if (s2 != sgn) atomicAdd(cq + (t - i), (s2 - sgn) * g);
+    }
+    Nw[lane] = 0u;
+
+    // k flips outside the best run: every event member checks whether it holds its flip's
+    // maximum; the holder adds the contribution and clears the entry
+    {
+      uint32_t x = Os1;
+      if (Ls >= 1) {
+        const int jb = jstar + 1 - 32 * lane;  // bits j > j* in this word
+        x |= Os & (jb <= 0 ? ~0u : (jb >= 32 ? 0u : ~0u << jb));
+      }
+      while (__any(x != 0u)) {
+        if (x != 0u) {
+          const int bb = 31 - __clz(x);
+          x &= ~(1u << bb);
+          const int j = 32 * lane + bb;
+          const uint64_t hi = ((uint64_t)k0 << 32) | k1;
+          const uint64_t kwin = (hi << (31 - bb)) | (bb == 31 ? 0ull : ((uint64_t)k2 >> (bb + 1)));
+          const uint64_t xx = qwin ^ kwin;
+          const int c = clz64(xx);
+          const int e = clz64(xx << (c + 1));
+          const uint32_t key = ext_key(c, e, min(j + 1, lmax), j);
+          const int p = j - c;
+          if (!(p >= trunc_lo && p <= trunc_hi) && evt[p] == key) {
+            evt[p] = 0u;
+            const float s2 = sign_of(key, vw);
+            if (s2 != sgn) atomicAdd(ck + p, (s2 - sgn) * g);
+          }
+        }
+      }
+    }
+
+    // k flips inside the best run, from the candidates near j*
+    if (jstar >= 0) {
+      const int near0 = jstar - 63;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int r = 2 * lane + h;
-        const int j2 = near0 + r;
-        kr[h] = 0u;
-        if (j2 >= jlo && j2 <= jhi) {
-          const int c2 = Cn[r];
-          kr[h] = mkkey(min(c2, min(j2 + 1, lmax)), j2);
-          cmax = max(cmax, c2);
+        const int r = 2 * lane + h, j2 = near0 + r;
+        if (j2 >= 0 && j2 < t) {
+          const uint64_t x2 = qwin ^ q_window(kw, j2);
+          const int c2 = clz64(x2);
+          Cn[r] = (uint8_t)c2;
+          En[r] = (uint8_t)(c2 < 63 ? clz64(x2 << (c2 + 1)) : 0);
         }
       }
-      uint32_t pre = max(kr[0], kr[1]), suf = pre;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t a = (uint32_t)__shfl_up((int)pre, d);
-        const uint32_t bb = (uint32_t)__shfl_down((int)suf, d);
-        const int cm = __shfl_xor(cmax, d);
-        if (lane >= d) pre = max(pre, a);
-        if (lane + d < 64) suf = max(suf, bb);
-        cmax = max(cmax, cm);
-      }
-      // inclusive prefix / suffix max per near index r
-      const uint32_t pre_prev = lane >= 1 ? (uint32_t)__shfl_up((int)pre, 1) : 0u;
-      const uint32_t suf_next = lane < 63 ? (uint32_t)__shfl_down((int)suf, 1) : 0u;
-      Pref[2 * lane] = max(pre_prev, kr[0]);
-      Pref[2 * lane + 1] = pre;
-      Suf[2 * lane] = suf;
-      Suf[2 * lane + 1] = max(suf_next, kr[1]);
-      const int p = trunc_lo + lane;
-      if (p <= trunc_hi) {
-        uint32_t nb = farbest;
-        const int rl = p - 1 - near0;          // near keys left of the flip
-        if (p - 1 >= jlo) nb = max(nb, Pref[rl]);
-        const int jend = min(jhi, p + cmax);   // candidates that can reach k[p]
-        if (jend + 1 <= jhi) nb = max(nb, Suf[jend + 1 - near0]);
-        for (int j2 = p; j2 <= jend; ++j2) {
-          const int r = j2 - near0;
-          const int c2 = Cn[r], e2 = En[r];
-          const int cap2 = min(j2 + 1, lmax);
-          const int d = j2 - p;
-          uint32_t k2;
-          if (d < min(c2, cap2)) k2 = mkkey(d, j2);
-          else if (d == c2 && c2 < cap2) k2 = ext_key(c2, e2, cap2, j2);
-          else k2 = mkkey(min(c2, cap2), j2);
-          nb = max(nb, k2);
-        }
-        const float s2 = sign_of(nb, vw);
-        if (s2 != sgn) atomicAdd(ck + p, (s2 - sgn) * g);
-      }
+      const uint32_t farbest = farL >= 0 ? mkkey(farL, set_maxbit(farw)) : 0u;
+      near_run_flips(lane, t, lmax, jstar, trunc_lo, trunc_hi, farbest, Cn, En, Pref, Suf, vw, sgn, g, ck);
     }
   }
   if (lane == 0) gps[wave] = gsum;
@@ -695,9 +956,14 @@ extern "C" int ksd_rosa_credits(const uint32_t *q_bits, const uint32_t *k_bits, 
   const size_t lds = (3 * (size_t)W + kCredWaves * (size_t)kCredWave32) * sizeof(uint32_t);
   if (lds > 64 * 1024) return fail(KSD_EINVAL, "rosa_credits: T too large for LDS");
   if (B * S > 0x7fffffff) return fail(KSD_EINVAL, "rosa_credits: too many streams");
-  hipLaunchKernelGGL(rosa_credits_kernel, dim3((unsigned)(B * S)), dim3(256), lds, (hipStream_t)stream,
-                     q_bits, k_bits, v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits,
-                     payload_partial);
+  if (T <= kBpMaxT)  // the bit-parallel kernel: one 32-candidate word per lane
+    hipLaunchKernelGGL(rosa_credits_bp_kernel, dim3((unsigned)(B * S)), dim3(256), 0, (hipStream_t)stream,
+                       q_bits, k_bits, v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits,
+                       payload_partial);
+  else
+    hipLaunchKernelGGL(rosa_credits_kernel, dim3((unsigned)(B * S)), dim3(256), lds, (hipStream_t)stream,
+                       q_bits, k_bits, v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits,
+                       payload_partial);
   return check_launch("rosa_credits");
 }
 

@@ -210,3 +210,61 @@ def test_rosa_mixer_eval_and_training():
     for name in ("payload", "q_proj.weight", "k_proj.weight", "v_proj.weight", "time_mix_q"):
         p = dict(m.named_parameters())[name]
         assert p.grad is not None and torch.isfinite(p.grad).all(), name
+
+
+def _credits_direct(q, k, v, gsign):
+    """ksd_rosa_credits on (n, T) bit streams, grad_sign (n, T): credits (n, 3, T)."""
+    from ksdraft_amd import _lib
+    n, T = q.shape
+    rng = np.random.default_rng(T)
+    proj = [_bits_to_proj(b, rng).T[None] for b in (q, k, v)]  # (1, T, n)
+    packed = [R.pack_bits(_g(p)).reshape(n, -1).contiguous() for p in proj]
+    _, mj = R.match_packed(*packed, T, want_j=True)
+    grad = _g(np.ascontiguousarray(gsign.T[None]))  # (1, T, n), payload 1
+    pay = torch.ones(n, device=DEV)
+    cred = torch.zeros((n, 3, T), device=DEV)
+    part = torch.empty((n,), device=DEV)
+    lmax = orr.default_max_match_len(T)
+    _lib.call("ksd_rosa_credits", packed[0].data_ptr(), packed[1].data_ptr(), packed[2].data_ptr(),
+              mj.contiguous().data_ptr(), grad.data_ptr(), pay.data_ptr(), 1, T, n, lmax,
+              cred.data_ptr(), part.data_ptr(), _lib.stream_ptr(torch.device(DEV)))
+    return cred.cpu().numpy()
+
+
+@pytest.mark.parametrize("T", [256, 300])
+def test_credits_structured_streams_bruteforce(T):
+    """Constant, periodic and varied-density streams (deep chains, buckets resolved by every
+    checkpoint and by their own chain) against the definition, every flip."""
+    rng = np.random.default_rng(1000 + T)
+    n = 16
+    q = _streams(rng, n, T)
+    k = np.concatenate([q[:5], _streams(rng, n - 5, T)])
+    k[5] = np.roll(q[5], 3)
+    v = _streams(rng, n, T)[::-1].copy()
+    gsign = rng.standard_normal((n, T)).astype(np.float32)
+    gsign[:, ::7] = 0.0  # positions whose gradient is zero contribute nothing
+    got = _credits_direct(q, k, v, gsign)
+    exp = orr.credits(q, k, v, gsign)
+    scale = np.abs(exp).max() + 1e-30
+    np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * scale)
+    assert np.array_equal(got == 0, exp == 0)
+
+
+def test_credits_t2100_sampled_flips():
+    """T above 2048 takes the candidate-per-lane kernel: sampled flips by definition."""
+    rng = np.random.default_rng(2100)
+    n, T = 2, 2100
+    q = _streams(rng, n, T)
+    k = np.concatenate([q[:1], _streams(rng, n - 1, T)])
+    v = _streams(rng, n, T)
+    gsign = rng.standard_normal((n, T)).astype(np.float32)
+    got = _credits_direct(q, k, v, gsign)
+    base, _, _ = orr.match(q, k, v)
+    for s in range(n):
+        for which in range(3):
+            for p in rng.choice(T, 5, replace=False):
+                fl = [b[s:s + 1].copy() for b in (q, k, v)]
+                fl[which][0, p] ^= 1
+                sp, _, _ = orr.match(*fl)
+                exp = float(((sp[0] - base[s]) * gsign[s].astype(np.float64)).sum())
+                assert abs(got[s, which, p] - exp) <= 1e-5 * max(1.0, abs(exp)), (s, which, p)
