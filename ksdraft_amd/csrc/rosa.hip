@@ -675,7 +675,7 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
 //    O_{L*+1} u (O_{L*} & {j > j*}) with j - c_j = p (a per-p table), if any.
 //  k flip inside the best run, and v flips: as in rosa_credits_kernel.
 constexpr int kBpMaxT = 2048;
-constexpr int kBpWave32 = 64 + 64 + kBpMaxT + kNear / 2 + 2 * kNear;  // u32 words per wave
+constexpr int kBpWave32 = 64 + 64 + kBpMaxT + 256;  // u32 words per wave
 
 __device__ __forceinline__ int set_maxbit(uint32_t word) {  // highest candidate of a wave set
   const uint64_t bal = __ballot(word != 0u);
@@ -683,6 +683,82 @@ __device__ __forceinline__ int set_maxbit(uint32_t word) {  // highest candidate
   const int hl = 63 - __clzll((long long)bal);
   const uint32_t hw = (uint32_t)__shfl((int)word, hl);
   return 32 * hl + 31 - __clz(hw);
+}
+
+// k flips inside the best run p in [trunc_lo, trunc_hi] (one lane per p, i = p - trunc_lo
+// < 62), from the near candidates j in [j* - 62, j* + 62] (two per lane). With a near
+// candidate's unchanged key K = (m, j), m = min(c, cap), a flip at p
+//   leaves K unchanged when p > j, or when p < s = j - m (+1 if the mismatch at j - m is
+//     the cap, which a flip there does not lift),
+//   truncates it to (j - p, j) when j - m < p <= j,
+//   lifts it to its extended key when p = j - c < j - m + 1, i.e. c < cap.
+// So the new best is the max of: the far best (farbest, no far key changes), the near keys
+// with j < p (prefix max), those with s > p (suffix max over s), the truncation (j_t - p,
+// j_t) with j_t the latest j >= j* whose run covers p (prefix max of j over run starts;
+// earlier j give smaller keys than j* itself), and the lifted keys with j - c = p. Each
+// term is a 64-entry table indexed by i, filled by scatter and scanned across the wave.
+__device__ __forceinline__ void near_flips_tables(int lane, int t, int lmax, int jstar, int trunc_lo,
+                                                  int trunc_hi, uint32_t farbest, uint64_t qwin,
+                                                  const uint32_t *kw, const uint32_t *vw, float sgn,
+                                                  float g, float *ck, uint32_t *tab) {
+  uint32_t *PK = tab, *SU = tab + 64, *TJ = tab + 128, *LF = tab + 192;
+  PK[lane] = 0u;  // PK[j - trunc_lo]: the key of j in the run
+  SU[lane] = 0u;
+  TJ[lane] = 0u;
+  LF[lane] = 0u;
+  __builtin_amdgcn_wave_barrier();
+  const int jlo = max(0, jstar - 62), jhi = min(t - 1, jstar + 62);
+  uint32_t always = farbest;  // keys no flip of the run changes: far, j < trunc_lo, s > trunc_hi + 1
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int j2 = jstar - 63 + 2 * lane + h;
+    if (j2 >= jlo && j2 <= jhi) {
+      const uint64_t x2 = qwin ^ q_window(kw, j2);
+      const int c2 = clz64(x2);
+      const int cap2 = min(j2 + 1, lmax);
+      const int m2 = min(c2, cap2);
+      const uint32_t key = mkkey(m2, j2);
+      const bool lift = c2 < cap2;
+      const int su = lift ? j2 - m2 : j2 - m2 + 1;
+      if (j2 < trunc_lo || su > trunc_hi + 1) always = max(always, key);
+      else if (su > trunc_lo) atomicMax(SU + su - trunc_lo, key);
+      if (j2 >= trunc_lo && j2 <= trunc_hi) PK[j2 - trunc_lo] = key;
+      const int sr = j2 - m2 + 1;
+      if (j2 >= jstar && sr <= trunc_hi) atomicMax(TJ + max(sr, trunc_lo) - trunc_lo, (uint32_t)(j2 + 1));
+      const int pl = j2 - c2;
+      if (lift && pl >= trunc_lo && pl <= trunc_hi)
+        atomicMax(LF + pl - trunc_lo, ext_key(c2, clz64(x2 << (c2 + 1)), cap2, j2));
+    }
+  }
+  // wave max of `always`: rows of 16 by DPP, then the four row results
+  always = group_max_u32<16>(always);
+  always = max(max((uint32_t)__builtin_amdgcn_readlane((int)always, 0), (uint32_t)__builtin_amdgcn_readlane((int)always, 16)),
+               max((uint32_t)__builtin_amdgcn_readlane((int)always, 32), (uint32_t)__builtin_amdgcn_readlane((int)always, 48)));
+  __builtin_amdgcn_wave_barrier();
+  uint32_t pk = lane >= 1 ? PK[lane - 1] : 0u;  // j < p: entries .. i - 1
+  uint32_t tj = TJ[lane];
+  uint32_t su = lane < 63 ? SU[lane + 1] : 0u;  // s > p: entries i + 1 ..
+  const uint32_t lf = LF[lane];
+  // prefix max of pk and tj, suffix max of su; every shuffle runs with all lanes active
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t a = (uint32_t)__shfl_up((int)pk, d);
+    const uint32_t b = (uint32_t)__shfl_up((int)tj, d);
+    const uint32_t c = (uint32_t)__shfl_down((int)su, d);
+    if (lane >= d) {
+      pk = max(pk, a);
+      tj = max(tj, b);
+    }
+    if (lane + d < 64) su = max(su, c);
+  }
+  const int p = trunc_lo + lane;
+  if (p <= trunc_hi) {
+    const int jt = (int)tj - 1;  // >= j*: j* covers every p of its run
+    uint32_t nb = max(max(always, pk), max(su, lf));
+    nb = max(nb, mkkey(jt - p, jt));
+    const float s2 = sign_of(nb, vw);
+    if (s2 != sgn) atomicAdd(ck + p, (s2 - sgn) * g);
+  }
 }
 
 __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
@@ -697,8 +773,7 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
   uint32_t *Nw = wsm[wave];                       // [64] best lifted key per bucket
   int *lat = (int *)(Nw + 64);                    // [64] latest j of A_i
   uint32_t *evt = Nw + 128;                       // [kBpMaxT] best lifted key per flip p
-  uint8_t *Cn = (uint8_t *)(evt + kBpMaxT), *En = Cn + kNear;
-  uint32_t *Pref = evt + kBpMaxT + kNear / 2, *Suf = Pref + kNear;
+  uint32_t *ntab = evt + kBpMaxT;                 // [256] near-flip tables
   const int64_t stream = blockIdx.x;
   const int64_t b = stream / S, s = stream % S;
   for (int i = threadIdx.x; i < 64; i += 256) {
@@ -710,7 +785,8 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
   __syncthreads();
   // this lane's k words: word w and the two below it (zeros before position 0)
   const uint32_t k0 = kw[lane], k1 = lane >= 1 ? kw[lane - 1] : 0u, k2 = lane >= 2 ? kw[lane - 2] : 0u;
-  const bool w0 = lane == 0, w1 = lane == 1;
+  const uint64_t k01 = ((uint64_t)k0 << 32) | k1, k12 = ((uint64_t)k1 << 32) | k2;
+  const int lane32 = 32 * lane;
   float *cq = cred + stream * 3 * T, *ck = cq + T, *cv = cq + 2 * T;
   const float pay = payload[s];
   float gsum = 0.0f;
@@ -744,14 +820,16 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
       const int a = max(lo - w0b, 0), e = min(hi - w0b, 31);        // its bits in this word
       if (a <= e) farm = ~(((e - a == 31) ? ~0u : ((2u << (e - a)) - 1u)) << a);
     }
-    // D_L and its complement {j >= L : mismatch at L} for this lane
+    // D_L and its complement {j >= L : mismatch at L} for this lane, without branches
+    // (L is wave-uniform): k[j - L] for the word's 32 j is one funnel shift of the word
+    // pair (k0:k1) or (k1:k2), and {j >= L} is ~0 shifted by L - 32 * lane clamped to
+    // [0, 32]
     auto level = [&](int L, uint32_t &D, uint32_t &Dn) __attribute__((always_inline)) {
-      const uint32_t KL = L == 0 ? k0 : (L <= 32 ? __builtin_amdgcn_alignbit(k0, k1, 32 - L)
-                                                 : __builtin_amdgcn_alignbit(k1, k2, 64 - L));
-      const uint32_t p0 = L < 32 ? ~0u << L : 0u, p1 = L <= 32 ? ~0u : ~0u << (L - 32);
-      const uint32_t pos = w0 ? p0 : (w1 ? p1 : ~0u);
-      const bool qbit = (qwin >> (63 - L)) & 1ull;
-      D = (qbit ? KL : ~KL) & pos;
+      const bool hi = L > 32;
+      const uint32_t KL = (uint32_t)((hi ? k12 : k01) >> ((hi ? 64 : 32) - L));
+      const uint32_t pos = (uint32_t)(~0ull << min(max(L - lane32, 0), 32));
+      const uint32_t qm = 0u - (uint32_t)((qwin >> (63 - L)) & 1ull);  // q[t - L] ? ~0 : 0
+      D = (KL ^ ~qm) & pos;
       Dn = pos & ~D;
     };
 
@@ -766,7 +844,7 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
       level(L, D, Dn);
       if (L <= imax) {
         if (__any((A & Dn) != 0u)) hasext |= 1ull << L;
-        if (L >= 1) {
+        if (L >= 1 && L >= Ls - 2) {  // lower levels: recomputed below when needed
           const int lj = set_maxbit(A);
           if (lane == 0) lat[L] = lj;
         }
@@ -811,13 +889,28 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
     auto unresolved = [&]() __attribute__((always_inline)) -> uint64_t {
       return __ballot(lane <= imax && ((hasext >> lane) & 1ull) && Nw[lane] == 0u);
     };
+    // candidates that mismatch at one of the offsets i < lc of the buckets u: a member of
+    // a checkpoint set O_lc has one mismatch, at its bucket c < lc, so this mask keeps
+    // every member of those buckets (members of other buckets only repeat a max)
+    auto bucket_mask = [&](uint64_t u, int lc) __attribute__((always_inline)) -> uint32_t {
+      u &= (1ull << lc) - 1ull;  // 1 <= lc <= 62
+      uint32_t msk = 0u;
+      while (u) {
+        const int i = __ffsll((long long)u) - 1;
+        u &= u - 1;
+        uint32_t D, Dn;
+        level(i, D, Dn);
+        msk |= Dn;
+      }
+      return msk;
+    };
     members(Os | Os1, true);
     uint64_t U = unresolved();
     if (U && Ls - 3 >= 1) {
-      members(O3 & ~Os, false);
+      members(O3 & ~Os & bucket_mask(U, Ls - 3), false);
       U = unresolved();
       if (U && Ls - 6 >= 1) {
-        members(O6 & ~O3, false);
+        members(O6 & ~O3 & bucket_mask(U, Ls - 6), false);
         U = unresolved();
       }
     }
@@ -840,6 +933,22 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
       }
       const int jp = set_maxbit(Tt);
       if (lane == 0) Nw[i] = mkkey(L, jp);
+    }
+
+    // latest j of A_i for the buckets 1 <= i < L* - 2 without an extension
+    if (Ls - 3 >= 1) {
+      uint64_t M = ~hasext & (((1ull << min(imax, Ls - 3)) - 1ull) << 1);
+      while (M) {
+        const int i = __ffsll((long long)M) - 1;
+        M &= M - 1;
+        uint32_t Ai = valid, D, Dn;
+        for (int L = 0; L < i; ++L) {
+          level(L, D, Dn);
+          Ai &= D;
+        }
+        const int lj = set_maxbit(Ai);
+        if (lane == 0) lat[i] = lj;
+      }
     }
 
     // q flips: one lane per offset i
@@ -882,19 +991,8 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
 
     // k flips inside the best run, from the candidates near j*
     if (jstar >= 0) {
-      const int near0 = jstar - 63;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int r = 2 * lane + h, j2 = near0 + r;
-        if (j2 >= 0 && j2 < t) {
-          const uint64_t x2 = qwin ^ q_window(kw, j2);
-          const int c2 = clz64(x2);
-          Cn[r] = (uint8_t)c2;
-          En[r] = (uint8_t)(c2 < 63 ? clz64(x2 << (c2 + 1)) : 0);
-        }
-      }
       const uint32_t farbest = farL >= 0 ? mkkey(farL, set_maxbit(farw)) : 0u;
-      near_run_flips(lane, t, lmax, jstar, trunc_lo, trunc_hi, farbest, Cn, En, Pref, Suf, vw, sgn, g, ck);
+      near_flips_tables(lane, t, lmax, jstar, trunc_lo, trunc_hi, farbest, qwin, kw, vw, sgn, g, ck, ntab);
     }
   }
   if (lane == 0) gps[wave] = gsum;
