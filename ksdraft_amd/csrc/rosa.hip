@@ -19,6 +19,8 @@
 // non-empty length is the best length and its highest surviving j the latest endpoint.
 // Candidates are walked in chunks of kCH words; each chunk carries two words of halo to
 // its left so every chain j'..j'+61 of its own candidates lies inside the chunk.
+#include <type_traits>
+
 #include "ksd_common.h"
 
 namespace ksd {
@@ -786,7 +788,10 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
   // this lane's k words: word w and the two below it (zeros before position 0)
   const uint32_t k0 = kw[lane], k1 = lane >= 1 ? kw[lane - 1] : 0u, k2 = lane >= 2 ? kw[lane - 2] : 0u;
   const uint64_t k01 = ((uint64_t)k0 << 32) | k1, k12 = ((uint64_t)k1 << 32) | k2;
-  const int lane32 = 32 * lane;
+  // {j >= L} for this lane's word as the low 32 bits of p01 >> (32 - L) (L <= 32) or
+  // p12 >> (64 - L) (L > 32): only words 0 and 1 hold positions below 63
+  const uint64_t p01 = lane == 0 ? ~0ull << 32 : ~0ull;
+  const uint64_t p12 = lane == 0 ? 0ull : (lane == 1 ? ~0ull << 32 : ~0ull);
   float *cq = cred + stream * 3 * T, *ck = cq + T, *cv = cq + 2 * T;
   const float pay = payload[s];
   float gsum = 0.0f;
@@ -822,49 +827,79 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
     }
     // D_L and its complement {j >= L : mismatch at L} for this lane, without branches
     // (L is wave-uniform): k[j - L] for the word's 32 j is one funnel shift of the word
-    // pair (k0:k1) or (k1:k2), and {j >= L} is ~0 shifted by L - 32 * lane clamped to
-    // [0, 32]
-    auto level = [&](int L, uint32_t &D, uint32_t &Dn) __attribute__((always_inline)) {
-      const bool hi = L > 32;
-      const uint32_t KL = (uint32_t)((hi ? k12 : k01) >> ((hi ? 64 : 32) - L));
-      const uint32_t pos = (uint32_t)(~0ull << min(max(L - lane32, 0), 32));
+    // pair (k0:k1) for L <= 32 or (k1:k2) above, and {j >= L} the same shift of a per-lane
+    // constant pair (HI picks the pair at compile time where the level range is known)
+    auto level_c = [&](auto hi_c, int L, uint32_t &D, uint32_t &Dn) __attribute__((always_inline)) {
+      constexpr bool HI = decltype(hi_c)::value;
+      const int sh = (HI ? 64 : 32) - L;
+      const uint32_t KL = (uint32_t)((HI ? k12 : k01) >> sh);
+      const uint32_t pos = (uint32_t)((HI ? p12 : p01) >> sh);
       const uint32_t qm = 0u - (uint32_t)((qwin >> (63 - L)) & 1ull);  // q[t - L] ? ~0 : 0
       D = (KL ^ ~qm) & pos;
       Dn = pos & ~D;
     };
+    auto level = [&](int L, uint32_t &D, uint32_t &Dn) __attribute__((always_inline)) {
+      if (L > 32) level_c(std::true_type{}, L, D, Dn);
+      else level_c(std::false_type{}, L, D, Dn);
+    };
 
-    // ascending pass over the levels 0 .. min(lmax, L* + 1) - 1
+    // ascending pass over the levels 0 .. min(lmax, L* + 1) - 1: the levels below
+    // L* - 7 only advance A, O and the extension flags; the last eight (unrolled) also
+    // record the checkpoints O_{L*-6}, O_{L*-3}, O_{L*}, O_{L*+1}, the latest j of A_L
+    // for L >= L* - 2, and the far candidates
     uint32_t A = valid, O = 0u, O6 = 0u, O3 = 0u, Os = 0u, Os1 = 0u;
     uint64_t hasext = 0;
     uint32_t farw = 0u;
     int farL = -1;
     const int Lend = min(lmax, Ls + 1);
-    for (int L = 0; L < Lend; ++L) {
+    const int L0 = min(max(0, Ls - 7), Lend);
+    auto step = [&](auto hi_c, int L, bool tail) __attribute__((always_inline)) {
       uint32_t D, Dn;
-      level(L, D, Dn);
-      if (L <= imax) {
-        if (__any((A & Dn) != 0u)) hasext |= 1ull << L;
-        if (L >= 1 && L >= Ls - 2) {  // lower levels: recomputed below when needed
+      level_c(hi_c, L, D, Dn);
+      if (L <= imax && __any((A & Dn) != 0u)) hasext |= 1ull << L;
+      if (tail) {
+        if (L >= 1 && L >= Ls - 2 && L <= imax) {  // lower levels: recomputed below when needed
           const int lj = set_maxbit(A);
           if (lane == 0) lat[L] = lj;
         }
+        if (__any((A & farm) != 0u)) {
+          farw = A & farm;
+          farL = L;
+        }
       }
-      if (__any((A & farm) != 0u)) {
-        farw = A & farm;
-        farL = L;
-      }
-      const uint32_t An = A & D;
       O = (O & D) | (A & Dn);
-      A = An;
-      const int L1 = L + 1;
-      if (L1 == Ls - 6) O6 = O;
-      if (L1 == Ls - 3) O3 = O;
-      if (L1 == Ls) Os = O;
-      if (L1 == Ls + 1) Os1 = O;
+      A &= D;
+    };
+    int Lm = 0;
+    for (; Lm < min(L0, 33); ++Lm) step(std::false_type{}, Lm, false);
+    for (; Lm < L0; ++Lm) step(std::true_type{}, Lm, false);
+    const bool far_below = L0 > 0 && !__any((A & farm) != 0u);  // far best below the tail
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) {
+      const int Lt = Ls - 7 + s8;
+      if (Lt >= 0 && Lt < Lend) {  // wave-uniform
+        if (Lt > 32) step(std::true_type{}, Lt, true);
+        else step(std::false_type{}, Lt, true);
+        if (s8 == 0) O6 = O;
+        if (s8 == 3) O3 = O;
+        if (s8 == 6) Os = O;
+        if (s8 == 7) Os1 = O;
+      }
     }
     if (Lend == Ls && __any((A & farm) != 0u)) {  // L* = lmax: A_{L*} is still non-empty
       farw = A & farm;
       farL = Lend;
+    }
+    if (far_below && __any((valid & farm) != 0u)) {  // the far candidates' own chain:
+      uint32_t Af = valid & farm, D, Dn;               // the last level where any survives
+      int L = 0;
+      for (; L < L0; ++L) {
+        level(L, D, Dn);
+        if (!__any((Af & D) != 0u)) break;
+        Af &= D;
+      }
+      farw = Af;
+      farL = L;
     }
 
     // members of a checkpoint set: bucket maxima, and (ev) the lifted keys per flip p
