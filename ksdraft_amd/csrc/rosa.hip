@@ -687,6 +687,20 @@ __device__ __forceinline__ int set_maxbit(uint32_t word) {  // highest candidate
   return 32 * hl + 31 - __clz(hw);
 }
 
+// Inclusive prefix max over the wave's 64 lanes by DPP (all lanes active): shifts by 1, 2,
+// 4 and 8 within each row of 16, then the last lane of rows 0 and 2 into rows 1 and 3
+// (row_bcast:15), then lane 31 into rows 2 and 3 (row_bcast:31). A lane without a source
+// reads 0, the identity of the max over unsigned keys.
+__device__ __forceinline__ uint32_t wave_prefix_max(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false));
+  return v;
+}
+
 // k flips inside the best run p in [trunc_lo, trunc_hi] (one lane per p, i = p - trunc_lo
 // < 62), from the near candidates j in [j* - 62, j* + 62] (two per lane). With a near
 // candidate's unchanged key K = (m, j), m = min(c, cap), a flip at p
@@ -737,22 +751,13 @@ __device__ __forceinline__ void near_flips_tables(int lane, int t, int lmax, int
   always = max(max((uint32_t)__builtin_amdgcn_readlane((int)always, 0), (uint32_t)__builtin_amdgcn_readlane((int)always, 16)),
                max((uint32_t)__builtin_amdgcn_readlane((int)always, 32), (uint32_t)__builtin_amdgcn_readlane((int)always, 48)));
   __builtin_amdgcn_wave_barrier();
-  uint32_t pk = lane >= 1 ? PK[lane - 1] : 0u;  // j < p: entries .. i - 1
-  uint32_t tj = TJ[lane];
-  uint32_t su = lane < 63 ? SU[lane + 1] : 0u;  // s > p: entries i + 1 ..
+  // prefix max of PK (j < p: entries .. i - 1) and TJ; the suffix max of SU (s > p:
+  // entries i + 1 ..) as a prefix max over the reversed table, turned back by one shuffle
+  const uint32_t pk = wave_prefix_max(lane >= 1 ? PK[lane - 1] : 0u);
+  const uint32_t tj = wave_prefix_max(TJ[lane]);
+  const uint32_t sr = wave_prefix_max(lane >= 1 ? SU[64 - lane] : 0u);
+  const uint32_t su = (uint32_t)__shfl((int)sr, 63 - lane);
   const uint32_t lf = LF[lane];
-  // prefix max of pk and tj, suffix max of su; every shuffle runs with all lanes active
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t a = (uint32_t)__shfl_up((int)pk, d);
-    const uint32_t b = (uint32_t)__shfl_up((int)tj, d);
-    const uint32_t c = (uint32_t)__shfl_down((int)su, d);
-    if (lane >= d) {
-      pk = max(pk, a);
-      tj = max(tj, b);
-    }
-    if (lane + d < 64) su = max(su, c);
-  }
   const int p = trunc_lo + lane;
   if (p <= trunc_hi) {
     const int jt = (int)tj - 1;  // >= j*: j* covers every p of its run
