@@ -683,7 +683,7 @@ __device__ __forceinline__ int set_maxbit(uint32_t word) {  // highest candidate
   const uint64_t bal = __ballot(word != 0u);
   if (bal == 0) return -1;
   const int hl = 63 - __clzll((long long)bal);
-  const uint32_t hw = (uint32_t)__shfl((int)word, hl);
+  const uint32_t hw = (uint32_t)__builtin_amdgcn_readlane((int)word, hl);  // hl is wave-uniform
   return 32 * hl + 31 - __clz(hw);
 }
 
@@ -954,40 +954,40 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
         U = unresolved();
       }
     }
-    while (U) {  // buckets with every lifted length below the last checkpoint: own chain
-      const int i = __ffsll((long long)U) - 1;
-      U &= U - 1;
-      uint32_t Ai = valid, D, Dn;
-      for (int L = 0; L < i; ++L) {
-        level(L, D, Dn);
-        Ai &= D;
-      }
-      level(i, D, Dn);
-      uint32_t Tt = Ai & Dn;
-      int L = i + 1;
-      for (; L < lmax; ++L) {
-        level(L, D, Dn);
-        const uint32_t T2 = Tt & D;
-        if (!__any(T2 != 0u)) break;
-        Tt = T2;
-      }
-      const int jp = set_maxbit(Tt);
-      if (lane == 0) Nw[i] = mkkey(L, jp);
-    }
-
-    // latest j of A_i for the buckets 1 <= i < L* - 2 without an extension
-    if (Ls - 3 >= 1) {
-      uint64_t M = ~hasext & (((1ull << min(imax, Ls - 3)) - 1ull) << 1);
-      while (M) {
-        const int i = __ffsll((long long)M) - 1;
-        M &= M - 1;
-        uint32_t Ai = valid, D, Dn;
-        for (int L = 0; L < i; ++L) {
-          level(L, D, Dn);
-          Ai &= D;
+    // Two kinds of bucket i need A_i again, walked in ascending i along one chain:
+    //  U: buckets with every lifted length below the last checkpoint; their candidates
+    //     A_i & Dn_i extended level by level until none survives;
+    //  M: buckets 1 <= i < L* - 2 without an extension (disjoint from U), for the latest
+    //     j of A_i.
+    const uint64_t M = Ls - 3 >= 1 ? ~hasext & (((1ull << min(imax, Ls - 3)) - 1ull) << 1) : 0ull;
+    {
+      uint64_t W = U | M;
+      uint32_t Ach = valid;  // A_Lch
+      int Lch = 0;
+      while (W) {
+        const int i = __ffsll((long long)W) - 1;
+        W &= W - 1;
+        uint32_t D, Dn;
+        for (; Lch < i; ++Lch) {
+          level(Lch, D, Dn);
+          Ach &= D;
         }
-        const int lj = set_maxbit(Ai);
-        if (lane == 0) lat[i] = lj;
+        if ((M >> i) & 1ull) {
+          const int lj = set_maxbit(Ach);
+          if (lane == 0) lat[i] = lj;
+          continue;
+        }
+        level(i, D, Dn);
+        uint32_t Tt = Ach & Dn;
+        int L = i + 1;
+        for (; L < lmax; ++L) {
+          level(L, D, Dn);
+          const uint32_t T2 = Tt & D;
+          if (!__any(T2 != 0u)) break;
+          Tt = T2;
+        }
+        const int jp = set_maxbit(Tt);
+        if (lane == 0) Nw[i] = mkkey(L, jp);
       }
     }
 
