@@ -60,6 +60,7 @@ def parse():
     p.add_argument("--no-ks3", action="store_true", help="skip the KS3 kernel report")
     p.add_argument("--no-rosa", action="store_true", help="skip the Rosa kernel report")
     p.add_argument("--no-c3", action="store_true", help="skip the config-3 LM-head report")
+    p.add_argument("--no-ln", action="store_true", help="skip the fused LayerNorm + quantize report")
     p.add_argument("--pmc-probe", action="store_true",
                    help="for rocprofv3 --pmc runs: a 256 MiB device copy (counter "
                         "calibration), then 3 launches of each GEMM of the step; no timing")
@@ -374,6 +375,39 @@ def rosa_kernel_times(dev, reps):
     return res
 
 
+def ln_quant_times(dev, reps):
+    """The fused pre-norm + A-operand quantization at BASELINE config 4's activation shape
+    (M = B*T = 8192 rows, d = 1536): nn.LayerNorm (model/block.py:27-41) then
+    quantize_last_dim (kernels/linear.py:69) in one pass, against torch's LayerNorm
+    followed by the library quantizer. x ~N(0,1), weight ~1, bias ~0. Bytes: read x, write
+    the int8 codes and fp16 scales."""
+    from ksdraft_amd.kernels import quant as kq
+    import torch.nn.functional as F
+    M, d = 8192, 1536
+    g = torch.Generator().manual_seed(0)
+    x32 = torch.randn(M, d, generator=g).to(dev)
+    w = (1.0 + 0.1 * torch.randn(d, generator=g)).to(dev)
+    b = (0.1 * torch.randn(d, generator=g)).to(dev)
+    res = {}
+    for tag, x in (("f32", x32), ("bf16", x32.to(torch.bfloat16))):
+        nbytes = M * d * x.element_size() + M * d + 2 * M * (d // 128)
+        stages = {
+            f"ln_quantize_{tag}": lambda x=x: kq.layer_norm_quantize(x, w, b),
+            f"cmp_torch_layer_norm_then_quantize_{tag}":
+                lambda x=x: kq.quantize_last_dim(F.layer_norm(x, (d,), w.to(x.dtype), b.to(x.dtype))),
+        }
+        for name, fn in stages.items():
+            def rep(fn=fn):
+                for _ in range(reps):
+                    fn()
+            _, _, ms = time_graph(rep, 3, warm=1)
+            us = ms * 1e3 / reps
+            res[name] = {"us": round(us, 3), "bytes": nbytes,
+                         "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                         "hbm_frac": round(nbytes / (us * 1e-6) / PEAK_HBM, 3)}
+    return res
+
+
 def cpu_baseline(x, w, dy, budget_s):
     """The oracle's restatement of the reference CPU path (quantize in numpy; GEMMs as
     dequantize + fp32 BLAS matmul, reference ksdraft/kernels/gemm.py:76-82), timed on
@@ -506,6 +540,7 @@ def main():
         "ks3_c4_kernels": None if args.no_ks3 else ks3_kernel_times(dev, args.kernel_reps),
         "rosa_c4_kernels": None if args.no_rosa else rosa_kernel_times(dev, args.kernel_reps),
         "lmhead_c3": None if args.no_c3 else lmhead_c3_times(dev, 3),
+        "ln_quant_c4": None if args.no_ln else ln_quant_times(dev, args.kernel_reps),
         "roofline": {
             "kernel": "ksd::g128::gemm_g128_kernel<f32> (fwd, dX, dW launches averaged)",
             "bound": "mfma",

@@ -162,6 +162,23 @@ int ksd_adamw_requant(float *param, const float *grad, float *exp_avg, float *ex
                       uint16_t *scales, void *stream);
 
 /*
+ * LayerNorm forward fused with the GS128 quantization of its output: the pre-norm of
+ * every block (reference ksdraft/model/block.py:27-41, nn.LayerNorm ln_attn / ln_ffn)
+ * followed by the Int8Linear A-operand quantization (ksdraft/kernels/linear.py:69,
+ * quantize_last_dim). No reference counterpart as one call.
+ *   x       (rows, d) of type x_dtype, row stride x_stride elements; 1 <= d <= 4096
+ *   weight, bias  (d,) fp32 or NULL (weight 1, bias 0: elementwise_affine=False)
+ *   y = (x - mean) * rstd * weight + bias, rstd = 1 / sqrt(biased var + eps), computed in
+ *           fp32 and rounded to x_dtype; codes/scales = quantize_last_dim(y, 128):
+ *   codes   (rows, d) int8; scales (rows, ceil(d/128)) fp16; group must be 128
+ *   y_out   NULL or (rows, d) of x_dtype; mean_out, rstd_out NULL or (rows,) fp32
+ */
+int ksd_layernorm_quant(const void *x, int x_dtype, int64_t rows, int64_t d, int64_t x_stride,
+                        const float *weight, const float *bias, float eps, int group,
+                        int8_t *codes, uint16_t *scales, void *y_out, float *mean_out,
+                        float *rstd_out, void *stream);
+
+/*
  * G1 / G2 — W8A8 GEMM, "NT" layout: Y = dequant(A) . dequant(W)^T with the ordered
  * per-group contract
  *     acc = 0;  for g in 0..K/group-1:  acc = fmaf(float(P_g), sa[m,g]*sw[n,g], acc)

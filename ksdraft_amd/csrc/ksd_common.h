@@ -279,6 +279,13 @@ __device__ __forceinline__ void cvt_raw8(const Raw8<DT> &r, bool ok, float *v) {
   }
 }
 
+// An fp32 value rounded to the element type DT and back (identity for fp32).
+template <int DT>
+__device__ __forceinline__ float round_to_dt(float v);
+template <> __device__ __forceinline__ float round_to_dt<KSD_F32>(float v) { return v; }
+template <> __device__ __forceinline__ float round_to_dt<KSD_BF16>(float v) { return bf16_round(v); }
+template <> __device__ __forceinline__ float round_to_dt<KSD_F16>(float v) { return f16_round(v); }
+
 // Store one fp32 value as the output element type.
 template <int DT> __device__ __forceinline__ void store_out(void *y, int64_t idx, float v);
 template <> __device__ __forceinline__ void store_out<KSD_F32>(void *y, int64_t idx, float v) {

@@ -26,11 +26,6 @@
 namespace ksd {
 
 // ---------------------------------------------------------------- shift + quantize
-template <int DT>
-__device__ __forceinline__ float round_to_dt(float v);
-template <> __device__ __forceinline__ float round_to_dt<KSD_F32>(float v) { return v; }
-template <> __device__ __forceinline__ float round_to_dt<KSD_BF16>(float v) { return bf16_round(v); }
-template <> __device__ __forceinline__ float round_to_dt<KSD_F16>(float v) { return f16_round(v); }
 
 // Load 8 consecutive features of a row as fp32 (k0 + 8 <= d on the vector path).
 template <int DT, bool VEC>

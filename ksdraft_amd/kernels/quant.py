@@ -170,3 +170,53 @@ def requant_transpose(codes: torch.Tensor, scales: torch.Tensor,
     _lib.call("ksd_requant_transpose", codes.data_ptr(), scales.data_ptr(), R, C, group_in,
               group, out_c.data_ptr(), out_s.data_ptr(), _lib.stream_ptr(dev))
     return out_c, out_s
+
+
+def layer_norm_quantize(x: torch.Tensor, weight: torch.Tensor | None = None,
+                        bias: torch.Tensor | None = None, eps: float = 1e-5,
+                        group: int = GROUP_SIZE, return_y: bool = False,
+                        return_stats: bool = False):
+    """F.layer_norm(x, (d,), weight, bias, eps) followed by quantize_last_dim(., group), in
+    one pass over x: the pre-norm of a block (reference ksdraft/model/block.py:27-41)
+    producing the A operand of the Int8Linear after it (kernels/linear.py:69).
+
+    y is computed in fp32 from x's values and rounded to x's dtype, the dtype torch's
+    LayerNorm returns; the codes are quantize_last_dim of that y. Returns (codes, scales),
+    then y if return_y, then (mean, rstd) fp32 per row if return_stats. d <= 4096, group 128.
+    """
+    x = _float_input(x)
+    if group != 128:
+        raise ValueError(f"layer_norm_quantize supports group 128, got {group}")
+    d = x.shape[-1] if x.dim() else 0
+    if d < 1 or d > 4096:
+        raise ValueError(f"layer_norm_quantize supports 1 <= d <= 4096, got {d}")
+    dev = _lib.require_gpu(x, *(t for t in (weight, bias) if t is not None))
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, d)
+    rows = x2.shape[0]
+    if x2.stride(-1) != 1 or (rows > 1 and x2.stride(0) < d):
+        x2 = x2.contiguous()
+    params = []
+    for name, p in (("weight", weight), ("bias", bias)):
+        if p is not None:
+            if p.shape != (d,):
+                raise ValueError(f"{name} must have shape ({d},), got {tuple(p.shape)}")
+            p = p.detach().to(device=dev, dtype=torch.float32).contiguous()
+        params.append(p)
+    ng = -(-d // group)
+    codes = torch.empty((rows, d), dtype=torch.int8, device=dev)
+    scales = torch.empty((rows, ng), dtype=SCALE_DTYPE, device=dev)
+    y = torch.empty((rows, d), dtype=x2.dtype, device=dev) if return_y else None
+    mean = torch.empty(rows, dtype=torch.float32, device=dev) if return_stats else None
+    rstd = torch.empty(rows, dtype=torch.float32, device=dev) if return_stats else None
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    stride = x2.stride(0) if rows > 1 else d
+    _lib.call("ksd_layernorm_quant", x2.data_ptr(), _lib.dtype_code(x2.dtype), rows, d, stride,
+              ptr(params[0]), ptr(params[1]), float(eps), group, codes.data_ptr(),
+              scales.data_ptr(), ptr(y), ptr(mean), ptr(rstd), _lib.stream_ptr(dev))
+    out = (codes.reshape(*lead, d), scales.reshape(*lead, ng))
+    if return_y:
+        out += (y.reshape(*lead, d),)
+    if return_stats:
+        out += (mean.reshape(lead), rstd.reshape(lead))
+    return out
