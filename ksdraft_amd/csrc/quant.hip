@@ -609,11 +609,27 @@ static void launch_rows(const void *x, int64_t rows, int64_t K, int64_t stride,
 // 512 s + 8 l .. 512 s + 8 l + 7 of slice s < NS (d <= 512 NS <= 4096, the row in
 // registers). The lane's weight and bias columns are loaded once per wave, and the next
 // row's x while the current one is reduced. mean and the biased variance are fp32 with
-// two passes and butterfly sums, so every lane holds the same bits; y = (x - mean) * rstd *
+// two passes and DPP wave sums, so every lane holds the same bits; y = (x - mean) * rstd *
 // w + b, rounded to x's dtype (torch's LayerNorm output dtype), is quantized exactly as
 // quant_rows_kernel does. VEC: d % 8 == 0 and 16-byte aligned rows, weight and bias.
 constexpr int kLnSlices = 8;  // d <= 512 * kLnSlices
 constexpr int kLnRows = 2;    // rows per wave
+
+// Sum over the wave's 64 lanes, the same bits in every lane (all lanes active): within
+// each row of 16 by DPP (pairs, quads, half-rows, rows: each step adds the partner's
+// partial, which holds the same set of lanes), then the four row sums in a fixed order.
+__device__ __forceinline__ float ln_wave_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
+}
 
 template <int DT, bool VEC>
 __device__ __forceinline__ void ln_load_x(const typename Elem<DT>::T *xr, int k0, int d, float *v) {
@@ -676,8 +692,7 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(
 #pragma unroll
       for (int s = 0; s < NS; ++s) ln_load_x<DT, VEC>((const T *)xv + rn * stride, s * 512 + lane * 8, d, xn[s]);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    sum = ln_wave_sum(sum);
     const float mean = sum / (float)d;
     float sq = 0.0f;
 #pragma unroll
@@ -688,8 +703,7 @@ __global__ __launch_bounds__(256) void ln_quant_kernel(
         sq += c * c;
       }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
+    sq = ln_wave_sum(sq);
     const float rstd = 1.0f / sqrtf(sq / (float)d + eps);
     if (lane == 0) {
       if (mean_out) mean_out[row] = mean;
