@@ -367,6 +367,90 @@ __global__ __launch_bounds__(512) void quant_dual_kernel(
   }
 }
 
+// Dual-layout quantization of an X operand (the T_FROM_CODES recipe quant(dequant(quant(
+// X))^T)) with a small LDS tile: as quant_dual_kernel, but the transposed tile holds the
+// row codes as int8, column-major with a 132-byte pitch (an odd word stride: at most 2-way
+// bank conflicts on the byte writes and the dword reads), and the 128 row scales; 17.4 KB
+// instead of 74 KB, so four blocks fit a CU. The column pass dequantizes code * scale
+// (exact in fp32, as in quant_dual_kernel) before its amax and codes.
+template <int DT>
+__global__ __launch_bounds__(512) void quant_dual_codes_kernel(
+    const void *__restrict__ xv, int64_t R, int64_t C, int8_t *__restrict__ codes,
+    uint16_t *__restrict__ scales, int8_t *__restrict__ codes_t, uint16_t *__restrict__ scales_t) {
+  using T = typename Elem<DT>::T;
+  constexpr int G = 128, PB = 132;
+  __shared__ __attribute__((aligned(16))) int8_t tq[128 * PB];  // [column][row]
+  __shared__ __attribute__((aligned(16))) float srow[128];
+  const int tid = threadIdx.x;
+  const int64_t c0 = (int64_t)blockIdx.x * 128, r0 = (int64_t)blockIdx.y * 128;
+  const int64_t ngC = (C + G - 1) / G, ngR = (R + G - 1) / G;
+
+  // ---- rows, as in quant_dual_kernel
+  const int rr = tid >> 4, sub = tid & 15;
+  const int64_t col = c0 + sub * 8;
+  const bool cok = col < C;
+  const T *xb = (const T *)xv + (cok ? col : 0);
+  Raw8<DT> raw[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) raw[p] = load_raw8<DT>(xb + min(r0 + 32 * p + rr, R - 1) * C);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int lr = 32 * p + rr;
+    const int64_t row = r0 + lr;
+    const bool ok = cok && row < R;
+    float v[8];
+    cvt_raw8<DT>(raw[p], ok, v);
+    const uint32_t am = group_max_u32<16>(__builtin_bit_cast(uint32_t, abs_max<8>(v)));
+    const float s = group_scale(__builtin_bit_cast(float, am));
+    uint32_t w[2];
+    codes_rcp_packed<8>(v, s, w);
+    const int64_t rowc = row < R ? row : 0;
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 q;
+    q.x = w[0];
+    q.y = w[1];
+    __builtin_amdgcn_raw_buffer_store_b64(q, rsrc(codes + rowc * C, C), ok ? (uint32_t)col : kOob, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsrc(scales + rowc * ngC, 2 * ngC),
+                                          ok && sub == 0 ? (uint32_t)(col / G) * 2 : kOob, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) tq[(sub * 8 + i) * PB + lr] = (int8_t)(w[i >> 2] >> (8 * (i & 3)));
+    if (sub == 0) srow[lr] = s;  // every row group of the tile has the same scale over its 16 lanes
+  }
+  __syncthreads();
+
+  // ---- columns: lane (c, part) takes column c, rows part * 32 .. + 32
+  constexpr int RPT = 32;
+  const int c = tid >> 2, part = tid & 3;
+  float colv[RPT];
+  const uint32_t *qc = (const uint32_t *)(tq + c * PB + part * RPT);
+  const float4 *sr = (const float4 *)(srow + part * RPT);
+#pragma unroll
+  for (int j4 = 0; j4 < RPT / 4; ++j4) {
+    const uint32_t qw = qc[j4];
+    const float4 sv = sr[j4];
+    const float ss[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+    for (int b = 0; b < 4; ++b) colv[4 * j4 + b] = (float)(int8_t)(qw >> (8 * b)) * ss[b];
+  }
+  const uint32_t am = group_max_u32<4>(__builtin_bit_cast(uint32_t, abs_max<RPT>(colv)));
+  const float s = group_scale(__builtin_bit_cast(float, am));
+  const int64_t gc = c0 + c;
+  if (gc >= C) return;
+  if (part == 0) scales_t[gc * ngR + blockIdx.y] = scale_bits(s);
+  uint32_t w[RPT / 4];
+  codes_rcp_packed<RPT>(colv, s, w);
+  int8_t *dst = codes_t + gc * R + r0 + part * RPT;
+  const int64_t rbase = r0 + part * RPT;
+  if (rbase + RPT <= R && (((uintptr_t)dst) & 15) == 0) {
+#pragma unroll
+    for (int j = 0; j < RPT / 4; j += 4) *(uint4 *)(dst + 4 * j) = make_uint4(w[j], w[j + 1], w[j + 2], w[j + 3]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < RPT; ++j)
+      if (rbase + j < R) dst[j] = (int8_t)(w[j / 4] >> (8 * (j % 4)));
+  }
+}
+
 // ---------------------------------------------------------------- cross entropy
 // Online (max, sum of exp) of one row: the running pair (m, s) absorbs a chunk with maximum
 // cm as m' = max(m, cm), s' = s * 2^((m - m') log2 e) + sum 2^((y - m') log2 e). A chunk
@@ -853,7 +937,7 @@ extern "C" int ksd_quantize_dual(const void *x, int x_dtype, int64_t R, int64_t 
   const dim3 grid((unsigned)cdiv(C, 128), (unsigned)cdiv(R, 128));
 #define KSD_DUAL(DT)                                                                                      \
   if (t_from_codes)                                                                                       \
-    quant_dual_kernel<DT, true><<<grid, 512, 0, st>>>(x, R, C, codes, scales, codes_t, scales_t);         \
+    quant_dual_codes_kernel<DT><<<grid, 512, 0, st>>>(x, R, C, codes, scales, codes_t, scales_t);         \
   else                                                                                                    \
     quant_dual_kernel<DT, false><<<grid, 512, 0, st>>>(x, R, C, codes, scales, codes_t, scales_t);
   switch (x_dtype) {
