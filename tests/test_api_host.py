@@ -39,3 +39,15 @@ def test_padded_length():
     assert quant._padded_length(100) == 128
     assert quant._padded_length(256, 32) == 256
     assert quant.GROUP_SIZE == 128 and quant.SCALE_DTYPE == torch.float16
+
+
+def test_layer_norm_quantize_host_checks():
+    # argument checks fire before any device work; CPU tensors are refused
+    with pytest.raises(TypeError):
+        quant.layer_norm_quantize(torch.zeros(2, 128, dtype=torch.int32))
+    with pytest.raises(ValueError, match="group 128"):
+        quant.layer_norm_quantize(torch.zeros(2, 128), group=64)
+    with pytest.raises(ValueError, match="d <= 4096"):
+        quant.layer_norm_quantize(torch.zeros(2, 4097))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        quant.layer_norm_quantize(torch.zeros(2, 128))
