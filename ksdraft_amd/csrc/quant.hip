@@ -689,15 +689,14 @@ static void launch_rows(const void *x, int64_t rows, int64_t K, int64_t stride,
 // ----------------------------------------------------------------------------------
 // LayerNorm forward (nn.LayerNorm, model/block.py:27-41: ln_attn / ln_ffn) fused with the
 // GS128 quantization of its output, the A operand of the Int8Linear that follows
-// (linear.py:69 quantize_last_dim). A wave owns RT consecutive rows; lane l holds elements
-// 512 s + 8 l .. 512 s + 8 l + 7 of slice s < NS (d <= 512 NS <= 4096, the row in
-// registers). The lane's weight and bias columns are loaded once per wave, and the next
-// row's x while the current one is reduced. mean and the biased variance are fp32 with
-// two passes and DPP wave sums, so every lane holds the same bits; y = (x - mean) * rstd *
-// w + b, rounded to x's dtype (torch's LayerNorm output dtype), is quantized exactly as
+// (linear.py:69 quantize_last_dim). One block per row, ceil(d / 8) lanes rounded up to
+// whole waves (d <= 4096: at most 8 waves); lane i holds elements 8i .. 8i + 7, so the 16
+// lanes of a 128-element group sit in one wave. mean and the biased variance are fp32,
+// two passes: each wave sums its lanes by DPP, and every lane adds the wave totals in
+// wave order from LDS, so all lanes hold the same bits. y = (x - mean) * rstd * w + b,
+// rounded to x's dtype (torch's LayerNorm output dtype), is quantized exactly as
 // quant_rows_kernel does. VEC: d % 8 == 0 and 16-byte aligned rows, weight and bias.
-constexpr int kLnSlices = 8;  // d <= 512 * kLnSlices
-constexpr int kLnRows = 2;    // rows per wave
+constexpr int kLnMaxD = 4096;
 
 // Sum over the wave's 64 lanes, the same bits in every lane (all lanes active): within
 // each row of 16 by DPP (pairs, quads, half-rows, rows: each step adds the partner's
@@ -716,129 +715,90 @@ __device__ __forceinline__ float ln_wave_sum(float v) {
 }
 
 template <int DT, bool VEC>
-__device__ __forceinline__ void ln_load_x(const typename Elem<DT>::T *xr, int k0, int d, float *v) {
-  if (VEC) {
-    cvt_raw8<DT>(load_raw8<DT>(xr + (k0 < d ? k0 : 0)), k0 < d, v);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = k0 + i < d ? Elem<DT>::load(xr + k0 + i) : 0.0f;
-  }
-}
-
-template <bool VEC>
-__device__ __forceinline__ void ln_load_param(const float *p, int k0, int d, float dflt, float *v) {
-  if (p == nullptr) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = dflt;
-  } else if (VEC) {
-    cvt_raw8<KSD_F32>(load_raw8<KSD_F32>(p + (k0 < d ? k0 : 0)), k0 < d, v);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = k0 + i < d ? p[k0 + i] : 0.0f;
-  }
-}
-
-template <int DT, bool VEC, int NS>
-__global__ __launch_bounds__(256) void ln_quant_kernel(
+__global__ __launch_bounds__(512) void ln_quant_kernel(
     const void *__restrict__ xv, int64_t rows, int d, int64_t stride, const float *__restrict__ w,
     const float *__restrict__ bvec, float eps, int ngroups, int8_t *__restrict__ codes,
     uint16_t *__restrict__ scales, void *__restrict__ y, float *__restrict__ mean_out,
     float *__restrict__ rstd_out) {
   using T = typename Elem<DT>::T;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * kLnRows;
-  if (row0 >= rows) return;  // wave-uniform
-  float wv[NS][8], bv[NS][8], xn[NS][8];
+  __shared__ float red[2][8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nw = blockDim.x >> 6;
+  const int64_t row = blockIdx.x;
+  const int k0 = tid * 8;
+  const bool kok = k0 < d;
+  const T *xr = (const T *)xv + row * stride;
+  float v[8], wv[8], bv[8];
+  if (VEC) {
+    cvt_raw8<DT>(load_raw8<DT>(xr + (kok ? k0 : 0)), kok, v);
+    if (w) cvt_raw8<KSD_F32>(load_raw8<KSD_F32>(w + (kok ? k0 : 0)), kok, wv);
+    if (bvec) cvt_raw8<KSD_F32>(load_raw8<KSD_F32>(bvec + (kok ? k0 : 0)), kok, bv);
+  } else {
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const int k0 = s * 512 + lane * 8;
-    ln_load_x<DT, VEC>((const T *)xv + row0 * stride, k0, d, xn[s]);
-    ln_load_param<VEC>(w, k0, d, 1.0f, wv[s]);
-    ln_load_param<VEC>(bvec, k0, d, 0.0f, bv[s]);
-  }
-#pragma unroll
-  for (int r = 0; r < kLnRows; ++r) {
-    const int64_t row = row0 + r;
-    if (row >= rows) break;  // wave-uniform
-    float v[NS][8];
-    float sum = 0.0f;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        v[s][i] = xn[s][i];
-        sum += v[s][i];
-      }
-    }
-    if (r + 1 < kLnRows) {  // the next row (a valid one) while this one is reduced
-      const int64_t rn = min(row + 1, rows - 1);
-#pragma unroll
-      for (int s = 0; s < NS; ++s) ln_load_x<DT, VEC>((const T *)xv + rn * stride, s * 512 + lane * 8, d, xn[s]);
-    }
-    sum = ln_wave_sum(sum);
-    const float mean = sum / (float)d;
-    float sq = 0.0f;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float c = s * 512 + lane * 8 + i < d ? v[s][i] - mean : 0.0f;
-        sq += c * c;
-      }
-    }
-    sq = ln_wave_sum(sq);
-    const float rstd = 1.0f / sqrtf(sq / (float)d + eps);
-    if (lane == 0) {
-      if (mean_out) mean_out[row] = mean;
-      if (rstd_out) rstd_out[row] = rstd;
-    }
-    int8_t *cr = codes + row * d;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const int k0 = s * 512 + lane * 8;
-      const bool kok = k0 < d;
-      float yv[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        yv[i] = k0 + i < d ? round_to_dt<DT>((v[s][i] - mean) * rstd * wv[s][i] + bv[s][i]) : 0.0f;
-      const uint32_t am = __builtin_bit_cast(uint32_t, abs_max<8>(yv));
-      const float sc = group_scale(__builtin_bit_cast(float, group_max_u32<16>(am)));
-      if (VEC && kok) {
-        uint32_t qw[2];
-        codes_rcp_packed<8>(yv, sc, qw);
-        *(uint2 *)(cr + k0) = make_uint2(qw[0], qw[1]);
-      } else if (kok) {
-        int8_t q[8];
-        codes_rcp<8>(yv, sc, q);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          if (k0 + i < d) cr[k0 + i] = q[i];
-      }
-      if (kok && (lane & 15) == 0) scales[row * ngroups + (k0 >> 7)] = scale_bits(sc);
-      if (y != nullptr && kok) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          if (k0 + i < d) store_out<DT>(y, row * d + k0 + i, yv[i]);
-      }
+    for (int i = 0; i < 8; ++i) {
+      const bool ok = k0 + i < d;
+      v[i] = ok ? Elem<DT>::load(xr + k0 + i) : 0.0f;
+      if (w) wv[i] = ok ? w[k0 + i] : 0.0f;
+      if (bvec) bv[i] = ok ? bvec[k0 + i] : 0.0f;
     }
   }
-}
-
-template <int DT, bool VEC>
-static void launch_ln(int ns, dim3 grid, hipStream_t st, const void *x, int64_t rows, int d,
-                      int64_t stride, const float *w, const float *b, float eps, int ng,
-                      int8_t *codes, uint16_t *scales, void *y, float *mo, float *ro) {
-#define KSD_LN(NS) ln_quant_kernel<DT, VEC, NS><<<grid, 256, 0, st>>>(x, rows, d, stride, w, b, eps, ng, codes, scales, y, mo, ro)
-  switch (ns) {
-    case 1: KSD_LN(1); break;
-    case 2: KSD_LN(2); break;
-    case 3: KSD_LN(3); break;
-    case 4: KSD_LN(4); break;
-    case 5: case 6: KSD_LN(6); break;
-    default: KSD_LN(8); break;
+  if (!w) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) wv[i] = 1.0f;
   }
-#undef KSD_LN
+  if (!bvec) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) bv[i] = 0.0f;
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) sum += v[i];
+  sum = ln_wave_sum(sum);
+  if (lane == 0) red[0][wave] = sum;
+  __syncthreads();
+  sum = red[0][0];
+  for (int i = 1; i < nw; ++i) sum += red[0][i];
+  const float mean = sum / (float)d;
+  float sq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float c = k0 + i < d ? v[i] - mean : 0.0f;
+    sq += c * c;
+  }
+  sq = ln_wave_sum(sq);
+  if (lane == 0) red[1][wave] = sq;
+  __syncthreads();
+  sq = red[1][0];
+  for (int i = 1; i < nw; ++i) sq += red[1][i];
+  const float rstd = 1.0f / sqrtf(sq / (float)d + eps);
+  if (tid == 0) {
+    if (mean_out) mean_out[row] = mean;
+    if (rstd_out) rstd_out[row] = rstd;
+  }
+  float yv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    yv[i] = k0 + i < d ? round_to_dt<DT>((v[i] - mean) * rstd * wv[i] + bv[i]) : 0.0f;
+  const uint32_t am = __builtin_bit_cast(uint32_t, abs_max<8>(yv));
+  const float sc = group_scale(__builtin_bit_cast(float, group_max_u32<16>(am)));
+  int8_t *cr = codes + row * d;
+  if (VEC && kok) {
+    uint32_t qw[2];
+    codes_rcp_packed<8>(yv, sc, qw);
+    *(uint2 *)(cr + k0) = make_uint2(qw[0], qw[1]);
+  } else if (kok) {
+    int8_t q[8];
+    codes_rcp<8>(yv, sc, q);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (k0 + i < d) cr[k0 + i] = q[i];
+  }
+  if (kok && (lane & 15) == 0) scales[row * ngroups + (k0 >> 7)] = scale_bits(sc);
+  if (y != nullptr && kok) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (k0 + i < d) store_out<DT>(y, row * d + k0 + i, yv[i]);
+  }
 }
 
 template <int DT>
@@ -1035,28 +995,28 @@ extern "C" int ksd_layernorm_quant(const void *x, int x_dtype, int64_t rows, int
                                    void *y_out, float *mean_out, float *rstd_out, void *stream) {
   if (group != 128) return fail(KSD_EINVAL, "layernorm_quant: group must be 128, got %d", group);
   if (rows < 0 || d < 1 || x_stride < d) return fail(KSD_EINVAL, "layernorm_quant: bad shape");
-  if (d > 512 * kLnSlices) return fail(KSD_EINVAL, "layernorm_quant: d above %d is not supported", 512 * kLnSlices);
+  if (d > kLnMaxD) return fail(KSD_EINVAL, "layernorm_quant: d above %d is not supported", kLnMaxD);
   if (!(eps >= 0.0f) || eps > 1.0f) return fail(KSD_EINVAL, "layernorm_quant: eps must be in [0, 1]");
   if (rows == 0) return KSD_OK;
   if (!x || !codes || !scales) return fail(KSD_EINVAL, "layernorm_quant: null pointer");
-  if (cdiv(rows, 4 * kLnRows) > 0x7fffffffLL) return fail(KSD_EINVAL, "layernorm_quant: too many rows");
+  if (rows > 0x7fffffffLL) return fail(KSD_EINVAL, "layernorm_quant: too many rows");
   hipStream_t st = (hipStream_t)stream;
   const int esz = x_dtype == KSD_F32 ? 4 : 2;
   const bool vec = (((uintptr_t)x) % 16 == 0) && ((x_stride * esz) % 16 == 0) && (d % 8 == 0) &&
                    (((uintptr_t)codes) % 8 == 0);
-  const bool vec_p = (((uintptr_t)weight) % 16 == 0) && (((uintptr_t)bias) % 16 == 0);
+  const bool v = vec && (((uintptr_t)weight) % 16 == 0) && (((uintptr_t)bias) % 16 == 0);
   const int ng = (int)cdiv(d, 128);
-  const int ns = (int)cdiv(d, 512);
-  const dim3 grid((unsigned)cdiv(rows, 4 * kLnRows));
-  const bool v = vec && vec_p;
-#define KSD_LN_ARGS ns, grid, st, x, rows, (int)d, x_stride, weight, bias, eps, ng, codes, scales, y_out, mean_out, rstd_out
+  const int threads = (int)cdiv(cdiv(d, 8), 64) * 64;
+  const dim3 grid((unsigned)rows);
+#define KSD_LN(DT, V) \
+  ln_quant_kernel<DT, V><<<grid, threads, 0, st>>>(x, rows, (int)d, x_stride, weight, bias, eps, ng, codes, scales, y_out, mean_out, rstd_out)
   switch (x_dtype) {
-    case KSD_F32: if (v) launch_ln<KSD_F32, true>(KSD_LN_ARGS); else launch_ln<KSD_F32, false>(KSD_LN_ARGS); break;
-    case KSD_BF16: if (v) launch_ln<KSD_BF16, true>(KSD_LN_ARGS); else launch_ln<KSD_BF16, false>(KSD_LN_ARGS); break;
-    case KSD_F16: if (v) launch_ln<KSD_F16, true>(KSD_LN_ARGS); else launch_ln<KSD_F16, false>(KSD_LN_ARGS); break;
+    case KSD_F32: if (v) KSD_LN(KSD_F32, true); else KSD_LN(KSD_F32, false); break;
+    case KSD_BF16: if (v) KSD_LN(KSD_BF16, true); else KSD_LN(KSD_BF16, false); break;
+    case KSD_F16: if (v) KSD_LN(KSD_F16, true); else KSD_LN(KSD_F16, false); break;
     default: return fail(KSD_ETYPE, "layernorm_quant expects float32, bfloat16 or float16 input");
   }
-#undef KSD_LN_ARGS
+#undef KSD_LN
   return check_launch("layernorm_quant");
 }
 
