@@ -252,9 +252,9 @@ __global__ __launch_bounds__(256) void quant_T_kernel(
 
 // ----------------------------------------------------------------------------------
 // Dual-layout quantization, G = 128: one pass over a 128 x 128 tile of x (R, C) emits the
-// row codes (quantize_last_dim(x), along C) and the column codes (along R) of either x
-// itself (quantize_last_dim(x.t())) or, T_FROM_CODES, the row-quantized values
-// dequantize(codes, scales) (the X^T recipe quant(dequant(quant(X))^T)). The rows are
+// row codes (quantize_last_dim(x), along C) and the column codes (along R) of x itself
+// (quantize_last_dim(x.t())); the X^T recipe quant(dequant(quant(X))^T) has its own
+// kernel, quant_dual_codes_kernel, below. The rows are
 // quantized from registers (16 lanes per row, 8 elements each), the values then go to LDS
 // transposed in quant_T_kernel's conflict-free layout, and 4 lanes per column quantize the
 // columns. Requires C % 8 == 0 and 16-byte aligned rows; rows past R read as zeros and
@@ -272,7 +272,7 @@ struct CeSrc {
 };
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <int DT, bool T_FROM_CODES, bool CE = false>
+template <int DT, bool CE = false>
 __global__ __launch_bounds__(512) void quant_dual_kernel(
     const void *__restrict__ xv, int64_t R, int64_t C, int8_t *__restrict__ codes,
     uint16_t *__restrict__ scales, int8_t *__restrict__ codes_t, uint16_t *__restrict__ scales_t,
@@ -334,11 +334,7 @@ __global__ __launch_bounds__(512) void quant_dual_kernel(
     __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsrc(scales + rowc * ngC, 2 * ngC),
                                           ok && sub == 0 ? (uint32_t)(col / G) * 2 : kOob, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float t = v[i];
-      if (T_FROM_CODES) t = (float)(int8_t)(w[i >> 2] >> (8 * (i & 3))) * s;  // dequantize (exact)
-      tile[lds_at(sub * 8 + i, lr)] = t;
-    }
+    for (int i = 0; i < 8; ++i) tile[lds_at(sub * 8 + i, lr)] = v[i];
   }
   __syncthreads();
 
@@ -367,7 +363,7 @@ __global__ __launch_bounds__(512) void quant_dual_kernel(
   }
 }
 
-// Dual-layout quantization of an X operand (the T_FROM_CODES recipe quant(dequant(quant(
+// Dual-layout quantization of an X operand (t_from_codes: the recipe quant(dequant(quant(
 // X))^T)) with a small LDS tile: as quant_dual_kernel, but the transposed tile holds the
 // row codes as int8, column-major with a 132-byte pitch (an odd word stride: at most 2-way
 // bank conflicts on the byte writes and the dword reads), and the 128 row scales; 17.4 KB
@@ -899,7 +895,7 @@ extern "C" int ksd_quantize_dual(const void *x, int x_dtype, int64_t R, int64_t 
   if (t_from_codes)                                                                                       \
     quant_dual_codes_kernel<DT><<<grid, 512, 0, st>>>(x, R, C, codes, scales, codes_t, scales_t);         \
   else                                                                                                    \
-    quant_dual_kernel<DT, false><<<grid, 512, 0, st>>>(x, R, C, codes, scales, codes_t, scales_t);
+    quant_dual_kernel<DT><<<grid, 512, 0, st>>>(x, R, C, codes, scales, codes_t, scales_t);
   switch (x_dtype) {
     case KSD_F32: KSD_DUAL(KSD_F32); break;
     case KSD_BF16: KSD_DUAL(KSD_BF16); break;
@@ -948,7 +944,7 @@ extern "C" int ksd_ce_backward_quant_dual(const float *logits, int64_t R, int64_
                     cdiv(C, 128) <= 0x7fffffff;
   if (fast) {
     const dim3 grid((unsigned)cdiv(C, 128), (unsigned)cdiv(R, 128));
-    quant_dual_kernel<KSD_F32, false, true><<<grid, 512, 0, st>>>(logits, R, C, codes, scales, codes_t,
+    quant_dual_kernel<KSD_F32, true><<<grid, 512, 0, st>>>(logits, R, C, codes, scales, codes_t,
                                                                   scales_t, ce);
     return check_launch("ce_backward_quant_dual");
   }
