@@ -28,7 +28,12 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr float kLutScale = (float)(127.0 / 3.2);   // _lut_index, ks3_int8.py:71
 constexpr float kLutDomain = 3.2f;                  // TANH_DOMAIN, ks3_int8.py:46
-constexpr float kTq16Step = (float)(4.0 / 127.0);   // ks3_int8.py:211
+// The warp step tq * (4/127). Composed (ks3_int8.py:211): a torch fp16 tensor times a
+// Python float is evaluated in fp32 with the constant in fp32. Fused (ks3_triton.py:59):
+// Triton keeps a Python-float scalar out of type promotion (triton/language/semantic.py,
+// computation_type_impl), so the product is an fp16 op and the constant is fp16(4/127).
+constexpr float kTq16Step = (float)(4.0 / 127.0);
+constexpr float kTq16StepFused = 0.031494140625f;  // fp16(4/127) = 2064 * 2^-16
 
 // ---------------------------------------------------------------- integer helpers
 // _round_div127 (ks3_int8.py:57-66): truncating quotient, +-1 when |remainder| > 63.
@@ -93,7 +98,9 @@ __device__ __forceinline__ SpineCol load_spine_col(const int8_t *codes, const ui
 template <bool FUSED>
 __device__ __forceinline__ int spine_sum(int ti, const SpineCol &c, const int8_t *lut) {
   const int tq = lut_at(lut, ti);
-  float w = f16_round(f16_round((float)tq * kTq16Step) + c.sh);
+  // tq * step is exact in fp32 (an int8 code times an fp16 value), so f16_round of it is
+  // the fp16 product
+  float w = f16_round(f16_round((float)tq * (FUSED ? kTq16StepFused : kTq16Step)) + c.sh);
   w = f16_round(c.sc * w);
   const int zq = lut_at(lut, FUSED ? (int)rintf(fminf(fmaxf(w, -kLutDomain), kLutDomain) * kLutScale)
                                    : lut_index(w));

@@ -545,7 +545,7 @@ __global__ __launch_bounds__(256) void ce_dy_kernel(const float *__restrict__ lo
 // passes torch's python-double scalars rounded to fp32.
 struct AdamArgs {
   float decay;      // 1 - lr * weight_decay
-  float w1;         // 1 - beta1 (lerp weight, < 0.5)
+  float w1;         // 1 - beta1 (lerp weight)
   float beta2, w2;  // beta2, 1 - beta2
   float eps;
   float step_size;  // lr / (1 - beta1^step)
@@ -598,7 +598,8 @@ __global__ __launch_bounds__(256) void adamw_requant_kernel(
   for (int i = 0; i < 8; ++i) {
     const float gi = clip ? gv[i] * c : gv[i];          // clip_grad_norm_: g.mul_(coef)
     const float pd = pv[i] * a.decay;                    // param.mul_(1 - lr * wd)
-    mv[i] = mv[i] + a.w1 * (gi - mv[i]);                 // exp_avg.lerp_(g, 1 - beta1)
+    // exp_avg.lerp_(g, 1 - beta1): torch's two forms, switched on the weight (uniform)
+    mv[i] = a.w1 < 0.5f ? mv[i] + a.w1 * (gi - mv[i]) : gi - (gi - mv[i]) * (1.0f - a.w1);
     vv[i] = vv[i] * a.beta2 + (a.w2 * gi) * gi;          // exp_avg_sq.mul_(b2).addcmul_(g, g, 1 - b2)
     const float den = sqrtf(vv[i]) / a.bc2_sqrt + a.eps;  // IEEE sqrt and division (build flags)
     pv[i] = pd + (-a.step_size) * (mv[i] / den);         // param.addcdiv_(m, den, -step_size)

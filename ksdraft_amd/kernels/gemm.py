@@ -31,6 +31,12 @@ def _validate(a_codes, a_scales, w_codes, w_scales, group):
     Kp = n_groups * group
     if Kp < K:
         raise ValueError(f"K {K} exceeds the scales' padded length {Kp}")
+    # The reference reads the scales through raw row strides and never checks their rows;
+    # here a short scale tensor would send the kernel's loads past its allocation.
+    if tuple(a_scales.shape) != (M, n_groups):
+        raise ValueError(f"a_scales shape {tuple(a_scales.shape)} != ({M}, {n_groups})")
+    if tuple(w_scales.shape) != (N, n_groups):
+        raise ValueError(f"w_scales shape {tuple(w_scales.shape)} != ({N}, {n_groups})")
     return M, N, K, n_groups, Kp
 
 

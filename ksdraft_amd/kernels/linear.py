@@ -172,24 +172,51 @@ class Int8Linear(nn.Module):
         self._dither = dither
         self._quantize_weight()
 
+    def invalidate_codes(self) -> None:
+        """Forget codes handed over by an optimizer (train.AdamWRequant.register_int8):
+        the next call requantizes the master. Needed after a write to the master that
+        torch does not version, i.e. through ``weight.data`` or a raw pointer."""
+        self._codes_key = None
+
+    def _codes_current(self) -> bool:
+        """True when train.AdamWRequant wrote the codes in the same pass that last
+        updated the master and the master has kept its storage and in-place version."""
+        key = getattr(self, "_codes_key", None)
+        return (key is not None and self.weight_codes is not None
+                and getattr(self, "_codes_owner", None) is not None
+                and getattr(self, "_dither", 0.0) <= 0
+                and key == (self.weight.data_ptr(), self.weight._version))
+
+    def _apply(self, fn, *args, **kwargs):
+        self.invalidate_codes()  # .to(), .cuda(), .half() ... may replace the master
+        return super()._apply(fn, *args, **kwargs)
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        self.invalidate_codes()  # load_state_dict writes the master in place
+        return super()._load_from_state_dict(*args, **kwargs)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         # live fp32 masters stay authoritative (linear.py:66): the codes are rebuilt on every
-        # call, except when train.AdamWRequant wrote them in the same pass that last updated
-        # the master and the master has not changed since (same storage, same in-place
-        # version); dithered codes are redrawn every call
-        key = getattr(self, "_codes_key", None)
-        if (self.weight_codes is None or getattr(self, "_dither", 0.0) > 0 or key is None
-                or key != (self.weight.data_ptr(), self.weight._version)):
+        # call unless an optimizer handed over the codes of the master as it is now
+        # (_codes_current); dithered codes are redrawn every call
+        if not self._codes_current():
             self._codes_key = None
             self._quantize_weight()
         if torch.is_grad_enabled() and (self.weight.requires_grad or x.requires_grad):
             if self.ste_training:
                 return self.fake_quant_forward(x)
-            return W8A8LinearFunction.apply(x, self.weight, self.bias, self.weight_codes,
-                                            self.weight_scales, GROUP_SIZE)
+            # other float dtypes (float64) go through .float() as the reference's
+            # quantize_last_dim(x2.float()) does (linear.py:69); the result is cast back
+            xin = x if x.dtype in _OUT_DTYPES else x.float()
+            y = W8A8LinearFunction.apply(xin, self.weight, self.bias, self.weight_codes,
+                                         self.weight_scales, GROUP_SIZE)
+            return y.to(x.dtype)
         # linear.py:68-73: fp32 GEMM, + bias in fp32, then cast to x.dtype (fused)
+        x2 = x.reshape(-1, x.shape[-1])
+        if x2.dtype not in _OUT_DTYPES:
+            x2 = x2.float()
         y, _, _ = w8a8_linear_forward(
-            x.reshape(-1, x.shape[-1]), self.weight_codes, self.weight_scales,
+            x2, self.weight_codes, self.weight_scales,
             self.bias.detach() if self.bias is not None else None)
         return y.reshape(*x.shape[:-1], self.out_features).to(x.dtype)
 

@@ -94,15 +94,25 @@ def dequantize_last_dim(codes: torch.Tensor, scales: torch.Tensor,
     K = codes.shape[-1]
     if group is None:
         group = _padded_length(K) // max(scales.shape[-1], 1)
+    if group <= 0:
+        raise ValueError(f"dequantize: group must be positive, got {group}")
+    lead = codes.shape[:-1]
+    # quant.py:64-67 multiplies codes grouped (..., Kp/group, group) by scales[..., None]:
+    # torch broadcasting decides which scale shapes are accepted (a single scale row or
+    # column broadcasts). Any other shape raises torch's own error, never reads past the
+    # scales.
+    nsc = _padded_length(K, group) // group
+    want = (*lead, nsc)
+    if torch.broadcast_shapes(want, tuple(scales.shape)) != want:
+        raise RuntimeError(f"scales of shape {tuple(scales.shape)} do not broadcast to the "
+                           f"grouped codes {want}")
     dev = _lib.require_gpu(codes, scales)
     if codes.dtype != torch.int8:
         codes = codes.to(torch.int8)  # float-typed integral codes (linear.py:79-80)
     if scales.dtype != SCALE_DTYPE:
         raise TypeError(f"scales must be {SCALE_DTYPE}, got {scales.dtype}")
-    lead = codes.shape[:-1]
     c2 = codes.reshape(-1, K).contiguous() if K else codes.reshape(-1, 0)
-    nsc = scales.shape[-1]
-    s2 = scales.reshape(-1, nsc).contiguous()
+    s2 = scales.expand(want).reshape(-1, nsc).contiguous()
     out = torch.empty((c2.shape[0], K), dtype=torch.float32, device=dev)
     _lib.call("ksd_dequantize_lastdim", c2.data_ptr(), s2.data_ptr(), c2.shape[0], K, nsc,
               group, out.data_ptr(), _lib.stream_ptr(dev))

@@ -55,7 +55,10 @@ def cross_entropy_stats(logits: torch.Tensor, targets: torch.Tensor,
     rloss = torch.empty(R, dtype=torch.float32, device=dev)
     _lib.call("ksd_ce_row_stats", logits.data_ptr(), R, C, targets.data_ptr(), int(ignore_index),
               rmax.data_ptr(), rinv.data_ptr(), rloss.data_ptr(), _lib.stream_ptr(dev))
-    n = (targets != ignore_index).sum().to(torch.float32)
+    # the rows the kernels count: a target in range and not ignored (with check_targets
+    # off, an out-of-range target is an ignored row for the kernels, so it is for n too)
+    C = logits.shape[1]
+    n = ((targets != ignore_index) & (targets >= 0) & (targets < C)).sum().to(torch.float32)
     return rloss.sum() / n, rmax, rinv, n
 
 
@@ -194,9 +197,15 @@ class AdamWRequant(torch.optim.Optimizer):
             raise ValueError("invalid AdamW hyper-parameter")
         super().__init__(params, dict(lr=lr, betas=tuple(betas), eps=eps, weight_decay=weight_decay))
         self._int8 = {}
+        self._steps = {}  # id(param) -> step count as a python int (no tensor read per step)
 
     def register_int8(self, module) -> None:
+        """After each step the module's codes are those of its updated master. The module
+        then skips its own per-call requantization until its master changes; a write to
+        the master through ``.data`` (which torch does not version) must be followed by
+        ``module.invalidate_codes()``."""
         self._int8[id(module.weight)] = module
+        module._codes_owner = self
 
     @torch.no_grad()
     def step(self, closure=None, clip_coef: torch.Tensor | None = None):
@@ -213,13 +222,22 @@ class AdamWRequant(torch.optim.Optimizer):
                     st["step"] = torch.tensor(0.0)
                     st["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
                     st["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
-                st["step"] += 1
+                n = self._steps.get(id(p))
+                if n is None:  # first step, or state loaded from a state_dict (a CPU tensor)
+                    n = int(st["step"])
+                n += 1
+                self._steps[id(p)] = n
+                st["step"].fill_(float(n))  # torch's AdamW state layout: a CPU scalar tensor
                 mod = self._int8.get(id(p))
                 res = adamw_requant_(p, p.grad.contiguous(), st["exp_avg"], st["exp_avg_sq"],
-                                     int(st["step"].item()), group["lr"], group["betas"],
+                                     n, group["lr"], group["betas"],
                                      group["eps"], group["weight_decay"], clip_coef,
                                      quantize=mod is not None)
                 if mod is not None:  # the codes now belong to the master as it is
                     mod.weight_codes, mod.weight_scales = res
                     mod._codes_key = (p.data_ptr(), p._version)
         return loss
+
+    def load_state_dict(self, state_dict):
+        super().load_state_dict(state_dict)
+        self._steps.clear()

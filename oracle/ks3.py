@@ -22,10 +22,15 @@ gradient given identical GEMM outputs); the LUT against an mpmath-free closed fo
 check (float64 tanh, tie distance); _round_div127 by brute force over integer ranges
 (tests/test_oracle_ks3.py).
 
-spine_fused_int8 (the project_fused contract) is parity unpinned at the bit level: the
-reference computes it in a Triton kernel that cannot run here, and Triton's fp16 scalar
-promotion and fp32 division are not fixed by its source. It is pinned only by the
-reference's own tolerance against the composed path (rel < 0.05 on the cell output,
+spine_fused_int8 (the project_fused contract) follows the Triton source's typing: the
+fp16 warp product with the constant rounded to fp16 (Triton's scalar rule, pinned by
+tests/test_oracle_ks3.py against the installed triton.language.semantic), fp32 LUT
+indices, the untruncated fp32 increment. It stays parity unpinned at the bit level in the
+two places the Triton source leaves to its backend: whether the fp32 `h / pre_scale`
+division of ks3_triton.py:74 and :153 is correctly rounded, and whether the backend
+contracts `x + s * (ps / 64)` (:70) and `tq16 * c + shift16` (:59) into FMAs, which
+Triton's default enable_fp_fusion=True permits but does not force. Those are pinned only by
+the reference's own tolerance against the composed path (rel < 0.05 on the cell output,
 tests/test_ks3_int8.py:82-84), checked on the golden cell.
 """
 
@@ -234,7 +239,12 @@ def spine_fused_int8(acc32, spine_codes, spine_scale, scale16, shift16, lut, gro
         return np.rint((v * k).astype(np.float32)).astype(np.int64)
 
     tq = lut[np.clip(idx32((x * f32(0.25)).astype(np.float32)) + 128, 0, 255)]
-    warp = h(sc * h(h(tq.astype(np.float32) * f32(4.0 / 127.0)) + sh))
+    # ks3_triton.py:59: `tq.to(tl.float16) * (4. / 127.)` is an fp16 op in Triton (a Python
+    # float scalar does not take part in type promotion, triton/language/semantic.py
+    # computation_type_impl), so the constant is fp16(4/127) and the product is rounded to
+    # fp16; the composed path (spine_features_int8) keeps torch's fp32 constant.
+    step16 = f32(np.float16(4.0 / 127.0))
+    warp = h(sc * h(h(tq.astype(np.float32) * step16) + sh))
     zq = lut[np.clip(idx32(warp) + 128, 0, 255)]
     a = 2 * c0 - 2 * c1 + c2 + c3
     b = -3 * c0 + 3 * c1 - 2 * c2 - c3

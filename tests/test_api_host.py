@@ -51,3 +51,64 @@ def test_layer_norm_quantize_host_checks():
         quant.layer_norm_quantize(torch.zeros(2, 4097))
     with pytest.raises(RuntimeError, match="GPU only"):
         quant.layer_norm_quantize(torch.zeros(2, 128))
+
+
+def test_gemm_rejects_scale_rows_that_do_not_match():
+    # the kernel reads scale rows by raw stride: a short scale tensor must raise before
+    # any launch instead of reading past its allocation
+    a = torch.zeros(4, 256, dtype=torch.int8)
+    w = torch.zeros(3, 256, dtype=torch.int8)
+    sa = torch.zeros(4, 2, dtype=torch.float16)
+    sw = torch.zeros(3, 2, dtype=torch.float16)
+    with pytest.raises(ValueError, match="a_scales shape"):
+        gemm.w8a8_gemm(a, sa[:2], w, sw)
+    with pytest.raises(ValueError, match="w_scales shape"):
+        gemm.w8a8_gemm(a, sa, w, sw[:1])
+    with pytest.raises(RuntimeError, match="GPU only"):
+        gemm.w8a8_gemm(a, sa, w, sw)
+
+
+def test_dequantize_scale_shapes_follow_torch_broadcasting():
+    codes = torch.zeros(4, 256, dtype=torch.int8)
+    # scale rows that neither match nor broadcast: torch's own broadcasting error class
+    with pytest.raises(RuntimeError, match="broadcast|size"):
+        quant.dequantize_last_dim(codes, torch.zeros(3, 2, dtype=torch.float16))
+    # an explicit group the scales do not cover
+    with pytest.raises(RuntimeError, match="broadcast|size"):
+        quant.dequantize_last_dim(codes, torch.zeros(4, 2, dtype=torch.float16), group=64)
+    # shapes the reference accepts by broadcasting pass the host checks (then need a GPU)
+    for sc in (torch.zeros(1, 2), torch.zeros(2), torch.zeros(4, 1)):
+        with pytest.raises(RuntimeError, match="GPU only"):
+            g = 128 if sc.shape[-1] == 2 else None
+            quant.dequantize_last_dim(codes, sc.half(), group=g)
+
+
+def test_int8_linear_codes_follow_writes_the_optimizer_did_not_make():
+    """Codes handed over by AdamWRequant are used only while the master is the one they
+    were made from: load_state_dict, .to() and invalidate_codes() drop them (host state
+    only; no kernel runs)."""
+    from ksdraft_amd.kernels.linear import Int8Linear
+    lin = Int8Linear(128, 4, bias=False)
+    lin.weight_codes = torch.zeros(4, 128, dtype=torch.int8)
+    lin.weight_scales = torch.zeros(4, 1, dtype=torch.float16)
+    lin._codes_owner = object()
+    lin._codes_key = (lin.weight.data_ptr(), lin.weight._version)
+    assert lin._codes_current()
+    with torch.no_grad():
+        lin.weight.add_(1.0)                      # a versioned in-place write
+    assert not lin._codes_current()
+    lin._codes_key = (lin.weight.data_ptr(), lin.weight._version)
+    lin.weight.data.copy_(torch.ones(4, 128))     # unversioned: needs invalidate_codes()
+    lin.invalidate_codes()
+    assert not lin._codes_current()
+    lin._codes_key = (lin.weight.data_ptr(), lin.weight._version)
+    lin.load_state_dict({"weight": torch.full((4, 128), 2.0)})
+    assert not lin._codes_current()
+    lin._codes_key = (lin.weight.data_ptr(), lin.weight._version)
+    lin.to(torch.float32)
+    assert not lin._codes_current()
+    # a module no optimizer registered never skips its requantization
+    lin2 = Int8Linear(128, 4, bias=False)
+    lin2.weight_codes, lin2.weight_scales = lin.weight_codes, lin.weight_scales
+    lin2._codes_key = (lin2.weight.data_ptr(), lin2.weight._version)
+    assert not lin2._codes_current()

@@ -140,3 +140,25 @@ def test_linear_cross_entropy_int8_autograd(xdtype):
     for ga, gb in ((xa.grad.float(), xb.grad.float()), (wa.grad, wb.grad)):
         err = (ga - gb).abs().max().item()
         assert err <= 2e-2 * gb.abs().max().item(), (err, gb.abs().max().item())
+
+
+def test_unchecked_out_of_range_targets_count_as_ignored_rows():
+    """check_targets=False (graph capture) treats an out-of-range target as an ignored row
+    in the kernels; the mean's denominator counts the same rows, so loss and dY equal those
+    of the same batch with those targets set to ignore_index."""
+    y, t = _case(64, 512, seed=17, ignore_frac=0.0)
+    bad = t.clone()
+    bad[5], bad[9], bad[20] = 512, -7, 10_000
+    fixed = bad.clone()
+    fixed[5] = fixed[9] = fixed[20] = T.IGNORE_INDEX
+    yd = y.to(DEV)
+    loss_b, rmax, rinv, n_b = T.cross_entropy_stats(yd, bad.to(DEV), check_targets=False)
+    loss_f, _, _, n_f = T.cross_entropy_stats(yd, fixed.to(DEV))
+    assert n_b.item() == n_f.item() == 61
+    assert torch.equal(loss_b, loss_f)
+    eloss, edy = _torch_ref(y, fixed)
+    assert abs(loss_b.item() - eloss) <= 2e-5 * abs(eloss)
+    gsc = torch.ones(1, device=DEV) / n_b
+    _, dy = T.cross_entropy_grad_int8(yd, bad.to(DEV), rmax, rinv, gsc, return_dy=True)
+    dy = dy.cpu().numpy()
+    assert np.all(np.abs(dy - edy) <= 1e-5 / 61)

@@ -86,3 +86,65 @@ def test_adamw_requant_optimizer_drives_int8linear():
     lin(x)
     assert lin.weight_codes is not codes
     _codes_match(lin.weight, (lin.weight_codes, lin.weight_scales))
+
+
+@pytest.mark.parametrize("betas", [(0.3, 0.999), (0.5, 0.9)])
+def test_adamw_requant_small_beta1_uses_torchs_second_lerp_form(betas):
+    """beta1 <= 0.5 puts the lerp weight 1 - beta1 at or above 0.5, where torch's lerp
+    switches to end - (end - self) * (1 - w); the kernel switches with it."""
+    g = torch.Generator().manual_seed(11)
+    shape = (96, 384)
+    p0 = (torch.randn(*shape, generator=g) * 0.02).to(DEV)
+    ref = p0.clone().requires_grad_(True)
+    opt = torch.optim.AdamW([ref], lr=3e-3, betas=betas, eps=1e-8, weight_decay=0.01,
+                            foreach=False)
+    p, m, v = p0.clone(), torch.zeros_like(p0), torch.zeros_like(p0)
+    for step in range(1, 4):
+        grad = (torch.randn(*shape, generator=g) * 0.01).to(DEV)
+        ref.grad = grad.clone()
+        opt.step()
+        res = T.adamw_requant_(p, grad, m, v, step, 3e-3, betas, 1e-8, 0.01)
+        torch.cuda.synchronize()
+        st = opt.state[ref]
+        for got, exp in ((p, ref.detach()), (m, st["exp_avg"]), (v, st["exp_avg_sq"])):
+            torch.testing.assert_close(got, exp, rtol=2e-6, atol=2e-6 * exp.abs().max().item())
+        _codes_match(p, res)
+
+
+def test_registered_int8linear_after_unversioned_write():
+    """A write through .data after the step is invisible to torch's version counter: the
+    module requantizes once invalidate_codes() is called, and after load_state_dict."""
+    torch.manual_seed(1)
+    lin = Int8Linear(256, 128).to(DEV)
+    with torch.no_grad():
+        lin.weight.normal_(0, 0.02)
+    opt = T.AdamWRequant(lin.parameters(), lr=1e-3)
+    opt.register_int8(lin)
+    x = torch.randn(32, 256, device=DEV)
+    lin(x).square().mean().backward()
+    opt.step()
+    lin.weight.data.copy_(torch.randn(128, 256, device=DEV) * 0.05)
+    lin.invalidate_codes()
+    lin(x)
+    _codes_match(lin.weight, (lin.weight_codes, lin.weight_scales))
+    sd = {k: v.clone() * 0.5 for k, v in lin.state_dict().items()}
+    lin.load_state_dict(sd)
+    with torch.no_grad():
+        lin(x)
+    _codes_match(lin.weight, (lin.weight_codes, lin.weight_scales))
+
+
+def test_int8linear_accepts_float64_like_the_reference():
+    """The reference quantizes x2.float() (linear.py:69) and casts y back to x's dtype."""
+    torch.manual_seed(2)
+    lin = Int8Linear(256, 64).to(DEV)
+    with torch.no_grad():
+        lin.weight.normal_(0, 0.02)
+        x = torch.randn(16, 256, device=DEV, dtype=torch.float64)
+        y = lin(x)
+        assert y.dtype == torch.float64
+        torch.testing.assert_close(y, lin(x.float()).double(), rtol=0, atol=0)
+    xg = x.clone().requires_grad_(True)
+    y = lin(xg)
+    y.sum().backward()
+    assert y.dtype == torch.float64 and xg.grad.dtype == torch.float64

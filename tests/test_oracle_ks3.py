@@ -127,3 +127,50 @@ def test_tanh_table_is_torch_fp16_tanh():
     t = torch.tanh(torch.from_numpy(x.copy())).numpy().view(np.uint16)
     assert np.array_equal(got, t)
     assert np.array_equal(tab[:0x2400], bits[:0x2400])
+
+
+def test_fused_warp_step_follows_triton_scalar_typing():
+    """ks3_triton.py:59 multiplies an fp16 tensor by the Python float 4/127. Triton's own
+    promotion rule (triton.language.semantic, computation_type_impl) keeps a float scalar
+    of no higher kind than the tensor out of promotion, so the op is fp16 and the constant
+    is rounded to fp16. The rule is read from the installed Triton, not restated; the
+    oracle's fused warp product must then differ from the fp32-constant product exactly
+    where fp16 rounding of the constant matters."""
+    sem = pytest.importorskip("triton.language.semantic")
+    tl = pytest.importorskip("triton.language")
+    impl = sem.TritonSemantic.computation_type_impl
+    # (tensor fp16, scalar fp32) -> fp16, for mul/add (not div/mod)
+    assert impl(None, tl.float16, False, tl.float32, True, False) == tl.float16
+    assert impl(None, tl.float32, True, tl.float16, False, False) == tl.float16
+    # a division would be promoted to fp32 (ps / 64. of :70 is fp32 anyway: ps is fp32)
+    assert impl(None, tl.float16, False, tl.float32, True, True) == tl.float32
+    tq = np.arange(-127, 128, dtype=np.float32)
+    c16 = np.float32(np.float16(4.0 / 127.0))
+    assert c16 == np.float32(0.031494140625)
+    fused = ok.h(tq * c16)
+    composed = ok.h(tq * np.float32(4.0 / 127.0))
+    # the two products differ for some table values: the choice is observable
+    assert 0 < int(np.sum(fused != composed)) < 255
+
+
+def test_rosa_shifted_matches_torch_ops():
+    """oracle.rosa.shifted against the reference's own expression run by torch on the CPU
+    (model/rosa.py:128-133: prev = F.pad(x)[:, :-1]; prev + (x - prev) * sigmoid(mix)) for
+    fp32, bf16 and fp16 x, bit-exact, with torch's sigmoid as the shared input."""
+    import torch
+    import torch.nn.functional as F
+    from oracle import rosa as orr
+    g = torch.Generator().manual_seed(5)
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        x = (torch.randn(2, 37, 96, generator=g) * 3).to(dt)
+        mix = torch.randn(96, generator=g) * 2
+        prev = F.pad(x, (0, 0, 1, 0))[:, :-1, :]
+        sig = torch.sigmoid(mix)
+        ref = prev + (x - prev) * sig
+        assert ref.dtype == torch.float32
+        got = orr.shifted(x.float().numpy(), sig.numpy(), str(dt).split(".")[-1])
+        assert np.array_equal(got.view(np.uint32), ref.numpy().view(np.uint32)), dt
+        # the oracle's own sigmoid (correctly rounded) is within two fp32 ulps of torch's
+        s32 = orr.sigmoid32(mix.numpy())
+        assert np.max(np.abs(s32.view(np.int32).astype(np.int64)
+                             - sig.numpy().view(np.int32).astype(np.int64))) <= 2
