@@ -223,6 +223,21 @@ int ksd_ks3_spine_fwd(const uint16_t *coords, int64_t M, int64_t F, const int8_t
                       int8_t *h_codes, uint16_t *h_scales, uint16_t *table, void *stream);
 
 /*
+ * ksd_ks3_spine_fwd without the table workspace, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It has no counterpart in the reference. The per-chart table lives in a
+ * library-owned device array of 8192 charts x 256 fp16 (4 MiB per GPU, held until the
+ * process ends); F > 8192 returns KSD_EINVAL. The call allocates nothing. The stream must
+ * belong to the current device. Calls that overlap on one GPU share the array and race.
+ * Arguments and outputs otherwise as ksd_ks3_spine_fwd.
+ */
+int ksd_ks3_spine_fwd_noalloc(const uint16_t *coords, int64_t M, int64_t F,
+                              const int8_t *spine_codes, const uint16_t *spine_scale,
+                              const uint16_t *warp_scale, const uint16_t *warp_shift,
+                              const int8_t *tanh_lut, int group, float *h, int8_t *h_codes,
+                              uint16_t *h_scales, void *stream);
+
+/*
  * K8 — the spine + requantization stage of project_fused / _fused_gemm_spine, 'int8' mode
  * (reference ksdraft/kernels/ks3_triton.py:47-75, 137-156 and 159-195), applied to the
  * fp32 down-projection accumulator. This is the reference's GPU-eval contract, which

@@ -1031,6 +1031,61 @@ extern "C" int ksd_ks3_spine_fwd(const uint16_t *coords, int64_t M, int64_t F,
   return check_launch("ks3_spine_fwd");
 }
 
+// ---------------------------------------------------------------- no-allocation variant
+// ksd_ks3_spine_fwd_noalloc runs ksd_ks3_spine_fwd with its per-chart increment table in
+// `scratch`, a file-scope device array of kScratchCharts x 256 fp16 (4 MiB), of which every
+// GPU the library runs on holds its own copy until the process ends. The table kernel of
+// each call rewrites every entry the element pass reads (rows below F), so nothing needs
+// clearing; calls that overlap on one GPU share the array and race. Host code never passes
+// the array's name to a kernel: its device address comes from hipGetSymbolAddress, once
+// per device, with that device current.
+constexpr int64_t kScratchCharts = 8192;
+static __device__ __align__(256) uint16_t scratch[kScratchCharts * 256];
+static uint16_t *g_scratch_addr[64];  // per device ordinal
+
+static int scratch_table(const char *who, hipStream_t st, uint16_t **out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(KSD_EHIP, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return fail(KSD_EINVAL, "%s: device ordinal %d out of range", who, dev);
+  if (st != nullptr) {
+    int sdev = -1;
+    e = hipStreamGetDevice(st, &sdev);
+    if (e != hipSuccess) return fail(KSD_EHIP, "%s: hipStreamGetDevice: %s", who, hipGetErrorString(e));
+    if (sdev != dev)
+      return fail(KSD_EINVAL, "%s: the stream belongs to device %d but device %d is current", who,
+                  sdev, dev);
+  }
+  uint16_t *p = __atomic_load_n(&g_scratch_addr[dev], __ATOMIC_ACQUIRE);
+  if (p == nullptr) {
+    void *q = nullptr;
+    e = hipGetSymbolAddress(&q, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || q == nullptr)
+      return fail(KSD_EHIP, "%s: hipGetSymbolAddress(scratch): %s", who, hipGetErrorString(e));
+    p = (uint16_t *)q;
+    __atomic_store_n(&g_scratch_addr[dev], p, __ATOMIC_RELEASE);
+  }
+  *out = p;
+  return KSD_OK;
+}
+
+extern "C" int ksd_ks3_spine_fwd_noalloc(const uint16_t *coords, int64_t M, int64_t F,
+                                         const int8_t *spine_codes, const uint16_t *spine_scale,
+                                         const uint16_t *warp_scale, const uint16_t *warp_shift,
+                                         const int8_t *tanh_lut, int group, float *h,
+                                         int8_t *h_codes, uint16_t *h_scales, void *stream) {
+  if (F > kScratchCharts)
+    return fail(KSD_EINVAL, "ks3_spine_fwd_noalloc: F=%lld charts exceeds the %lld-chart scratch table",
+                (long long)F, (long long)kScratchCharts);
+  if (F < 0 || M < 0)
+    return fail(KSD_EINVAL, "ks3_spine_fwd_noalloc: negative shape (%lld, %lld)", (long long)M, (long long)F);
+  uint16_t *table = nullptr;
+  const int rc = scratch_table("ks3_spine_fwd_noalloc", (hipStream_t)stream, &table);
+  if (rc) return rc;
+  return ksd_ks3_spine_fwd(coords, M, F, spine_codes, spine_scale, warp_scale, warp_shift, tanh_lut,
+                           group, h, h_codes, h_scales, table, stream);
+}
+
 extern "C" int ksd_ks3_spine_fused(const float *acc, int64_t M, int64_t F,
                                    const int8_t *spine_codes, const uint16_t *spine_scale,
                                    const uint16_t *warp_scale, const uint16_t *warp_shift,
