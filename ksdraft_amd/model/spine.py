@@ -1,0 +1,56 @@
+"""DSpine gated adjacent injection (mirror of reference ksdraft/model/spine.py:38-68).
+
+    p_t  = feature_up(feature_down(z_t))                 this layer's predicted feature
+    g_t  = sigmoid(gate_q(z_t) + gate_p(p_{t-1}) + b)
+    z'_t = z_t + g_t * inject(p_{t-1})
+
+with p_{-1} = 0, or position 0 seeded from the previous layer's prediction. The gates and
+the injection are low-rank pairs (rank 32; the feature pair rank 64) whose up-projections
+start at zero. ``to_int8`` keeps these surfaces in float (the reference's conversion
+doctrine, int8_convert.py:1-16): at rank 32/64 the reduction is shorter than one 128-wide
+quantization group.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+import torch.nn.functional as F
+
+
+class _LowRank(nn.Module):
+    def __init__(self, width: int, rank: int):
+        super().__init__()
+        self.down = nn.Linear(width, rank, bias=False)
+        self.up = nn.Linear(rank, width, bias=False)
+        nn.init.zeros_(self.up.weight)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.up(self.down(x))
+
+
+class AdjacentInjection(nn.Module):
+    def __init__(self, width: int, rank: int = 32, feature_rank: int = 64):
+        super().__init__()
+        self.width = width
+        self.feature_down = nn.Linear(width, feature_rank, bias=False)
+        self.feature_up = nn.Linear(feature_rank, width, bias=False)
+        self.gate_q = _LowRank(width, rank)
+        self.gate_p = _LowRank(width, rank)
+        self.gate_bias = nn.Parameter(torch.zeros(width))
+        self.inject = _LowRank(width, rank)
+
+    def extra_repr(self) -> str:
+        return f"width={self.width}"
+
+    def predicted_feature(self, z: torch.Tensor) -> torch.Tensor:
+        return self.feature_up(self.feature_down(z))
+
+    def forward(self, z: torch.Tensor, prev_layer_feature: torch.Tensor | None = None):
+        """(z', p): the injected stream and this layer's predicted feature."""
+        p = self.predicted_feature(z)
+        p_prev = F.pad(p, (0, 0, 1, 0))[:, :-1, :]
+        if prev_layer_feature is not None:
+            p_prev = torch.cat([prev_layer_feature[:, :1, :], p_prev[:, 1:, :]], dim=1)
+        gate = torch.sigmoid(self.gate_q(z) + self.gate_p(p_prev) + self.gate_bias)
+        return z + gate * self.inject(p_prev), p

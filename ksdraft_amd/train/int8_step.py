@@ -1,0 +1,86 @@
+"""The INT8 draft training step: the reference trainer's step
+(ksdraft/train/__init__.py:145-174) on a ``to_int8(model, trainable=True)`` model.
+
+    logits-free loss:  ce = LinearCrossEntropyInt8(output_norm(stream), tied head)
+                       ts = mean over layers of 1 - cos(feature, embedding[next token])
+                       loss = ce + transfer_weight * ts          (distillation_losses, :65-99)
+    backward           every linear INT8 (Int8Linear / KS3Int8Cell / the head's GEMMs)
+    clip               the clip_grad_norm_ factor as a device scalar (no gradient rewrite)
+    optimizer          AdamWRequant: torch AdamW's update fused with the int8 repack of every
+                       registered Int8Linear master (the head's codes included)
+
+The teacher-KL term needs teacher top-k signals, which config 5 does not have (a synthetic
+teacher hidden state drives only the ``teacher_proj`` seam); it is not part of this step.
+Nothing in the step reads a value back to the host except the loss check of the
+cross-entropy targets.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from ..kernels.linear import Int8Linear
+from . import IGNORE_INDEX, AdamWRequant, LinearCrossEntropyInt8
+
+
+def clip_coefficient(params, max_norm: float) -> torch.Tensor:
+    """The factor torch.nn.utils.clip_grad_norm_ multiplies every gradient by:
+    min(1, max_norm / (||g||_2 + 1e-6)) over all gradients, as a 1-element device tensor."""
+    grads = [p.grad for p in params if p.grad is not None]
+    norms = torch.stack([torch.linalg.vector_norm(g.float()) for g in grads])
+    total = torch.linalg.vector_norm(norms)
+    return torch.clamp(max_norm / (total + 1e-6), max=1.0).reshape(1)
+
+
+def transfer_space_loss(features, embedding_weight: torch.Tensor, tgt: torch.Tensor):
+    """distillation_losses' transfer term (train/__init__.py:79-85)."""
+    tgt_emb = F.normalize(embedding_weight[tgt].float(), dim=-1)
+    ts = 0.0
+    for f in features:
+        ts = ts + (1 - (F.normalize(f.float(), dim=-1) * tgt_emb).sum(-1)).mean()
+    return ts / max(1, len(features))
+
+
+class Int8DraftTrainer:
+    """One optimizer step per ``step(tokens, teacher_states)`` on an INT8 draft model.
+
+    tokens (B, T + 1): inputs tokens[:, :-1], targets tokens[:, 1:] (train/__init__.py:152).
+    The model must come from ``to_int8(model, trainable=True)`` (its head is an Int8Linear
+    tied to the embedding)."""
+
+    def __init__(self, model, lr: float = 3e-4, betas=(0.9, 0.999), eps: float = 1e-8,
+                 weight_decay: float = 0.01, grad_clip: float = 1.0,
+                 transfer_weight: float = 0.5):
+        if not isinstance(getattr(model, "head", None), Int8Linear):
+            raise ValueError("Int8DraftTrainer needs to_int8(model, trainable=True)")
+        self.model = model
+        self.grad_clip = grad_clip
+        self.transfer_weight = transfer_weight
+        self.opt = AdamWRequant(model.parameters(), lr=lr, betas=betas, eps=eps,
+                                weight_decay=weight_decay)
+        for mod in model.modules():
+            if isinstance(mod, Int8Linear):
+                self.opt.register_int8(mod)
+
+    def loss(self, tokens: torch.Tensor, teacher_states: torch.Tensor | None = None):
+        """(loss, ce, transfer) as device tensors, with the graph for backward."""
+        model = self.model
+        inp, tgt = tokens[:, :-1], tokens[:, 1:]
+        h, features = model.backbone(inp, teacher_states)
+        head = model.head
+        if not head._codes_current():
+            head._quantize_weight()
+        ce = LinearCrossEntropyInt8.apply(h, head.weight, head.weight_codes, head.weight_scales,
+                                          tgt.reshape(-1), IGNORE_INDEX, 128)
+        ts = transfer_space_loss(features, model.embedding.weight, tgt)
+        return ce + self.transfer_weight * ts, ce, ts
+
+    def step(self, tokens: torch.Tensor, teacher_states: torch.Tensor | None = None):
+        self.model.train()
+        loss, ce, ts = self.loss(tokens, teacher_states)
+        self.opt.zero_grad(set_to_none=True)
+        loss.backward()
+        coef = clip_coefficient(self.model.parameters(), self.grad_clip)
+        self.opt.step(clip_coef=coef)
+        return loss.detach(), ce.detach(), ts.detach()

@@ -1,0 +1,65 @@
+"""The float-tier model around the INT8 tier (CPU only): shapes, parameter counts against
+the reference's formulas (config.py:71-91), the tie of head and embedding after a device
+move (draft.py:49-51), identity-block init (block.py docstring), and the Horner spine
+against the explicit Hermite / Chebyshev basis (reference tests/test_ks3.py:15-37)."""
+
+import pytest
+import torch
+
+from ksdraft_amd.config import KSDraftConfig, baseline_config
+from ksdraft_amd.model import KSDraftModel, spine_horner
+from ksdraft_amd.model.spine import AdjacentInjection
+
+
+def test_baseline_config_counts():
+    cfg = baseline_config()
+    assert cfg.charts == 5888 and cfg.d_model == 1536 and cfg.rosa_streams == 512
+    # SURVEY Appendix B figures, from the reference's formulas
+    assert cfg.ks3_params() == 18_135_040
+    assert cfg.rosa_params() == 3_153_920
+    assert cfg.total_params() == 741_556_224
+    with pytest.raises(ValueError):
+        KSDraftConfig(dtype="fp8")
+
+
+def test_model_tie_and_identity_init():
+    cfg = KSDraftConfig(vocab_size=97, layers=2, d_model=128, rosa_streams=16, ks3_charts=64)
+    m = KSDraftModel(cfg, teacher_dim=32)
+    assert m.head.weight is m.embedding.weight
+    core = cfg.layers * cfg.layer_params() + cfg.embedding_params()
+    assert m.param_counts()["core"] == core
+    # every additive update starts at zero: the blocks' residual branches vanish
+    x = torch.randn(2, 5, 128)
+    for blk in m.blocks:
+        h, p = blk.injection(x)
+        assert torch.equal(h, x)
+        assert torch.equal(blk.ffn(x), torch.zeros_like(x))
+
+
+def test_spine_horner_matches_basis():
+    g = torch.Generator().manual_seed(0)
+    t = torch.randn(50, 7, 1, generator=g)
+    z = torch.randn(50, 7, 1, generator=g)
+    c = torch.randn(7, 6, generator=g)
+    s, w = spine_horner(t, z, c)
+    p0, p1, p2, p3, p4, p5 = c.unbind(-1)
+    t2, t3 = t * t, t * t * t
+    sb = (p0 * (2 * t3 - 3 * t2 + 1) + p1 * (-2 * t3 + 3 * t2) + p2 * (t3 - 2 * t2 + t)
+          + p3 * (t3 - t2))
+    wb = p4 * (2 * z * z - 1) + p5 * (4 * z * z * z - 3 * z)
+    torch.testing.assert_close(s, sb, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(w, wb, rtol=1e-5, atol=1e-5)
+
+
+def test_injection_seeds_position_zero_from_previous_layer():
+    torch.manual_seed(1)
+    inj = AdjacentInjection(32, rank=4, feature_rank=8)
+    for lr in (inj.gate_q, inj.gate_p, inj.inject):
+        torch.nn.init.normal_(lr.up.weight, std=0.1)
+    z = torch.randn(2, 6, 32)
+    prev = torch.randn(2, 6, 32)
+    out0, p = inj(z)
+    out1, _ = inj(z, prev)
+    assert torch.equal(out0[:, 1:], out1[:, 1:])      # only position 0 takes the seed
+    assert not torch.equal(out0[:, 0], out1[:, 0])
+    torch.testing.assert_close(p, inj.feature_up(inj.feature_down(z)))
