@@ -61,6 +61,9 @@ def parse():
     p.add_argument("--no-rosa", action="store_true", help="skip the Rosa kernel report")
     p.add_argument("--no-c3", action="store_true", help="skip the config-3 LM-head report")
     p.add_argument("--no-ln", action="store_true", help="skip the fused LayerNorm + quantize report")
+    p.add_argument("--no-c5", action="store_true", help="skip the config-5 draft train step")
+    p.add_argument("--c5-steps", type=int, default=3)
+    p.add_argument("--only-c5", action="store_true", help="run only the config-5 step (profiling)")
     p.add_argument("--pmc-probe", action="store_true",
                    help="for rocprofv3 --pmc runs: a 256 MiB device copy (counter "
                         "calibration), then 3 launches of each GEMM of the step; no timing")
@@ -408,6 +411,86 @@ def ln_quant_times(dev, reps):
     return res
 
 
+def draft_c5(dev, steps, warmup):
+    """the full KSDraft draft training step, INT8 forward + backward
+    through every linear. 24 DraftBlocks (Rosa 512 streams, DSpine injection, KS3 5888
+    charts) at d = 1536, vocabulary 150144 with the tied int8 head and the fused
+    cross-entropy, a synthetic bf16 teacher state ~N(0,1) (d 1536) on the teacher_proj
+    seam, B 4 x T 2048 uniform token ids (T + 1 drawn for the shift), AdamW (lr 3e-4, wd
+    0.01) fused with the int8 repack, grad-norm clip 1.0. Random init: the reference's
+    inits with the zero-init surfaces woken to N(0, 0.02). tok/s = 8192 / step time (HIP
+    events over `steps` steps after `warmup`); the forward, backward and optimizer parts
+    of the step are timed with events too."""
+    from ksdraft_amd.config import baseline_config
+    from ksdraft_amd.model import KSDraftModel, to_int8
+    from ksdraft_amd.train.int8_step import Int8DraftTrainer, clip_coefficient
+    cfg = baseline_config()
+    torch.manual_seed(0)
+    fm = KSDraftModel(cfg, teacher_dim=cfg.d_model, device=dev)
+    with torch.no_grad():
+        for name, p in fm.named_parameters():
+            if name.endswith(("up.weight", "out_proj.weight", "teacher_proj.weight")):
+                p.normal_(0, 0.02)
+    model = to_int8(fm, trainable=True)
+    del fm
+    torch.cuda.empty_cache()
+    tr = Int8DraftTrainer(model, lr=3e-4, weight_decay=0.01, grad_clip=1.0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    B, T = 4, 2048
+    tokens = torch.randint(0, cfg.vocab_size, (B, T + 1), device=dev, generator=g)
+    teacher = torch.randn(B, T, cfg.d_model, device=dev, generator=g).to(torch.bfloat16)
+    for _ in range(warmup):
+        tr.step(tokens, teacher)
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    losses = []
+    t0 = time.perf_counter()
+    for i in range(steps):
+        e = ev[i]
+        e[0].record()
+        tr.model.train()
+        loss, ce, ts = tr.loss(tokens, teacher)
+        e[1].record()
+        tr.opt.zero_grad(set_to_none=True)
+        loss.backward()
+        e[2].record()
+        coef = clip_coefficient(tr.model.parameters(), tr.grad_clip)
+        tr.opt.step(clip_coef=coef)
+        e[3].record()
+        losses.append(loss.detach())
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    fwd = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]))
+    bwd = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]))
+    opt = float(np.mean([e[2].elapsed_time(e[3]) for e in ev]))
+    step_ms = float(np.mean([e[0].elapsed_time(e[3]) for e in ev]))
+    res = {
+        "tok_per_s": round(B * T / (step_ms * 1e-3), 1),
+        "ms_per_step": round(step_ms, 3),
+        "wall_ms_per_step": round(wall * 1e3, 3),
+        "forward_ms": round(fwd, 3), "backward_ms": round(bwd, 3), "optimizer_ms": round(opt, 3),
+        "steps": steps, "warmup": warmup,
+        "loss_first_last": [round(float(losses[0]), 4), round(float(losses[-1]), 4)],
+        "params": sum(p.numel() for p in model.parameters()),
+        "int8_gemm_ops_per_step": _c5_gemm_ops(cfg, B * T),
+        "peak_mem_gb": round(torch.cuda.max_memory_allocated(dev) / 2**30, 2),
+        "workload": "BASELINE config 5: 24 layers, d 1536, 512 streams, 5888 charts, vocab "
+                    "150144, B 4 x T 2048, teacher state bf16 (d 1536)",
+    }
+    res["int8_gemm_tops"] = round(res["int8_gemm_ops_per_step"] / (step_ms * 1e-3) / 1e12, 1)
+    del tr, model
+    torch.cuda.empty_cache()
+    return res
+
+
+def _c5_gemm_ops(cfg, tokens):
+    """int8 GEMM ops of one config-5 step: per layer the KS3 down/up (fwd, dX, dW each) and
+    the Rosa q/k/v/out, plus the head and teacher_proj (no dX: its input needs no grad)."""
+    d, F_, S, V = cfg.d_model, cfg.charts, cfg.rosa_streams, cfg.vocab_size
+    per_layer = 3 * 2 * tokens * d * F_ * 2 + 3 * 2 * tokens * d * S * 4
+    return cfg.layers * per_layer + 3 * 2 * tokens * d * V + 2 * 2 * tokens * d * d
+
+
 def cpu_baseline(x, w, dy, budget_s):
     """The oracle's restatement of the reference CPU path (quantize in numpy; GEMMs as
     dequantize + fp32 BLAS matmul, reference ksdraft/kernels/gemm.py:76-82), timed on
@@ -470,6 +553,9 @@ def main():
     xc, wc, dyc, x, w, dy = make_inputs(dev)
     if args.pmc_probe:
         pmc_probe(x, w, dy)
+        return
+    if args.only_c5:
+        print(json.dumps({"draft_c5": draft_c5(dev, args.c5_steps, 1)}), flush=True)
         return
 
     # eager: warm-up then K timed steps
@@ -536,6 +622,7 @@ def main():
         "eager_ms_per_step": round(eager_ms, 4),
         "eager_wall_ms_per_step": round(eager_wall_ms, 4),
         "draft_train_step_tok_s": None,
+        "draft_c5": None,
         "kernels": kern,
         "ks3_c4_kernels": None if args.no_ks3 else ks3_kernel_times(dev, args.kernel_reps),
         "rosa_c4_kernels": None if args.no_rosa else rosa_kernel_times(dev, args.kernel_reps),
@@ -554,6 +641,10 @@ def main():
             "ops_per_launch": GEMM_OPS,
         },
     }
+    if not args.no_c5:
+        torch.cuda.empty_cache()
+        out["draft_c5"] = draft_c5(dev, args.c5_steps, 1)
+        out["draft_train_step_tok_s"] = out["draft_c5"]["tok_per_s"]
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(xc, wc, dyc, args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -194,6 +194,23 @@ int ksd_w8a8_gemm_nt(const int8_t *a, const uint16_t *a_scales, const int8_t *w,
                      const float *bias, void *y, int y_dtype, void *stream);
 
 /*
+ * G1 / G2 with split K — the same GEMM for launches with few output tiles (the dW of a
+ * narrow layer: N x K output, K = tokens). For group 128, a shape with fewer than 192
+ * tiles of 128 x 128 is split into S = ksd_w8a8_gemm_splits(M, N, K) contiguous K parts
+ * (S = min(256 / tiles, K/128 / 8, 8), at least 1; a function of the shape only). Part p
+ * covers the groups [floor(p*G/S), floor((p+1)*G/S)), G = K/128, each summed in the ordered
+ * contract above from zero; the parts are then added in ascending order in fp32, then the
+ * bias: y = ((part_0 + part_1) + ...) + bias. With S = 1 this is ksd_w8a8_gemm_nt exactly.
+ * Replaces _w8a8_gemm_kernel / w8a8_gemm (reference ksdraft/kernels/gemm.py:18-50, 53-90).
+ *   workspace  16-byte aligned fp32 scratch of at least S*M*N*4 bytes (unused when S = 1)
+ */
+int ksd_w8a8_gemm_splits(int64_t M, int64_t N, int64_t K, int group, int *splits);
+int ksd_w8a8_gemm_nt_ws(const int8_t *a, const uint16_t *a_scales, const int8_t *w,
+                        const uint16_t *w_scales, int64_t M, int64_t N, int64_t K, int group,
+                        const float *bias, void *y, int y_dtype, float *workspace,
+                        int64_t workspace_bytes, void *stream);
+
+/*
  * Test-only export of the exact int32 group partials P_g of the GEMM above
  * (the tl.dot result of reference ksdraft/kernels/gemm.py:42).
  *   partials (K/group, M, N) int32

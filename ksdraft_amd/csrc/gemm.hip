@@ -28,6 +28,8 @@
 //   * LDS rows are 128 bytes; the 16-byte chunk index is XOR-swizzled with (row & 7).
 #include "ksd_common.h"
 
+#include <type_traits>
+
 namespace ksd {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -325,18 +327,21 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_nt_kernel(
 //     DMA goes out as one scalar-based instruction per 1 KB (64-bit SGPR base + 32-bit
 //     per-lane offset), and the LDS chunk swizzle XORs with (row >> 1) & 7: 16 consecutive
 //     rows of one chunk column fill a 256-byte bank window (64 banks, no conflicts).
-//   * Per wave and step: tile 0's four MFMAs and the fp16 scale outer product, under the
-//     VALU epilogue of the previous step's tile 1; one barrier; tile 1's MFMAs, each
-//     followed by the LDS reads of the next step's fragments for the k slice it just
-//     consumed (the fragments double-buffer across steps), under this step's tile-0
-//     epilogue. Tile 1's partial and scales wait in registers for the next step.
-//   * A finished tile moves to a second accumulator and leaves in eight chunks of four
-//     elements, one chunk per following step, through buffer stores whose descriptor
-//     drops rows past M and columns past N. The output writes of all CUs are thus spread
-//     over the next tile instead of bursting at every tile end.
-//   * Waits: a wave's vector-memory loads complete in issue order, so "at most n
-//     outstanding" (n = the instructions issued after step q+1's DMA) proves that DMA done;
-//     pending stores only make such a wait stricter.
+//   * The step body is instantiated once per ring slot, so every LDS offset is an
+//     immediate. Per wave and step: one barrier, the DMA of step q+3, the fragment reads
+//     of step q, then the VALU epilogue of step q-1 (its partials finished long ago) while
+//     those reads are in flight, then both tiles' MFMA chains and their fp16 scale outer
+//     products.
+//   * The int32 chains start from the bits of 1.5*2^23 (12582912.0f) instead of zero:
+//     |P_g| < 2^22 keeps C + P_g in one binade with unit ulp, so the partial's bits read as
+//     an fp32 are exactly 12582912 + P_g and one exact v_sub_f32 gives float(P_g) (the
+//     half-rate v_cvt_f32_i32 is not needed). The contract is unchanged:
+//     acc = fmaf(float(P_g), sa*sw, acc).
+//   * A finished tile is stored at once (32 buffer stores per lane) through descriptors
+//     that drop rows past M and columns past N.
+//   * Waits: a wave's vector-memory operations complete in issue order, so "at most n
+//     outstanding" (n = the instructions issued after step q's DMA) proves that DMA done;
+//     stores issued after it only make such a wait stricter.
 namespace g128 {
 constexpr uint32_t SLOT = BM * BK;
 // raw buffer resources: offsets at or past num_records drop stores
@@ -384,59 +389,73 @@ template <int OUT> __device__ __forceinline__ uint32_t out_bits(float v) {
     return __builtin_bit_cast(uint16_t, h);
   }
 }
-struct Frags {
-  v4i a[4][2], b[4];
-  uint32_t sa[2], sw;
-};
+constexpr int kSeedBits = 0x4B400000;
+constexpr float kSeedF = 12582912.0f;
 
+// K-part p of `splits` covers steps [part_lo(p), part_lo(p + 1)) of the KT steps.
+__host__ __device__ __forceinline__ int part_lo(int p, int KT, int splits) {
+  return (int)((int64_t)p * KT / splits);
+}
+
+// Work unit u = (tile u / splits, K-part u % splits). With splits > 1, Y is the fp32
+// workspace: part p of a tile goes to Y + p * part_stride (elements), raw (no bias), and a
+// combine kernel adds the parts in order.
 template <int OUT, bool BIAS>
 __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
     const int8_t *__restrict__ A, const uint16_t *__restrict__ AS,
     const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int M, int N, int K,
-    int tiles_n, int ntiles, const float *__restrict__ bias, void *__restrict__ Y) {
+    int tiles_n, int ntiles, const float *__restrict__ bias, void *__restrict__ Y,
+    int splits, int64_t part_stride) {
   __shared__ __attribute__((aligned(16))) int8_t sA[NSLOT][BM * BK];
   __shared__ __attribute__((aligned(16))) int8_t sW[NSLOT][BN * BK];
   __shared__ __attribute__((aligned(16))) uint32_t sS[NSLOT][256];
-  constexpr int DEPTH = 3;  // steps of DMA in flight ahead of the step being computed
+  constexpr int DEPTH = NSLOT - 1;
   constexpr int ES = OUT == KSD_F32 ? 4 : 2;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3, half = lane >> 5, l32 = lane & 31;
   const int G = K / BK, KT = K / BK;
+  const int nunits = ntiles * splits;
 
-  int t_begin, t_count;
+  int u_begin, u_end;
   {
     const int nb = gridDim.x, per = nb / 8, rem = nb % 8, x = blockIdx.x % 8, i = blockIdx.x / 8;
     const int lb = x * per + min(x, rem) + i;
-    t_begin = (int)((int64_t)ntiles * lb / nb);
-    t_count = (int)((int64_t)ntiles * (lb + 1) / nb) - t_begin;
+    u_begin = (int)((int64_t)nunits * lb / nb);
+    u_end = (int)((int64_t)nunits * (lb + 1) / nb);
   }
-  const int T = t_count * KT;
+  auto unit_len = [&](int u) __attribute__((always_inline)) {
+    const int pp = u % splits;
+    return part_lo(pp + 1, KT, splits) - part_lo(pp, KT, splits);
+  };
+  int T = 0;
+  for (int u = u_begin; u < u_end; ++u) T += unit_len(u);
   if (T == 0) return;
 
-  // ---- DMA: wave w fills A and W rows [16w, 16w+16) of a step (two 1 KB instructions
-  // each); waves 0-3 also 64 scale rows (A [0,64), [64,128), W [0,64), [64,128)).
   const int drow0 = wave * 16 + (lane >> 3), drow1 = drow0 + 8;
   const int dch0 = ((lane & 7) ^ ((drow0 >> 1) & 7)) << 4;
   const int dch1 = ((lane & 7) ^ ((drow1 >> 1) & 7)) << 4;
   const bool s_load = wave < 4, s_isA = wave < 2;
-  const int NW = s_load ? 5 : 4;  // vector-memory instructions per DMA step
+  const int NW = s_load ? 5 : 4;
   const int srow = (wave & 1) * 64 + lane;
   const uint32_t ldsA = lds_addr(&sA[0][0]) + wave * 2048;
   const uint32_t ldsW = lds_addr(&sW[0][0]) + wave * 2048;
   const uint32_t ldsS = lds_addr(&sS[0][0]) + ((s_isA ? 0 : 128) + (wave & 1) * 64) * 4;
   const uint16_t *const SB = s_isA ? AS : WS;
-  const int8_t *ba, *bw;  // cursor: the next DMA step's tile bases (+ k) ...
+  const int8_t *ba, *bw;
   const uint16_t *bs;
-  uint32_t oa0, oa1, ow0, ow1, os;  // ... and per-lane offsets (rows clamped into range)
-  int cur_t = t_begin, cur_kt = 0;
+  uint32_t oa0, oa1, ow0, ow1, os;
+  int cur_u = u_begin, cur_kt = 0, cur_len = __builtin_amdgcn_readfirstlane(unit_len(u_begin));
   auto rebase = [&]() __attribute__((always_inline)) {
-    const int m0 = (cur_t / tiles_n) * BM, n0 = (cur_t % tiles_n) * BN;
-    ba = A + (int64_t)m0 * K;
-    bw = W + (int64_t)n0 * K;
+    // every value here is wave-uniform; readfirstlane keeps the DMA bases in SGPRs
+    const int cu_ = __builtin_amdgcn_readfirstlane(cur_u);
+    const int t = cu_ / splits, k0 = __builtin_amdgcn_readfirstlane(part_lo(cu_ % splits, KT, splits));
+    const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
+    ba = A + (int64_t)m0 * K + (int64_t)k0 * BK;
+    bw = W + (int64_t)n0 * K + (int64_t)k0 * BK;
     const int r0 = s_isA ? m0 : n0, rmax = s_isA ? M : N;
-    bs = SB + (int64_t)r0 * G;
+    bs = SB + (int64_t)r0 * G + k0;
     oa0 = (uint32_t)((min(m0 + drow0, M - 1) - m0) * K + dch0);
     oa1 = (uint32_t)((min(m0 + drow1, M - 1) - m0) * K + dch1);
     ow0 = (uint32_t)((min(n0 + drow0, N - 1) - n0) * K + dch0);
@@ -454,13 +473,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
     ba += BK;
     bw += BK;
     bs += 1;
-    if (++cur_kt == KT) {
+    if (++cur_kt == cur_len) {
       cur_kt = 0;
-      if (++cur_t < t_begin + t_count) rebase();
+      if (++cur_u < u_end) {
+        cur_len = __builtin_amdgcn_readfirstlane(unit_len(cur_u));
+        rebase();
+      }
     }
   };
 
-  // ---- fragment addresses in slot 0 (slot s adds s * SLOT, or s * 1024 for scales)
+  // fragment addresses in slot 0
   uint32_t adA[4][2], adB[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
@@ -471,157 +493,150 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
   }
   const uint32_t adSa = lds_addr(&sS[0][0]) + (wm * 64 + l32) * 4;
   const uint32_t adSw = lds_addr(&sS[0][0]) + (128 + wn * 32 + l32) * 4;
-  // lanes 32-63 supply k = 4..7 of the scale outer product: zeros
   const uint32_t smask = half ? 0u : 0xffffu;
+  const v16i kSeed = (v16i){kSeedBits, kSeedBits, kSeedBits, kSeedBits, kSeedBits, kSeedBits,
+                            kSeedBits, kSeedBits, kSeedBits, kSeedBits, kSeedBits, kSeedBits,
+                            kSeedBits, kSeedBits, kSeedBits, kSeedBits};
 
-  auto chain = [&](const Frags &f, int i) __attribute__((always_inline)) -> v16i {
-    v16i p = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[0][i], f.b[0], (v16i){}, 0, 0, 0);
-#pragma unroll
-    for (int kk = 1; kk < 4; ++kk) p = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[kk][i], f.b[kk], p, 0, 0, 0);
-    return p;
-  };
-  // sa (x) sw: an fp16 MFMA whose only non-zero k slot is 0, so every product is exact
-  auto scale = [&](const Frags &f, int i) __attribute__((always_inline)) -> v16f {
-    const v2u au = {f.sa[i] & smask, 0u}, bu = {f.sw & smask, 0u};
-    return __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, au), __builtin_bit_cast(v4h, bu),
-                                               (v16f){}, 0, 0, 0);
-  };
-  v16f acc[2], acc_old[2];
-  acc[0] = acc[1] = acc_old[0] = acc_old[1] = (v16f){};
-  auto ep = [&](int i, const v16i &p, const v16f &s) __attribute__((always_inline)) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[i][e] = fmaf((float)p[e], s[e], acc[i][e]);
-  };
+  // keep the seed in VGPRs (the MFMA reads srcC from VGPRs; left to itself the compiler
+  // keeps the constant in SGPRs and copies it before every chain)
+  v16i seedv = kSeed;
+  asm volatile("" : "+v"(seedv));
+  v16f acc0 = (v16f){}, acc1 = (v16f){};
+  // the previous step's partials and scale products: their epilogue runs one step later,
+  // when the MFMAs that made them have long finished (S* = 0: nothing to add)
+  v16i P0 = seedv, P1 = seedv;
+  v16f S0 = (v16f){}, S1 = (v16f){};
+  int kt = 0, uk = u_begin, klen = unit_len(u_begin);
 
-  // ---- gradual store of the finished tile (acc_old): chunk c = elements 2c, 2c+1 of both
-  // 32-row halves. Element e of a lane sits at row (e>>2)*8 + half*4 + (e&3) of its half.
-  __amdgpu_buffer_rsrc_t ors0 = __builtin_amdgcn_make_buffer_rsrc(Y, 0, 0, kBufFlags), ors1 = ors0;
-  int ovoff = 0, pend = 8;
-  auto drain = [&](int c) __attribute__((always_inline)) {
-    typedef uint32_t v16u __attribute__((ext_vector_type(16)));
-    // (whole-vector bit casts: a bit cast of one vector element reads element 0 here)
-    v16u o0, o1;
-    if constexpr (OUT == KSD_F32) {
-      o0 = __builtin_bit_cast(v16u, acc_old[0]);
-      o1 = __builtin_bit_cast(v16u, acc_old[1]);
-    }
-#define KSD_DRAIN(C)                                                                      \
-  case C:                                                                                 \
-    _Pragma("unroll") for (int ee = 0; ee < 2; ++ee) {                                    \
-      const int e = (C) * 2 + ee;                                                         \
-      const int vo = ovoff + ((e >> 2) * 8 + (e & 3)) * N * ES;                           \
-      if constexpr (OUT == KSD_F32) {                                                     \
-        __builtin_amdgcn_raw_buffer_store_b32(o0[e], ors0, vo, 0, 0);                     \
-        __builtin_amdgcn_raw_buffer_store_b32(o1[e], ors1, vo, 0, 0);                     \
-      } else {                                                                            \
-        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)out_bits<OUT>(acc_old[0][e]), ors0, vo, 0, 0); \
-        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)out_bits<OUT>(acc_old[1][e]), ors1, vo, 0, 0); \
-      }                                                                                   \
-    }                                                                                     \
-    break;
-    switch (c) {
-      KSD_DRAIN(0) KSD_DRAIN(1) KSD_DRAIN(2) KSD_DRAIN(3)
-      KSD_DRAIN(4) KSD_DRAIN(5) KSD_DRAIN(6) KSD_DRAIN(7)
-      default: break;
-    }
-#undef KSD_DRAIN
-  };
-  auto retire = [&](int t) __attribute__((always_inline)) {  // acc -> acc_old (tile t)
-    while (pend < 8) drain(pend++);
+  auto store_tile = [&](int u) __attribute__((always_inline)) {
+    const int t = u / splits;
+    char *const Yp = (char *)Y + (int64_t)(u % splits) * part_stride * ES;
     const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
     const int col = n0 + wn * 32 + l32;
     const int64_t r0 = (int64_t)m0 + wm * 64;
     const int64_t rows0 = max((int64_t)0, min((int64_t)32, (int64_t)M - r0));
     const int64_t rows1 = max((int64_t)0, min((int64_t)32, (int64_t)M - r0 - 32));
-    ors0 = __builtin_amdgcn_make_buffer_rsrc((char *)Y + r0 * N * ES, 0, (int)(rows0 * N * ES), kBufFlags);
-    ors1 = __builtin_amdgcn_make_buffer_rsrc((char *)Y + (r0 + 32) * N * ES, 0, (int)(rows1 * N * ES), kBufFlags);
-    ovoff = col < N ? (half * 4 * N + col) * ES : (int)kOob;
+    __amdgpu_buffer_rsrc_t r0s = __builtin_amdgcn_make_buffer_rsrc(Yp + r0 * N * ES, 0, (int)(rows0 * N * ES), kBufFlags);
+    __amdgpu_buffer_rsrc_t r1s = __builtin_amdgcn_make_buffer_rsrc(Yp + (r0 + 32) * N * ES, 0, (int)(rows1 * N * ES), kBufFlags);
+    const int voff = col < N ? (half * 4 * N + col) * ES : (int)kOob;
     const float b = BIAS ? (col < N ? bias[col] : 0.0f) : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int e = 0; e < 16; ++e) {
+      const int vo = voff + ((e >> 2) * 8 + (e & 3)) * N * ES;
+      const float y0 = BIAS ? acc0[e] + b : acc0[e];
+      const float y1 = BIAS ? acc1[e] + b : acc1[e];
+      if constexpr (OUT == KSD_F32) {
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y0), r0s, vo, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y1), r1s, vo, 0, 0);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)out_bits<OUT>(y0), r0s, vo, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)out_bits<OUT>(y1), r1s, vo, 0, 0);
+      }
+    }
+  };
+  auto epilogue = [&]() __attribute__((always_inline)) {
+    const v16f f0 = __builtin_bit_cast(v16f, P0), f1 = __builtin_bit_cast(v16f, P1);
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc_old[i][e] = BIAS ? acc[i][e] + b : acc[i][e];
-    acc[0] = acc[1] = (v16f){};
-    pend = 0;
+    for (int e = 0; e < 16; ++e) {
+      acc0[e] = fmaf(f0[e] - kSeedF, S0[e], acc0[e]);
+      acc1[e] = fmaf(f1[e] - kSeedF, S1[e], acc1[e]);
+    }
   };
 
   const int pre = min(DEPTH, T);
   for (int i = 0; i < pre; ++i) dma_step((uint32_t)i);
-  wait_vm((pre - 1) * NW);
-  fenced_barrier();
-  Frags F0, F1;
-  {
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      F0.b[kk] = lds16(adB[kk]);
-      F0.a[kk][0] = lds16(adA[kk][0]);
-      F0.a[kk][1] = lds16(adA[kk][1]);
-    }
-    F0.sa[0] = lds4(adSa);
-    F0.sa[1] = lds4(adSa + 128);
-    F0.sw = lds4(adSw);
-  }
-  v16i P1 = (v16i){};
-  v16f S1 = (v16f){};
-  int kt = 0, tk = t_begin;
-  auto step = [&](int q, Frags &cur, Frags &nxt) __attribute__((always_inline)) {
-    const v16i p0 = chain(cur, 0);
-    const v16f s0 = scale(cur, 0);
-    ep(1, P1, S1);  // tile 1 of step q-1 (zeros before the first step and after a retire)
-#pragma unroll
-    for (int m = 0; m < 5; ++m) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);  // VALU
-    }
-    // outstanding after step q+1's DMA: step q+2's (DMA issued in the previous step)
-    if (q + 1 < T) wait_vm(q + 2 < T ? NW : 0);
+
+  auto step = [&](auto slot_c, int q) __attribute__((always_inline)) {
+    constexpr int S = decltype(slot_c)::value;
+    constexpr uint32_t so = S * SLOT, ss = S * 1024;
+    const int after = min(T - 1 - q, DEPTH - 1);
+    wait_vm(after == 2 ? 2 * NW : (after == 1 ? NW : 0));
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     fenced_barrier();
-    // step q+1's fragments, slice kk right after the tile-1 MFMA that last reads slice kk
-    // of `cur` (at q = T-1 the reads hit a stale slot and are never used)
-    const uint32_t ns = (uint32_t)((q + 1) & (NSLOT - 1));
-    const uint32_t so = ns * SLOT, ss = ns * 1024;
-    v16i p1 = (v16i){};
+    if (q + DEPTH < T) dma_step((uint32_t)((S + DEPTH) % NSLOT));
+    v4i b[4], a0[4], a1[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      p1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[kk][1], cur.b[kk], p1, 0, 0, 0);
-      nxt.b[kk] = lds16(adB[kk] + so);
-      nxt.a[kk][0] = lds16(adA[kk][0] + so);
-      nxt.a[kk][1] = lds16(adA[kk][1] + so);
+      b[kk] = lds16(adB[kk] + so);
+      a0[kk] = lds16(adA[kk][0] + so);
     }
-    S1 = scale(cur, 1);
-    nxt.sa[0] = lds4(adSa + ss);
-    nxt.sa[1] = lds4(adSa + ss + 128);
-    nxt.sw = lds4(adSw + ss);
-    P1 = p1;
-    ep(0, p0, s0);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);  // DS read
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+    for (int kk = 0; kk < 4; ++kk) a1[kk] = lds16(adA[kk][1] + so);
+    const uint32_t sa0 = lds4(adSa + ss), sa1 = lds4(adSa + ss + 128), sw = lds4(adSw + ss);
+    // the previous step's epilogue while this step's fragments are in flight
+    epilogue();
+    v16i p0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0[0], b[0], seedv, 0, 0, 0);
+    v16i p1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1[0], b[0], seedv, 0, 0, 0);
+#pragma unroll
+    for (int kk = 1; kk < 4; ++kk) {
+      p0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0[kk], b[kk], p0, 0, 0, 0);
+      p1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1[kk], b[kk], p1, 0, 0, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
-    if (++kt == KT) {
-      ep(1, P1, S1);
-      retire(tk);
-      P1 = (v16i){};
+    const v2u sw2 = {sw & smask, 0u};
+    const v2u sa02 = {sa0 & smask, 0u}, sa12 = {sa1 & smask, 0u};
+    S0 = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, sa02), __builtin_bit_cast(v4h, sw2), (v16f){}, 0, 0, 0);
+    S1 = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, sa12), __builtin_bit_cast(v4h, sw2), (v16f){}, 0, 0, 0);
+    P0 = p0;
+    P1 = p1;
+    if (++kt == klen) {  // unit end (uniform): fold in this step, store, restart the sums
+      epilogue();
+      store_tile(uk);
+      acc0 = (v16f){};
+      acc1 = (v16f){};
+      S0 = (v16f){};
       S1 = (v16f){};
       kt = 0;
-      ++tk;
-    } else if (pend < 8) {
-      drain(pend++);
+      if (++uk < u_end) klen = unit_len(uk);
     }
-    if (q + DEPTH < T) dma_step((uint32_t)((q + DEPTH) & (NSLOT - 1)));
   };
-  for (int q = 0; q < T; q += 2) {
-    step(q, F0, F1);
+  using C0 = std::integral_constant<int, 0>;
+  using C1 = std::integral_constant<int, 1>;
+  using C2 = std::integral_constant<int, 2>;
+  using C3 = std::integral_constant<int, 3>;
+  for (int q = 0; q < T; q += NSLOT) {
+    step(C0{}, q);
     if (q + 1 >= T) break;
-    step(q + 1, F1, F0);
+    step(C1{}, q + 1);
+    if (q + 2 >= T) break;
+    step(C2{}, q + 2);
+    if (q + 3 >= T) break;
+    step(C3{}, q + 3);
   }
-  while (pend < 8) drain(pend++);
+}
+// y = ((p_0 + p_1) + ...) + bias, then the output type: the parts of a split launch in
+// ascending order, one fp32 rounding per add. 4 consecutive elements per thread.
+template <int OUT, bool BIAS>
+__global__ __launch_bounds__(256) void splitk_combine_kernel(const float *__restrict__ ws, int splits,
+                                                            int64_t part_stride, int64_t n_elems, int N,
+                                                            const float *__restrict__ bias,
+                                                            void *__restrict__ Y) {
+  const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i0 >= n_elems) return;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t i = i0 + j;
+    if (i >= n_elems) break;
+    float y = ws[i];
+    for (int pp = 1; pp < splits; ++pp) y = y + ws[(int64_t)pp * part_stride + i];
+    if (BIAS) y = y + bias[i % N];
+    if constexpr (OUT == KSD_F32) ((float *)Y)[i] = y;
+    else ((uint16_t *)Y)[i] = (uint16_t)out_bits<OUT>(y);
+  }
 }
 }  // namespace g128
+
+// Split count of the GS128 GEMM for a shape: a launch with fewer than 192 output tiles of
+// 128 x 128 splits K into up to 8 parts of at least 8 steps, aiming at 256 work units. It is
+// a function of the shape only (the contract must not depend on the device).
+static int g128_splits(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN), KT = K / BK;
+  if (tiles <= 0 || tiles >= 192) return 1;
+  int64_t s = 256 / tiles;
+  s = s < KT / 8 ? s : KT / 8;
+  s = s < 8 ? s : 8;
+  return s < 1 ? 1 : (int)s;
+}
 
 // one workgroup per CU; the CU count is a device constant, cached per device
 static int cu_count() {
@@ -640,34 +655,47 @@ static int cu_count() {
 template <int GROUP, int OUT, bool BIAS, int MODE>
 static void launch(const int8_t *a, const uint16_t *as, const int8_t *w, const uint16_t *ws,
                    int M, int N, int K, const float *bias, void *y, int32_t *partials,
-                   hipStream_t st) {
+                   hipStream_t st, int splits = 1, float *workspace = nullptr) {
   const int tn = (N + BN - 1) / BN, tm = (M + BM - 1) / BM;
   const int ntiles = tm * tn;
-  const int grid = min(ntiles, cu_count());
-  if constexpr (GROUP == 128 && MODE == 0)
-    g128::gemm_g128_kernel<OUT, BIAS><<<dim3(grid), dim3(NTHREADS), 0, st>>>(
-        a, as, w, ws, M, N, K, tn, ntiles, bias, y);
-  else
+  if constexpr (GROUP == 128 && MODE == 0) {
+    if (splits > 1) {
+      const int64_t nel = (int64_t)M * N;
+      const int grid = min(ntiles * splits, cu_count());
+      g128::gemm_g128_kernel<KSD_F32, false><<<dim3(grid), dim3(NTHREADS), 0, st>>>(
+          a, as, w, ws, M, N, K, tn, ntiles, nullptr, workspace, splits, nel);
+      const int64_t cb = (nel + 1023) / 1024;
+      g128::splitk_combine_kernel<OUT, BIAS><<<dim3((unsigned)cb), dim3(256), 0, st>>>(
+          workspace, splits, nel, nel, N, bias, y);
+    } else {
+      const int grid = min(ntiles, cu_count());
+      g128::gemm_g128_kernel<OUT, BIAS><<<dim3(grid), dim3(NTHREADS), 0, st>>>(
+          a, as, w, ws, M, N, K, tn, ntiles, bias, y, 1, 0);
+    }
+  } else {
+    const int grid = min(ntiles, cu_count());
     gemm_nt_kernel<GROUP, OUT, BIAS, MODE><<<dim3(grid), dim3(NTHREADS), 0, st>>>(
         a, as, w, ws, M, N, K, tn, ntiles, bias, y, partials);
+  }
 }
 
 template <int GROUP, int OUT>
 static void launch_b(const int8_t *a, const uint16_t *as, const int8_t *w, const uint16_t *ws,
-                     int M, int N, int K, const float *bias, void *y, hipStream_t st) {
-  if (bias) launch<GROUP, OUT, true, 0>(a, as, w, ws, M, N, K, bias, y, nullptr, st);
-  else launch<GROUP, OUT, false, 0>(a, as, w, ws, M, N, K, bias, y, nullptr, st);
+                     int M, int N, int K, const float *bias, void *y, hipStream_t st,
+                     int splits, float *workspace) {
+  if (bias) launch<GROUP, OUT, true, 0>(a, as, w, ws, M, N, K, bias, y, nullptr, st, splits, workspace);
+  else launch<GROUP, OUT, false, 0>(a, as, w, ws, M, N, K, bias, y, nullptr, st, splits, workspace);
 }
 
 template <int GROUP>
 static int launch_o(const int8_t *a, const uint16_t *as, const int8_t *w, const uint16_t *ws,
                     int M, int N, int K, const float *bias, void *y, int y_dtype,
-                    hipStream_t st) {
+                    hipStream_t st, int splits = 1, float *workspace = nullptr) {
   switch (y_dtype) {
-    case KSD_F32: launch_b<GROUP, KSD_F32>(a, as, w, ws, M, N, K, bias, y, st); break;
-    case KSD_BF16: launch_b<GROUP, KSD_BF16>(a, as, w, ws, M, N, K, bias, y, st); break;
-    case KSD_F16: launch_b<GROUP, KSD_F16>(a, as, w, ws, M, N, K, bias, y, st); break;
-    case KSD_F16_SAT: launch_b<GROUP, KSD_F16_SAT>(a, as, w, ws, M, N, K, bias, y, st); break;
+    case KSD_F32: launch_b<GROUP, KSD_F32>(a, as, w, ws, M, N, K, bias, y, st, splits, workspace); break;
+    case KSD_BF16: launch_b<GROUP, KSD_BF16>(a, as, w, ws, M, N, K, bias, y, st, splits, workspace); break;
+    case KSD_F16: launch_b<GROUP, KSD_F16>(a, as, w, ws, M, N, K, bias, y, st, splits, workspace); break;
+    case KSD_F16_SAT: launch_b<GROUP, KSD_F16_SAT>(a, as, w, ws, M, N, K, bias, y, st, splits, workspace); break;
     default: return fail(KSD_ETYPE, "w8a8_gemm: unsupported output dtype %d", y_dtype);
   }
   return check_launch("w8a8_gemm_nt");
@@ -703,6 +731,33 @@ extern "C" int ksd_w8a8_gemm_nt(const int8_t *a, const uint16_t *a_scales, const
     case 64: return launch_o<64>(a, a_scales, w, w_scales, (int)M, (int)N, (int)K, bias, y, y_dtype, st);
     default: return launch_o<128>(a, a_scales, w, w_scales, (int)M, (int)N, (int)K, bias, y, y_dtype, st);
   }
+}
+
+extern "C" int ksd_w8a8_gemm_splits(int64_t M, int64_t N, int64_t K, int group, int *splits) {
+  int rc = gemm_checks(reinterpret_cast<const int8_t *>(16), reinterpret_cast<const int8_t *>(16),
+                       M, N, K, group);
+  if (rc != KSD_OK) return rc;
+  if (!splits) return fail(KSD_EINVAL, "w8a8_gemm_splits: null output");
+  *splits = group == 128 ? g128_splits(M, N, K) : 1;
+  return KSD_OK;
+}
+
+extern "C" int ksd_w8a8_gemm_nt_ws(const int8_t *a, const uint16_t *a_scales, const int8_t *w,
+                                   const uint16_t *w_scales, int64_t M, int64_t N, int64_t K,
+                                   int group, const float *bias, void *y, int y_dtype,
+                                   float *workspace, int64_t workspace_bytes, void *stream) {
+  int rc = gemm_checks(a, w, M, N, K, group);
+  if (rc != KSD_OK) return rc;
+  if (M == 0 || N == 0 || K == 0) return KSD_OK;
+  const int splits = group == 128 ? g128_splits(M, N, K) : 1;
+  if (splits == 1)
+    return ksd_w8a8_gemm_nt(a, a_scales, w, w_scales, M, N, K, group, bias, y, y_dtype, stream);
+  const int64_t need = (int64_t)splits * M * N * 4;
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15) != 0)
+    return fail(KSD_EINVAL, "w8a8_gemm_nt_ws: needs a 16-byte aligned fp32 workspace of %lld bytes "
+                "(%d K parts), got %lld", (long long)need, splits, (long long)workspace_bytes);
+  return launch_o<128>(a, a_scales, w, w_scales, (int)M, (int)N, (int)K, bias, y, y_dtype,
+                       (hipStream_t)stream, splits, workspace);
 }
 
 extern "C" int ksd_w8a8_group_partials(const int8_t *a, const int8_t *w, int64_t M, int64_t N,

@@ -3,8 +3,10 @@
 ``w8a8_gemm`` keeps the reference signature, validation and errors (gemm.py:53-90) and
 returns fp32 (M, N). The kernel computes, per output element, the ordered per-group
 contract acc = fmaf(float(P_g), sa*sw, acc) for g ascending, with P_g the exact int32
-group dot product. ``w8a8_gemm_out`` exposes the fused epilogue (fp32 bias, bf16/fp16
-output) used by the linear layer and the KS3 cell.
+group dot product. Shapes with few output tiles (``gemm_splits`` > 1) split the groups into
+contiguous parts, each summed that way from zero, and add the parts in order.
+``w8a8_gemm_out`` exposes the fused epilogue (fp32 bias, bf16/fp16 output) used by the
+linear layer and the KS3 cell.
 """
 
 from __future__ import annotations
@@ -95,9 +97,32 @@ def w8a8_gemm_out(a_codes: torch.Tensor, a_scales: torch.Tensor, w_codes: torch.
         if bias is not None:
             out += bias.to(out_dtype)
         return out
-    _lib.call("ksd_w8a8_gemm_nt", a.data_ptr(), as_.data_ptr(), w.data_ptr(), ws.data_ptr(),
-              M, N, K, group, _lib.ptr(bias), out.data_ptr(), code, _lib.stream_ptr(dev))
+    splits = gemm_splits(M, N, K, group)
+    if splits > 1:  # few output tiles: K split into parts, summed in order (fp32 workspace)
+        work = torch.empty(splits * M * N, dtype=torch.float32, device=dev)
+        _lib.call("ksd_w8a8_gemm_nt_ws", a.data_ptr(), as_.data_ptr(), w.data_ptr(),
+                  ws.data_ptr(), M, N, K, group, _lib.ptr(bias), out.data_ptr(), code,
+                  work.data_ptr(), work.numel() * 4, _lib.stream_ptr(dev))
+    else:
+        _lib.call("ksd_w8a8_gemm_nt", a.data_ptr(), as_.data_ptr(), w.data_ptr(), ws.data_ptr(),
+                  M, N, K, group, _lib.ptr(bias), out.data_ptr(), code, _lib.stream_ptr(dev))
     return out
+
+
+_SPLITS: dict = {}
+
+
+def gemm_splits(M: int, N: int, K: int, group: int = GROUP_SIZE) -> int:
+    """K parts the GEMM of this shape is split into (a function of the shape; 1 for most
+    shapes, more when there are too few 128 x 128 output tiles to fill the device)."""
+    key = (M, N, K, group)
+    s = _SPLITS.get(key)
+    if s is None:
+        import ctypes
+        c = ctypes.c_int(0)
+        _lib.call("ksd_w8a8_gemm_splits", M, N, K, group, ctypes.byref(c))
+        s = _SPLITS[key] = c.value
+    return s
 
 
 def w8a8_gemm(a_codes: torch.Tensor, a_scales: torch.Tensor, w_codes: torch.Tensor,

@@ -41,7 +41,7 @@ def lib() -> ctypes.CDLL:
         _lib.ksd_half_to_float.restype = ctypes.c_float
         _lib.ksd_oracle_partials.argtypes = [P, P, I64, I64, I64, I, P]
         _lib.ksd_oracle_partials.restype = None
-        _lib.ksd_oracle_gemm_ordered.argtypes = [P, P, P, P, I64, I64, I64, I, P, P, I64, P]
+        _lib.ksd_oracle_gemm_ordered.argtypes = [P, P, P, P, I64, I64, I64, I, P, P, I64, I, P]
         _lib.ksd_oracle_gemm_ordered.restype = None
         _lib.ksd_oracle_rosa_match.argtypes = [P, P, P, I64, I64, I, P, P, P]
         _lib.ksd_oracle_rosa_match.restype = None

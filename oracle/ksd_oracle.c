@@ -64,24 +64,33 @@ void ksd_oracle_partials(const int8_t *a, const int8_t *w, int64_t M, int64_t N,
  */
 void ksd_oracle_gemm_ordered(const int8_t *a, const uint16_t *as, const int8_t *w,
                              const uint16_t *ws, int64_t M, int64_t N, int64_t K, int group,
-                             const float *bias, const int64_t *rows, int64_t n_rows, float *y) {
+                             const float *bias, const int64_t *rows, int64_t n_rows, int splits,
+                             float *y) {
   const int64_t G = K / group;
   const int64_t R = rows ? n_rows : M;
+  if (splits < 1) splits = 1;
 #pragma omp parallel for collapse(2) schedule(static)
   for (int64_t r = 0; r < R; ++r)
     for (int64_t n = 0; n < N; ++n) {
       const int64_t m = rows ? rows[r] : r;
       const int8_t *ar = a + m * K;
       const int8_t *wr = w + n * K;
-      float acc = 0.0f;
-      for (int64_t g = 0; g < G; ++g) {
-        int32_t p = 0;
-        for (int64_t k = g * group; k < (g + 1) * group; ++k) p += (int32_t)ar[k] * (int32_t)wr[k];
-        const float s = ksd_half_to_float(as[m * G + g]) * ksd_half_to_float(ws[n * G + g]);
-        acc = fmaf((float)p, s, acc);
+      float total = 0.0f;
+      /* K part q: groups [floor(q G / S), floor((q+1) G / S)), summed from zero in order;
+         the parts are added in ascending order */
+      for (int q = 0; q < splits; ++q) {
+        const int64_t g0 = (int64_t)q * G / splits, g1 = (int64_t)(q + 1) * G / splits;
+        float acc = 0.0f;
+        for (int64_t g = g0; g < g1; ++g) {
+          int32_t p = 0;
+          for (int64_t k = g * group; k < (g + 1) * group; ++k) p += (int32_t)ar[k] * (int32_t)wr[k];
+          const float s = ksd_half_to_float(as[m * G + g]) * ksd_half_to_float(ws[n * G + g]);
+          acc = fmaf((float)p, s, acc);
+        }
+        total = q == 0 ? acc : total + acc;
       }
-      if (bias) acc = acc + bias[n];
-      y[r * N + n] = acc;
+      if (bias) total = total + bias[n];
+      y[r * N + n] = total;
     }
 }
 

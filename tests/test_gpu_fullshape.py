@@ -105,7 +105,8 @@ def test_config3_lm_head_full_shape():
     y, xtq, xts = w8a8_linear_forward_train(x, wq, ws, None, 128, torch.float32)
     xq, xs = oq.quantize_last_dim(_np(x))
     rows = _rows(M, 32, 2)
-    assert _eq(_np(y[rows]), og.gemm_ordered(xq[rows], xs[rows], _np(wq), _np(ws)))
+    assert _eq(_np(y[rows]), og.gemm_ordered(xq[rows], xs[rows], _np(wq), _np(ws),
+                                                     splits=og.splits_for(M, N, Kd)))
     exq, exs = oq.requant_transpose(xq, xs)
     assert _eq(_np(xtq), exq) and _eq(_np(xts), exs)
 
@@ -134,10 +135,12 @@ def test_config3_lm_head_full_shape():
     eq, es = oq.quantize_last_dim(np.ascontiguousarray(real))
     assert _eq(_np(wtq[krows]), eq) and _eq(_np(wts[krows]), es)
     dx = kg.w8a8_gemm(gq, gs, wtq, wts)
-    assert _eq(_np(dx[rows]), og.gemm_ordered(_np(gq[rows]), _np(gs[rows]), _np(wtq), _np(wts)))
+    assert _eq(_np(dx[rows]), og.gemm_ordered(_np(gq[rows]), _np(gs[rows]), _np(wtq), _np(wts),
+                                                      splits=og.splits_for(M, Kd, N)))
     # dW = dY^T . X^T: 150144 output rows over the 4096 tokens
     dw = kg.w8a8_gemm(gtq, gts, xtq, xts)
-    assert _eq(_np(dw[vrows]), og.gemm_ordered(_np(gtq[vrows]), _np(gts[vrows]), exq, exs))
+    assert _eq(_np(dw[vrows]), og.gemm_ordered(_np(gtq[vrows]), _np(gts[vrows]), exq, exs,
+                                                       splits=og.splits_for(N, Kd, M)))
 
     # the autograd function composes exactly these launches
     xg = x.clone().requires_grad_(True)
@@ -205,12 +208,13 @@ def test_config4_ks3_cell_full_shape():
     x2n = _np(x2.float())
     exq, exs = oq.quantize_last_dim(x2n[rows])
     assert _eq(_np(xq[rows]), exq) and _eq(_np(xs[rows]), exs)
-    coords = ok.coords_from_gemm(og.gemm_ordered(exq, exs, p["down_codes"], p["down_scales"]))
+    coords = ok.coords_from_gemm(og.gemm_ordered(exq, exs, p["down_codes"], p["down_scales"],
+                                                        splits=og.splits_for(M, Fn, d)))
     assert _eq(_np(coords16[rows]).astype(np.float32), coords)
     hfeat = ok.spine_features_int8(coords, p["spine_codes"], p["spine_scale"], sc, sh, lut)
     ehq, ehs = oq.quantize_last_dim(hfeat)
     assert _eq(_np(hq[rows]), ehq) and _eq(_np(hs[rows]), ehs)
-    ey = og.gemm_ordered(ehq, ehs, p["up_codes"], p["up_scales"])
+    ey = og.gemm_ordered(ehq, ehs, p["up_codes"], p["up_scales"], splits=og.splits_for(M, d, Fn))
     assert torch.equal(y.detach().reshape(M, d)[rows].cpu(), torch.from_numpy(ey).to(torch.bfloat16))
 
     # backward stages
@@ -223,7 +227,8 @@ def test_config4_ks3_cell_full_shape():
     upTq, upTs = kq.requant_transpose(cell.up_codes, cell.up_scales)
     assert _eq(_np(upTq), upT[0]) and _eq(_np(upTs), upT[1])
     value = kg.w8a8_gemm_out(gq, gs, upTq, upTs, out_dtype=torch.float16)
-    assert _eq(_np(value[rows]).astype(np.float32), ok.h(og.gemm_ordered(egq, egs, *upT)))
+    assert _eq(_np(value[rows]).astype(np.float32), ok.h(og.gemm_ordered(egq, egs, *upT,
+                                                                                    splits=og.splits_for(M, Fn, d))))
     scale16, shift16 = cell._warp_scalars(torch.float16)
     v = K.ks3_vjp(value, coords16, cell.spine_codes, cell.spine_scale, scale16, shift16,
                   cell.warp_scale_raw, cell.warp_shift_raw)
@@ -237,16 +242,18 @@ def test_config4_ks3_cell_full_shape():
         tq, ts = oq.quantize_last_dim(np.ascontiguousarray(dc.T))
         assert _eq(_np(v["dct_codes"][:, r]), tq) and _eq(_np(v["dct_scales"][:, grp:grp + 1]), ts)
     downT = oq.requant_transpose(p["down_codes"], p["down_scales"])
-    edx = og.gemm_ordered(_np(v["dc_codes"][rows]), _np(v["dc_scales"][rows]), *downT)
+    edx = og.gemm_ordered(_np(v["dc_codes"][rows]), _np(v["dc_scales"][rows]), *downT,
+                          splits=og.splits_for(M, d, Fn))
     assert torch.equal(xd.grad.reshape(M, d)[rows].cpu(), torch.from_numpy(edx).to(torch.bfloat16))
     xT = oq.requant_transpose(_np(xq), _np(xs))
     frows = _rows(Fn, 24, 7)
-    eddown = og.gemm_ordered(_np(v["dct_codes"][frows]), _np(v["dct_scales"][frows]), *xT)
+    eddown = og.gemm_ordered(_np(v["dct_codes"][frows]), _np(v["dct_scales"][frows]), *xT,
+                             splits=og.splits_for(Fn, d, M))
     assert _eq(_np(cell.master_down.grad[frows]), ok.h(eddown))
     gT = oq.quantize_last_dim(np.ascontiguousarray(g16n.T))
     hT = oq.requant_transpose(_np(hq), _np(hs))
     drows = _rows(d, 24, 8)
-    edup = og.gemm_ordered(gT[0][drows], gT[1][drows], *hT)
+    edup = og.gemm_ordered(gT[0][drows], gT[1][drows], *hT, splits=og.splits_for(d, Fn, M))
     assert _eq(_np(cell.master_up.grad[drows]), ok.h(edup))
 
 

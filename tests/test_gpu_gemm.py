@@ -149,3 +149,23 @@ def test_many_tiles_persistent_chunks():
     y = kg.w8a8_gemm(*_gpu(aq, as_, wq, ws)).cpu().numpy()
     rows = np.arange(0, 2304, 37)
     assert np.array_equal(y[rows], og.gemm_ordered(aq, as_, wq, ws, rows=rows))
+
+
+@pytest.mark.parametrize("M,K,N", [(512, 8192, 1536), (1536, 8192, 512), (256, 2048, 256),
+                                   (200, 4096, 130), (64, 16384, 96)])
+def test_split_k_shapes_bit_exact(M, K, N):
+    """Shapes with few output tiles run split into K parts (the dW of narrow layers, e.g.
+    the Rosa projections at 8192 tokens): bit-exact against the split contract, for every
+    output type and with bias."""
+    S = og.splits_for(M, N, K)
+    assert S > 1 and kg.gemm_splits(M, N, K) == S
+    aq, as_, wq, ws = _operands(31 + M, M, K, N)
+    ta = _gpu(aq, as_, wq, ws)
+    y = kg.w8a8_gemm(*ta).cpu().numpy()
+    assert np.array_equal(y.view(np.uint32), og.gemm_ordered(aq, as_, wq, ws).view(np.uint32))
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(M))
+    exp = torch.from_numpy(og.gemm_ordered(aq, as_, wq, ws, bias=bias.numpy()))
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        got = kg.w8a8_gemm_out(*ta, bias=bias.to(DEV), out_dtype=dt).cpu()
+        assert torch.equal(got, exp.to(dt)), dt
+    np.testing.assert_allclose(y, og.gemm_reference(aq, as_, wq, ws), rtol=1e-4, atol=1e-3)

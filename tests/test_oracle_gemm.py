@@ -108,3 +108,47 @@ def test_ragged_k_pads_like_reference():
                                rtol=1e-6, atol=1e-6)
     with pytest.raises(ValueError):
         og.gemm_reference(aq, as_[:, :0], wq, ws[:, :0])
+
+
+def test_split_policy_matches_the_library():
+    """The oracle's split rule equals the library's for shapes on both sides of the
+    192-tile threshold (a pure host query: no device work)."""
+    import ctypes
+    from ksdraft_amd import _lib
+    c = ctypes.c_int(0)
+    shapes = [(512, 1536, 8192), (1536, 512, 8192), (1536, 1536, 8192), (256, 256, 2048),
+              (128, 128, 1024), (128, 128, 896), (64, 64, 128), (8192, 1536, 1536),
+              (1536, 5888, 8192), (2048, 3072, 4096), (130, 257, 16384), (1, 1, 65536)]
+    for M, N, K in shapes:
+        _lib.call("ksd_w8a8_gemm_splits", M, N, K, 128, ctypes.byref(c))
+        assert c.value == og.splits_for(M, N, K), (M, N, K, c.value)
+        _lib.call("ksd_w8a8_gemm_splits", M, N, K, 64, ctypes.byref(c))
+        assert c.value == 1
+    assert og.splits_for(512, 1536, 8192) == 5 and og.splits_for(1536, 1536, 8192) == 1
+
+
+def test_split_contract_is_the_ordered_sum_of_its_parts():
+    """With S parts the contract is ((part_0 + part_1) + ...) + bias, each part the ordered
+    contract over its groups: recomposed here from unsplit oracle calls on K slices."""
+    rng = np.random.default_rng(8)
+    M, N, K, S = 40, 24, 1280, 3
+    a = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    w = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    sa = (rng.random((M, K // 128)) * 0.05 + 1e-3).astype(np.float16)
+    sw = (rng.random((N, K // 128)) * 0.05 + 1e-3).astype(np.float16)
+    bias = rng.standard_normal(N).astype(np.float32)
+    y = og.gemm_ordered(a, sa, w, sw, bias=bias, splits=S)
+    G = K // 128
+    parts = []
+    for q in range(S):
+        g0, g1 = q * G // S, (q + 1) * G // S
+        parts.append(og.gemm_ordered(a[:, g0 * 128:g1 * 128], sa[:, g0:g1], w[:, g0 * 128:g1 * 128],
+                                     sw[:, g0:g1], splits=1))
+    tot = parts[0]
+    for p_ in parts[1:]:
+        tot = (tot + p_).astype(np.float32)
+    tot = (tot + bias[None, :]).astype(np.float32)
+    assert np.array_equal(y.view(np.uint32), tot.view(np.uint32))
+    # and the unsplit contract agrees to rounding
+    y1 = og.gemm_ordered(a, sa, w, sw, bias=bias, splits=1)
+    np.testing.assert_allclose(y, y1, rtol=1e-5, atol=1e-5 * np.abs(y1).max())
