@@ -246,6 +246,7 @@ class KS3Int8Cell(nn.Module):
 
         self.register_buffer("tanh_lut", make_tanh_lut(down.device))
         self.trainable = trainable
+        self._master_codes_keys = {}  # master name -> (storage, version) its codes came from
         if trainable:
             for name, value in (("down", down), ("up", up),
                                 ("coefficients", coeffs),
@@ -306,14 +307,37 @@ class KS3Int8Cell(nn.Module):
                                self.tanh_lut, self.group)
         return hq, hs, coords16
 
+    def invalidate_codes(self) -> None:
+        """Forget down/up codes handed over by an optimizer (train.AdamWRequant): the next
+        forward requantizes the masters. Needed after a write to a master that torch does
+        not version (through ``.data`` or a raw pointer)."""
+        self._master_codes_keys = {}
+
+    def _apply(self, fn, *args, **kwargs):
+        self.invalidate_codes()
+        return super()._apply(fn, *args, **kwargs)
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        self.invalidate_codes()
+        return super()._load_from_state_dict(*args, **kwargs)
+
+    def _master_codes_current(self, name: str) -> bool:
+        """True when train.AdamWRequant wrote `name`'s codes in the pass that last updated
+        the master, and the master has kept its storage and in-place version since."""
+        keys = getattr(self, "_master_codes_keys", None) or {}
+        m = getattr(self, "master_" + name)
+        return (getattr(self, "_codes_owner", None) is not None
+                and keys.get(name) == (m.data_ptr(), m._version))
+
     @torch.no_grad()
     def _repack_masters(self):
-        """ks3_int8.py:262-277."""
-        dq, ds = quantize_last_dim(self.master_down, self.group)
-        uq, us = quantize_last_dim(self.master_up, self.group)
+        """ks3_int8.py:262-277. The down/up codes are skipped when the optimizer already
+        wrote them from the masters as they are (the same quantize_last_dim)."""
+        if not self._master_codes_current("down"):
+            self.down_codes, self.down_scales = quantize_last_dim(self.master_down, self.group)
+        if not self._master_codes_current("up"):
+            self.up_codes, self.up_scales = quantize_last_dim(self.master_up, self.group)
         sq, ss = pack_spine(self.master_coefficients, self.group)
-        self.down_codes, self.down_scales = dq, ds
-        self.up_codes, self.up_scales = uq, us
         self.spine_codes, self.spine_scale = sq, ss
         scale_t = F.softplus(self.master_raw_scale.detach()) + 1e-4
         shift_t = 0.5 * torch.tanh(self.master_raw_shift.detach())

@@ -47,10 +47,21 @@ class AdjacentInjection(nn.Module):
         return self.feature_up(self.feature_down(z))
 
     def forward(self, z: torch.Tensor, prev_layer_feature: torch.Tensor | None = None):
-        """(z', p): the injected stream and this layer's predicted feature."""
-        p = self.predicted_feature(z)
+        """(z', p): the injected stream and this layer's predicted feature.
+
+        The low-rank maps that read the same input run as one GEMM with their weights
+        stacked (z: feature_down and gate_q.down; p_prev: gate_p.down and inject.down),
+        and gate_q(z) + gate_p(p_prev) as one GEMM over the concatenated rank: the same
+        sums as spine.py:62-68, in one pass over each (M, d) operand instead of two."""
+        r1 = self.feature_down.out_features
+        zd = F.linear(z, torch.cat([self.feature_down.weight, self.gate_q.down.weight]))
+        p = self.feature_up(zd[..., :r1])
         p_prev = F.pad(p, (0, 0, 1, 0))[:, :-1, :]
         if prev_layer_feature is not None:
             p_prev = torch.cat([prev_layer_feature[:, :1, :], p_prev[:, 1:, :]], dim=1)
-        gate = torch.sigmoid(self.gate_q(z) + self.gate_p(p_prev) + self.gate_bias)
-        return z + gate * self.inject(p_prev), p
+        r2 = self.gate_p.down.out_features
+        pd = F.linear(p_prev, torch.cat([self.gate_p.down.weight, self.inject.down.weight]))
+        pre = F.linear(torch.cat([zd[..., r1:], pd[..., :r2]], dim=-1),
+                       torch.cat([self.gate_q.up.weight, self.gate_p.up.weight], dim=1),
+                       self.gate_bias)
+        return z + torch.sigmoid(pre) * self.inject.up(pd[..., r2:]), p

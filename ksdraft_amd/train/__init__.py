@@ -203,17 +203,33 @@ class AdamWRequant(torch.optim.Optimizer):
         """After each step the module's codes are those of its updated master. The module
         then skips its own per-call requantization until its master changes; a write to
         the master through ``.data`` (which torch does not version) must be followed by
-        ``module.invalidate_codes()``."""
-        self._int8[id(module.weight)] = module
+        ``module.invalidate_codes()``. Accepts an Int8Linear (its ``weight``) or a
+        trainable KS3Int8Cell (its ``master_down`` and ``master_up``, whose codes the
+        cell's forward repack would otherwise rebuild every call)."""
+        if hasattr(module, "master_down"):
+            for name in ("down", "up"):
+                self._int8[id(getattr(module, "master_" + name))] = (module, name)
+        else:
+            self._int8[id(module.weight)] = (module, None)
         module._codes_owner = self
+
+    # parameters at least this large take the fused one-pass kernel; smaller ones (norms,
+    # biases, gate vectors) are batched into torch's multi-tensor AdamW
+    FUSED_MIN_NUMEL = 1 << 16
 
     @torch.no_grad()
     def step(self, closure=None, clip_coef: torch.Tensor | None = None):
+        """One AdamW step. Registered Int8Linear masters go through the fused update +
+        int8 repack kernel, one launch each (clip_coef applied on load); every other
+        parameter goes through torch's own multi-tensor AdamW (torch.optim.adamw with
+        foreach), after one multi-tensor multiply by clip_coef, as clip_grad_norm_ does."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
+        from torch.optim.adamw import adamw as torch_adamw
         for group in self.param_groups:
+            fl = ([], [], [], [], [])  # params, grads, exp_avg, exp_avg_sq, steps
             for p in group["params"]:
                 if p.grad is None:
                     continue
@@ -222,20 +238,42 @@ class AdamWRequant(torch.optim.Optimizer):
                     st["step"] = torch.tensor(0.0)
                     st["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
                     st["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+                reg = self._int8.get(id(p))
+                if reg is None and (p.numel() < self.FUSED_MIN_NUMEL or p.dtype != torch.float32
+                                    or not p.is_contiguous() or not p.grad.is_contiguous()):
+                    for lst, v in zip(fl, (p, p.grad, st["exp_avg"], st["exp_avg_sq"], st["step"])):
+                        lst.append(v)
+                    continue
                 n = self._steps.get(id(p))
                 if n is None:  # first step, or state loaded from a state_dict (a CPU tensor)
                     n = int(st["step"])
                 n += 1
                 self._steps[id(p)] = n
                 st["step"].fill_(float(n))  # torch's AdamW state layout: a CPU scalar tensor
-                mod = self._int8.get(id(p))
                 res = adamw_requant_(p, p.grad.contiguous(), st["exp_avg"], st["exp_avg_sq"],
                                      n, group["lr"], group["betas"],
                                      group["eps"], group["weight_decay"], clip_coef,
-                                     quantize=mod is not None)
-                if mod is not None:  # the codes now belong to the master as it is
+                                     quantize=reg is not None)
+                if reg is None:
+                    continue
+                # the codes now belong to the master as it is
+                mod, name = reg
+                key = (p.data_ptr(), p._version)
+                if name is None:
                     mod.weight_codes, mod.weight_scales = res
-                    mod._codes_key = (p.data_ptr(), p._version)
+                    mod._codes_key = key
+                else:
+                    setattr(mod, name + "_codes", res[0])
+                    setattr(mod, name + "_scales", res[1])
+                    mod._master_codes_keys[name] = key
+            if fl[0]:
+                if clip_coef is not None:
+                    torch._foreach_mul_(fl[1], clip_coef.reshape(()).to(fl[1][0].dtype))
+                beta1, beta2 = group["betas"]
+                torch_adamw(fl[0], fl[1], fl[2], fl[3], [], fl[4], foreach=True,
+                            amsgrad=False, beta1=beta1, beta2=beta2, lr=group["lr"],
+                            weight_decay=group["weight_decay"], eps=group["eps"],
+                            maximize=False)
         return loss
 
     def load_state_dict(self, state_dict):

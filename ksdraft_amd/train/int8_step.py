@@ -5,7 +5,8 @@
                        ts = mean over layers of 1 - cos(feature, embedding[next token])
                        loss = ce + transfer_weight * ts          (distillation_losses, :65-99)
     backward           every linear INT8 (Int8Linear / KS3Int8Cell / the head's GEMMs)
-    clip               the clip_grad_norm_ factor as a device scalar (no gradient rewrite)
+    clip               the clip_grad_norm_ factor as a device scalar: applied on load by the
+                       int8 optimizer kernel, by one multi-tensor multiply for the rest
     optimizer          AdamWRequant: torch AdamW's update fused with the int8 repack of every
                        registered Int8Linear master (the head's codes included)
 
@@ -20,16 +21,19 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
+from ..kernels.ks3_int8 import KS3Int8Cell
 from ..kernels.linear import Int8Linear
 from . import IGNORE_INDEX, AdamWRequant, LinearCrossEntropyInt8
 
 
 def clip_coefficient(params, max_norm: float) -> torch.Tensor:
     """The factor torch.nn.utils.clip_grad_norm_ multiplies every gradient by:
-    min(1, max_norm / (||g||_2 + 1e-6)) over all gradients, as a 1-element device tensor."""
+    min(1, max_norm / (||g||_2 + 1e-6)) over all gradients, as a 1-element device tensor.
+    The per-tensor norms are one multi-tensor launch (torch._foreach_norm), as in
+    clip_grad_norm_'s own foreach path."""
     grads = [p.grad for p in params if p.grad is not None]
-    norms = torch.stack([torch.linalg.vector_norm(g.float()) for g in grads])
-    total = torch.linalg.vector_norm(norms)
+    norms = torch._foreach_norm(grads, 2.0)
+    total = torch.linalg.vector_norm(torch.stack(norms))
     return torch.clamp(max_norm / (total + 1e-6), max=1.0).reshape(1)
 
 
@@ -60,7 +64,7 @@ class Int8DraftTrainer:
         self.opt = AdamWRequant(model.parameters(), lr=lr, betas=betas, eps=eps,
                                 weight_decay=weight_decay)
         for mod in model.modules():
-            if isinstance(mod, Int8Linear):
+            if isinstance(mod, Int8Linear) or (isinstance(mod, KS3Int8Cell) and mod.trainable):
                 self.opt.register_int8(mod)
 
     def loss(self, tokens: torch.Tensor, teacher_states: torch.Tensor | None = None):

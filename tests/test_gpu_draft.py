@@ -170,6 +170,14 @@ def test_int8_draft_step_stagewise_bit_exact(monkeypatch):
         eq, es = oq.quantize_last_dim(_np(mod.weight))
         assert np.array_equal(mod.weight_codes.cpu().numpy(), eq)
         assert np.array_equal(mod.weight_scales.cpu().numpy().view(np.uint16), es.view(np.uint16))
+    for r in rec.cell.values():  # the KS3 cells' down/up codes come from the optimizer too
+        cell = r["mod"]
+        for name in ("down", "up"):
+            assert cell._master_codes_current(name)
+            eq, es = oq.quantize_last_dim(_np(getattr(cell, "master_" + name)))
+            assert np.array_equal(getattr(cell, name + "_codes").cpu().numpy(), eq)
+            assert np.array_equal(getattr(cell, name + "_scales").cpu().numpy().view(np.uint16),
+                                  es.view(np.uint16))
     # and a full second step runs on the optimizer's codes
     l2, _, _ = trainer.step(tokens, teacher)
     assert torch.isfinite(l2)

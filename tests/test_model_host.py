@@ -63,3 +63,26 @@ def test_injection_seeds_position_zero_from_previous_layer():
     assert torch.equal(out0[:, 1:], out1[:, 1:])      # only position 0 takes the seed
     assert not torch.equal(out0[:, 0], out1[:, 0])
     torch.testing.assert_close(p, inj.feature_up(inj.feature_down(z)))
+
+
+def test_injection_stacked_gemms_equal_the_reference_composition():
+    """AdjacentInjection's stacked low-rank GEMMs compute spine.py:62-68's sums."""
+    import torch.nn.functional as F
+    torch.manual_seed(4)
+    inj = AdjacentInjection(48, rank=6, feature_rank=10)
+    for lr in (inj.gate_q, inj.gate_p, inj.inject):
+        torch.nn.init.normal_(lr.up.weight, std=0.2)
+    torch.nn.init.normal_(inj.gate_bias, std=0.1)
+    z = torch.randn(3, 9, 48, dtype=torch.float64)
+    prev = torch.randn(3, 9, 48, dtype=torch.float64)
+    inj = inj.double()
+    for pl in (None, prev):
+        got, p = inj(z, pl)
+        pr = inj.feature_up(inj.feature_down(z))
+        pp = F.pad(pr, (0, 0, 1, 0))[:, :-1, :]
+        if pl is not None:
+            pp = torch.cat([pl[:, :1, :], pp[:, 1:, :]], dim=1)
+        gate = torch.sigmoid(inj.gate_q(z) + inj.gate_p(pp) + inj.gate_bias)
+        ref = z + gate * inj.inject(pp)
+        torch.testing.assert_close(got, ref, rtol=1e-12, atol=1e-12)
+        torch.testing.assert_close(p, pr, rtol=1e-12, atol=1e-12)
