@@ -205,6 +205,17 @@ int ksd_w8a8_gemm_nt(const int8_t *a, const uint16_t *a_scales, const int8_t *w,
  *   workspace  16-byte aligned fp32 scratch of at least S*M*N*4 bytes (unused when S = 1)
  */
 int ksd_w8a8_gemm_splits(int64_t M, int64_t N, int64_t K, int group, int *splits);
+/*
+ * The general entry: split K as above, plus an optional residual operand added in the
+ * store (the residual adds of reference ksdraft/model/block.py:39-41, h = x + linear(...)):
+ *   residual  NULL or (M, N) of type y_dtype (KSD_F32, KSD_BF16 or KSD_F16; group 128):
+ *             y = out(out(gemm + bias) + residual), one rounding to the output type per
+ *             op as the torch add on tensors of that dtype; may alias y
+ */
+int ksd_w8a8_gemm_nt_ex(const int8_t *a, const uint16_t *a_scales, const int8_t *w,
+                        const uint16_t *w_scales, int64_t M, int64_t N, int64_t K, int group,
+                        const float *bias, const void *residual, void *y, int y_dtype,
+                        float *workspace, int64_t workspace_bytes, void *stream);
 int ksd_w8a8_gemm_nt_ws(const int8_t *a, const uint16_t *a_scales, const int8_t *w,
                         const uint16_t *w_scales, int64_t M, int64_t N, int64_t K, int group,
                         const float *bias, void *y, int y_dtype, float *workspace,

@@ -405,7 +405,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
     const int8_t *__restrict__ A, const uint16_t *__restrict__ AS,
     const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int M, int N, int K,
     int tiles_n, int ntiles, const float *__restrict__ bias, void *__restrict__ Y,
-    int splits, int64_t part_stride) {
+    int splits, int64_t part_stride, const void *__restrict__ R) {
   __shared__ __attribute__((aligned(16))) int8_t sA[NSLOT][BM * BK];
   __shared__ __attribute__((aligned(16))) int8_t sW[NSLOT][BN * BK];
   __shared__ __attribute__((aligned(16))) uint32_t sS[NSLOT][256];
@@ -521,11 +521,43 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
     __amdgpu_buffer_rsrc_t r1s = __builtin_amdgcn_make_buffer_rsrc(Yp + (r0 + 32) * N * ES, 0, (int)(rows1 * N * ES), kBufFlags);
     const int voff = col < N ? (half * 4 * N + col) * ES : (int)kOob;
     const float b = BIAS ? (col < N ? bias[col] : 0.0f) : 0.0f;
+    // residual R (M, N) in the output type: y = out(out(acc + b) + r), the order of
+    // `x + linear(...)` on tensors of the output dtype (one rounding per op)
+    float r0v[16], r1v[16];
+    if (R != nullptr) {
+      __amdgpu_buffer_rsrc_t q0 = __builtin_amdgcn_make_buffer_rsrc((char *)R + r0 * N * ES, 0, (int)(rows0 * N * ES), kBufFlags);
+      __amdgpu_buffer_rsrc_t q1 = __builtin_amdgcn_make_buffer_rsrc((char *)R + (r0 + 32) * N * ES, 0, (int)(rows1 * N * ES), kBufFlags);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int vo = voff + ((e >> 2) * 8 + (e & 3)) * N * ES;
+        if constexpr (OUT == KSD_F32) {
+          r0v[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(q0, vo, 0, 0));
+          r1v[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(q1, vo, 0, 0));
+        } else if constexpr (OUT == KSD_BF16) {
+          r0v[e] = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(q0, vo, 0, 0) << 16);
+          r1v[e] = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(q1, vo, 0, 0) << 16);
+        } else {
+          r0v[e] = (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(q0, vo, 0, 0));
+          r1v[e] = (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(q1, vo, 0, 0));
+        }
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int vo = voff + ((e >> 2) * 8 + (e & 3)) * N * ES;
-      const float y0 = BIAS ? acc0[e] + b : acc0[e];
-      const float y1 = BIAS ? acc1[e] + b : acc1[e];
+      float y0 = BIAS ? acc0[e] + b : acc0[e];
+      float y1 = BIAS ? acc1[e] + b : acc1[e];
+      if (R != nullptr) {
+        if constexpr (OUT == KSD_BF16) {
+          y0 = __builtin_bit_cast(float, (uint32_t)f32_to_bf16(y0) << 16);
+          y1 = __builtin_bit_cast(float, (uint32_t)f32_to_bf16(y1) << 16);
+        } else if constexpr (OUT != KSD_F32) {
+          y0 = f16_round(y0);
+          y1 = f16_round(y1);
+        }
+        y0 = y0 + r0v[e];
+        y1 = y1 + r1v[e];
+      }
       if constexpr (OUT == KSD_F32) {
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y0), r0s, vo, 0, 0);
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y1), r1s, vo, 0, 0);
@@ -610,7 +642,7 @@ template <int OUT, bool BIAS>
 __global__ __launch_bounds__(256) void splitk_combine_kernel(const float *__restrict__ ws, int splits,
                                                             int64_t part_stride, int64_t n_elems, int N,
                                                             const float *__restrict__ bias,
-                                                            void *__restrict__ Y) {
+                                                            void *__restrict__ Y, const void *__restrict__ R) {
   const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i0 >= n_elems) return;
 #pragma unroll
@@ -620,6 +652,16 @@ __global__ __launch_bounds__(256) void splitk_combine_kernel(const float *__rest
     float y = ws[i];
     for (int pp = 1; pp < splits; ++pp) y = y + ws[(int64_t)pp * part_stride + i];
     if (BIAS) y = y + bias[i % N];
+    if (R != nullptr) {
+      if constexpr (OUT == KSD_F32) {
+        y = y + ((const float *)R)[i];
+      } else if constexpr (OUT == KSD_BF16) {
+        y = __builtin_bit_cast(float, (uint32_t)f32_to_bf16(y) << 16) +
+            __builtin_bit_cast(float, (uint32_t)((const uint16_t *)R)[i] << 16);
+      } else {
+        y = f16_round(y) + (float)__builtin_bit_cast(_Float16, ((const uint16_t *)R)[i]);
+      }
+    }
     if constexpr (OUT == KSD_F32) ((float *)Y)[i] = y;
     else ((uint16_t *)Y)[i] = (uint16_t)out_bits<OUT>(y);
   }
@@ -655,7 +697,8 @@ static int cu_count() {
 template <int GROUP, int OUT, bool BIAS, int MODE>
 static void launch(const int8_t *a, const uint16_t *as, const int8_t *w, const uint16_t *ws,
                    int M, int N, int K, const float *bias, void *y, int32_t *partials,
-                   hipStream_t st, int splits = 1, float *workspace = nullptr) {
+                   hipStream_t st, int splits = 1, float *workspace = nullptr,
+                   const void *residual = nullptr) {
   const int tn = (N + BN - 1) / BN, tm = (M + BM - 1) / BM;
   const int ntiles = tm * tn;
   if constexpr (GROUP == 128 && MODE == 0) {
@@ -663,14 +706,14 @@ static void launch(const int8_t *a, const uint16_t *as, const int8_t *w, const u
       const int64_t nel = (int64_t)M * N;
       const int grid = min(ntiles * splits, cu_count());
       g128::gemm_g128_kernel<KSD_F32, false><<<dim3(grid), dim3(NTHREADS), 0, st>>>(
-          a, as, w, ws, M, N, K, tn, ntiles, nullptr, workspace, splits, nel);
+          a, as, w, ws, M, N, K, tn, ntiles, nullptr, workspace, splits, nel, nullptr);
       const int64_t cb = (nel + 1023) / 1024;
       g128::splitk_combine_kernel<OUT, BIAS><<<dim3((unsigned)cb), dim3(256), 0, st>>>(
-          workspace, splits, nel, nel, N, bias, y);
+          workspace, splits, nel, nel, N, bias, y, residual);
     } else {
       const int grid = min(ntiles, cu_count());
       g128::gemm_g128_kernel<OUT, BIAS><<<dim3(grid), dim3(NTHREADS), 0, st>>>(
-          a, as, w, ws, M, N, K, tn, ntiles, bias, y, 1, 0);
+          a, as, w, ws, M, N, K, tn, ntiles, bias, y, 1, 0, residual);
     }
   } else {
     const int grid = min(ntiles, cu_count());
@@ -682,20 +725,21 @@ static void launch(const int8_t *a, const uint16_t *as, const int8_t *w, const u
 template <int GROUP, int OUT>
 static void launch_b(const int8_t *a, const uint16_t *as, const int8_t *w, const uint16_t *ws,
                      int M, int N, int K, const float *bias, void *y, hipStream_t st,
-                     int splits, float *workspace) {
-  if (bias) launch<GROUP, OUT, true, 0>(a, as, w, ws, M, N, K, bias, y, nullptr, st, splits, workspace);
-  else launch<GROUP, OUT, false, 0>(a, as, w, ws, M, N, K, bias, y, nullptr, st, splits, workspace);
+                     int splits, float *workspace, const void *residual) {
+  if (bias) launch<GROUP, OUT, true, 0>(a, as, w, ws, M, N, K, bias, y, nullptr, st, splits, workspace, residual);
+  else launch<GROUP, OUT, false, 0>(a, as, w, ws, M, N, K, bias, y, nullptr, st, splits, workspace, residual);
 }
 
 template <int GROUP>
 static int launch_o(const int8_t *a, const uint16_t *as, const int8_t *w, const uint16_t *ws,
                     int M, int N, int K, const float *bias, void *y, int y_dtype,
-                    hipStream_t st, int splits = 1, float *workspace = nullptr) {
+                    hipStream_t st, int splits = 1, float *workspace = nullptr,
+                    const void *residual = nullptr) {
   switch (y_dtype) {
-    case KSD_F32: launch_b<GROUP, KSD_F32>(a, as, w, ws, M, N, K, bias, y, st, splits, workspace); break;
-    case KSD_BF16: launch_b<GROUP, KSD_BF16>(a, as, w, ws, M, N, K, bias, y, st, splits, workspace); break;
-    case KSD_F16: launch_b<GROUP, KSD_F16>(a, as, w, ws, M, N, K, bias, y, st, splits, workspace); break;
-    case KSD_F16_SAT: launch_b<GROUP, KSD_F16_SAT>(a, as, w, ws, M, N, K, bias, y, st, splits, workspace); break;
+    case KSD_F32: launch_b<GROUP, KSD_F32>(a, as, w, ws, M, N, K, bias, y, st, splits, workspace, residual); break;
+    case KSD_BF16: launch_b<GROUP, KSD_BF16>(a, as, w, ws, M, N, K, bias, y, st, splits, workspace, residual); break;
+    case KSD_F16: launch_b<GROUP, KSD_F16>(a, as, w, ws, M, N, K, bias, y, st, splits, workspace, residual); break;
+    case KSD_F16_SAT: launch_b<GROUP, KSD_F16_SAT>(a, as, w, ws, M, N, K, bias, y, st, splits, workspace, residual); break;
     default: return fail(KSD_ETYPE, "w8a8_gemm: unsupported output dtype %d", y_dtype);
   }
   return check_launch("w8a8_gemm_nt");
@@ -742,22 +786,42 @@ extern "C" int ksd_w8a8_gemm_splits(int64_t M, int64_t N, int64_t K, int group, 
   return KSD_OK;
 }
 
+extern "C" int ksd_w8a8_gemm_nt_ex(const int8_t *a, const uint16_t *a_scales, const int8_t *w,
+                                   const uint16_t *w_scales, int64_t M, int64_t N, int64_t K,
+                                   int group, const float *bias, const void *residual, void *y,
+                                   int y_dtype, float *workspace, int64_t workspace_bytes,
+                                   void *stream) {
+  int rc = gemm_checks(a, w, M, N, K, group);
+  if (rc != KSD_OK) return rc;
+  if (residual != nullptr) {
+    if (group != 128) return fail(KSD_EINVAL, "w8a8_gemm: a residual needs group 128");
+    if (y_dtype == KSD_F16_SAT) return fail(KSD_ETYPE, "w8a8_gemm: no residual with the saturating fp16 output");
+  }
+  if (M == 0 || N == 0) return KSD_OK;
+  if (K == 0) return fail(KSD_EINVAL, "w8a8_gemm_nt_ex: K = 0 (the host wrapper handles it)");
+  const int splits = group == 128 ? g128_splits(M, N, K) : 1;
+  hipStream_t st = (hipStream_t)stream;
+  if (splits > 1) {
+    const int64_t need = (int64_t)splits * M * N * 4;
+    if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15) != 0)
+      return fail(KSD_EINVAL, "w8a8_gemm: needs a 16-byte aligned fp32 workspace of %lld bytes "
+                  "(%d K parts), got %lld", (long long)need, splits, (long long)workspace_bytes);
+  }
+  switch (group) {
+    case 32: return launch_o<32>(a, a_scales, w, w_scales, (int)M, (int)N, (int)K, bias, y, y_dtype, st);
+    case 64: return launch_o<64>(a, a_scales, w, w_scales, (int)M, (int)N, (int)K, bias, y, y_dtype, st);
+    default: return launch_o<128>(a, a_scales, w, w_scales, (int)M, (int)N, (int)K, bias, y, y_dtype,
+                                  st, splits, workspace, residual);
+  }
+}
+
 extern "C" int ksd_w8a8_gemm_nt_ws(const int8_t *a, const uint16_t *a_scales, const int8_t *w,
                                    const uint16_t *w_scales, int64_t M, int64_t N, int64_t K,
                                    int group, const float *bias, void *y, int y_dtype,
                                    float *workspace, int64_t workspace_bytes, void *stream) {
-  int rc = gemm_checks(a, w, M, N, K, group);
-  if (rc != KSD_OK) return rc;
-  if (M == 0 || N == 0 || K == 0) return KSD_OK;
-  const int splits = group == 128 ? g128_splits(M, N, K) : 1;
-  if (splits == 1)
-    return ksd_w8a8_gemm_nt(a, a_scales, w, w_scales, M, N, K, group, bias, y, y_dtype, stream);
-  const int64_t need = (int64_t)splits * M * N * 4;
-  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15) != 0)
-    return fail(KSD_EINVAL, "w8a8_gemm_nt_ws: needs a 16-byte aligned fp32 workspace of %lld bytes "
-                "(%d K parts), got %lld", (long long)need, splits, (long long)workspace_bytes);
-  return launch_o<128>(a, a_scales, w, w_scales, (int)M, (int)N, (int)K, bias, y, y_dtype,
-                       (hipStream_t)stream, splits, workspace);
+  if (M == 0 || N == 0 || K == 0) return gemm_checks(a, w, M, N, K, group);
+  return ksd_w8a8_gemm_nt_ex(a, a_scales, w, w_scales, M, N, K, group, bias, nullptr, y, y_dtype,
+                             workspace, workspace_bytes, stream);
 }
 
 extern "C" int ksd_w8a8_group_partials(const int8_t *a, const int8_t *w, int64_t M, int64_t N,

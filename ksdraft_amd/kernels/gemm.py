@@ -74,10 +74,13 @@ def _prepare(a_codes, a_scales, w_codes, w_scales, group):
 def w8a8_gemm_out(a_codes: torch.Tensor, a_scales: torch.Tensor, w_codes: torch.Tensor,
                   w_scales: torch.Tensor, group: int = GROUP_SIZE, *,
                   bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
-                  fp16_saturate: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+                  fp16_saturate: bool = False, out: torch.Tensor | None = None,
+                  residual: torch.Tensor | None = None) -> torch.Tensor:
     """(M,K)x(N,K)^T -> (M,N) with the fused epilogue: + bias (fp32) then cast.
 
-    fp16_saturate: fp16 output clamped to +-65504 (ks3_int8.py:241-242)."""
+    fp16_saturate: fp16 output clamped to +-65504 (ks3_int8.py:241-242).
+    residual: (M, N) tensor of the output dtype added in the store, as
+    ``residual + (gemm + bias).to(out_dtype)`` computes it (group 128)."""
     dev, M, N, K, a, as_, w, ws = _prepare(a_codes, a_scales, w_codes, w_scales, group)
     if fp16_saturate:
         out_dtype = torch.float16
@@ -92,17 +95,26 @@ def w8a8_gemm_out(a_codes: torch.Tensor, a_scales: torch.Tensor, w_codes: torch.
         bias = bias.to(device=dev, dtype=torch.float32).contiguous()
         if bias.numel() != N:
             raise ValueError(f"bias has {bias.numel()} elements, expected {N}")
+    if residual is not None:
+        if residual.shape != (M, N) or residual.dtype != out_dtype or fp16_saturate:
+            raise ValueError("residual must be an (M, N) tensor of the output dtype")
+        residual = residual.contiguous()
     if K == 0:
         out.zero_()
         if bias is not None:
             out += bias.to(out_dtype)
+        if residual is not None:
+            out.copy_(residual + out)
         return out
     splits = gemm_splits(M, N, K, group)
-    if splits > 1:  # few output tiles: K split into parts, summed in order (fp32 workspace)
-        work = torch.empty(splits * M * N, dtype=torch.float32, device=dev)
-        _lib.call("ksd_w8a8_gemm_nt_ws", a.data_ptr(), as_.data_ptr(), w.data_ptr(),
-                  ws.data_ptr(), M, N, K, group, _lib.ptr(bias), out.data_ptr(), code,
-                  work.data_ptr(), work.numel() * 4, _lib.stream_ptr(dev))
+    if splits > 1 or residual is not None:
+        # few output tiles: K split into parts, summed in order (fp32 workspace)
+        work = (torch.empty(splits * M * N, dtype=torch.float32, device=dev) if splits > 1
+                else None)
+        _lib.call("ksd_w8a8_gemm_nt_ex", a.data_ptr(), as_.data_ptr(), w.data_ptr(),
+                  ws.data_ptr(), M, N, K, group, _lib.ptr(bias), _lib.ptr(residual),
+                  out.data_ptr(), code, _lib.ptr(work), 0 if work is None else work.numel() * 4,
+                  _lib.stream_ptr(dev))
     else:
         _lib.call("ksd_w8a8_gemm_nt", a.data_ptr(), as_.data_ptr(), w.data_ptr(), ws.data_ptr(),
                   M, N, K, group, _lib.ptr(bias), out.data_ptr(), code, _lib.stream_ptr(dev))

@@ -360,13 +360,18 @@ class KS3Int8Cell(nn.Module):
         y = w8a8_gemm(hq, hs, self.up_codes, self.up_scales, self.group)
         return y.reshape(*x.shape[:-1], self.out_features).to(self._out_dtype(x))
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
         """ks3_int8.py:290-314: trainable -> _KS3Int8Train; eval on the GPU -> the fused
-        (project_fused) contract."""
+        (project_fused) contract. With ``residual`` (shaped like the output, of its dtype)
+        the result is residual + cell(x), the add done in the up-projection's store."""
+        out_dt = self._out_dtype(x)
+        fuse = (residual is not None and residual.dtype == out_dt
+                and out_dt in (torch.float32, torch.bfloat16, torch.float16))
         if self.trainable:
-            return _KS3Int8Train.apply(
+            y = _KS3Int8Train.apply(
                 x, self.master_down, self.master_up, self.master_coefficients,
-                self.master_raw_scale, self.master_raw_shift, self)
+                self.master_raw_scale, self.master_raw_shift, self, residual if fuse else None)
+            return y if fuse or residual is None else residual + y
         self._check_supported()
         x2 = x.reshape(-1, x.shape[-1])
         xq, xs = quantize_last_dim(x2.float(), self.group)
@@ -377,8 +382,13 @@ class KS3Int8Cell(nn.Module):
             self.spine_codes, self.spine_scale,
             scale_dq.reshape(-1), shift_dq.reshape(-1),
             self.tanh_lut, self.group, self.nonlinear)
+        if fuse:
+            y = w8a8_gemm_out(hq, hs, self.up_codes, self.up_scales, self.group, out_dtype=out_dt,
+                              residual=residual.reshape(-1, self.out_features))
+            return y.reshape(*x.shape[:-1], self.out_features)
         y = w8a8_gemm(hq, hs, self.up_codes, self.up_scales, self.group)
-        return y.reshape(*x.shape[:-1], self.out_features).to(self._out_dtype(x))
+        y = y.reshape(*x.shape[:-1], self.out_features).to(out_dt)
+        return y if residual is None else residual + y
 
 
 def _handoff_gemm(a, as_, w, ws, group):
@@ -396,16 +406,22 @@ class _KS3Int8Train(torch.autograd.Function):
     fp16 geometry VJP, fp16 gradient handoff."""
 
     @staticmethod
-    def forward(ctx, inputs, down, up, coefficients, raw_scale, raw_shift, cell):
+    def forward(ctx, inputs, down, up, coefficients, raw_scale, raw_shift, cell, residual=None):
         cell._repack_masters()
         x = inputs.reshape(-1, inputs.shape[-1]).float()
         xq, xs = quantize_last_dim(x, cell.group)
         hq, hs, coords16 = cell._project_codes(xq, xs)
-        y = w8a8_gemm(hq, hs, cell.up_codes, cell.up_scales, cell.group)
+        out_dt = cell._out_dtype(inputs)
+        if residual is not None:  # residual + y, added in the up-projection's store
+            y = w8a8_gemm_out(hq, hs, cell.up_codes, cell.up_scales, cell.group, out_dtype=out_dt,
+                              residual=residual.reshape(-1, cell.out_features))
+        else:
+            y = w8a8_gemm(hq, hs, cell.up_codes, cell.up_scales, cell.group)
         ctx.cell = cell
         ctx.input_shape = inputs.shape
+        ctx.has_residual = residual is not None
         ctx.save_for_backward(xq, xs, hq, hs, coords16)
-        return y.reshape(*inputs.shape[:-1], cell.out_features).to(cell._out_dtype(inputs))
+        return y.reshape(*inputs.shape[:-1], cell.out_features).to(out_dt)
 
     @staticmethod
     def backward(ctx, grad_out):
@@ -438,5 +454,6 @@ class _KS3Int8Train(torch.autograd.Function):
         dup = _handoff_gemm(gT_q, gT_s, hT_q, hT_s, group)
 
         dx = dx.reshape(ctx.input_shape).to(grad_out.dtype)
+        dres = grad_out if ctx.has_residual and ctx.needs_input_grad[7] else None
         return (dx, ddown, dup, _grad_handoff(dcoeff), _grad_handoff(v["dscale"]),
-                _grad_handoff(v["dshift"]), None)
+                _grad_handoff(v["dshift"]), None, dres)

@@ -35,26 +35,29 @@ def _out_dtype(dtype: torch.dtype) -> torch.dtype:
 
 def w8a8_linear_forward(x2: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
                         bias: torch.Tensor | None, group: int = GROUP_SIZE,
-                        out_dtype: torch.dtype | None = None):
-    """y = W8A8(x2, W) + bias in one quantize + one GEMM launch (linear.py:68-73).
+                        out_dtype: torch.dtype | None = None,
+                        residual: torch.Tensor | None = None):
+    """y = W8A8(x2, W) + bias in one quantize + one GEMM launch (linear.py:68-73), plus an
+    optional residual (M, N) of the output dtype added in the GEMM's store.
 
     Returns (y, xq, xs); the activation codes are what the backward keeps."""
     xq, xs = quantize_last_dim(x2, group)          # == quantize_last_dim(x2.float())
     y = w8a8_gemm_out(xq, xs, wq, ws, group, bias=bias,
-                      out_dtype=_out_dtype(out_dtype or x2.dtype))
+                      out_dtype=_out_dtype(out_dtype or x2.dtype), residual=residual)
     return y, xq, xs
 
 
 def w8a8_linear_forward_train(x2: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
                               bias: torch.Tensor | None, group: int = GROUP_SIZE,
-                              out_dtype: torch.dtype | None = None):
+                              out_dtype: torch.dtype | None = None,
+                              residual: torch.Tensor | None = None):
     """w8a8_linear_forward that also builds dW's activation operand in the same pass
     over x: X^T requantized along the tokens from the row codes (the double-quant recipe
     of ks3_int8.py:417-420, quantize_dual). The backward needs only that operand, not
     the row codes. Returns (y, xtq (K, M), xts (K, ceil(M/group)))."""
     xq, xs, xtq, xts = quantize_dual(x2, group, t_from_codes=True)
     y = w8a8_gemm_out(xq, xs, wq, ws, group, bias=bias,
-                      out_dtype=_out_dtype(out_dtype or x2.dtype))
+                      out_dtype=_out_dtype(out_dtype or x2.dtype), residual=residual)
     return y, xtq, xts
 
 
@@ -89,18 +92,21 @@ def w8a8_linear_backward(g: torch.Tensor, xq: torch.Tensor | None, xs: torch.Ten
 
 
 class W8A8LinearFunction(torch.autograd.Function):
-    """y = W8A8(x, W) + b with int8 backward GEMMs; returns fp32-master gradients."""
+    """y = W8A8(x, W) + b (+ residual) with int8 backward GEMMs; returns fp32-master
+    gradients. The residual, when given, is added in the GEMM's store and its gradient
+    is the upstream gradient itself."""
 
     @staticmethod
-    def forward(ctx, x, weight, bias, wq, ws, group):
+    def forward(ctx, x, weight, bias, wq, ws, group, residual=None):
         K = x.shape[-1]
         N = wq.shape[0]
         x2 = x.reshape(-1, K)
+        r2 = None if residual is None else residual.reshape(-1, N)
         if ctx.needs_input_grad[1]:
             # dW's operand X^T comes out of the same pass over x as the forward's codes
-            y, xtq, xts = w8a8_linear_forward_train(x2, wq, ws, bias, group, x.dtype)
+            y, xtq, xts = w8a8_linear_forward_train(x2, wq, ws, bias, group, x.dtype, r2)
         else:
-            y, _, _ = w8a8_linear_forward(x2, wq, ws, bias, group, x.dtype)
+            y, _, _ = w8a8_linear_forward(x2, wq, ws, bias, group, x.dtype, r2)
             xtq = xts = None
         ctx.save_for_backward(xtq, xts, wq, ws)
         ctx.x_shape = x.shape
@@ -125,7 +131,8 @@ class W8A8LinearFunction(torch.autograd.Function):
         db = None
         if ctx.has_bias and ctx.needs_input_grad[2]:
             db = g.float().sum(0)
-        return dx, dw, db, None, None, None
+        dres = grad_out if len(ctx.needs_input_grad) > 6 and ctx.needs_input_grad[6] else None
+        return dx, dw, db, None, None, None, dres
 
 
 class Int8Linear(nn.Module):
@@ -195,30 +202,40 @@ class Int8Linear(nn.Module):
         self.invalidate_codes()  # load_state_dict writes the master in place
         return super()._load_from_state_dict(*args, **kwargs)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
+        """y = linear(x) (linear.py:62-73); with ``residual`` (shaped like y, x's dtype),
+        residual + linear(x), the residual added in the GEMM's store."""
         # live fp32 masters stay authoritative (linear.py:66): the codes are rebuilt on every
         # call unless an optimizer handed over the codes of the master as it is now
         # (_codes_current); dithered codes are redrawn every call
         if not self._codes_current():
             self._codes_key = None
             self._quantize_weight()
-        if torch.is_grad_enabled() and (self.weight.requires_grad or x.requires_grad):
+        fuse_res = (residual is not None and x.dtype in _OUT_DTYPES
+                    and residual.dtype == x.dtype and not self.ste_training)
+        if torch.is_grad_enabled() and (self.weight.requires_grad or x.requires_grad
+                                        or (residual is not None and residual.requires_grad)):
             if self.ste_training:
-                return self.fake_quant_forward(x)
+                y = self.fake_quant_forward(x)
+                return y if residual is None else residual + y
             # other float dtypes (float64) go through .float() as the reference's
             # quantize_last_dim(x2.float()) does (linear.py:69); the result is cast back
             xin = x if x.dtype in _OUT_DTYPES else x.float()
             y = W8A8LinearFunction.apply(xin, self.weight, self.bias, self.weight_codes,
-                                         self.weight_scales, GROUP_SIZE)
-            return y.to(x.dtype)
+                                         self.weight_scales, GROUP_SIZE,
+                                         residual if fuse_res else None)
+            y = y.to(x.dtype)
+            return y if fuse_res or residual is None else residual + y
         # linear.py:68-73: fp32 GEMM, + bias in fp32, then cast to x.dtype (fused)
         x2 = x.reshape(-1, x.shape[-1])
         if x2.dtype not in _OUT_DTYPES:
             x2 = x2.float()
+        r2 = residual.reshape(-1, self.out_features) if fuse_res else None
         y, _, _ = w8a8_linear_forward(
             x2, self.weight_codes, self.weight_scales,
-            self.bias.detach() if self.bias is not None else None)
-        return y.reshape(*x.shape[:-1], self.out_features).to(x.dtype)
+            self.bias.detach() if self.bias is not None else None, residual=r2)
+        y = y.reshape(*x.shape[:-1], self.out_features).to(x.dtype)
+        return y if fuse_res or residual is None else residual + y
 
     def fake_quant_forward(self, x: torch.Tensor) -> torch.Tensor:
         """Reference STE path (linear.py:75-97): fp32 GEMM on quantize-dequantized

@@ -4,6 +4,9 @@ ksdraft/model/block.py:24-42):
     h     = x + Rosa(LN_attn(x))
     h, p  = AdjacentInjection(h, p_prev_layer)
     y     = h + KS3(LN_ffn(h))
+
+Both residual adds are passed to the mixer and the cell as ``residual=``: the INT8 surfaces
+add them in their output GEMM's store, the float ones add them after.
 """
 
 from __future__ import annotations
@@ -28,6 +31,7 @@ class DraftBlock(nn.Module):
         self.ffn = KS3(d, config.ks3_charts or None)
 
     def forward(self, x: torch.Tensor, prev_layer_feature: torch.Tensor | None = None):
-        h = x + self.rosa(self.ln_attn(x))
+        # the two residual adds ride in the output projections' stores (INT8 surfaces)
+        h = self.rosa(self.ln_attn(x), residual=x)
         h, feature = self.injection(h, prev_layer_feature)
-        return h + self.ffn(self.ln_ffn(h)), feature
+        return self.ffn(self.ln_ffn(h), residual=h), feature

@@ -53,7 +53,9 @@ class KS3(nn.Module):
     def warp_shift(self) -> torch.Tensor:
         return 0.5 * torch.tanh(self.raw_shift.float())
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
+        if residual is not None:
+            return residual + self.forward(x)
         coords = self.down(x)
         gdt = torch.float64 if coords.dtype == torch.float64 else torch.float32
         h = coords.to(gdt).clamp(-65504.0, 65504.0)

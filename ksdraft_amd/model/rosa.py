@@ -85,10 +85,19 @@ class RosaMixer(nn.Module):
             outs.append(y.reshape(B, T, -1))
         return outs
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def _out(self, hard: torch.Tensor, residual: torch.Tensor | None) -> torch.Tensor:
+        from ..kernels.linear import Int8Linear
+        if residual is None:
+            return self.out_proj(hard)
+        if isinstance(self.out_proj, Int8Linear):
+            return self.out_proj(hard, residual=residual)
+        return residual + self.out_proj(hard)
+
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
         """x (B, T, d) -> (B, T, d) (rosa.py:135-165). Training on the GPU uses the exact
         credit backward (HardRosaGPU); eval computes the hard match without gradients to
-        the symbol projections, like the reference path."""
+        the symbol projections, like the reference path. With ``residual`` the result is
+        residual + mixer(x), the add fused into the output projection's store."""
         if not x.is_cuda:
             raise RuntimeError("ksdraft_amd's Rosa mixer runs on the GPU only (no CPU path)")
         from ..kernels.rosa_credit_gpu import HardRosaGPU
@@ -96,7 +105,7 @@ class RosaMixer(nn.Module):
             q_in, k_in, v_in = self._shifted(x)
             q_full, k_full, v_full = self.q_proj(q_in), self.k_proj(k_in), self.v_proj(v_in)
             hard = HardRosaGPU.apply(q_full, k_full, v_full, self.payload)
-            return self.out_proj(hard.to(x.dtype))
+            return self._out(hard.to(x.dtype), residual)
         if self._int8_projections() and not torch.is_grad_enabled():
             q_full, k_full, v_full = self._fused_projections(x)
         else:
@@ -108,4 +117,4 @@ class RosaMixer(nn.Module):
             sign, _ = R.match_packed(qb.reshape(B * S, -1), kb.reshape(B * S, -1),
                                      vb.reshape(B * S, -1), T)
         out = self.payload[None, :, None] * sign.reshape(B, S, T).float()
-        return self.out_proj(out.permute(0, 2, 1).to(x.dtype))
+        return self._out(out.permute(0, 2, 1).to(x.dtype), residual)

@@ -86,14 +86,16 @@ class _Recorder:
     def _hook(name, mod, store):
         r = store.setdefault(name, {"mod": mod})
 
-        def fwd(m, inp, out):
+        def fwd(m, inp, kwargs, out):
             r["x"] = inp[0].detach().clone()
             r["y"] = out.detach().clone()
+            res = kwargs.get("residual")
+            r["res"] = None if res is None else res.detach().clone()
 
         def bwd(m, gin, gout):
             r["g"] = gout[0].detach().clone()
             r["dx"] = None if gin[0] is None else gin[0].detach().clone()
-        mod.register_forward_hook(fwd)
+        mod.register_forward_hook(fwd, with_kwargs=True)
         mod.register_full_backward_hook(bwd)
 
 
@@ -121,20 +123,28 @@ def test_int8_draft_step_stagewise_bit_exact(monkeypatch):
         w = _np(masters[name + ".weight"])
         b = None if mod.bias is None else _np(masters[name + ".bias"])
         exp = chains.linear_chain(x, w, b, gy)
-        assert _bits(_np(r["y"]).reshape(exp["y"].shape), exp["y"]), name
+        ey = exp["y"]
+        if r["res"] is not None:  # the block's residual add, fused in the store
+            ey = (_np(r["res"]).reshape(ey.shape) + ey).astype(np.float32)
+        assert _bits(_np(r["y"]).reshape(ey.shape), ey), name
         if r["dx"] is not None:
             assert _bits(_np(r["dx"]).reshape(exp["dx"].shape), exp["dx"]), name
         assert _bits(_np(mod.weight.grad), exp["dw"]), name
 
+    assert sum(r["res"] is not None for r in rec.lin.values()) == 2  # both out_proj
     # KS3 cells
     assert len(rec.cell) == 2
+    assert all(r["res"] is not None for r in rec.cell.values())
     for name, r in rec.cell.items():
         mod = r["mod"]
         mk = lambda k: _np(masters[f"{name}.master_{k}"])  # noqa: E731
         x = _np(r["x"]).reshape(-1, mod.in_features)
         exp = chains.ks3_cell_chain(mk("down"), mk("up"), mk("coefficients"), mk("raw_scale"),
                                     mk("raw_shift"), x, _np(r["g"]).reshape(x.shape[0], -1))
-        assert _bits(_np(r["y"]).reshape(exp["y"].shape), exp["y"]), name
+        ey = exp["y"]
+        if r["res"] is not None:
+            ey = (_np(r["res"]).reshape(ey.shape) + ey).astype(np.float32)
+        assert _bits(_np(r["y"]).reshape(ey.shape), ey), name
         assert _bits(_np(r["dx"]).reshape(exp["dx"].shape), exp["dx"]), name
         assert _bits(_np(mod.master_down.grad), chains.handoff(exp["ddown"])), name
         assert _bits(_np(mod.master_up.grad), chains.handoff(exp["dup"])), name

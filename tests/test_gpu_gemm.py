@@ -169,3 +169,52 @@ def test_split_k_shapes_bit_exact(M, K, N):
         got = kg.w8a8_gemm_out(*ta, bias=bias.to(DEV), out_dtype=dt).cpu()
         assert torch.equal(got, exp.to(dt)), dt
     np.testing.assert_allclose(y, og.gemm_reference(aq, as_, wq, ws), rtol=1e-4, atol=1e-3)
+
+
+@pytest.mark.parametrize("M,K,N", [(200, 640, 260), (256, 2048, 256)])
+def test_residual_store(M, K, N):
+    """y = out(out(gemm + bias) + r): the residual add of `x + linear(x')` in the output
+    dtype, fused in the store, bit-exact against the oracle GEMM followed by torch's add
+    in that dtype; also in place (y aliasing r) and on a split-K shape."""
+    aq, as_, wq, ws = _operands(41 + M, M, K, N)
+    ta = _gpu(aq, as_, wq, ws)
+    g = torch.Generator().manual_seed(K)
+    bias = torch.randn(N, generator=g)
+    base = torch.from_numpy(og.gemm_ordered(aq, as_, wq, ws, bias=bias.numpy()))
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        r = (torch.randn(M, N, generator=g) * 3).to(dt)
+        exp = r + base.to(dt)
+        got = kg.w8a8_gemm_out(*ta, bias=bias.to(DEV), out_dtype=dt, residual=r.to(DEV)).cpu()
+        assert torch.equal(got, exp), dt
+        rd = r.to(DEV)
+        kg.w8a8_gemm_out(*ta, bias=bias.to(DEV), out_dtype=dt, residual=rd, out=rd)
+        assert torch.equal(rd.cpu(), exp), dt
+    with pytest.raises(ValueError):
+        kg.w8a8_gemm_out(*ta, residual=torch.zeros(M, N, device=DEV), fp16_saturate=True)
+
+
+def test_int8linear_residual_autograd():
+    """Int8Linear(x, residual=r) = r + Int8Linear(x), forward and backward (r's gradient is
+    the upstream gradient), in training and eval."""
+    from ksdraft_amd.kernels import Int8Linear
+    torch.manual_seed(9)
+    lin = Int8Linear(256, 384).to(DEV)
+    with torch.no_grad():
+        lin.weight.normal_(0, 0.05)
+        lin.bias.normal_(0, 0.1)
+    x = torch.randn(3, 40, 256, device=DEV)
+    r = torch.randn(3, 40, 384, device=DEV)
+    xa, ra = x.clone().requires_grad_(True), r.clone().requires_grad_(True)
+    xb, rb = x.clone().requires_grad_(True), r.clone().requires_grad_(True)
+    ya = lin(xa, residual=ra)
+    yb = rb + lin(xb)
+    assert torch.equal(ya, yb)
+    g = torch.randn_like(ya)
+    ya.backward(g)
+    wga = lin.weight.grad.clone()
+    lin.weight.grad = None
+    yb.backward(g)
+    assert torch.equal(xa.grad, xb.grad) and torch.equal(ra.grad, rb.grad)
+    assert torch.equal(wga, lin.weight.grad)
+    with torch.no_grad():
+        assert torch.equal(lin(x, residual=r), r + lin(x))

@@ -268,3 +268,47 @@ def test_credits_t2100_sampled_flips():
                 sp, _, _ = orr.match(*fl)
                 exp = float(((sp[0] - base[s]) * gsign[s].astype(np.float64)).sum())
                 assert abs(got[s, which, p] - exp) <= 1e-5 * max(1.0, abs(exp)), (s, which, p)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rosa_mixer_int8_projections_eval_fused_branch(dtype):
+    """RosaMixer in eval with Int8Linear q/k/v/out (the to_int8 surfaces): the time shift
+    and the three input quantizations run as one kernel, then the W8A8 GEMMs (+ bias) and
+    the match. Checked stage by stage against the oracle: the shifted inputs' codes, the
+    projections (ordered-group contract + bias, in x's dtype), the match signs, and the
+    output projection of payload * sign."""
+    from ksdraft_amd.kernels.linear import Int8Linear
+    from oracle import gemm as og
+    torch.manual_seed(5)
+    d, S, B, T = 256, 32, 2, 40
+    m = RosaMixer(d, S).to(DEV)
+    with torch.no_grad():
+        for lin in (m.q_proj, m.k_proj, m.v_proj, m.out_proj):
+            lin.weight.normal_(0, 0.05)
+            lin.bias.normal_(0, 0.05)
+        for mix in (m.time_mix_q, m.time_mix_k, m.time_mix_v):
+            mix.normal_(0, 1.0)
+    for name in ("q_proj", "k_proj", "v_proj", "out_proj"):
+        setattr(m, name, Int8Linear.from_float(getattr(m, name)))
+    m.eval()
+    x = (torch.randn(B, T, d) * 1.5).to(dtype).to(DEV)
+    with torch.no_grad():
+        y = m(x)
+    xv = x.float().cpu().numpy()
+    bits = []
+    for proj, mix in ((m.q_proj, m.time_mix_q), (m.k_proj, m.time_mix_k), (m.v_proj, m.time_mix_v)):
+        sig = torch.sigmoid(mix.detach().float()).cpu().numpy()
+        lerp = orr.shifted(xv, sig, str(dtype).split(".")[-1]).reshape(B * T, d)
+        xq, xs = oq.quantize_last_dim(lerp)
+        wq, ws = oq.quantize_last_dim(proj.weight.detach().cpu().numpy())
+        pre = og.gemm_ordered(xq, xs, wq, ws, bias=proj.bias.detach().cpu().numpy())
+        pre = torch.from_numpy(pre).to(dtype).float().numpy()   # the projection's output dtype
+        bits.append(orr.bits_of(pre.reshape(B, T, S)).transpose(0, 2, 1).reshape(B * S, T))
+    sign, _, _ = orr.match(*bits)
+    hard = (m.payload.detach().cpu().numpy()[None, :, None] * sign.reshape(B, S, T)).transpose(0, 2, 1)
+    hin = torch.from_numpy(np.ascontiguousarray(hard)).to(dtype).float().numpy().reshape(B * T, S)
+    hq, hs = oq.quantize_last_dim(hin)
+    oq_, os_ = oq.quantize_last_dim(m.out_proj.weight.detach().cpu().numpy())
+    exp = og.gemm_ordered(hq, hs, oq_, os_, bias=m.out_proj.bias.detach().cpu().numpy())
+    exp = torch.from_numpy(exp).to(dtype).reshape(B, T, d)
+    assert torch.equal(y.cpu(), exp)
