@@ -179,6 +179,18 @@ int ksd_layernorm_quant(const void *x, int x_dtype, int64_t rows, int64_t d, int
                         float *rstd_out, void *stream);
 
 /*
+ * §8(f) rank 4 — int8 embedding gather: rows of a per-row GS-quantized embedding table
+ * (the tied table of reference ksdraft/model/draft.py:34, 51; quantized as the head's
+ * weight, kernels/quant.py:30-52), dequantized by token id (nn.Embedding's lookup,
+ * draft.py:68): out[i, :] = codes[ids[i], :] * scales[ids[i], :/group], exact in fp32.
+ *   codes (V, d) int8, scales (V, ceil(d/group)) fp16, ids (n,) int64
+ *   out (n, d) of out_dtype (KSD_F32, KSD_BF16, KSD_F16); an id outside [0, V) gives zeros
+ */
+int ksd_embedding_gather_int8(const int8_t *codes, const uint16_t *scales, const int64_t *ids,
+                              int64_t n, int64_t V, int64_t d, int group, void *out,
+                              int out_dtype, void *stream);
+
+/*
  * G1 / G2 — W8A8 GEMM, "NT" layout: Y = dequant(A) . dequant(W)^T with the ordered
  * per-group contract
  *     acc = 0;  for g in 0..K/group-1:  acc = fmaf(float(P_g), sa[m,g]*sw[n,g], acc)

@@ -833,6 +833,75 @@ extern "C" int ksd_quantize_lastdim(const void *x, int x_dtype, int64_t rows, in
   return check_launch("quantize_lastdim");
 }
 
+// ----------------------------------------------------------------------------------
+// Int8 embedding gather: out[i, :] = codes[ids[i], :] * scales[ids[i], :/G], the row of a
+// per-row GS-quantized table dequantized by token id (exact in fp32, as dequantize). One
+// wave per row, 8 elements per lane per pass; an id outside [0, V) gives a zero row (the
+// host checks ids before the launch unless told not to).
+template <int OUT, bool VEC>
+__global__ __launch_bounds__(256) void embed_gather_kernel(
+    const int8_t *__restrict__ codes, const uint16_t *__restrict__ scales,
+    const int64_t *__restrict__ ids, int64_t n, int64_t V, int64_t d, int64_t nsc, int group,
+    void *__restrict__ out) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= n) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t id = ids[row];
+  const bool ok = id >= 0 && id < V;
+  const int8_t *src = codes + (ok ? id : 0) * d;
+  const uint16_t *sc = scales + (ok ? id : 0) * nsc;
+  for (int64_t c0 = (int64_t)lane * 8; c0 < d; c0 += 64 * 8) {
+    float v[8];
+    if (VEC) {
+      const uint2 w = *(const uint2 *)(src + c0);
+      const float s = ok ? f16_to_f32(sc[c0 / group]) : 0.0f;  // 8 | group: one scale
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        v[j] = (float)(int8_t)((j < 4 ? w.x : w.y) >> (8 * (j & 3))) * s;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t c = c0 + j;
+        v[j] = (ok && c < d) ? (float)src[c] * f16_to_f32(sc[c / group]) : 0.0f;
+      }
+    }
+    const int64_t base = row * d + c0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (!VEC && c0 + j >= d) break;
+      if constexpr (OUT == KSD_F32) ((float *)out)[base + j] = v[j];
+      else if constexpr (OUT == KSD_BF16) ((uint16_t *)out)[base + j] = f32_to_bf16(v[j]);
+      else ((uint16_t *)out)[base + j] = f16_bits(v[j]);
+    }
+  }
+}
+
+extern "C" int ksd_embedding_gather_int8(const int8_t *codes, const uint16_t *scales,
+                                         const int64_t *ids, int64_t n, int64_t V, int64_t d,
+                                         int group, void *out, int out_dtype, void *stream) {
+  if (!valid_group(group)) return fail(KSD_EINVAL, "embedding_gather: group must be 32, 64 or 128");
+  if (n < 0 || V < 0 || d < 0) return fail(KSD_EINVAL, "embedding_gather: negative shape");
+  if (n == 0 || d == 0) return KSD_OK;
+  if (V == 0) return fail(KSD_EINVAL, "embedding_gather: empty table");
+  if (!codes || !scales || !ids || !out) return fail(KSD_EINVAL, "embedding_gather: null pointer");
+  if (cdiv(n, 4) > 0x7fffffffLL) return fail(KSD_EINVAL, "embedding_gather: too many rows");
+  const int64_t nsc = cdiv(d, group);
+  const bool vec = d % 8 == 0 && ((uintptr_t)codes & 7) == 0;
+  const dim3 g((unsigned)cdiv(n, 4)), b(256);
+  hipStream_t st = (hipStream_t)stream;
+#define KSD_EMB(O)                                                                              \
+  if (vec) embed_gather_kernel<O, true><<<g, b, 0, st>>>(codes, scales, ids, n, V, d, nsc, group, out); \
+  else embed_gather_kernel<O, false><<<g, b, 0, st>>>(codes, scales, ids, n, V, d, nsc, group, out);
+  switch (out_dtype) {
+    case KSD_F32: KSD_EMB(KSD_F32) break;
+    case KSD_BF16: KSD_EMB(KSD_BF16) break;
+    case KSD_F16: KSD_EMB(KSD_F16) break;
+    default: return fail(KSD_ETYPE, "embedding_gather: unsupported output dtype %d", out_dtype);
+  }
+#undef KSD_EMB
+  return check_launch("embedding_gather_int8");
+}
+
 extern "C" int ksd_dequantize_lastdim(const int8_t *codes, const uint16_t *scales,
                                       int64_t rows, int64_t K, int64_t n_scales, int group,
                                       float *out, void *stream) {

@@ -6,20 +6,23 @@ time-mix vectors, the DSpine injection and the embedding stay float (the referen
 conversion doctrine). The reference builds the cells without trainable masters
 (int8_convert.py:40); ``trainable=True`` builds them with masters and also turns the tied
 head into an ``Int8Linear`` sharing the embedding's weight, so every linear of the step
-runs INT8 forward and backward (the config-5 training step).
+runs INT8 forward and backward (the config-5 training step). ``int8_embedding=True``
+also swaps the embedding lookup for the int8 gather over the head's codes (the staged
+surface the reference's doctrine names).
 """
 
 from __future__ import annotations
 
 import copy
 
+from ..kernels.embedding import Int8Embedding
 from ..kernels.ks3_int8 import KS3Int8Cell
 from ..kernels.linear import Int8Linear
 from .draft import KSDraftModel
 
 
 def to_int8(model: KSDraftModel, group: int = 128, nonlinear: str = "int8", *,
-            trainable: bool = False) -> KSDraftModel:
+            trainable: bool = False, int8_embedding: bool = False) -> KSDraftModel:
     conv = copy.deepcopy(model)
     swapped = 0
     for block in conv.blocks:
@@ -39,8 +42,14 @@ def to_int8(model: KSDraftModel, group: int = 128, nonlinear: str = "int8", *,
         head.weight_codes = head.weight_scales = None
         conv.head = head
         swapped += 1
+    if int8_embedding:  # the staged int8-embedding surface: lookups from the head's codes
+        emb = Int8Embedding.from_float(conv.embedding, group)
+        if isinstance(conv.head, Int8Linear):
+            emb.codes_from = conv.head
+        conv.embedding = emb
+        swapped += 1
     conv._int8_tier = {"group": group, "nonlinear": nonlinear, "swapped_surfaces": swapped,
-                       "trainable": trainable}
+                       "trainable": trainable, "int8_embedding": int8_embedding}
     return conv
 
 

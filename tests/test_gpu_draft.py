@@ -203,3 +203,28 @@ def test_clip_coefficient_matches_torch():
     torch.nn.utils.clip_grad_norm_(ps, 1.0)
     for g0, p in zip(grads, ps):
         torch.testing.assert_close(g0 * coef, p.grad, rtol=1e-6, atol=1e-7)
+
+
+def test_int8_draft_step_with_int8_embedding():
+    """to_int8(int8_embedding=True): the lookup reads the tied head's codes; the looked-up
+    rows equal the oracle dequantization of Q(master)[ids], and training steps run."""
+    torch.manual_seed(0)
+    cfg = KSDraftConfig(vocab_size=512, layers=1, d_model=256, rosa_streams=64, ks3_charts=384)
+    m = KSDraftModel(cfg).to(DEV)
+    with torch.no_grad():
+        m.embedding.weight.normal_(0, 0.02)
+    model = to_int8(m, trainable=True, int8_embedding=True)
+    assert model.embedding.weight is model.head.weight and model.embedding.codes_from is model.head
+    seen = {}
+    model.embedding.register_forward_hook(lambda mod, i, o: seen.__setitem__("y", o.detach().clone()))
+    trainer = Int8DraftTrainer(model, lr=1e-3)
+    tokens = torch.randint(0, 512, (2, 33), generator=torch.Generator().manual_seed(2)).to(DEV)
+    for step in range(2):
+        master = _np(model.embedding.weight)
+        loss, _, _ = trainer.step(tokens)
+        assert torch.isfinite(loss)
+        ec, es = oq.quantize_last_dim(master)
+        ids = tokens[:, :-1].reshape(-1).cpu().numpy()
+        exp = oq.dequantize_last_dim(ec[ids], es[ids])
+        assert _bits(_np(seen["y"]).reshape(exp.shape), exp), step
+    assert model.head._codes_current()  # the optimizer's codes feed the next lookup

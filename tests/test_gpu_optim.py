@@ -148,3 +148,42 @@ def test_int8linear_accepts_float64_like_the_reference():
     y = lin(xg)
     y.sum().backward()
     assert y.dtype == torch.float64 and xg.grad.dtype == torch.float64
+
+
+def test_int8_embedding_gather_and_ste_backward():
+    """The int8 lookup equals the oracle dequantization of the looked-up rows, bit-exact,
+    for every output dtype and group; its gradient is nn.Embedding's (scatter-add)."""
+    from ksdraft_amd.kernels.embedding import Int8Embedding, embedding_gather_int8
+    from ksdraft_amd.kernels import quant as kq
+    g = torch.Generator().manual_seed(13)
+    V, d = 1000, 1536
+    w = torch.randn(V, d, generator=g) * 0.05
+    ids = torch.randint(0, V, (3, 77), generator=g)
+    for group in (128, 64, 32):
+        codes, scales = kq.quantize_last_dim(w.to(DEV), group)
+        ec, es = oq.quantize_last_dim(w.numpy(), group)
+        exp = oq.dequantize_last_dim(ec[ids.numpy().reshape(-1)], es[ids.numpy().reshape(-1)], group)
+        for dt in (torch.float32, torch.bfloat16, torch.float16):
+            got = embedding_gather_int8(codes, scales, ids.to(DEV), group, dt)
+            assert got.shape == (3, 77, d)
+            assert torch.equal(got.reshape(-1, d).cpu(), torch.from_numpy(exp).to(dt)), (group, dt)
+    with pytest.raises(IndexError):
+        embedding_gather_int8(codes, scales, torch.tensor([V], device=DEV), 32)
+    # ragged d (not a multiple of 8) takes the scalar path
+    w2 = torch.randn(50, 300, generator=g)
+    c2, s2 = kq.quantize_last_dim(w2.to(DEV))
+    i2 = torch.tensor([0, 49, 7, 7], device=DEV)
+    e2 = oq.dequantize_last_dim(*oq.quantize_last_dim(w2.numpy()))[[0, 49, 7, 7]]
+    assert torch.equal(embedding_gather_int8(c2, s2, i2).cpu(), torch.from_numpy(e2))
+    # module: forward from the master's codes, backward = nn.Embedding's scatter-add
+    emb = Int8Embedding(V, d).to(DEV)
+    with torch.no_grad():
+        emb.weight.copy_(w.to(DEV))
+    y = emb(ids.to(DEV))
+    gy = torch.randn(3, 77, d, generator=g).to(DEV)
+    y.backward(gy)
+    ref = torch.nn.Embedding(V, d).to(DEV)
+    with torch.no_grad():
+        ref.weight.copy_(w.to(DEV))
+    ref(ids.to(DEV)).backward(gy)
+    assert torch.equal(emb.weight.grad, ref.weight.grad)
