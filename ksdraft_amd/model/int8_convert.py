@@ -7,8 +7,10 @@ conversion doctrine). The reference builds the cells without trainable masters
 (int8_convert.py:40); ``trainable=True`` builds them with masters and also turns the tied
 head into an ``Int8Linear`` sharing the embedding's weight, so every linear of the step
 runs INT8 forward and backward (the config-5 training step). ``int8_embedding=True``
-also swaps the embedding lookup for the int8 gather over the head's codes (the staged
-surface the reference's doctrine names).
+also swaps the embedding lookup for the int8 gather over the head's codes, and
+``int8_injection=True`` the DSpine injection's low-rank maps for Int8Linear (their rank-32/64
+reductions pad to one 128-wide group, quant.py:9-10): the staged surfaces the reference's
+doctrine keeps float until gated.
 """
 
 from __future__ import annotations
@@ -22,7 +24,8 @@ from .draft import KSDraftModel
 
 
 def to_int8(model: KSDraftModel, group: int = 128, nonlinear: str = "int8", *,
-            trainable: bool = False, int8_embedding: bool = False) -> KSDraftModel:
+            trainable: bool = False, int8_embedding: bool = False,
+            int8_injection: bool = False) -> KSDraftModel:
     conv = copy.deepcopy(model)
     swapped = 0
     for block in conv.blocks:
@@ -33,6 +36,15 @@ def to_int8(model: KSDraftModel, group: int = 128, nonlinear: str = "int8", *,
         block.ffn = KS3Int8Cell(cell=block.ffn, group=group, nonlinear=nonlinear,
                                 trainable=trainable)
         swapped += 1
+        if int8_injection:  # DSpine's low-rank maps: reduction 32/64 pads to one group
+            inj = block.injection
+            for name in ("feature_down", "feature_up"):
+                setattr(inj, name, Int8Linear.from_float(getattr(inj, name)))
+                swapped += 1
+            for lr in (inj.gate_q, inj.gate_p, inj.inject):
+                lr.down = Int8Linear.from_float(lr.down)
+                lr.up = Int8Linear.from_float(lr.up)
+                swapped += 2
     if conv.teacher_proj is not None:
         conv.teacher_proj = Int8Linear.from_float(conv.teacher_proj)
         swapped += 1
@@ -49,7 +61,8 @@ def to_int8(model: KSDraftModel, group: int = 128, nonlinear: str = "int8", *,
         conv.embedding = emb
         swapped += 1
     conv._int8_tier = {"group": group, "nonlinear": nonlinear, "swapped_surfaces": swapped,
-                       "trainable": trainable, "int8_embedding": int8_embedding}
+                       "trainable": trainable, "int8_embedding": int8_embedding,
+                       "int8_injection": int8_injection}
     return conv
 
 

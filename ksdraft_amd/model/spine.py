@@ -53,6 +53,15 @@ class AdjacentInjection(nn.Module):
         stacked (z: feature_down and gate_q.down; p_prev: gate_p.down and inject.down),
         and gate_q(z) + gate_p(p_prev) as one GEMM over the concatenated rank: the same
         sums as spine.py:62-68, in one pass over each (M, d) operand instead of two."""
+        if not isinstance(self.feature_down, nn.Linear):
+            # INT8 surfaces (to_int8(int8_injection=True)): each low-rank map is its own
+            # W8A8 GEMM, composed as spine.py:62-68 writes it
+            p = self.predicted_feature(z)
+            p_prev = F.pad(p, (0, 0, 1, 0))[:, :-1, :]
+            if prev_layer_feature is not None:
+                p_prev = torch.cat([prev_layer_feature[:, :1, :], p_prev[:, 1:, :]], dim=1)
+            gate = torch.sigmoid(self.gate_q(z) + self.gate_p(p_prev) + self.gate_bias)
+            return z + gate * self.inject(p_prev), p
         r1 = self.feature_down.out_features
         zd = F.linear(z, torch.cat([self.feature_down.weight, self.gate_q.down.weight]))
         p = self.feature_up(zd[..., :r1])

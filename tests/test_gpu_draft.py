@@ -44,7 +44,7 @@ def _bits(a, b):
     return np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-def _model():
+def _model(int8_injection=False):
     torch.manual_seed(0)
     cfg = KSDraftConfig(vocab_size=512, layers=2, d_model=256, rosa_streams=64, ks3_charts=384)
     m = KSDraftModel(cfg, teacher_dim=256).to(DEV)
@@ -55,7 +55,7 @@ def _model():
             if name.endswith(("up.weight", "out_proj.weight", "teacher_proj.weight",
                               "embedding.weight")):
                 p.normal_(0, 0.02)
-    return to_int8(m, trainable=True)
+    return to_int8(m, trainable=True, int8_injection=int8_injection)
 
 
 class _Recorder:
@@ -99,8 +99,9 @@ class _Recorder:
         mod.register_full_backward_hook(bwd)
 
 
-def test_int8_draft_step_stagewise_bit_exact(monkeypatch):
-    model = _model()
+@pytest.mark.parametrize("int8_injection", [False, True])
+def test_int8_draft_step_stagewise_bit_exact(monkeypatch, int8_injection):
+    model = _model(int8_injection)
     rec = _Recorder(model, monkeypatch)
     trainer = Int8DraftTrainer(model, lr=1e-3)
     g = torch.Generator().manual_seed(1)
@@ -114,8 +115,9 @@ def test_int8_draft_step_stagewise_bit_exact(monkeypatch):
     torch.cuda.synchronize()
     assert torch.isfinite(loss)
 
-    # Int8Linear surfaces: Rosa q/k/v/out of both blocks and the teacher seam
-    assert len(rec.lin) == 2 * 4 + 1
+    # Int8Linear surfaces: Rosa q/k/v/out of both blocks and the teacher seam (and the
+    # DSpine injection's eight low-rank maps per block)
+    assert len(rec.lin) == 2 * 4 + 1 + (2 * 8 if int8_injection else 0)
     for name, r in rec.lin.items():
         mod = r["mod"]
         x = _np(r["x"]).reshape(-1, mod.in_features)
