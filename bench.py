@@ -478,6 +478,26 @@ def draft_c5(dev, steps, warmup):
                     "150144, B 4 x T 2048, teacher state bf16 (d 1536)",
     }
     res["int8_gemm_tops"] = round(res["int8_gemm_ops_per_step"] / (step_ms * 1e-3) / 1e12, 1)
+    # the staged int8 embedding lookup (codes of the tied head) against the float lookup
+    from ksdraft_amd.kernels.embedding import embedding_gather_int8
+    head = model.head
+    if not head._codes_current():
+        head._quantize_weight()
+    ids = tokens[:, :-1]
+    emb_w = model.embedding.weight.detach()
+    n_ids, dm = ids.numel(), cfg.d_model
+    for name, nbytes, fn in (
+            ("int8_embedding_gather", n_ids * (dm + 2 * dm // 128 + 4 * dm + 8),
+             lambda: embedding_gather_int8(head.weight_codes, head.weight_scales, ids,
+                                           check_ids=False)),
+            ("cmp_float_embedding", n_ids * (8 * dm + 8),
+             lambda: torch.nn.functional.embedding(ids, emb_w))):
+        def rep(fn=fn):
+            for _ in range(20):
+                fn()
+        _, _, ms = time_graph(rep, 3, warm=1)
+        us = ms * 1e3 / 20
+        res[name] = {"us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
     del tr, model
     torch.cuda.empty_cache()
     return res
@@ -491,45 +511,63 @@ def _c5_gemm_ops(cfg, tokens):
     return cfg.layers * per_layer + 3 * 2 * tokens * d * V + 2 * 2 * tokens * d * d
 
 
-def cpu_baseline(x, w, dy, budget_s):
-    """The oracle's restatement of the reference CPU path (quantize in numpy; GEMMs as
-    dequantize + fp32 BLAS matmul, reference ksdraft/kernels/gemm.py:76-82), timed on
-    this host's cores on a bounded sample of the same workload (full shape, as many
-    steps as fit the budget after one warm-up)."""
-    from oracle import gemm as og
-    from oracle import quant as oq
+def _cpu_model() -> str:
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        threads = 1
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(x, w, dy, budget_s):
+    """The reference's CPU path for the config-2 step, timed on this host's cores: the
+    operand quantizations of the oracle (numpy restatement of quant.py:30-67) and each GEMM
+    as the reference's CPU branch computes it (gemm.py:76-82): dequantize both operands,
+    then torch's fp32 matmul. torch uses every core of the process affinity; 2 warm-up
+    steps, then the median of at least 5 timed steps (more while the budget lasts)."""
+    from oracle import quant as oq
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
     X, W, DY = x.numpy(), w.numpy(), dy.numpy()
+
+    def mm(aq, as_, wq, ws):  # gemm.py:77-82
+        a = torch.from_numpy(oq.dequantize_last_dim(aq, as_))
+        b = torch.from_numpy(oq.dequantize_last_dim(wq, ws))
+        return a @ b.T
 
     def cstep():
         wq, ws = oq.quantize_last_dim(W)
         xq, xs = oq.quantize_last_dim(X)
-        og.gemm_reference(xq, xs, wq, ws)
+        mm(xq, xs, wq, ws)
         gq, gs = oq.quantize_last_dim(DY)
         wtq, wts = oq.requant_transpose(wq, ws)
-        og.gemm_reference(gq, gs, wtq, wts)
+        mm(gq, gs, wtq, wts)
         gtq, gts = oq.quantize_transpose(DY)
         xtq, xts = oq.requant_transpose(xq, xs)
-        og.gemm_reference(gtq, gts, xtq, xts)
+        mm(gtq, gts, xtq, xts)
 
-    cstep()
+    for _ in range(2):
+        cstep()
     times = []
     t_end = time.perf_counter() + budget_s
-    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 10):
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 15):
         t0 = time.perf_counter()
         cstep()
         times.append(time.perf_counter() - t0)
     t = float(np.median(times))
+    cfg = torch.__config__.show()
+    blas = "MKL" if "MKL" in cfg else ("OpenBLAS" if "OpenBLAS" in cfg else "torch BLAS")
     return {
-        "value": round(3 * GEMM_OPS / t / 1e12, 4), "unit": "TOPS", "cores": int(threads),
+        "value": round(3 * GEMM_OPS / t / 1e12, 4), "unit": "TOPS", "cores": cores,
         "kind": "port",
-        "sample": (f"full config-2 step (M={M}, K=N={K}) x {len(times)} after 1 warm-up, "
-                   f"median {t:.3f} s/step; numpy quantization passes single-threaded, "
-                   f"BLAS matmuls on {threads} threads"),
+        "sample": (f"full config-2 step (M={M}, K=N={K}: quantize W, X, dY; requant W^T, X^T; "
+                   f"three dequantize + fp32 matmul GEMMs), median of {len(times)} after 2 "
+                   f"warm-ups, {t:.3f} s/step; host {_cpu_model()}, torch "
+                   f"{torch.__version__} with {torch.get_num_threads()} threads ({blas}); "
+                   f"numpy quantization single-threaded"),
     }
 
 
