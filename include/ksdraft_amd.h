@@ -354,6 +354,36 @@ int ksd_rosa_shift_quant(const void *x, int x_dtype, int64_t B, int64_t T, int64
                          int8_t *v_codes, uint16_t *v_scales, void *stream);
 
 /*
+ * R1, training form — RosaMixer._shifted (reference ksdraft/model/rosa.py:128-133) fused
+ * with the training quantization of each projection input: the row codes of the forward
+ * GEMM (Int8Linear, ksdraft/kernels/linear.py:69) and dW's operand, the input transposed and
+ * requantized along the tokens from those row codes (the recipe of
+ * ksdraft/kernels/ks3_int8.py:417-420). Group 128. m = 0, 1, 2 is q, k, v:
+ *   x            (B, T, d) of type x_dtype, dense, d % 8 == 0, 16-byte aligned
+ *   sig_q/k/v    (d,) fp32: torch.sigmoid(time_mix_q/k/v), 16-byte aligned
+ *   codes[m]     (B*T, d) int8;   scales[m]   (B*T, ceil(d/128)) fp16
+ *   codes_t[m]   (d, B*T) int8;   scales_t[m] (d, ceil(B*T/128)) fp16
+ */
+int ksd_rosa_shift_quant_dual(const void *x, int x_dtype, int64_t B, int64_t T, int64_t d,
+                              const float *sig_q, const float *sig_k, const float *sig_v,
+                              int8_t *const *codes, uint16_t *const *scales,
+                              int8_t *const *codes_t, uint16_t *const *scales_t, void *stream);
+
+/*
+ * Backward of the time shift of RosaMixer._shifted (reference ksdraft/model/rosa.py:128-133,
+ * the autograd of its three lerps): given g_m = dL/dm_in (fp32, (B, T, d)),
+ *   dx[r]     = sum_m g_m[r] sig_m + [t(r) + 1 < T] (g_m[r+1] - g_m[r+1] sig_m)   (x's dtype)
+ *   dsig_m[i] = sum_r g_m[r, i] (x[r, i] - prev[r, i])
+ * dsig comes as per-row-block partials (n_blocks, 3, d) fp32, n_blocks from
+ * ksd_rosa_shift_backward_blocks; their sum over the first axis is dL/dsig_m.
+ */
+int ksd_rosa_shift_backward_blocks(int64_t B, int64_t T, int64_t *n_blocks);
+int ksd_rosa_shift_backward(const void *x, int x_dtype, int64_t B, int64_t T, int64_t d,
+                            const float *g_q, const float *g_k, const float *g_v,
+                            const float *sig_q, const float *sig_k, const float *sig_v,
+                            void *dx, float *dsig_partials, void *stream);
+
+/*
  * The (x > 0) symbol bits of Rosa projections (reference ksdraft/model/rosa.py:156-158,
  * ksdraft/kernels/rosa_credit_gpu.py:68-70), packed per stream along T.
  *   x     (B, T, S) of type x_dtype, dense

@@ -55,6 +55,9 @@ SIGNATURES = {
     "ksd_ks3_tanh16": [_P, _I64, _P, _P],
     "ksd_rosa_shift_quant": [_P, _INT, _I64, _I64, _I64, _P, _P, _P, _INT,
                              _P, _P, _P, _P, _P, _P, _P],
+    "ksd_rosa_shift_quant_dual": [_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P],
+    "ksd_rosa_shift_backward_blocks": [_I64, _I64, _P],
+    "ksd_rosa_shift_backward": [_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "ksd_rosa_pack_bits": [_P, _INT, _I64, _I64, _I64, _P, _P],
     "ksd_rosa_match": [_P, _P, _P, _I64, _I64, _INT, _P, _P, _P],
     "ksd_rosa_hard": [_P, _P, _I64, _I64, _I64, _P, _INT, _P],

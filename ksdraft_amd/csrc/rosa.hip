@@ -157,6 +157,235 @@ __global__ void __launch_bounds__(256) rosa_shift_quant_kernel(
   }
 }
 
+// ---------------------------------------------------------------- shift + dual quantize
+// Training form of rosa_shift_quant_kernel, group 128. One pass over a 128 x 128 tile of x
+// (rows = tokens, columns = features) emits, for each of q_in, k_in and v_in, the row codes
+// of the forward GEMM and the operand dW needs: X^T requantized along the tokens from those
+// row codes, the double-quant recipe quant(dequant(quant(X))^T) (ks3_int8.py:417-420) that
+// the Int8Linear training forward applies to its input. The row phase is
+// quant_dual_codes_kernel's, with each shifted value formed on load from x[r] and x[r - 1]
+// (0 at the first token of a sequence) exactly as rosa_shift_quant_kernel forms it; the three
+// tiles of row codes (column-major, 132-byte pitch) and row scales then go through LDS to
+// the column phase. Requires C % 8 == 0 and 16-byte aligned rows.
+struct ShiftDualOut {
+  int8_t *codes[3];
+  uint16_t *scales[3];
+  int8_t *codes_t[3];
+  uint16_t *scales_t[3];
+};
+
+template <int DT>
+__global__ __launch_bounds__(512) void rosa_shift_dual_kernel(
+    const void *__restrict__ xv, int R, int C, int T, const float *__restrict__ sig_q,
+    const float *__restrict__ sig_k, const float *__restrict__ sig_v, ShiftDualOut out) {
+  using E = Elem<DT>;
+  constexpr int G = 128, PB = 132;
+  __shared__ __attribute__((aligned(16))) int8_t tq[3][128 * PB];  // [m][column][row]
+  __shared__ __attribute__((aligned(16))) float srow[3][128];
+  const int tid = threadIdx.x;
+  const int c0 = (int)blockIdx.x * 128, r0 = (int)blockIdx.y * 128;
+  const int ngC = (C + G - 1) / G, ngR = (R + G - 1) / G;
+
+  // ---- rows: lane (rr, sub) takes rows r0 + 32 p + rr (p = 0..3), columns c0 + 8 sub .. + 8
+  const int rr = tid >> 4, sub = tid & 15;
+  const int col = c0 + sub * 8;
+  const bool cok = col < C;
+  const int cc = cok ? col : 0;
+  const typename E::T *xb = (const typename E::T *)xv + cc;
+  float sg[3][8];
+  cvt_raw8<KSD_F32>(load_raw8<KSD_F32>(sig_q + cc), cok, sg[0]);
+  cvt_raw8<KSD_F32>(load_raw8<KSD_F32>(sig_k + cc), cok, sg[1]);
+  cvt_raw8<KSD_F32>(load_raw8<KSD_F32>(sig_v + cc), cok, sg[2]);
+  Raw8<DT> raw[4], rawp[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int rs = min(r0 + 32 * p + rr, R - 1);
+    raw[p] = load_raw8<DT>(xb + (int64_t)rs * C);
+    rawp[p] = load_raw8<DT>(xb + (int64_t)(rs > 0 ? rs - 1 : 0) * C);
+  }
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int lr = 32 * p + rr;
+    const int row = r0 + lr;
+    const bool ok = cok && row < R;
+    float xr[8], pv[8], diff[8];
+    cvt_raw8<DT>(raw[p], ok, xr);
+    cvt_raw8<DT>(rawp[p], ok && row % T != 0, pv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) diff[e] = xr[e] - pv[e];
+    if constexpr (DT == KSD_BF16) {
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) bf16_round2(diff[e], diff[e + 1]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) diff[e] = round_to_dt<DT>(diff[e]);
+    }
+    const int rowc = row < R ? row : 0;
+#pragma unroll
+    for (int m = 0; m < 3; ++m) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = pv[e] + diff[e] * sg[m][e];
+      const uint32_t am = group_max_u32<16>(__builtin_bit_cast(uint32_t, abs_max<8>(v)));
+      const float s = group_scale(__builtin_bit_cast(float, am));
+      uint32_t w[2];
+      codes_rcp_packed<8>(v, s, w);
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      u32x2 q;
+      q.x = w[0];
+      q.y = w[1];
+      __builtin_amdgcn_raw_buffer_store_b64(q, rsrc(out.codes[m] + (int64_t)rowc * C, C),
+                                            ok ? (uint32_t)col : kOob, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsrc(out.scales[m] + (int64_t)rowc * ngC, 2 * ngC),
+                                            ok && sub == 0 ? (uint32_t)(col / G) * 2 : kOob, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) tq[m][(sub * 8 + i) * PB + lr] = (int8_t)(w[i >> 2] >> (8 * (i & 3)));
+      if (sub == 0) srow[m][lr] = s;  // the 16 lanes of a row group share its scale
+    }
+  }
+  __syncthreads();
+
+  // ---- columns: lane (c, part) takes column c, rows part * 32 .. + 32, of each tile
+  constexpr int RPT = 32;
+  const int c = tid >> 2, part = tid & 3;
+  const int gc = c0 + c;
+  const int rbase = r0 + part * RPT;
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {  // unrolled: `out` is indexed by constants only
+    float colv[RPT];
+    const uint32_t *qc = (const uint32_t *)(tq[m] + c * PB + part * RPT);
+    const float4 *sr = (const float4 *)(srow[m] + part * RPT);
+#pragma unroll
+    for (int j4 = 0; j4 < RPT / 4; ++j4) {
+      const uint32_t qw = qc[j4];
+      const float4 sv = sr[j4];
+      const float ss[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+      for (int b = 0; b < 4; ++b) colv[4 * j4 + b] = (float)(int8_t)(qw >> (8 * b)) * ss[b];
+    }
+    const uint32_t am = group_max_u32<4>(__builtin_bit_cast(uint32_t, abs_max<RPT>(colv)));
+    const float s = group_scale(__builtin_bit_cast(float, am));
+    uint32_t w[RPT / 4];
+    codes_rcp_packed<RPT>(colv, s, w);
+    if (gc < C) {
+      if (part == 0) out.scales_t[m][(int64_t)gc * ngR + blockIdx.y] = scale_bits(s);
+      int8_t *dst = out.codes_t[m] + (int64_t)gc * R + rbase;
+      if (rbase + RPT <= R && (((uintptr_t)dst) & 15) == 0) {
+#pragma unroll
+        for (int j = 0; j < RPT / 4; j += 4) *(uint4 *)(dst + 4 * j) = make_uint4(w[j], w[j + 1], w[j + 2], w[j + 3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < RPT; ++j)
+          if (rbase + j < R) dst[j] = (int8_t)(w[j / 4] >> (8 * (j % 4)));
+      }
+    }
+  }
+}
+
+// Backward of the time shift, q_in = prev + (x - prev) * s_q (and k, v; rosa.py:128-133),
+// given the three input gradients g_q, g_k, g_v (fp32, the projections' dX):
+//   dx[r]   = sum_m g_m[r] * s_m + [r + 1 in r's sequence] (g_m[r+1] - g_m[r+1] * s_m)
+//   ds_m[c] = sum_r g_m[r, c] * (x[r, c] - prev[r, c])    (the gradient of sigmoid(mix_m))
+// with x - prev rounded to x's dtype as in the forward and dx stored in x's dtype. A block is
+// 4 waves; a lane owns 4 consecutive features and wave w walks its RB rows downward, so
+// g_m[r + 1] and x[r] come from the previous iteration. The block's ds sums (its 4 waves
+// added in order) go to ds_part (row block, 3, C); the caller adds the row blocks. The grid
+// is (ceil(C / 256), ceil(R / (4 RB))).
+template <int DT, int RB, bool VEC>
+__global__ __launch_bounds__(256) void rosa_shift_bwd_kernel(
+    const void *__restrict__ xv, const float *__restrict__ gq, const float *__restrict__ gk,
+    const float *__restrict__ gv, const float *__restrict__ sig_q, const float *__restrict__ sig_k,
+    const float *__restrict__ sig_v, int R, int C, int T, void *__restrict__ dx,
+    float *__restrict__ ds_part) {
+  using E = Elem<DT>;
+  __shared__ float red[4][3][256];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = ((int)blockIdx.x * 64 + lane) * 4;
+  const bool cok = c < C;
+  const float *g[3] = {gq, gk, gv};
+  const float *sp[3] = {sig_q, sig_k, sig_v};
+  auto ld4 = [&](const float *p, int row, bool ok, float *v) {
+    if (VEC) {
+      const float4 a = ok ? *(const float4 *)(p + (int64_t)row * C + c) : float4{0.f, 0.f, 0.f, 0.f};
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = ok && c + i < C ? p[(int64_t)row * C + c + i] : 0.0f;
+    }
+  };
+  auto ldx4 = [&](int row, bool ok, float *v) {
+    const typename E::T *p = (const typename E::T *)xv + (int64_t)row * C + c;
+    if constexpr (VEC && DT == KSD_F32) {
+      ld4((const float *)xv, row, ok, v);
+    } else if constexpr (VEC) {
+      uint2 a = ok ? *(const uint2 *)p : uint2{0u, 0u};
+      const uint16_t h[4] = {(uint16_t)(a.x & 0xffffu), (uint16_t)(a.x >> 16), (uint16_t)(a.y & 0xffffu),
+                             (uint16_t)(a.y >> 16)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = ok ? E::load(&h[i]) : 0.0f;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = ok && c + i < C ? E::load(p + i) : 0.0f;
+    }
+  };
+  float s[3][4], ds[3][4], gn[3][4];
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    ld4(sp[m], 0, cok, s[m]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ds[m][i] = 0.0f;
+  }
+  const int lo = (int)blockIdx.y * 4 * RB + wave * RB;
+  const int hi = min(lo + RB, R) - 1;  // rows lo..hi, walked downward
+  if (lo <= hi) {
+    // the row after hi contributes its prev-term when it continues hi's sequence
+    const bool nxt = hi + 1 < R && (hi + 1) % T != 0;
+#pragma unroll
+    for (int m = 0; m < 3; ++m) ld4(g[m], hi + 1, cok && nxt, gn[m]);
+    float xr[4];
+    ldx4(hi, cok, xr);
+    for (int r = hi; r >= lo; --r) {
+      const bool has_prev = r % T != 0;
+      float xp[4], diff[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
+      ldx4(r > 0 ? r - 1 : 0, cok && r > 0, xp);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) diff[i] = round_to_dt<DT>(xr[i] - (has_prev ? xp[i] : 0.0f));
+#pragma unroll
+      for (int m = 0; m < 3; ++m) {
+        float gr[4];
+        ld4(g[m], r, cok, gr);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[i] += gr[i] * s[m][i];
+          acc[i] += gn[m][i] - gn[m][i] * s[m][i];
+          ds[m][i] += gr[i] * diff[i];
+          gn[m][i] = has_prev ? gr[i] : 0.0f;
+        }
+      }
+      if (cok) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (VEC || c + i < C) store_out<DT>(dx, (int64_t)r * C + c + i, acc[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xr[i] = xp[i];
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 3; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][m][lane * 4 + i] = ds[m][i];
+  __syncthreads();
+  // 768 sums per block (3 x 256 features), 256 threads: 3 each, the waves added in order
+  const int f = (int)threadIdx.x, cf = (int)blockIdx.x * 256 + f;
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    const float v = ((red[0][m][f] + red[1][m][f]) + red[2][m][f]) + red[3][m][f];
+    if (cf < C) ds_part[((int64_t)blockIdx.y * 3 + m) * C + cf] = v;
+  }
+}
+
 // ---------------------------------------------------------------- bit packing
 // (B, T, S) -> words (B, S, W): one thread per (stream s, word w).
 template <int DT>
@@ -346,6 +575,96 @@ extern "C" int ksd_rosa_shift_quant(const void *x, int x_dtype, int64_t B, int64
 #undef KSD_SQ_V
 #undef KSD_SQ
   return check_launch("rosa_shift_quant");
+}
+
+extern "C" int ksd_rosa_shift_quant_dual(const void *x, int x_dtype, int64_t B, int64_t T, int64_t d,
+                                         const float *sig_q, const float *sig_k, const float *sig_v,
+                                         int8_t *const *codes, uint16_t *const *scales,
+                                         int8_t *const *codes_t, uint16_t *const *scales_t,
+                                         void *stream) {
+  if (B < 0 || T < 0 || d < 0) return fail(KSD_EINVAL, "rosa_shift_quant_dual: negative shape");
+  if (x_dtype != KSD_F32 && x_dtype != KSD_BF16 && x_dtype != KSD_F16)
+    return fail(KSD_ETYPE, "rosa_shift_quant_dual: x must be float32, bfloat16 or float16");
+  const int64_t rows = B * T;
+  if (rows == 0 || d == 0) return KSD_OK;
+  if (!x || !sig_q || !sig_k || !sig_v || !codes || !scales || !codes_t || !scales_t)
+    return fail(KSD_EINVAL, "rosa_shift_quant_dual: null pointer");
+  ShiftDualOut out;
+  for (int m = 0; m < 3; ++m) {
+    if (!codes[m] || !scales[m] || !codes_t[m] || !scales_t[m])
+      return fail(KSD_EINVAL, "rosa_shift_quant_dual: null output pointer");
+    out.codes[m] = codes[m];
+    out.scales[m] = scales[m];
+    out.codes_t[m] = codes_t[m];
+    out.scales_t[m] = scales_t[m];
+  }
+  if (rows > 0x7fffffff - 256 || d > (1 << 24))
+    return fail(KSD_EINVAL, "rosa_shift_quant_dual: too large");
+  const size_t esz = x_dtype == KSD_F32 ? 4 : 2;
+  auto al = [](const void *p, size_t a) { return ((uintptr_t)p % a) == 0; };
+  bool ok = d % 8 == 0 && al(x, 16) && (d * esz) % 16 == 0 && al(sig_q, 16) && al(sig_k, 16) &&
+            al(sig_v, 16);
+  for (int m = 0; m < 3; ++m) ok = ok && al(codes[m], 8) && al(scales[m], 2) && al(scales_t[m], 2);
+  if (!ok)
+    return fail(KSD_EINVAL, "rosa_shift_quant_dual: needs d %% 8 == 0 and 16-byte aligned rows");
+  const dim3 grid((unsigned)cdiv(d, 128), (unsigned)cdiv(rows, 128));
+  hipStream_t st = (hipStream_t)stream;
+  switch (x_dtype) {
+    case KSD_F32:
+      hipLaunchKernelGGL(rosa_shift_dual_kernel<KSD_F32>, grid, dim3(512), 0, st, x, (int)rows, (int)d,
+                         (int)T, sig_q, sig_k, sig_v, out);
+      break;
+    case KSD_BF16:
+      hipLaunchKernelGGL(rosa_shift_dual_kernel<KSD_BF16>, grid, dim3(512), 0, st, x, (int)rows, (int)d,
+                         (int)T, sig_q, sig_k, sig_v, out);
+      break;
+    default:
+      hipLaunchKernelGGL(rosa_shift_dual_kernel<KSD_F16>, grid, dim3(512), 0, st, x, (int)rows, (int)d,
+                         (int)T, sig_q, sig_k, sig_v, out);
+      break;
+  }
+  return check_launch("rosa_shift_quant_dual");
+}
+
+constexpr int kShiftBwdRows = 16;  // rows per wave of rosa_shift_bwd_kernel (4 waves a block)
+
+extern "C" int ksd_rosa_shift_backward_blocks(int64_t B, int64_t T, int64_t *n_blocks) {
+  if (!n_blocks || B < 0 || T < 0) return fail(KSD_EINVAL, "rosa_shift_backward_blocks: bad argument");
+  *n_blocks = cdiv(B * T, 4 * kShiftBwdRows);
+  return KSD_OK;
+}
+
+extern "C" int ksd_rosa_shift_backward(const void *x, int x_dtype, int64_t B, int64_t T, int64_t d,
+                                       const float *g_q, const float *g_k, const float *g_v,
+                                       const float *sig_q, const float *sig_k, const float *sig_v,
+                                       void *dx, float *dsig_partials, void *stream) {
+  if (B < 0 || T < 0 || d < 0) return fail(KSD_EINVAL, "rosa_shift_backward: negative shape");
+  if (x_dtype != KSD_F32 && x_dtype != KSD_BF16 && x_dtype != KSD_F16)
+    return fail(KSD_ETYPE, "rosa_shift_backward: x must be float32, bfloat16 or float16");
+  const int64_t rows = B * T;
+  if (rows == 0 || d == 0) return KSD_OK;
+  if (!x || !g_q || !g_k || !g_v || !sig_q || !sig_k || !sig_v || !dx || !dsig_partials)
+    return fail(KSD_EINVAL, "rosa_shift_backward: null pointer");
+  if (rows > 0x7fffffff - 256 || d > (1 << 24)) return fail(KSD_EINVAL, "rosa_shift_backward: too large");
+  const size_t esz = x_dtype == KSD_F32 ? 4 : 2;
+  auto al = [](const void *p, size_t a) { return ((uintptr_t)p % a) == 0; };
+  const bool vec = d % 4 == 0 && al(x, 4 * esz) && al(g_q, 16) && al(g_k, 16) && al(g_v, 16) &&
+                   al(sig_q, 16) && al(sig_k, 16) && al(sig_v, 16) && al(dx, 4 * esz);
+  const dim3 grid((unsigned)cdiv(d, 256), (unsigned)cdiv(rows, 4 * kShiftBwdRows));
+  hipStream_t st = (hipStream_t)stream;
+#define KSD_SB(DT, V)                                                                              \
+  hipLaunchKernelGGL((rosa_shift_bwd_kernel<DT, kShiftBwdRows, V>), grid, dim3(256), 0, st, x, g_q,  \
+                     g_k, g_v, sig_q, sig_k, sig_v, (int)rows, (int)d, (int)T, dx, dsig_partials)
+#define KSD_SB_V(DT) \
+  if (vec) KSD_SB(DT, true); else KSD_SB(DT, false)
+  switch (x_dtype) {
+    case KSD_F32: KSD_SB_V(KSD_F32); break;
+    case KSD_BF16: KSD_SB_V(KSD_BF16); break;
+    default: KSD_SB_V(KSD_F16); break;
+  }
+#undef KSD_SB_V
+#undef KSD_SB
+  return check_launch("rosa_shift_backward");
 }
 
 extern "C" int ksd_rosa_pack_bits(const void *x, int x_dtype, int64_t B, int64_t T, int64_t S,

@@ -4,8 +4,11 @@ Same module surface: ``_match_payload_sign`` and ``RosaMixer`` (parameters, init
 ``_shifted``, ``forward``). The match runs in ksd_rosa_match (bit-sliced longest-suffix
 search, any T up to 65536; the reference's own form needs O(T^2) int64 tensors per
 length); training on the GPU goes through ``HardRosaGPU`` (exact counterfactual credits).
-With Int8Linear projections (``to_int8`` surfaces) in eval, the time shift and the three
-input quantizations are one kernel (ksd_rosa_shift_quant).
+With Int8Linear projections (``to_int8`` surfaces) the time shift and the three input
+quantizations are one kernel: ksd_rosa_shift_quant in eval, and in training
+ksd_rosa_shift_quant_dual (each input's row codes and dW's transposed operand) with
+ksd_rosa_shift_backward for the shift's gradient (ShiftedInt8Projections); the shifted
+inputs are never materialised.
 """
 
 from __future__ import annotations
@@ -33,6 +36,10 @@ def _match_payload_sign(qbits: torch.Tensor, kbits: torch.Tensor, vbits: torch.T
 
 class RosaMixer(nn.Module):
     """rosa.py:101-165."""
+
+    # training with Int8Linear q/k/v: shift + dual quantization fused (False: torch's
+    # _shifted, then each Int8Linear quantizes its own input)
+    fused_shift = True
 
     def __init__(self, d_model: int, streams: int = 512, bits: int = 1):
         super().__init__()
@@ -68,6 +75,30 @@ class RosaMixer(nn.Module):
         from ..kernels.linear import Int8Linear
         return all(isinstance(getattr(self, n), Int8Linear) for n in ("q_proj", "k_proj", "v_proj"))
 
+    def _fused_training_projections(self, x: torch.Tensor):
+        """Training with Int8Linear q/k/v: ShiftedInt8Projections, or None when its
+        preconditions fail (then the composed path runs)."""
+        from ..kernels.linear import Int8Linear
+        projs = (self.q_proj, self.k_proj, self.v_proj)
+        mixes = (self.time_mix_q, self.time_mix_k, self.time_mix_v)
+        if not (self.fused_shift and self._int8_projections()
+                and x.dtype in (torch.float32, torch.bfloat16, torch.float16)
+                and x.shape[-1] % 8 == 0 and all(m.dtype == torch.float32 for m in mixes)
+                and not any(p.ste_training for p in projs)):
+            return None
+        x = x.contiguous()
+        if x.data_ptr() % 16:
+            return None
+        args = []
+        for p in projs:
+            assert isinstance(p, Int8Linear)
+            if not p._codes_current():  # as Int8Linear.forward: live masters stay authoritative
+                p._codes_key = None
+                p._quantize_weight()
+            args += [p.weight, p.bias, p.weight_codes, p.weight_scales]
+        sig = [torch.sigmoid(m) for m in mixes]
+        return R.ShiftedInt8Projections.apply(x, *sig, *args)
+
     def _fused_projections(self, x: torch.Tensor):
         """Eval with Int8Linear q/k/v: shift + quantize in one pass, then the W8A8 GEMMs
         (+ bias) exactly as Int8Linear.forward computes them (linear.py:62-73)."""
@@ -102,8 +133,12 @@ class RosaMixer(nn.Module):
             raise RuntimeError("ksdraft_amd's Rosa mixer runs on the GPU only (no CPU path)")
         from ..kernels.rosa_credit_gpu import HardRosaGPU
         if self.training:
-            q_in, k_in, v_in = self._shifted(x)
-            q_full, k_full, v_full = self.q_proj(q_in), self.k_proj(k_in), self.v_proj(v_in)
+            fused = self._fused_training_projections(x) if torch.is_grad_enabled() else None
+            if fused is not None:
+                q_full, k_full, v_full = fused
+            else:
+                q_in, k_in, v_in = self._shifted(x)
+                q_full, k_full, v_full = self.q_proj(q_in), self.k_proj(k_in), self.v_proj(v_in)
             hard = HardRosaGPU.apply(q_full, k_full, v_full, self.payload)
             return self._out(hard.to(x.dtype), residual)
         if self._int8_projections() and not torch.is_grad_enabled():

@@ -128,6 +128,33 @@ def shifted(x, sig, dtype="float32"):
     return (prev + (diff * np.asarray(sig, np.float32)).astype(np.float32)).astype(np.float32)
 
 
+def shifted_backward(x, sig, grads, dtype="float32"):
+    """Backward of the three lerps of rosa.py:128-133, in float64 (the gradient the
+    autograd of _shifted computes, without its intermediate roundings).
+
+    x (B, T, d) values of `dtype`; sig (3, d) the fp32 sigmoids of time_mix_q/k/v; grads
+    the three dL/d(m_in), (B, T, d). m_in = prev + (x - prev) * s_m, prev = x shifted one
+    token (0 at t = 0), x - prev rounded to `dtype` as the forward rounds it. Returns
+    (dx (B, T, d) float64, dsig (3, d) float64)."""
+    x = np.asarray(x, np.float32)
+    prev = np.concatenate([np.zeros_like(x[:, :1]), x[:, :-1]], 1)
+    diff = (x - prev).astype(np.float32)
+    if dtype == "bfloat16":
+        diff = _bf16_round(diff)
+    elif dtype == "float16":
+        diff = diff.astype(np.float16).astype(np.float32)
+    diff = diff.astype(np.float64)
+    dx = np.zeros(x.shape, np.float64)
+    dsig = np.zeros((3, x.shape[-1]), np.float64)
+    for m, g in enumerate(grads):
+        g = np.asarray(g, np.float64)
+        s = np.asarray(sig[m], np.float64)
+        dx += g * s                          # through x - prev, into x[t]
+        dx[:, :-1] += (g * (1.0 - s))[:, 1:]  # through prev (+ and - terms), into x[t - 1]
+        dsig[m] = (g * diff).sum(axis=(0, 1))
+    return dx, dsig
+
+
 def bits_of(x):
     """(x > 0) as uint8 (rosa.py:156-158, rosa_credit_gpu.py:68-70)."""
     return (np.asarray(x) > 0).astype(np.uint8)

@@ -7,7 +7,9 @@ stage: hooks capture each surface's device inputs and upstream gradients, and th
 chains (tests/chains.py) recompute its outputs and gradients from those inputs and the
 fp32 masters.
 
-Bars: Int8Linear (Rosa q/k/v/out, teacher_proj) y, dX, dW bit-exact; KS3Int8Cell y, dx,
+Bars: Int8Linear (Rosa q/k/v/out, teacher_proj) y, dX, dW bit-exact (q/k/v through the
+fused shift + dual quantization, whose input gradient is within fp32 summation order of
+the oracle's float64 shift backward); KS3Int8Cell y, dx,
 ddown, dup bit-exact, dcoeff/dscale/dshift within the VJP-reduction tolerance; the Rosa
 hard output bit-exact and its credits within 1e-5; the head's loss within 2e-5 of float64
 torch; after the optimizer step, every registered layer's int8 codes bit-exact against the
@@ -18,6 +20,7 @@ import numpy as np
 import pytest
 import torch
 
+import ksdraft_amd.kernels.rosa as krosa
 import ksdraft_amd.kernels.rosa_credit_gpu as rcg
 from ksdraft_amd.config import KSDraftConfig
 from ksdraft_amd.kernels.ks3_int8 import KS3Int8Cell
@@ -82,6 +85,23 @@ class _Recorder:
                 return out
         monkeypatch.setattr(rcg, "HardRosaGPU", Recording)
 
+        # the Rosa q/k/v projections in training: shift + dual quantization + 3 GEMMs
+        orig_shift = krosa.ShiftedInt8Projections
+        shift = self.shift = []
+
+        class RecordingShift:
+            @staticmethod
+            def apply(x, sq, sk, sv, *args):
+                outs = orig_shift.apply(x, sq, sk, sv, *args)
+                r = {"x": x.detach().clone(), "sig": [t.detach().clone() for t in (sq, sk, sv)],
+                     "out": [o.detach().clone() for o in outs]}
+                for i, o in enumerate(outs):
+                    o.register_hook(lambda g, i=i: r.__setitem__(f"g{i}", g.detach().clone()))
+                x.register_hook(lambda g: r.__setitem__("dx", g.detach().clone()))
+                shift.append(r)
+                return outs
+        monkeypatch.setattr(krosa, "ShiftedInt8Projections", RecordingShift)
+
     @staticmethod
     def _hook(name, mod, store):
         r = store.setdefault(name, {"mod": mod})
@@ -120,6 +140,9 @@ def test_int8_draft_step_stagewise_bit_exact(monkeypatch, int8_injection):
     assert len(rec.lin) == 2 * 4 + 1 + (2 * 8 if int8_injection else 0)
     for name, r in rec.lin.items():
         mod = r["mod"]
+        if "x" not in r:  # the fused shift + q/k/v path runs instead of the module's forward
+            assert name.endswith(("rosa.q_proj", "rosa.k_proj", "rosa.v_proj")), name
+            continue
         x = _np(r["x"]).reshape(-1, mod.in_features)
         gy = _np(r["g"]).reshape(-1, mod.out_features)
         w = _np(masters[name + ".weight"])
@@ -133,7 +156,25 @@ def test_int8_draft_step_stagewise_bit_exact(monkeypatch, int8_injection):
             assert _bits(_np(r["dx"]).reshape(exp["dx"].shape), exp["dx"]), name
         assert _bits(_np(mod.weight.grad), exp["dw"]), name
 
-    assert sum(r["res"] is not None for r in rec.lin.values()) == 2  # both out_proj
+    assert sum(r.get("res") is not None for r in rec.lin.values()) == 2  # both out_proj
+
+    # Rosa q/k/v: the fused shift + projections against the oracle shift and linear chain
+    assert len(rec.shift) == 2
+    for blk, r in enumerate(rec.shift):
+        x = _np(r["x"])
+        d = x.shape[-1]
+        dxs = []
+        for m, proj in enumerate(("q_proj", "k_proj", "v_proj")):
+            name = f"blocks.{blk}.rosa.{proj}"
+            lerp = orr.shifted(x, _np(r["sig"][m]), "float32").reshape(-1, d)
+            gy = _np(r[f"g{m}"]).reshape(lerp.shape[0], -1)
+            exp = chains.linear_chain(lerp, _np(masters[name + ".weight"]),
+                                      _np(masters[name + ".bias"]), gy)
+            assert _bits(_np(r["out"][m]).reshape(exp["y"].shape), exp["y"]), name
+            assert _bits(_np(model.get_submodule(name).weight.grad), exp["dw"]), name
+            dxs.append(exp["dx"].reshape(x.shape))
+        edx, _ = orr.shifted_backward(x, np.stack([_np(t) for t in r["sig"]]), dxs)
+        np.testing.assert_allclose(_np(r["dx"]), edx, rtol=1e-5, atol=1e-6 * np.abs(edx).max())
     # KS3 cells
     assert len(rec.cell) == 2
     assert all(r["res"] is not None for r in rec.cell.values())

@@ -312,3 +312,113 @@ def test_rosa_mixer_int8_projections_eval_fused_branch(dtype):
     exp = og.gemm_ordered(hq, hs, oq_, os_, bias=m.out_proj.bias.detach().cpu().numpy())
     exp = torch.from_numpy(exp).to(dtype).reshape(B, T, d)
     assert torch.equal(y.cpu(), exp)
+
+
+def _x_of(dtype, shape, gen, scale=1.5):
+    t = torch.randn(*shape, generator=gen) * scale
+    return t.to(getattr(torch, dtype)).to(DEV)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("B,T,d", [(2, 33, 320), (1, 130, 256), (3, 64, 1536), (2, 100, 136)])
+def test_shift_quantize_dual(dtype, B, T, d):
+    """Training form of the fused shift: each input's row codes and its transposed,
+    requantized operand bit-exact against quantize_last_dim and requant_transpose of the
+    oracle's shift (the Int8Linear training recipe applied to _shifted's outputs)."""
+    gen = torch.Generator().manual_seed(B * 1000 + T + d)
+    x = _x_of(dtype, (B, T, d), gen)
+    sig = [torch.sigmoid(torch.randn(d, generator=gen) * 2).to(DEV) for _ in range(3)]
+    got = R.shift_quantize_dual(x, *sig)
+    xv = x.float().cpu().numpy()
+    for m in range(3):
+        lerp = orr.shifted(xv, sig[m].cpu().numpy(), dtype).reshape(B * T, d)
+        xq, xs = oq.quantize_last_dim(lerp)
+        xtq, xts = oq.requant_transpose(xq, xs)
+        codes, scales, codes_t, scales_t = (t.cpu().numpy() for t in got[m])
+        assert np.array_equal(codes, xq), m
+        assert np.array_equal(scales.view(np.uint16), xs.view(np.uint16)), m
+        assert np.array_equal(codes_t, xtq), m
+        assert np.array_equal(scales_t.view(np.uint16), xts.view(np.uint16)), m
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("B,T,d", [(2, 33, 320), (1, 130, 260), (3, 70, 1536), (2, 17, 258)])
+def test_shift_backward(dtype, B, T, d):
+    """The shift's backward against the oracle's float64 gradient: dx within fp32 rounding
+    of six terms (one bf16 rounding for bf16 x), dsig within fp32 accumulation over the
+    tokens (bounded by the sum of |g * (x - prev)|)."""
+    gen = torch.Generator().manual_seed(B * 7 + T + d)
+    x = _x_of(dtype, (B, T, d), gen)
+    sig = torch.sigmoid(torch.randn(3, d, generator=gen) * 2).to(DEV)
+    gs = [torch.randn(B, T, d, generator=gen).to(DEV) for _ in range(3)]
+    dx, dsig = R.shift_backward(x, *gs, sig[0], sig[1], sig[2])
+    assert dx.dtype == x.dtype and dx.shape == x.shape
+    edx, edsig = orr.shifted_backward(x.float().cpu().numpy(), sig.cpu().numpy(),
+                                      [g.cpu().numpy() for g in gs], dtype)
+    got = dx.float().cpu().numpy()
+    if dtype == "float32":
+        np.testing.assert_allclose(got, edx, rtol=1e-5, atol=1e-6 * np.abs(edx).max())
+    else:
+        np.testing.assert_allclose(got, edx, rtol=2.0 ** -8, atol=1e-6 * np.abs(edx).max())
+    xv = x.float().cpu().numpy()
+    prev = np.concatenate([np.zeros_like(xv[:, :1]), xv[:, :-1]], 1)
+    bound = sum(np.abs(g.cpu().numpy() * (xv - prev)).sum(axis=(0, 1)) for g in gs)
+    assert np.all(np.abs(dsig.cpu().numpy() - edsig) <= 1e-5 * bound + 1e-30)
+
+
+def _int8_mixer(d, S, seed):
+    from ksdraft_amd.kernels.linear import Int8Linear
+    torch.manual_seed(seed)
+    m = RosaMixer(d, S)
+    with torch.no_grad():
+        for p in (m.time_mix_q, m.time_mix_k, m.time_mix_v):
+            p.normal_(0, 1)
+        m.out_proj.weight.normal_(0, 0.05)
+        for p in (m.q_proj, m.k_proj, m.v_proj):
+            p.bias.normal_(0, 0.1)
+    m = m.to(DEV)
+    for name in ("q_proj", "k_proj", "v_proj", "out_proj"):
+        setattr(m, name, Int8Linear.from_float(getattr(m, name)))
+    return m
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_shifted_int8_projections_training_match_composed(dtype):
+    """Training with Int8Linear q/k/v: the fused shift + dual quantization path
+    (ShiftedInt8Projections) against torch's _shifted followed by the three Int8Linear
+    layers on the same inputs. q/k/v outputs, dW and db bit-exact (the same int8 operands
+    and GEMMs); dx and the time-mix gradients within fp32 summation order."""
+    import copy
+    m1 = _int8_mixer(256, 64, 3)
+    m2 = copy.deepcopy(m1)
+    m2.fused_shift = False
+    m1.train(), m2.train()
+    x0 = torch.randn(2, 40, 256, generator=torch.Generator().manual_seed(4)).to(dtype).to(DEV)
+    x1 = x0.clone().requires_grad_(True)
+    x2 = x0.clone().requires_grad_(True)
+    outs1 = m1._fused_training_projections(x1)
+    assert outs1 is not None
+    q_in, k_in, v_in = m2._shifted(x2)
+    outs2 = (m2.q_proj(q_in), m2.k_proj(k_in), m2.v_proj(v_in))
+    gen = torch.Generator().manual_seed(5)
+    gs = [torch.randn(o.shape, generator=gen).to(DEV) * 1e-2 for o in outs2]
+    for a, b in zip(outs1, outs2):
+        assert a.dtype == b.dtype == torch.float32
+        assert torch.equal(a, b)
+    torch.autograd.backward(outs1, gs)
+    torch.autograd.backward(outs2, gs)
+    for name in ("q_proj", "k_proj", "v_proj"):
+        p1, p2 = getattr(m1, name), getattr(m2, name)
+        assert torch.equal(p1.weight.grad, p2.weight.grad), name
+        assert torch.equal(p1.bias.grad, p2.bias.grad), name
+    assert x1.grad.dtype == x2.grad.dtype == dtype
+    rt = 1e-5 if dtype == torch.float32 else 2.0 ** -7
+    torch.testing.assert_close(x1.grad.float(), x2.grad.float(), rtol=rt,
+                               atol=rt * x2.grad.float().abs().max().item())
+    for name in ("time_mix_q", "time_mix_k", "time_mix_v"):
+        g1, g2 = getattr(m1, name).grad, getattr(m2, name).grad
+        torch.testing.assert_close(g1, g2, rtol=1e-4, atol=1e-4 * g2.abs().max().item())
+    # and the whole training forward of the mixer agrees
+    y1 = m1(x0)
+    y2 = m2(x0)
+    assert torch.equal(y1, y2)

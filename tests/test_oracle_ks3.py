@@ -174,3 +174,29 @@ def test_rosa_shifted_matches_torch_ops():
         s32 = orr.sigmoid32(mix.numpy())
         assert np.max(np.abs(s32.view(np.int32).astype(np.int64)
                              - sig.numpy().view(np.int32).astype(np.int64))) <= 2
+
+
+def test_rosa_shifted_backward_matches_torch_autograd():
+    """oracle.rosa.shifted_backward against torch autograd of the reference's expression
+    (model/rosa.py:128-133) in float64 on the CPU, with the sigmoid outputs as leaves; the
+    forward's x - prev rounding is fixed by running it in x's dtype and the lerp in float64."""
+    import torch
+    import torch.nn.functional as F
+    from oracle import rosa as orr
+    g = torch.Generator().manual_seed(7)
+    for dt in (torch.float32, torch.bfloat16):
+        x = (torch.randn(3, 21, 40, generator=g) * 2).to(dt)
+        sig = torch.sigmoid(torch.randn(3, 40, generator=g) * 2).double().requires_grad_(True)
+        xd = x.double().requires_grad_(True)
+        prev = F.pad(xd, (0, 0, 1, 0))[:, :-1, :]
+        diff_r = (x - F.pad(x, (0, 0, 1, 0))[:, :-1, :]).double()  # rounded in x's dtype
+        # x - prev carries x's rounding in value and the identity in gradient
+        diff = (xd - prev) + (diff_r - (xd - prev)).detach()
+        grads = [torch.randn(3, 21, 40, generator=g, dtype=torch.float64) for _ in range(3)]
+        loss = sum(((prev + diff * sig[m]) * grads[m]).sum() for m in range(3))
+        loss.backward()
+        dx, dsig = orr.shifted_backward(x.float().numpy(), sig.detach().float().numpy(),
+                                        [t.numpy() for t in grads], str(dt).split(".")[-1])
+        np.testing.assert_allclose(dx, xd.grad.numpy(), rtol=1e-6, atol=1e-9)
+        # sig enters the oracle rounded to fp32; the reference keeps it in float64
+        np.testing.assert_allclose(dsig, sig.grad.numpy(), rtol=1e-5, atol=1e-6)
