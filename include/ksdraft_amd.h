@@ -294,6 +294,25 @@ int ksd_ks3_spine_fused(const float *acc, int64_t M, int64_t F, const int8_t *sp
                         int8_t *h_codes, uint16_t *h_scales, float *table, void *stream);
 
 /*
+ * K6/K8, the 'fp32' and 'fp16' nonlinear modes — _spine_features (reference
+ * ksdraft/kernels/ks3_int8.py:172-203, rank 1) followed by quantize_last_dim(h), or the
+ * same stage of project_fused for NL = 0 / 1 (ksdraft/kernels/ks3_triton.py:76-98, 137-156).
+ *   x          (M, F): KSD_F16 coordinates (composed path) or the KSD_F32 down-projection
+ *              accumulator (project_fused contract; clamped to +-65504)
+ *   spine_codes (F, 6) int8, spine_scale (F,) fp16: pack_spine's buffers
+ *   warp_scale, warp_shift (F,) fp32: the dequantized warp scalars in the path's
+ *              arithmetic (composed 'fp32': fp32; composed 'fp16' and both fused modes: fp16
+ *              values), softplus/tanh already applied (KS3Int8Cell._warp_scalars)
+ *   mode       0 = 'fp32', 1 = 'fp16'
+ *   h          optional (M, F) fp32 features; h_codes (M, F) int8 + h_scales
+ *              (M, ceil(F/group)) fp16 optional, together
+ */
+int ksd_ks3_spine_float(const void *x, int x_dtype, int64_t M, int64_t F,
+                        const int8_t *spine_codes, const uint16_t *spine_scale,
+                        const float *warp_scale, const float *warp_shift, int mode, int group,
+                        float *h, int8_t *h_codes, uint16_t *h_scales, void *stream);
+
+/*
  * Number of row blocks (the first dim of the partials workspace) ksd_ks3_vjp uses for M
  * rows: ceil(M / 512). Fixes the order of the column reductions.
  */

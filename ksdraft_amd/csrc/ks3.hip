@@ -982,6 +982,183 @@ static void launch_fused(bool vec, dim3 grid, hipStream_t st, const float *acc, 
 
 static int64_t vjp_row_blocks(int64_t M) { return cdiv(M, kVjpRowsPerBlock); }
 
+// ---------------------------------------------------------------- float nonlinear modes
+// _spine_features in the 'fp32' and 'fp16' modes (ks3_int8.py:172-203), rank 1, with the
+// features requantized along F in the same pass (quantize_last_dim(h), group G). SRC is
+// KSD_F16 for the composed path (the coordinates the GEMM epilogue rounded to fp16 and
+// clamped) or KSD_F32 for the project_fused contract (the fp32 down-GEMM accumulator,
+// clamped to +-65504 here, ks3_triton.py:146). sc / sh are the warp scalars as fp32 values
+// (the caller passes the fp32 or fp16 dequantization the path uses).
+//   fp32:  t = 4 tanh(x / 4), z = tanh(sc (t + sh)), the Horner cubic and warp in fp32,
+//          h = relu(x + (poly + warped) ps)^2, every op rounded to fp32 (tanh: tanhf).
+//   fp16:  th = fp16(x / 4), t = fp16(4 tanh(th)), warp = fp16(sc (t + sh)) (two fp32
+//          ops), z = fp16(tanh(warp)), the Horner steps as fp16 ops, h = relu(fp16(x +
+//          (poly + warped) ps)) and fp16(h h). tanh of an fp16 value rounded to fp16 comes
+//          from the kTanh16 table (staged in LDS); fp16(4 tanh(th)) equals 4 table(th)
+//          for |th| >= 2^-12 (where the table value is a normal fp16, so the exact scaling
+//          by 4 commutes with the rounding) and 4 th below (tanh(th) rounds to th in
+//          fp32 there). Both forms are checked against torch for every fp16 input.
+// A block is 4 waves; a wave walks RT consecutive rows, a lane owns 8 consecutive charts
+// (its per-chart constants stay in registers), a group is G/8 adjacent lanes.
+template <int MODE>
+__device__ __forceinline__ float tanh_fwd(float v, const uint16_t *tab, bool times4) {
+  if constexpr (MODE == 0) {
+    return times4 ? 4.0f * tanhf(v) : tanhf(v);
+  } else {
+    const uint32_t u = f16_bits(v), m = u & 0x7fffu;
+    if (m > 0x7c00u) return v;                                      // NaN
+    if (times4 && m < 0x0c00u) return 4.0f * v;                     // |th| < 2^-12
+    const float t = f16_to_f32(tab[min(m, (uint32_t)KSD_TANH16_LIMIT)]);
+    const float r = times4 ? 4.0f * t : t;
+    return (u & 0x8000u) ? -r : r;
+  }
+}
+
+template <int MODE, int SRC, int G, bool VEC, int RT>
+__global__ __launch_bounds__(256) void ks3_spine_float_kernel(
+    const void *__restrict__ xin, int M, int Fn, const int8_t *__restrict__ codes,
+    const uint16_t *__restrict__ ps16, const float *__restrict__ scv, const float *__restrict__ shv,
+    float *__restrict__ h_out, int8_t *__restrict__ hq, uint16_t *__restrict__ hs, int ngroups) {
+  constexpr int LPG = G / 8;
+  __shared__ uint16_t tab[MODE == 1 ? KSD_TANH16_LIMIT + 2 : 2];
+  if constexpr (MODE == 1) {
+    for (int i = threadIdx.x; i <= KSD_TANH16_LIMIT; i += 256) tab[i] = kTanh16[i];
+    __syncthreads();
+  }
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = ((int)blockIdx.x * 4 + wave) * RT;
+  if (row0 >= M) return;  // wave-uniform, after the block's only barrier
+  const int k0 = ((int)blockIdx.y * 64 + (int)(threadIdx.x & 63)) * 8;
+  // per-chart constants of the lane's 8 charts (0 past F)
+  float A[8], B[8], C0[8], C2[8], C4[8], C5[8], PS[8], SC[8], SH[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int f = k0 + e;
+    const bool ok = f < Fn;
+    const int fc = ok ? f : 0;
+    const float c0 = codes[6 * fc], c1 = codes[6 * fc + 1], c2 = codes[6 * fc + 2];
+    const float c3 = codes[6 * fc + 3], c4 = codes[6 * fc + 4], c5 = codes[6 * fc + 5];
+    // the combinations are small integers, exact in fp32 and in fp16 (|a| <= 762)
+    A[e] = ok ? 2.0f * c0 - 2.0f * c1 + c2 + c3 : 0.0f;
+    B[e] = ok ? -3.0f * c0 + 3.0f * c1 - 2.0f * c2 - c3 : 0.0f;
+    C0[e] = ok ? c0 : 0.0f;
+    C2[e] = ok ? c2 : 0.0f;
+    C4[e] = ok ? c4 : 0.0f;
+    C5[e] = ok ? c5 : 0.0f;
+    PS[e] = ok ? f16_to_f32(ps16[fc]) : 0.0f;
+    SC[e] = ok ? scv[fc] : 0.0f;
+    SH[e] = ok ? shv[fc] : 0.0f;
+  }
+#pragma unroll 1
+  for (int i = 0; i < RT; ++i) {
+    const int row = row0 + i;
+    if (row >= M) break;  // wave-uniform
+    float x[8], hv[8];
+    if constexpr (SRC == KSD_F16) {
+      const uint16_t *xr = (const uint16_t *)xin + (int64_t)row * Fn;
+      if (VEC && k0 < Fn) {
+        const uint4 w = *(const uint4 *)(xr + k0);
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = f16_to_f32((uint16_t)(ww[e / 2] >> (16 * (e & 1))));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = k0 + e < Fn ? f16_to_f32(xr[k0 + e]) : 0.0f;
+      }
+    } else {
+      const float *xr = (const float *)xin + (int64_t)row * Fn;
+      if (VEC && k0 < Fn) {
+        const float4 a = *(const float4 *)(xr + k0), b = *(const float4 *)(xr + k0 + 4);
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = k0 + e < Fn ? xr[k0 + e] : 0.0f;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = fminf(fmaxf(x[e], -kScaleMax), kScaleMax);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v;
+      if constexpr (MODE == 0) {
+        const float t = tanh_fwd<0>(x[e] * 0.25f, tab, true);
+        const float z = tanh_fwd<0>(SC[e] * (t + SH[e]), tab, false);
+        float poly = A[e] * t + B[e];
+        poly = poly * t + C2[e];
+        poly = poly * t + C0[e];
+        float wp = 4.0f * C5[e] * z + 2.0f * C4[e];
+        wp = wp * z - 3.0f * C5[e];
+        wp = wp * z - C4[e];
+        v = x[e] + (poly + wp) * PS[e];
+        v = v < 0.0f ? 0.0f : v;
+        v = v * v;
+      } else {
+        const float th = f16_round(x[e] * 0.25f);
+        const float t = f16_round(tanh_fwd<1>(th, tab, true));
+        const float warp = f16_round(SC[e] * (t + SH[e]));
+        const float z = tanh_fwd<1>(warp, tab, false);
+        float poly = f16_round(f16_round(A[e] * t) + B[e]);
+        poly = f16_round(f16_round(poly * t) + C2[e]);
+        poly = f16_round(f16_round(poly * t) + C0[e]);
+        float wp = f16_round(f16_round(4.0f * C5[e] * z) + 2.0f * C4[e]);
+        wp = f16_round(f16_round(wp * z) - 3.0f * C5[e]);
+        wp = f16_round(f16_round(wp * z) - C4[e]);
+        v = f16_round(x[e] + (poly + wp) * PS[e]);
+        v = v < 0.0f ? 0.0f : v;
+        v = f16_round(v * v);
+      }
+      hv[e] = k0 + e < Fn ? v : 0.0f;
+    }
+    if (h_out) {
+      float *hr = h_out + (int64_t)row * Fn;
+      if (VEC && k0 < Fn) {
+        *(float4 *)(hr + k0) = make_float4(hv[0], hv[1], hv[2], hv[3]);
+        *(float4 *)(hr + k0 + 4) = make_float4(hv[4], hv[5], hv[6], hv[7]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (k0 + e < Fn) hr[k0 + e] = hv[e];
+      }
+    }
+    if (hq) {  // quantize_last_dim(h): the group's lanes share one amax (all lanes active)
+      const uint32_t am = group_max_u32<LPG>(__builtin_bit_cast(uint32_t, abs_max<8>(hv)));
+      const float s = group_scale(__builtin_bit_cast(float, am));
+      if (VEC) {
+        uint32_t qw[2];
+        codes_rcp_packed<8>(hv, s, qw);
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        u32x2 q;
+        q.x = qw[0];
+        q.y = qw[1];
+        __builtin_amdgcn_raw_buffer_store_b64(q, rsrc(hq + (int64_t)row * Fn, Fn),
+                                              k0 < Fn ? (uint32_t)k0 : kOob, 0, 0);
+      } else if (k0 < Fn) {
+        int8_t q[8];
+        codes_rcp<8>(hv, s, q);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (k0 + e < Fn) hq[(int64_t)row * Fn + k0 + e] = q[e];
+      }
+      if (k0 < Fn && (k0 / 8) % LPG == 0) hs[(int64_t)row * ngroups + k0 / G] = scale_bits(s);
+    }
+  }
+}
+
+template <int MODE, int SRC, int G>
+static void launch_spine_float(bool vec, dim3 grid, hipStream_t st, const void *x, int64_t M,
+                               int64_t F, const int8_t *codes, const uint16_t *ps,
+                               const float *sc, const float *sh, float *h, int8_t *hq,
+                               uint16_t *hs, int64_t ng) {
+  constexpr int RT = 16;
+  if (vec)
+    hipLaunchKernelGGL((ks3_spine_float_kernel<MODE, SRC, G, true, RT>), grid, dim3(256), 0, st, x,
+                       (int)M, (int)F, codes, ps, sc, sh, h, hq, hs, (int)ng);
+  else
+    hipLaunchKernelGGL((ks3_spine_float_kernel<MODE, SRC, G, false, RT>), grid, dim3(256), 0, st, x,
+                       (int)M, (int)F, codes, ps, sc, sh, h, hq, hs, (int)ng);
+}
+constexpr int kSpineFloatRows = 4 * 16;  // rows per block of ks3_spine_float_kernel
+
 }  // namespace ksd
 
 using namespace ksd;
@@ -1110,6 +1287,47 @@ extern "C" int ksd_ks3_spine_fused(const float *acc, int64_t M, int64_t F,
   }
 #undef KSD_FUSED_ARGS
   return check_launch("ks3_spine_fused");
+}
+
+extern "C" int ksd_ks3_spine_float(const void *x, int x_dtype, int64_t M, int64_t F,
+                                   const int8_t *spine_codes, const uint16_t *spine_scale,
+                                   const float *warp_scale, const float *warp_shift, int mode,
+                                   int group, float *h, int8_t *h_codes, uint16_t *h_scales,
+                                   void *stream) {
+  if (M < 0 || F < 0) return fail(KSD_EINVAL, "ks3_spine_float: negative shape");
+  if (!valid_group(group)) return fail(KSD_EINVAL, "ks3_spine_float: group must be 32, 64 or 128");
+  if (mode != 0 && mode != 1) return fail(KSD_EINVAL, "ks3_spine_float: mode must be 0 (fp32) or 1 (fp16)");
+  if (x_dtype != KSD_F16 && x_dtype != KSD_F32)
+    return fail(KSD_ETYPE, "ks3_spine_float: x must be fp16 coordinates or the fp32 accumulator");
+  if (!x || !spine_codes || !spine_scale || !warp_scale || !warp_shift)
+    return fail(KSD_EINVAL, "ks3_spine_float: null input pointer");
+  if ((h_codes == nullptr) != (h_scales == nullptr))
+    return fail(KSD_EINVAL, "ks3_spine_float: h_codes and h_scales go together");
+  if (!h && !h_codes) return fail(KSD_EINVAL, "ks3_spine_float: no output requested");
+  if (M == 0 || F == 0) return KSD_OK;
+  if (F > (1LL << 28) || M > 0x7fffffffLL - kSpineFloatRows)
+    return fail(KSD_EINVAL, "ks3_spine_float: too large");
+  const size_t esz = x_dtype == KSD_F32 ? 4 : 2;
+  const bool vec = (F & 7) == 0 && ((uintptr_t)x % 16) == 0 && (F * esz) % 16 == 0 &&
+                   ((uintptr_t)h % 16) == 0 && ((uintptr_t)h_codes % 8) == 0;
+  const int64_t ng = cdiv(F, group);
+  dim3 grid((unsigned)cdiv(M, kSpineFloatRows), (unsigned)cdiv(F, 512));
+  hipStream_t st = (hipStream_t)stream;
+#define KSD_SFA vec, grid, st, x, M, F, spine_codes, spine_scale, warp_scale, warp_shift, h, h_codes, h_scales, ng
+#define KSD_SF_G(MO, SR)                                                  \
+  switch (group) {                                                        \
+    case 32: launch_spine_float<MO, SR, 32>(KSD_SFA); break;              \
+    case 64: launch_spine_float<MO, SR, 64>(KSD_SFA); break;              \
+    default: launch_spine_float<MO, SR, 128>(KSD_SFA); break;             \
+  }
+  if (mode == 0) {
+    if (x_dtype == KSD_F16) { KSD_SF_G(0, KSD_F16) } else { KSD_SF_G(0, KSD_F32) }
+  } else {
+    if (x_dtype == KSD_F16) { KSD_SF_G(1, KSD_F16) } else { KSD_SF_G(1, KSD_F32) }
+  }
+#undef KSD_SF_G
+#undef KSD_SFA
+  return check_launch("ks3_spine_float");
 }
 
 extern "C" int ksd_ks3_vjp_row_blocks(int64_t M, int64_t *n_row_blocks) {

@@ -42,8 +42,9 @@ def embedding_gather_int8(codes: torch.Tensor, scales: torch.Tensor, ids: torch.
         if bool(bad.any()):
             raise IndexError(f"index {int(flat[bad][0])} is out of range for {V} rows")
     out = torch.empty((flat.numel(), d), dtype=out_dtype, device=dev)
-    _lib.call("ksd_embedding_gather_int8", codes.contiguous().data_ptr(),
-              scales.contiguous().data_ptr(), flat.data_ptr(), flat.numel(), V, d, group,
+    codes, scales = codes.contiguous(), scales.contiguous()  # outlive the enqueued kernel
+    _lib.call("ksd_embedding_gather_int8", codes.data_ptr(),
+              scales.data_ptr(), flat.data_ptr(), flat.numel(), V, d, group,
               out.data_ptr(), code, _lib.stream_ptr(dev))
     return out.reshape(*ids.shape, d)
 

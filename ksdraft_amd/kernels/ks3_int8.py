@@ -13,9 +13,15 @@ Compute runs in libksdraft_amd.so:
   * the fp16 geometry VJP, emitting dc as the two int8 GEMM operands and the eight
     column sums: ksd_ks3_vjp + ksd_ks3_vjp_finalize;
   * the transposed operands: ksd_requant_transpose / ksd_quantize_transpose.
-The spine kernels implement rank 1 (subspace_rank == 1, the only rank the draft model
-builds, model/block.py:32) in the 'int8' nonlinear mode, the reference default; the
-'fp16' and 'fp32' parity modes raise NotImplementedError at forward time.
+  * the 'fp16' and 'fp32' nonlinear modes (ks3_int8.py:172-203): ksd_ks3_spine_float,
+    composed (on the fp16 coordinates) and under the project_fused contract (on the fp32
+    accumulator), with the features' requantization in the same pass.
+The cell evaluates rank 1 (subspace_rank == 1, the only rank the draft model builds,
+model/block.py:32). The reference cannot evaluate a higher rank either: its _project
+reshapes the (charts * rank,) packed row scales to (charts,) (ks3_int8.py:253), and its
+backward multiplies a (charts * rank,) warp gradient by a (charts,) one (:394-395); here a
+rank above 1 raises NotImplementedError (a RuntimeError, as the reference's shape errors
+are) at forward time.
 """
 
 from __future__ import annotations
@@ -104,9 +110,11 @@ def spine_int8(coords16: torch.Tensor, spine_codes: torch.Tensor, spine_scale: t
     hq = torch.empty((M, Fn), dtype=torch.int8, device=dev) if want_codes else None
     hs = (torch.empty((M, -(-Fn // group)), dtype=FP16, device=dev) if want_codes else None)
     table = torch.empty((max(Fn, 1), 256), dtype=FP16, device=dev)   # per-chart increments
-    _lib.call("ksd_ks3_spine_fwd", coords16.data_ptr(), M, Fn, sc.data_ptr(),
-              _c(spine_scale.reshape(Fn)).data_ptr(), _c(warp_scale16.reshape(Fn)).data_ptr(),
-              _c(warp_shift16.reshape(Fn)).data_ptr(), _c(tanh_lut).data_ptr(), group,
+    # operands bound to names: a converted temporary must outlive the enqueued kernel
+    ps, ws, wh, lut = (_c(spine_scale.reshape(Fn)), _c(warp_scale16.reshape(Fn)),
+                       _c(warp_shift16.reshape(Fn)), _c(tanh_lut))
+    _lib.call("ksd_ks3_spine_fwd", coords16.data_ptr(), M, Fn, sc.data_ptr(), ps.data_ptr(),
+              ws.data_ptr(), wh.data_ptr(), lut.data_ptr(), group,
               _lib.ptr(h), _lib.ptr(hq), _lib.ptr(hs), table.data_ptr(), _lib.stream_ptr(dev))
     return h, hq, hs
 
@@ -124,11 +132,44 @@ def spine_fused_int8(acc: torch.Tensor, spine_codes: torch.Tensor, spine_scale: 
     hq = torch.empty((M, Fn), dtype=torch.int8, device=dev)
     hs = torch.empty((M, -(-Fn // group)), dtype=FP16, device=dev)
     table = torch.empty((max(Fn, 1), 256), dtype=torch.float32, device=dev)
-    _lib.call("ksd_ks3_spine_fused", acc.data_ptr(), M, Fn, _c(spine_codes.reshape(Fn, 6)).data_ptr(),
-              _c(spine_scale.reshape(Fn)).data_ptr(), _c(warp_scale16.reshape(Fn)).data_ptr(),
-              _c(warp_shift16.reshape(Fn)).data_ptr(), _c(tanh_lut).data_ptr(), group,
+    sc, ps, ws, wh, lut = (_c(spine_codes.reshape(Fn, 6)), _c(spine_scale.reshape(Fn)),
+                           _c(warp_scale16.reshape(Fn)), _c(warp_shift16.reshape(Fn)), _c(tanh_lut))
+    _lib.call("ksd_ks3_spine_fused", acc.data_ptr(), M, Fn, sc.data_ptr(), ps.data_ptr(),
+              ws.data_ptr(), wh.data_ptr(), lut.data_ptr(), group,
               hq.data_ptr(), hs.data_ptr(), table.data_ptr(), _lib.stream_ptr(dev))
     return hq, hs
+
+
+_MODES = {"fp32": 0, "fp16": 1}
+
+
+def spine_float(x: torch.Tensor, spine_codes: torch.Tensor, spine_scale: torch.Tensor,
+                warp_scale: torch.Tensor, warp_shift: torch.Tensor, nonlinear: str,
+                group: int = GROUP_SIZE, *, want_h: bool = False, want_codes: bool = True):
+    """The 'fp32' / 'fp16' spine features (ks3_int8.py:172-203, rank 1) fused with
+    quantize_last_dim(h, group).
+
+    x: (M, F) float16 coordinates (the composed path) or the float32 down-GEMM
+    accumulator (the project_fused contract, clamped to +-65504 in the kernel);
+    warp_scale / warp_shift: (F,) values of the arithmetic the path uses (fp32 or fp16),
+    passed as fp32. Returns (h fp32 (M, F) or None, h_codes or None, h_scales or None)."""
+    dev = _lib.require_gpu(x, spine_codes, spine_scale, warp_scale, warp_shift)
+    if nonlinear not in _MODES:
+        raise ValueError(f"spine_float implements 'fp32' and 'fp16' (got {nonlinear!r})")
+    if x.dim() != 2 or x.dtype not in (FP16, torch.float32):
+        raise TypeError("x must be a 2-D float16 or float32 tensor")
+    M, Fn = x.shape
+    x = _c(x)
+    h = torch.empty((M, Fn), dtype=torch.float32, device=dev) if want_h else None
+    hq = torch.empty((M, Fn), dtype=torch.int8, device=dev) if want_codes else None
+    hs = torch.empty((M, -(-Fn // group)), dtype=FP16, device=dev) if want_codes else None
+    # operands bound to names: a converted temporary must outlive the enqueued kernel
+    sc, ps = _c(spine_codes.reshape(Fn, 6)), _c(spine_scale.reshape(Fn).to(FP16))
+    ws, wh = _c(warp_scale.reshape(Fn).float()), _c(warp_shift.reshape(Fn).float())
+    _lib.call("ksd_ks3_spine_float", x.data_ptr(), _lib.dtype_code(x.dtype), M, Fn,
+              sc.data_ptr(), ps.data_ptr(), ws.data_ptr(), wh.data_ptr(),
+              _MODES[nonlinear], group, _lib.ptr(h), _lib.ptr(hq), _lib.ptr(hs), _lib.stream_ptr(dev))
+    return h, hq, hs
 
 
 def ks3_vjp(value16: torch.Tensor, coords16: torch.Tensor, spine_codes: torch.Tensor,
@@ -170,9 +211,11 @@ def ks3_vjp(value16: torch.Tensor, coords16: torch.Tensor, spine_codes: torch.Te
         return out
     partials = torch.empty((nrb, 8, Fn), dtype=torch.float32, device=dev)
     st = _lib.stream_ptr(dev)
+    # operands bound to names: a converted temporary must outlive the enqueued kernel
     sc16, sh16 = _c(warp_scale16.reshape(Fn)), _c(warp_shift16.reshape(Fn))
-    _lib.call("ksd_ks3_vjp", _c(value16).data_ptr(), _c(coords16).data_ptr(), M, Fn,
-              _c(spine_codes.reshape(Fn, 6)).data_ptr(), _c(spine_scale.reshape(Fn)).data_ptr(),
+    v16, c16 = _c(value16), _c(coords16)
+    scd, ps = _c(spine_codes.reshape(Fn, 6)), _c(spine_scale.reshape(Fn))
+    _lib.call("ksd_ks3_vjp", v16.data_ptr(), c16.data_ptr(), M, Fn, scd.data_ptr(), ps.data_ptr(),
               sc16.data_ptr(), sh16.data_ptr(), group, _lib.ptr(out["dc"]),
               out["dc_codes"].data_ptr(), out["dc_scales"].data_ptr(), out["dct_codes"].data_ptr(),
               out["dct_scales"].data_ptr(), partials.data_ptr(), nrb, st)
@@ -264,23 +307,39 @@ class KS3Int8Cell(nn.Module):
         return scale, shift
 
     def _check_supported(self):
-        if self.nonlinear != "int8":
-            raise NotImplementedError(
-                f"ksdraft_amd implements the 'int8' nonlinear mode (got {self.nonlinear!r})")
         if self.subspace_rank != 1:
-            raise NotImplementedError("ksdraft_amd's KS3 kernels implement subspace_rank 1")
+            raise NotImplementedError(
+                "KS3Int8Cell evaluates subspace_rank 1; the reference cell fails for a higher "
+                "rank too (ks3_int8.py:253 reshapes the (charts*rank,) row scales to (charts,))")
+
+    def _arith(self):
+        return torch.float32 if self.nonlinear == "fp32" else FP16
+
+    def _spine(self, coords16, scale, shift, *, want_h=False, want_codes=True):
+        """The composed spine of this cell's mode on fp16 coordinates (M, F)."""
+        if self.nonlinear == "int8":
+            return spine_int8(coords16, self.spine_codes, self.spine_scale, scale.to(FP16),
+                              shift.to(FP16), self.tanh_lut, self.group, want_h=want_h,
+                              want_codes=want_codes)
+        return spine_float(coords16, self.spine_codes, self.spine_scale, scale, shift,
+                           self.nonlinear, self.group, want_h=want_h, want_codes=want_codes)
 
     def _spine_features(self, x, mean, c0, c1, c2, c3, c4, c5, ps, scale, shift):
         """ks3_int8.py:167-234. x/mean (..., charts, 1) fp32 holding fp16 values (the
         coordinates _project materialises); c* int8 codes (charts, 1); ps (charts,) fp16;
-        scale/shift (charts,) fp16. Returns the fp32 ReLU^2 features shaped like x."""
+        scale/shift (charts,) in the mode's arithmetic (fp32 for 'fp32', else fp16).
+        Returns the fp32 ReLU^2 features shaped like x."""
         self._check_supported()
         lead = x.shape
         Fn = self.num_subspaces
         codes = torch.stack([c.reshape(Fn) for c in (c0, c1, c2, c3, c4, c5)], -1).to(torch.int8)
         coords16 = x.reshape(-1, Fn).to(FP16)
-        h, _, _ = spine_int8(coords16, codes, ps.to(FP16), scale.to(FP16), shift.to(FP16),
-                             self.tanh_lut, self.group, want_h=True, want_codes=False)
+        if self.nonlinear == "int8":
+            h, _, _ = spine_int8(coords16, codes, ps.to(FP16), scale.to(FP16), shift.to(FP16),
+                                 self.tanh_lut, self.group, want_h=True, want_codes=False)
+        else:
+            h, _, _ = spine_float(coords16, codes, ps.to(FP16), scale, shift, self.nonlinear,
+                                  self.group, want_h=True, want_codes=False)
         return h.reshape(lead)
 
     def _coords16(self, xq, xs, down_codes, down_scales):
@@ -292,9 +351,8 @@ class KS3Int8Cell(nn.Module):
         self._check_supported()
         M = x.shape[0]
         coords16 = self._coords16(codes, scales, down_codes, down_scales)
-        scale, shift = self._warp_scalars(FP16)
-        h, _, _ = spine_int8(coords16, self.spine_codes, self.spine_scale, scale, shift,
-                             self.tanh_lut, self.group, want_h=True, want_codes=False)
+        scale, shift = self._warp_scalars(self._arith())
+        h, _, _ = self._spine(coords16, scale, shift, want_h=True, want_codes=False)
         return h.reshape(M, -1), coords16.float().reshape(M, self.num_subspaces,
                                                           self.subspace_rank)
 
@@ -302,9 +360,8 @@ class KS3Int8Cell(nn.Module):
         """_project + quantize_last_dim(h) in two kernels: (hq, hs, coords16)."""
         self._check_supported()
         coords16 = self._coords16(xq, xs, self.down_codes, self.down_scales)
-        scale, shift = self._warp_scalars(FP16)
-        _, hq, hs = spine_int8(coords16, self.spine_codes, self.spine_scale, scale, shift,
-                               self.tanh_lut, self.group)
+        scale, shift = self._warp_scalars(self._arith())
+        _, hq, hs = self._spine(coords16, scale, shift)
         return hq, hs, coords16
 
     def invalidate_codes(self) -> None:

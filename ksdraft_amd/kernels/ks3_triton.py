@@ -2,9 +2,12 @@
 
 The reference's Triton kernel fuses the down-projection GEMM, the Horner spine, ReLU^2 and
 the per-group requantization (ks3_triton.py:100-156). Here the GEMM is ksd_w8a8_gemm_nt
-(fp32 accumulator out) and the spine + both requantizations are ksd_ks3_spine_fused, which
-follows the fused kernel's own arithmetic contract (fp32 coordinates and LUT index, no
-truncation, group pre-scale, second requantization), not the composed one.
+(fp32 accumulator out) and the spine + requantization follow the fused kernel's own
+arithmetic contract, not the composed one: 'int8' (NL == 2) is ksd_ks3_spine_fused (fp32
+coordinates and LUT index, no truncation, group pre-scale, second requantization); 'fp16'
+and 'fp32' (NL == 1, 0; ks3_triton.py:76-98) are ksd_ks3_spine_float on the accumulator
+(the coordinates not rounded to fp16, the warp scalars in fp16), every fp16/fp32 op of
+the Triton source rounded separately.
 """
 
 from __future__ import annotations
@@ -12,7 +15,7 @@ from __future__ import annotations
 import torch
 
 from .gemm import w8a8_gemm
-from .ks3_int8 import spine_fused_int8
+from .ks3_int8 import spine_float, spine_fused_int8
 
 FP16 = torch.float16
 TANH_DOMAIN = 3.2
@@ -33,9 +36,10 @@ def project_fused(
     if group & (group - 1):
         raise ValueError("group must be a power of two (32 or 128)")
     nl = {"fp32": 0, "fp16": 1, "int8": 2}[nonlinear]
-    if nl != 2:
-        raise NotImplementedError(
-            f"ksdraft_amd implements project_fused for nonlinear='int8' (got {nonlinear!r})")
     acc = w8a8_gemm(a_codes, a_scales, w_codes, w_scales, group)
-    return spine_fused_int8(acc, spine_codes, spine_scale, warp_scale.to(FP16),
-                            warp_shift.to(FP16), tanh_lut, group)
+    if nl == 2:
+        return spine_fused_int8(acc, spine_codes, spine_scale, warp_scale.to(FP16),
+                                warp_shift.to(FP16), tanh_lut, group)
+    _, hq, hs = spine_float(acc, spine_codes, spine_scale, warp_scale.to(FP16).float(),
+                            warp_shift.to(FP16).float(), nonlinear, group)
+    return hq, hs

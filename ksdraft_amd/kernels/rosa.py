@@ -201,6 +201,7 @@ def hard_out(sign: torch.Tensor, payload: torch.Tensor, out_dtype=torch.float32)
     B, S, T = sign.shape
     out = torch.empty((B, T, S), dtype=out_dtype, device=dev)
     p = payload.to(device=dev, dtype=torch.float32).contiguous()
-    _lib.call("ksd_rosa_hard", sign.contiguous().data_ptr(), p.data_ptr(), B, T, S,
+    sign = sign.contiguous()  # bound to a name: it must outlive the enqueued kernel
+    _lib.call("ksd_rosa_hard", sign.data_ptr(), p.data_ptr(), B, T, S,
               out.data_ptr(), _lib.dtype_code(out_dtype), _lib.stream_ptr(dev))
     return out

@@ -6,6 +6,7 @@ Follows reference ksdraft/kernels/ks3_int8.py:
   * _lut_index                     :69-72
   * pack_spine / warp scalars      :87-92, 139-146, 158-165
   * _spine_features, 'int8' mode   :205-234  (rank 1)
+  * _spine_features, 'fp32' / 'fp16' modes :172-203 (rank 1)
   * _project (coords)              :238-260
   * _KS3Int8Train.backward geometry VJP :354-401
 and reference ksdraft/kernels/ks3_triton.py:
@@ -21,6 +22,14 @@ from the reference's own CPU path (bit-exact spine features and VJP coordinate
 gradient given identical GEMM outputs); the LUT against an mpmath-free closed form
 check (float64 tanh, tie distance); _round_div127 by brute force over integer ranges
 (tests/test_oracle_ks3.py).
+
+spine_features_float ('fp32' / 'fp16') is pinned by tests/golden/ks3_modes_golden.npz,
+written by tests/golden/make_ks3_modes_golden.py from the reference's own CPU path: 'fp16'
+bit-exact, 'fp32' within the difference between the float64-based tanh here and torch's
+fp32 tanh (tests/test_oracle_ks3.py). The same function is the fused contract of those
+modes (ks3_triton.py:76-98) when given the clamped fp32 accumulator and fp16 warp scalars;
+there it is parity unpinned at the bit level where Triton's default FMA contraction
+(enable_fp_fusion) may fuse a multiply and an add that the source writes separately.
 
 spine_fused_int8 (the project_fused contract) follows the Triton source's typing: the
 fp16 warp product with the constant rounded to fp16 (Triton's scalar rule, pinned by
@@ -128,6 +137,53 @@ def spine_features_int8(coords, spine_codes, spine_scale, scale16, shift16, lut)
     hq = np.maximum(hq, 0)
     hq16 = h(hq.astype(np.float32))
     return (h(hq16 * hq16) * (pre * pre).astype(np.float32)).astype(np.float32)
+
+
+def spine_features_float(x, spine_codes, spine_scale, scale, shift, mode):
+    """ks3_int8.py:172-203, the 'fp32' and 'fp16' modes, rank 1 (mean = x).
+
+    x (M, F) fp32 coordinates (fp16 values on the composed path); spine_codes (F, 6) int8;
+    spine_scale (F,) fp16; scale/shift (F,) the warp scalars in the mode's arithmetic
+    (fp32 values for 'fp32', fp16 values for 'fp16'). Returns h (M, F) fp32."""
+    x = np.asarray(x, np.float32)
+    c = np.asarray(spine_codes, np.float32)
+    c0, c1, c2, c3, c4, c5 = (c[:, k][None, :] for k in range(6))
+    ps = np.asarray(spine_scale, np.float16).astype(np.float32)[None, :]
+    sc = np.asarray(scale, np.float32)[None, :]
+    sh = np.asarray(shift, np.float32)[None, :]
+    a = 2 * c0 - 2 * c1 + c2 + c3      # small integers: exact
+    b = -3 * c0 + 3 * c1 - 2 * c2 - c3
+    if mode == "fp32":  # every torch op rounded to fp32
+        t = (f32(4.0) * tanh32((x * f32(0.25)).astype(np.float32))).astype(np.float32)
+        z = tanh32((sc * (t + sh).astype(np.float32)).astype(np.float32))
+
+        def mul(u, v):
+            return (u * v).astype(np.float32)
+        poly = (mul(a, t) + b).astype(np.float32)
+        poly = (mul(poly, t) + c2).astype(np.float32)
+        poly = (mul(poly, t) + c0).astype(np.float32)
+        wp = (mul(f32(4.0) * c5, z) + f32(2.0) * c4).astype(np.float32)
+        wp = (mul(wp, z) - f32(3.0) * c5).astype(np.float32)
+        wp = (mul(wp, z) - c4).astype(np.float32)
+        hv = (x + mul((poly + wp).astype(np.float32), ps)).astype(np.float32)
+        hv = np.where(hv < 0, f32(0.0), hv)
+        return mul(hv, hv)
+    if mode != "fp16":
+        raise ValueError(mode)
+    # every fp16 tensor op: evaluated in fp32, rounded to fp16 (h)
+    th = h(x * f32(0.25))
+    t = h(f32(4.0) * tanh32(th))
+    warp = h(sc * (t + sh).astype(np.float32))
+    z = h(tanh32(warp))
+    poly = h(h(a * t) + b)
+    poly = h(h(poly * t) + c2)
+    poly = h(h(poly * t) + c0)
+    wp = h(h(f32(4.0) * c5 * z) + f32(2.0) * c4)
+    wp = h(h(wp * z) - f32(3.0) * c5)
+    wp = h(h(wp * z) - c4)
+    hv = h(x + ((poly + wp).astype(np.float32) * ps).astype(np.float32))
+    hv = np.where(hv < 0, f32(0.0), hv)
+    return h(hv * hv)
 
 
 def coords_from_gemm(y32):

@@ -333,7 +333,5 @@ def test_project_and_spine_features_api(gold):
     h2 = cell._spine_features(coords, coords, *(c[..., k] for k in range(6)),
                               cell.spine_scale, scale, shift)
     assert torch.equal(h2.reshape(h.shape), h)
-    with pytest.raises(NotImplementedError):
-        K.KS3Int8Cell(_Cell(gold).to(DEV), nonlinear="fp16")(_g(x))
     with pytest.raises(ValueError):
         K.KS3Int8Cell(_Cell(gold).to(DEV), nonlinear="bf16")

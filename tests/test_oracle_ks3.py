@@ -200,3 +200,62 @@ def test_rosa_shifted_backward_matches_torch_autograd():
         np.testing.assert_allclose(dx, xd.grad.numpy(), rtol=1e-6, atol=1e-9)
         # sig enters the oracle rounded to fp32; the reference keeps it in float64
         np.testing.assert_allclose(dsig, sig.grad.numpy(), rtol=1e-5, atol=1e-6)
+
+
+def _modes_golden():
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "ks3_modes_golden.npz")
+    return np.load(path)
+
+
+def test_spine_float_modes_match_reference_golden():
+    """oracle.ks3.spine_features_float against the reference's own CPU _spine_features
+    ('fp16' bit-exact; 'fp32' within the tanh difference: the oracle's tanh is float64
+    rounded to fp32, torch's is its own fp32 routine), on the coordinates and warp scalars
+    the reference itself used (tests/golden/make_ks3_modes_golden.py)."""
+    from oracle import ks3 as ok
+    from oracle.quant import dequantize_last_dim
+    g = _modes_golden()
+    sc32 = dequantize_last_dim(g["warp_scale_codes"], g["warp_scale_scales"], 128).reshape(-1)
+    sh32 = dequantize_last_dim(g["warp_shift_codes"], g["warp_shift_scales"], 128).reshape(-1)
+    for mode in ("fp16", "fp32"):
+        sc, sh = (ok.h(sc32), ok.h(sh32)) if mode == "fp16" else (sc32, sh32)
+        for case in ("std1", "std8"):
+            coords = g[f"{mode}/{case}/coords"]
+            assert np.array_equal(ok.h(coords), coords)  # fp16 values, as _project makes them
+            got = ok.spine_features_float(coords, g["spine_codes"], g["spine_scale"], sc, sh, mode)
+            ref = g[f"{mode}/{case}/h"]
+            if mode == "fp16":
+                assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), case
+            else:
+                np.testing.assert_allclose(got, ref, rtol=2e-6, atol=1e-6 * np.abs(ref).max())
+                assert np.mean(got != ref) < 0.05, case
+
+
+def test_spine_float_tanh_forms_match_torch_on_every_fp16_input():
+    """The fp16 mode's two tanh forms as the kernel evaluates them from the generated
+    table (fp16(tanh32(x)) = table(x); fp16(4 tanh32(x)) = 4 table(x) for |x| >= 2^-12,
+    4 x below) equal torch's `torch.tanh(x.float()).to(fp16)` and
+    `(4.0 * torch.tanh(x.float())).to(fp16)` for every finite fp16 x."""
+    import importlib.util
+    import os
+    import torch
+    here = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    spec = importlib.util.spec_from_file_location(
+        "gen_tanh16", os.path.join(here, "ksdraft_amd", "csrc", "gen_tanh16.py"))
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    tab = gen.table()
+    bits = np.arange(0x7c01, dtype=np.uint32).astype(np.uint16)  # 0 .. +inf
+    bits = np.concatenate([bits, bits | 0x8000])
+    x16 = bits.view(np.float16)
+    m = np.minimum(bits & 0x7fff, gen.LIMIT)
+    t1 = tab[m].view(np.float16).astype(np.float32)
+    t1 = np.where(bits & 0x8000, -t1, t1)
+    xf = x16.astype(np.float32)
+    t4 = np.where((bits & 0x7fff) < 0x0c00, 4 * xf, 4 * t1)
+    xt = torch.from_numpy(x16.copy()).float()
+    ref1 = torch.tanh(xt).to(torch.float16).numpy()
+    ref4 = (4.0 * torch.tanh(xt)).to(torch.float16).numpy()
+    assert np.array_equal(t1.astype(np.float16).view(np.uint16), ref1.view(np.uint16))
+    assert np.array_equal(t4.astype(np.float16).view(np.uint16), ref4.view(np.uint16))
