@@ -463,6 +463,34 @@ int ksd_rosa_credit_grads(const float *credits, const void *q, const void *k, co
                           int dtype, const float *payload_partial, int64_t B, int64_t T, int64_t S,
                           void *gq, void *gk, void *gv, float *gpayload, void *stream);
 
+/*
+ * The transfer-space term of distillation_losses (reference ksdraft/train/__init__.py:79-85),
+ * per layer feature f (M, d) fp32 against e_hat = normalize(embedding[targets]) (M, d) fp32:
+ *   ksd_transfer_cos   cos[r] = <f_r, e_r> / max(|f_r|, 1e-12), norm[r] = |f_r|
+ *   ksd_transfer_grad  df = d/df of coef * (1 - cos) (F.normalize's gradient), and
+ *                      grad_e (+)= -coef * f_r / max(|f_r|, 1e-12) (written when first != 0);
+ *                      coef a device fp32 scalar (upstream gradient x weight / M)
+ */
+int ksd_transfer_cos(const float *f, const float *e_hat, int64_t M, int64_t d, float *cos_out,
+                     float *norm_out, void *stream);
+int ksd_transfer_grad(const float *f, const float *e_hat, const float *cos_in,
+                      const float *norm_in, const float *coef, int64_t M, int64_t d, float *df,
+                      float *grad_e, int first, void *stream);
+
+/*
+ * The gated update of the DSpine adjacent injection (reference ksdraft/model/spine.py:62-68):
+ *   out = z + sigmoid(pre) * u,  pre = bias + zs[:, 0:64] . wc^T,  u = zs[:, 64:96] . wiu^T
+ * zs (M, 96) fp32 = [gate_q.down(z) | gate_p.down(p_prev) | inject.down(p_prev)], wc (d, 64)
+ * = [gate_q.up.weight | gate_p.up.weight], wiu (d, 32) = inject.up.weight, bias (d,) or NULL;
+ * z, out (M, d) fp32. The backward writes dpre = g u s (1 - s) and du = g s (s = sigmoid(pre))
+ * for the upstream gradient g, recomputing pre and u.
+ */
+int ksd_injection_update(const float *zs, const float *wc, const float *wiu, const float *bias,
+                         const float *z, int64_t M, int64_t d, float *out, void *stream);
+int ksd_injection_update_backward(const float *zs, const float *wc, const float *wiu,
+                                  const float *bias, const float *grad_out, int64_t M, int64_t d,
+                                  float *dpre, float *du, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,7 +14,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libksdraft_amd.so")
-SOURCES = ["quant.hip", "gemm.hip", "ks3.hip", "rosa.hip"]
+SOURCES = ["quant.hip", "gemm.hip", "ks3.hip", "rosa.hip", "draft.hip"]
 OBJDIR = os.path.join(HERE, "_build")
 # generated at build time (git-ignored): fp16 tanh table for the KS3 kernels
 TANH_INC = os.path.join(CSRC, "tanh16_table.inc")

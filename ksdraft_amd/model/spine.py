@@ -8,7 +8,9 @@ with p_{-1} = 0, or position 0 seeded from the previous layer's prediction. The 
 the injection are low-rank pairs (rank 32; the feature pair rank 64) whose up-projections
 start at zero. ``to_int8`` keeps these surfaces in float (the reference's conversion
 doctrine, int8_convert.py:1-16): at rank 32/64 the reduction is shorter than one 128-wide
-quantization group.
+quantization group. On the GPU the float injection runs as one autograd function
+(kernels.draft.FusedInjection: the gated update in one HIP pass, p_prev never
+materialised, split-K weight gradients); on the CPU, as torch ops.
 """
 
 from __future__ import annotations
@@ -30,6 +32,8 @@ class _LowRank(nn.Module):
 
 
 class AdjacentInjection(nn.Module):
+    fused = True  # GPU, fp32: kernels.draft.FusedInjection (False: the torch composition)
+
     def __init__(self, width: int, rank: int = 32, feature_rank: int = 64):
         super().__init__()
         self.width = width
@@ -42,6 +46,13 @@ class AdjacentInjection(nn.Module):
 
     def extra_repr(self) -> str:
         return f"width={self.width}"
+
+    def _use_fused(self, z: torch.Tensor) -> bool:
+        ranks = (self.gate_q.down.out_features, self.gate_p.down.out_features,
+                 self.inject.down.out_features)
+        return (self.fused and z.is_cuda and z.dim() == 3 and z.dtype == torch.float32
+                and ranks == (32, 32, 32)
+                and all(p.dtype == torch.float32 for p in self.parameters()))
 
     def predicted_feature(self, z: torch.Tensor) -> torch.Tensor:
         return self.feature_up(self.feature_down(z))
@@ -62,6 +73,14 @@ class AdjacentInjection(nn.Module):
                 p_prev = torch.cat([prev_layer_feature[:, :1, :], p_prev[:, 1:, :]], dim=1)
             gate = torch.sigmoid(self.gate_q(z) + self.gate_p(p_prev) + self.gate_bias)
             return z + gate * self.inject(p_prev), p
+        if self._use_fused(z):
+            from ..kernels.draft import FusedInjection
+            prev0 = None if prev_layer_feature is None else prev_layer_feature[:, :1, :]
+            return FusedInjection.apply(
+                z.contiguous(), prev0, self.feature_down.weight, self.gate_q.down.weight,
+                self.feature_up.weight, self.gate_p.down.weight, self.inject.down.weight,
+                self.gate_q.up.weight, self.gate_p.up.weight, self.gate_bias,
+                self.inject.up.weight)
         r1 = self.feature_down.out_features
         zd = F.linear(z, torch.cat([self.feature_down.weight, self.gate_q.down.weight]))
         p = self.feature_up(zd[..., :r1])

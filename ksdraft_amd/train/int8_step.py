@@ -38,8 +38,14 @@ def clip_coefficient(params, max_norm: float) -> torch.Tensor:
 
 
 def transfer_space_loss(features, embedding_weight: torch.Tensor, tgt: torch.Tensor):
-    """distillation_losses' transfer term (train/__init__.py:79-85)."""
+    """distillation_losses' transfer term (train/__init__.py:79-85). On the GPU the
+    per-layer cosines and their gradients are two HIP row kernels per layer
+    (kernels.draft.TransferSpaceLoss); the normalized target embeddings stay torch ops."""
     tgt_emb = F.normalize(embedding_weight[tgt].float(), dim=-1)
+    if tgt_emb.is_cuda and len(features) and all(f.is_cuda for f in features):
+        from ..kernels.draft import TransferSpaceLoss
+        d = tgt_emb.shape[-1]
+        return TransferSpaceLoss.apply(tgt_emb.reshape(-1, d), *features)
     ts = 0.0
     for f in features:
         ts = ts + (1 - (F.normalize(f.float(), dim=-1) * tgt_emb).sum(-1)).mean()
