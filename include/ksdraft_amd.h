@@ -355,6 +355,14 @@ int ksd_ks3_vjp_finalize(const float *partials, int64_t n_row_blocks, int64_t F,
  * Test-only export: fp16 tanh of n fp16 values through the table the VJP reads,
  * i.e. torch.tanh on an fp16 tensor (reference ksdraft/kernels/ks3_int8.py:365-366).
  */
+/*
+ * K11 — _grad_handoff (reference ksdraft/kernels/ks3_int8.py:75-84) on the device: out =
+ * fp32(fp16(t)) when every fp16(t[i]) is finite, else t, decided by *flag (int32, zeroed by
+ * the caller; set to 1 here when an element overflows fp16 or is NaN). t, out (n,) fp32;
+ * out may alias t.
+ */
+int ksd_grad_handoff(const float *t, int64_t n, int *flag, float *out, void *stream);
+
 int ksd_ks3_tanh16(const uint16_t *x, int64_t n, uint16_t *y, void *stream);
 
 /*

@@ -54,6 +54,7 @@ SIGNATURES = {
                     _P, _P, _P, _P, _P, _P, _I64, _P],
     "ksd_ks3_vjp_finalize": [_P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P],
     "ksd_ks3_tanh16": [_P, _I64, _P, _P],
+    "ksd_grad_handoff": [_P, _I64, _P, _P, _P],
     "ksd_rosa_shift_quant": [_P, _INT, _I64, _I64, _I64, _P, _P, _P, _INT,
                              _P, _P, _P, _P, _P, _P, _P],
     "ksd_rosa_shift_quant_dual": [_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P],

@@ -1159,6 +1159,32 @@ static void launch_spine_float(bool vec, dim3 grid, hipStream_t st, const void *
 }
 constexpr int kSpineFloatRows = 4 * 16;  // rows per block of ks3_spine_float_kernel
 
+// ---------------------------------------------------------------- gradient handoff
+// _grad_handoff (ks3_int8.py:75-84) without a host round trip: the fp16 conversion of a
+// gradient is used when every element of it is finite, else the fp32 gradient itself. The
+// decision is one device flag (set by any element whose fp16 conversion overflows or is
+// NaN; the caller zeroes it), read by the selecting pass; the result is written as fp32,
+// the masters' dtype, which is what autograd makes of either branch.
+__global__ __launch_bounds__(256) void handoff_flag_kernel(const float *__restrict__ t, int64_t n,
+                                                           int *__restrict__ flag) {
+  bool bad = false;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const uint16_t h = f16_bits(t[i]);
+    bad |= (h & 0x7c00u) == 0x7c00u;  // inf or NaN in fp16
+  }
+  if (__syncthreads_or(bad) && threadIdx.x == 0) atomicOr(flag, 1);
+}
+
+__global__ __launch_bounds__(256) void handoff_select_kernel(const float *__restrict__ t, int64_t n,
+                                                             const int *__restrict__ flag,
+                                                             float *__restrict__ out) {
+  const bool keep32 = *flag != 0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const float v = t[i];
+    out[i] = keep32 ? v : f16_round(v);
+  }
+}
+
 }  // namespace ksd
 
 using namespace ksd;
@@ -1397,4 +1423,16 @@ extern "C" int ksd_ks3_tanh16(const uint16_t *x, int64_t n, uint16_t *y, void *s
   hipLaunchKernelGGL(ks3_tanh16_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
                      (hipStream_t)stream, x, n, y);
   return check_launch("ks3_tanh16");
+}
+
+extern "C" int ksd_grad_handoff(const float *t, int64_t n, int *flag, float *out, void *stream) {
+  if (n < 0) return fail(KSD_EINVAL, "grad_handoff: negative size");
+  if (n == 0) return KSD_OK;
+  if (!t || !flag || !out) return fail(KSD_EINVAL, "grad_handoff: null pointer");
+  const int64_t blocks = cdiv(n, 256 * 8);
+  const unsigned grid = (unsigned)(blocks < 4096 ? blocks : 4096);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(handoff_flag_kernel, dim3(grid), dim3(256), 0, st, t, n, flag);
+  hipLaunchKernelGGL(handoff_select_kernel, dim3(grid), dim3(256), 0, st, t, n, (const int *)flag, out);
+  return check_launch("grad_handoff");
 }

@@ -94,6 +94,8 @@ def tn(a: torch.Tensor, b: torch.Tensor, chunks: int = 8) -> torch.Tensor:
     M = a.shape[0]
     if M % chunks or M < 64 * chunks:
         return a.t() @ b
+    if a.shape[1] > b.shape[1]:  # transpose the narrower operand: (b^T a)^T
+        return tn(b, a, chunks).t()
     ac = a.reshape(chunks, M // chunks, a.shape[1]).transpose(1, 2).contiguous()
     bc = b.reshape(chunks, M // chunks, b.shape[1])
     if not bc.is_contiguous():
@@ -203,7 +205,7 @@ class FusedInjection(torch.autograd.Function):
         dz = torch.addmm(g2, dzd, wa)                          # dout + dzd . wa
         dwa = tn(dzd, z2)                                      # (96, d)
         zdt, wdt = ctx.dtypes
-        cast = (lambda t: t.to(wdt))
+        cast = (lambda t: t.to(wdt).contiguous())
         return (dz.reshape(B, T, d).to(zdt), dprev0, cast(dwa[:r1]), cast(dwa[r1:]), cast(dwfu),
                 cast(dwb[:r2]), cast(dwb[r2:]), cast(dwc[:, :r2]), cast(dwc[:, r2:]),
                 None if db is None else cast(db), cast(dwiu))

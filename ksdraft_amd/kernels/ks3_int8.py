@@ -448,14 +448,22 @@ class KS3Int8Cell(nn.Module):
         return y if residual is None else residual + y
 
 
+def grad_handoff_device(t: torch.Tensor) -> torch.Tensor:
+    """The values _grad_handoff hands to autograd for an fp32 master (ks3_int8.py:75-84),
+    as fp32, without reading anything back to the host: fp16(t) when every element of it is
+    finite, else t (ksd_grad_handoff, decided on the device)."""
+    dev = _lib.require_gpu(t)
+    t = _c(t.float())
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = torch.empty_like(t)
+    _lib.call("ksd_grad_handoff", t.data_ptr(), t.numel(), flag.data_ptr(), out.data_ptr(),
+              _lib.stream_ptr(dev))
+    return out
+
+
 def _handoff_gemm(a, as_, w, ws, group):
-    """_grad_handoff(w8a8_gemm(...)) without the fp32 round trip: the GEMM writes fp16
-    (the conversion _grad_handoff applies); only if that overflows is the fp32 result
-    recomputed and returned, as _grad_handoff does (ks3_int8.py:81-84)."""
-    t16 = w8a8_gemm_out(a, as_, w, ws, group, out_dtype=FP16)
-    if bool(torch.isfinite(t16).all()):
-        return t16
-    return w8a8_gemm(a, as_, w, ws, group)
+    """grad_handoff_device(w8a8_gemm(...)): the fp32 GEMM output, handed off on the device."""
+    return grad_handoff_device(w8a8_gemm(a, as_, w, ws, group))
 
 
 class _KS3Int8Train(torch.autograd.Function):
@@ -512,5 +520,6 @@ class _KS3Int8Train(torch.autograd.Function):
 
         dx = dx.reshape(ctx.input_shape).to(grad_out.dtype)
         dres = grad_out if ctx.has_residual and ctx.needs_input_grad[7] else None
-        return (dx, ddown, dup, _grad_handoff(dcoeff), _grad_handoff(v["dscale"]),
-                _grad_handoff(v["dshift"]), None, dres)
+        # dcoeff / dscale / dshift are fp16 already: _grad_handoff would return them (or,
+        # with a non-finite entry, the same values as fp32), and autograd casts to fp32
+        return (dx, ddown, dup, dcoeff, v["dscale"], v["dshift"], None, dres)
