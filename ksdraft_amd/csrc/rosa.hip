@@ -990,8 +990,36 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
 //  k flip at p outside the best run: the largest lifted key among the members j of
 //    O_{L*+1} u (O_{L*} & {j > j*}) with j - c_j = p (a per-p table), if any.
 //  k flip inside the best run, and v flips: as in rosa_credits_kernel.
+// LDS per wave: the bucket maxima and latest-j tables (64 words each) and the per-p event
+// table in 16-bit entries, two to a word. For one p the members' keys order as their
+// (lifted length, c) pairs do (j = p + c), so an entry holds (length << 6) | c, at most
+// 12 bits. The near-run flip tables (256 words) reuse the event table's first words: the
+// k-flip pass leaves every event entry zero before they are written, and they are cleared
+// after use. 4.6 KB per wave lets 8 four-wave blocks share a CU.
 constexpr int kBpMaxT = 2048;
-constexpr int kBpWave32 = 64 + 64 + kBpMaxT + 256;  // u32 words per wave
+constexpr int kBpWave32 = 64 + 64 + kBpMaxT / 2;  // u32 words per wave
+
+__device__ __forceinline__ uint32_t evt_key16(uint32_t key, int c) {
+  return ((uint32_t)key_len(key) << 6) | (uint32_t)c;
+}
+// entry p := max(entry p, k16); the word's other entry may be updated by another lane at
+// the same time, hence the compare-and-swap
+__device__ __forceinline__ void evt_max16(uint32_t *evt, int p, uint32_t k16) {
+  uint32_t *w = evt + (p >> 1);
+  const int sh = (p & 1) * 16;
+  uint32_t old = *(volatile uint32_t *)w;
+  while (((old >> sh) & 0xffffu) < k16) {
+    const uint32_t prev = atomicCAS(w, old, (old & ~(0xffffu << sh)) | (k16 << sh));
+    if (prev == old) break;
+    old = prev;
+  }
+}
+__device__ __forceinline__ uint32_t evt_get16(const uint32_t *evt, int p) {
+  return ((const volatile uint16_t *)evt)[p];
+}
+__device__ __forceinline__ void evt_clear16(uint32_t *evt, int p) {
+  ((volatile uint16_t *)evt)[p] = 0;
+}
 
 __device__ __forceinline__ int set_maxbit(uint32_t word) {  // highest candidate of a wave set
   const uint64_t bal = __ballot(word != 0u);
@@ -1093,8 +1121,8 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   uint32_t *Nw = wsm[wave];                       // [64] best lifted key per bucket
   int *lat = (int *)(Nw + 64);                    // [64] latest j of A_i
-  uint32_t *evt = Nw + 128;                       // [kBpMaxT] best lifted key per flip p
-  uint32_t *ntab = evt + kBpMaxT;                 // [256] near-flip tables
+  uint32_t *evt = Nw + 128;                       // [kBpMaxT] 16-bit event entries per flip p
+  uint32_t *ntab = evt;                           // [256] near-flip tables (aliasing evt)
   const int64_t stream = blockIdx.x;
   const int64_t b = stream / S, s = stream % S;
   for (int i = threadIdx.x; i < 64; i += 256) {
@@ -1102,7 +1130,7 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
     kw[i] = i < W ? kb[stream * W + i] : 0u;
     vw[i] = i < W ? vb[stream * W + i] : 0u;
   }
-  for (int i = lane; i < 64 + kBpMaxT; i += 64) Nw[i < 64 ? i : 64 + i] = 0u;  // Nw and evt
+  for (int i = lane; i < 64 + kBpMaxT / 2; i += 64) Nw[i < 64 ? i : 64 + i] = 0u;  // Nw and evt
   __syncthreads();
   // this lane's k words: word w and the two below it (zeros before position 0)
   const uint32_t k0 = kw[lane], k1 = lane >= 1 ? kw[lane - 1] : 0u, k2 = lane >= 2 ? kw[lane - 2] : 0u;
@@ -1236,7 +1264,7 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
           const uint32_t key = ext_key(c, e, min(j + 1, lmax), j);
           if (c <= imax) atomicMax(Nw + c, key);
           const int p = j - c;
-          if (ev && key > best && !(p >= trunc_lo && p <= trunc_hi)) atomicMax(evt + p, key);
+          if (ev && key > best && !(p >= trunc_lo && p <= trunc_hi)) evt_max16(evt, p, evt_key16(key, c));
         }
       }
     };
@@ -1334,8 +1362,8 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
           const int e = clz64(xx << (c + 1));
           const uint32_t key = ext_key(c, e, min(j + 1, lmax), j);
           const int p = j - c;
-          if (!(p >= trunc_lo && p <= trunc_hi) && evt[p] == key) {
-            evt[p] = 0u;
+          if (!(p >= trunc_lo && p <= trunc_hi) && evt_get16(evt, p) == evt_key16(key, c)) {
+            evt_clear16(evt, p);
             const float s2 = sign_of(key, vw);
             if (s2 != sgn) atomicAdd(ck + p, (s2 - sgn) * g);
           }
@@ -1347,6 +1375,10 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
     if (jstar >= 0) {
       const uint32_t farbest = farL >= 0 ? mkkey(farL, set_maxbit(farw)) : 0u;
       near_flips_tables(lane, t, lmax, jstar, trunc_lo, trunc_hi, farbest, qwin, kw, vw, sgn, g, ck, ntab);
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ntab[64 * k + lane] = 0u;  // the event entries they covered
+      __builtin_amdgcn_wave_barrier();
     }
   }
   if (lane == 0) gps[wave] = gsum;
