@@ -499,6 +499,20 @@ int ksd_injection_update_backward(const float *zs, const float *wc, const float 
                                   const float *bias, const float *grad_out, int64_t M, int64_t d,
                                   float *dpre, float *du, void *stream);
 
+/*
+ * nn.LayerNorm's backward (reference ksdraft/model/block.py:27-41) fused with the gradient
+ * of the residual branch that reads the same input (the block's x + mixer(ln(x)),
+ * block.py:39-41): dx = LN_backward(dy) + dres (dres may be NULL), and per-block partial
+ * sums of dweight = sum dy xhat and dbias = sum dy, partials (n_blocks, 2, d) fp32 with
+ * n_blocks from ksd_layernorm_backward_blocks; their sum over the first axis is (dw, db).
+ * x, dy, dres, dx (M, d) fp32 with d a multiple of 256 (<= 2048), 16-byte aligned rows;
+ * mean, rstd (M,) fp32 from the forward; weight (d,) fp32.
+ */
+int ksd_layernorm_backward_blocks(int64_t M, int64_t *n_blocks);
+int ksd_layernorm_backward(const float *x, const float *dy, const float *dres, const float *mean,
+                           const float *rstd, const float *weight, int64_t M, int64_t d,
+                           float *dx, float *partials, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -64,6 +64,8 @@ SIGNATURES = {
     "ksd_transfer_cos": [_P, _P, _I64, _I64, _P, _P, _P],
     "ksd_transfer_grad": [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _INT, _P],
     "ksd_injection_update": [_P, _P, _P, _P, _P, _I64, _I64, _P, _P],
+    "ksd_layernorm_backward_blocks": [_I64, _P],
+    "ksd_layernorm_backward": [_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P],
     "ksd_injection_update_backward": [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P],
     "ksd_rosa_match": [_P, _P, _P, _I64, _I64, _INT, _P, _P, _P],
     "ksd_rosa_hard": [_P, _P, _I64, _I64, _I64, _P, _INT, _P],

@@ -11,6 +11,9 @@
 //       evaluated from the (M, 96) low-rank operand and the (d, 96) weights in one pass
 //       over z (no pre / u / sigmoid tensors), and its backward's elementwise part
 //       (dpre = dout u s (1 - s), du = dout s, the same pre and u recomputed).
+//   ln_bwd_kernel
+//       nn.LayerNorm's backward fused with the residual branch's gradient (the block's
+//       x + mixer(ln(x)), reference ksdraft/model/block.py:39-41).
 // All arithmetic is fp32 (the float surfaces of the step); the sums run in this file's
 // order, so results are within fp32 rounding of torch's, not bit-equal.
 #include "ksd_common.h"
@@ -160,6 +163,100 @@ __global__ __launch_bounds__(256) void inj_up_kernel(
   }
 }
 
+// ---------------------------------------------------------------- layer norm backward
+// nn.LayerNorm's backward (reference ksdraft/model/block.py:27-41) for rows of x (M, d)
+// with the per-row mean and rstd of the forward, fused with the gradient of the residual
+// branch that reads the same x (the block's x + mixer(ln(x))):
+//   xhat = (x - mean) rstd,  g = dy w,
+//   dx   = rstd (g - xhat mean(g xhat) - mean(g)) + dres,
+// and the block's share of dw = sum dy xhat, db = sum dy over its rows, written as
+// partials (n_blocks, 2, d) that the caller adds (the four waves' sums added in wave
+// order). A wave walks kLnBwdRows / 4 rows; a lane owns NQ groups of 4 columns (d = 256 NQ,
+// 16-byte access), keeping its columns' dw / db sums in registers.
+constexpr int kLnBwdRows = 16;  // rows per block
+
+template <int NQ, bool RES>
+__global__ __launch_bounds__(256) void ln_bwd_kernel(
+    const float *__restrict__ x, const float *__restrict__ dy, const float *__restrict__ dres,
+    const float *__restrict__ mean, const float *__restrict__ rstd, const float *__restrict__ w,
+    int M, float *__restrict__ dx, float *__restrict__ part) {
+  constexpr int d = 256 * NQ, NV = 4 * NQ;
+  __shared__ __attribute__((aligned(16))) float red[2][d];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  float aw[NV], ab[NV], wv[NV];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const float4 v = *(const float4 *)(w + q * 256 + lane * 4);
+    wv[4 * q] = v.x; wv[4 * q + 1] = v.y; wv[4 * q + 2] = v.z; wv[4 * q + 3] = v.w;
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    aw[i] = 0.0f;
+    ab[i] = 0.0f;
+  }
+  constexpr float inv_d = 1.0f / (float)d;
+  const int r_end = min((int)(blockIdx.x + 1) * kLnBwdRows, M);
+  for (int r = (int)blockIdx.x * kLnBwdRows + wave; r < r_end; r += 4) {  // wave-uniform
+    const int64_t o = (int64_t)r * d + lane * 4;
+    const float mu = mean[r], rs = rstd[r];
+    float xh[NV], gg[NV];
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const float4 a = *(const float4 *)(x + o + q * 256), b = *(const float4 *)(dy + o + q * 256);
+      const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = 4 * q + k;
+        xh[i] = (av[k] - mu) * rs;
+        gg[i] = bv[k] * wv[i];
+        s1 += gg[i] * xh[i];
+        s2 += gg[i];
+        aw[i] += bv[k] * xh[i];
+        ab[i] += bv[k];
+      }
+    }
+    s1 = wave_sum(s1) * inv_d;
+    s2 = wave_sum(s2) * inv_d;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      float4 rv = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (RES) rv = *(const float4 *)(dres + o + q * 256);
+      const float rr[4] = {rv.x, rv.y, rv.z, rv.w};
+      float out[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = 4 * q + k;
+        out[k] = rs * (gg[i] - xh[i] * s1 - s2) + rr[k];
+      }
+      *(float4 *)(dx + o + q * 256) = make_float4(out[0], out[1], out[2], out[3]);
+    }
+  }
+  // the block's column sums, the four waves added in order
+#pragma unroll 1
+  for (int wv_ = 0; wv_ < 4; ++wv_) {
+    if (wave == wv_) {
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        float4 *p0 = (float4 *)(red[0] + q * 256 + lane * 4), *p1 = (float4 *)(red[1] + q * 256 + lane * 4);
+        float4 a = make_float4(aw[4 * q], aw[4 * q + 1], aw[4 * q + 2], aw[4 * q + 3]);
+        float4 b = make_float4(ab[4 * q], ab[4 * q + 1], ab[4 * q + 2], ab[4 * q + 3]);
+        if (wv_ > 0) {
+          const float4 a0 = *p0, b0 = *p1;
+          a = make_float4(a0.x + a.x, a0.y + a.y, a0.z + a.z, a0.w + a.w);
+          b = make_float4(b0.x + b.x, b0.y + b.y, b0.z + b.z, b0.w + b.w);
+        }
+        *p0 = a;
+        *p1 = b;
+      }
+    }
+    __syncthreads();
+  }
+  for (int idx = threadIdx.x; idx < 2 * d; idx += 256)
+    part[(int64_t)blockIdx.x * 2 * d + idx] = red[idx / d][idx % d];
+}
+
 }  // namespace ksd
 
 using namespace ksd;
@@ -235,4 +332,47 @@ extern "C" int ksd_injection_update_backward(const float *zs, const float *wc, c
   hipLaunchKernelGGL(inj_up_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, zs, wc, wiu, bias,
                      (const float *)nullptr, grad_out, (int)M, (int)d, (float *)nullptr, dpre, du);
   return check_launch("injection_update_backward");
+}
+
+
+extern "C" int ksd_layernorm_backward_blocks(int64_t M, int64_t *n_blocks) {
+  if (!n_blocks || M < 0) return fail(KSD_EINVAL, "layernorm_backward_blocks: bad argument");
+  *n_blocks = cdiv(M, kLnBwdRows);
+  return KSD_OK;
+}
+
+extern "C" int ksd_layernorm_backward(const float *x, const float *dy, const float *dres,
+                                      const float *mean, const float *rstd, const float *weight,
+                                      int64_t M, int64_t d, float *dx, float *partials,
+                                      void *stream) {
+  if (M < 0 || d < 0) return fail(KSD_EINVAL, "layernorm_backward: negative shape");
+  if (M == 0 || d == 0) return KSD_OK;
+  if (d % 256 || d > 2048)
+    return fail(KSD_EINVAL, "layernorm_backward: d must be a multiple of 256, at most 2048");
+  if (!x || !dy || !mean || !rstd || !weight || !dx || !partials)
+    return fail(KSD_EINVAL, "layernorm_backward: null pointer");
+  if (((uintptr_t)x | (uintptr_t)dy | (uintptr_t)dres | (uintptr_t)weight | (uintptr_t)dx) % 16)
+    return fail(KSD_EINVAL, "layernorm_backward: rows must be 16-byte aligned");
+  if (M > 0x7fffffffLL - kLnBwdRows) return fail(KSD_EINVAL, "layernorm_backward: too large");
+  const dim3 grid((unsigned)cdiv(M, kLnBwdRows));
+  hipStream_t st = (hipStream_t)stream;
+#define KSD_LNB(NQ)                                                                                 \
+  if (dres)                                                                                        \
+    hipLaunchKernelGGL((ln_bwd_kernel<NQ, true>), grid, dim3(256), 0, st, x, dy, dres, mean, rstd, \
+                       weight, (int)M, dx, partials);                                              \
+  else                                                                                             \
+    hipLaunchKernelGGL((ln_bwd_kernel<NQ, false>), grid, dim3(256), 0, st, x, dy, dres, mean, rstd,\
+                       weight, (int)M, dx, partials);
+  switch (d / 256) {
+    case 1: KSD_LNB(1) break;
+    case 2: KSD_LNB(2) break;
+    case 3: KSD_LNB(3) break;
+    case 4: KSD_LNB(4) break;
+    case 5: KSD_LNB(5) break;
+    case 6: KSD_LNB(6) break;
+    case 7: KSD_LNB(7) break;
+    default: KSD_LNB(8) break;
+  }
+#undef KSD_LNB
+  return check_launch("layernorm_backward");
 }

@@ -4,6 +4,8 @@
                       (reference ksdraft/train/__init__.py:79-85) with its gradient
   FusedInjection      the float DSpine adjacent injection (reference
                       ksdraft/model/spine.py:38-68), forward and backward
+  ResidualLayerNorm   nn.LayerNorm whose backward also takes the gradient of the residual
+                      branch reading the same input (reference ksdraft/model/block.py:39-41)
 
 Both are fp32 and agree with the torch composition of the reference to fp32 rounding
 (their sums run in another order); the INT8 surfaces of the step are elsewhere. The
@@ -13,6 +15,8 @@ weight gradients of the low-rank maps reduce over all M tokens into a (rank, d) 
 """
 
 from __future__ import annotations
+
+import ctypes
 
 import torch
 
@@ -209,3 +213,47 @@ class FusedInjection(torch.autograd.Function):
         return (dz.reshape(B, T, d).to(zdt), dprev0, cast(dwa[:r1]), cast(dwa[r1:]), cast(dwfu),
                 cast(dwb[:r2]), cast(dwb[r2:]), cast(dwc[:, :r2]), cast(dwc[:, r2:]),
                 None if db is None else cast(db), cast(dwiu))
+
+
+# ---------------------------------------------------------------- layer norm
+def layernorm_backward(x2, dy2, dres2, mean, rstd, weight):
+    """(dx, dweight, dbias) of nn.LayerNorm for fp32 rows (M, d), plus dres2 (or None)."""
+    dev = _lib.require_gpu(x2, dy2, mean, rstd, weight)
+    M, d = x2.shape
+    nb = ctypes.c_int64(0)
+    _lib.call("ksd_layernorm_backward_blocks", M, ctypes.byref(nb))
+    dx = torch.empty_like(x2)
+    part = torch.empty((max(nb.value, 1), 2, d), dtype=torch.float32, device=dev)
+    _lib.call("ksd_layernorm_backward", x2.data_ptr(), dy2.data_ptr(), _lib.ptr(dres2),
+              mean.data_ptr(), rstd.data_ptr(), weight.data_ptr(), M, d, dx.data_ptr(),
+              part.data_ptr(), _lib.stream_ptr(dev))
+    dwb = part[:nb.value].sum(0)
+    return dx, dwb[0], dwb[1]
+
+
+class ResidualLayerNorm(torch.autograd.Function):
+    """(layer_norm(x), x): nn.LayerNorm (block.py:27-41) and the residual branch's copy of
+    its input as a second output, so that the backward receives both gradients and forms
+    dx = LN_backward(dy) + dres in one pass (ksd_layernorm_backward) instead of autograd
+    adding them. x (..., d) fp32 with d % 256 == 0; the forward is torch's."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, eps):
+        d = x.shape[-1]
+        y, mean, rstd = torch.native_layer_norm(x, (d,), weight, bias, eps)
+        ctx.save_for_backward(x, mean, rstd, weight)
+        ctx.has_bias = bias is not None
+        return y, x.view_as(x)
+
+    @staticmethod
+    def backward(ctx, dy, dres):
+        x, mean, rstd, weight = ctx.saved_tensors
+        d = x.shape[-1]
+        x2 = _f32c(x.reshape(-1, d))
+        M = x2.shape[0]
+        dy2 = torch.zeros_like(x2) if dy is None else _f32c(dy.reshape(M, d))
+        dr2 = None if dres is None else _f32c(dres.reshape(M, d))
+        dx, dw, db = layernorm_backward(x2, dy2, dr2, _f32c(mean.reshape(M)),
+                                        _f32c(rstd.reshape(M)), _f32c(weight))
+        return (dx.reshape(x.shape).to(x.dtype), dw.to(weight.dtype),
+                db.to(weight.dtype) if ctx.has_bias else None, None)

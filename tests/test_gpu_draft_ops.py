@@ -99,3 +99,33 @@ def test_fused_injection_matches_composition(with_prev, B, T, d):
         close(v1, v2, "dprev")
     for n in g2:
         close(g1[n], g2[n], n)
+
+
+@pytest.mark.parametrize("d,M", [(1536, 300), (256, 17), (512, 64)])
+@pytest.mark.parametrize("with_res", [True, False])
+def test_residual_layer_norm_matches_torch(d, M, with_res):
+    """ResidualLayerNorm: the forward is torch's; dx = LN_backward(dy) + dres, dweight and
+    dbias against torch's LayerNorm + residual add (fp32, rtol 1e-5)."""
+    from ksdraft_amd.kernels.draft import ResidualLayerNorm
+    g = torch.Generator().manual_seed(d + M)
+    x0 = torch.randn(2, M, d, generator=g) * 2 + 0.5
+    w0 = torch.randn(d, generator=g) * 0.3 + 1
+    b0 = torch.randn(d, generator=g) * 0.1
+    gy = torch.randn(2, M, d, generator=g)
+    gr = torch.randn(2, M, d, generator=g)
+    outs = []
+    for fused in (True, False):
+        x = x0.to(DEV).requires_grad_(True)
+        w = w0.to(DEV).requires_grad_(True)
+        b = b0.to(DEV).requires_grad_(True)
+        if fused:
+            y, res = ResidualLayerNorm.apply(x, w, b, 1e-5)
+        else:
+            y, res = F.layer_norm(x, (d,), w, b, 1e-5), x
+        grads = [gy.to(DEV)] + ([gr.to(DEV)] if with_res else [])
+        torch.autograd.backward([y, res] if with_res else [y], grads)
+        outs.append((y.detach(), x.grad, w.grad, b.grad))
+    (y1, dx1, dw1, db1), (y2, dx2, dw2, db2) = outs
+    assert torch.equal(y1, y2)
+    for a, b_, n in ((dx1, dx2, "dx"), (dw1, dw2, "dw"), (db1, db2, "db")):
+        torch.testing.assert_close(a, b_, rtol=1e-5, atol=1e-5 * b_.abs().max().item(), msg=n)
