@@ -134,23 +134,26 @@ __global__ __launch_bounds__(256) void inj_up_kernel(
   const float bc = bias ? bias[c] : 0.0f;
   for (int i = 0; i < nr; ++i) {
     const float4 *sr = (const float4 *)(srow + i * kInjRank);
-    float pre = bc, u = 0.0f;
+    // four independent partial sums per float4 lane slot: short dependency chains
+    float pa[4] = {0.f, 0.f, 0.f, 0.f}, ua[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k4 = 0; k4 < 16; ++k4) {
       const float4 v = sr[k4];
-      pre = fmaf(v.x, w[4 * k4], pre);
-      pre = fmaf(v.y, w[4 * k4 + 1], pre);
-      pre = fmaf(v.z, w[4 * k4 + 2], pre);
-      pre = fmaf(v.w, w[4 * k4 + 3], pre);
+      pa[0] = fmaf(v.x, w[4 * k4], pa[0]);
+      pa[1] = fmaf(v.y, w[4 * k4 + 1], pa[1]);
+      pa[2] = fmaf(v.z, w[4 * k4 + 2], pa[2]);
+      pa[3] = fmaf(v.w, w[4 * k4 + 3], pa[3]);
     }
 #pragma unroll
     for (int k4 = 16; k4 < 24; ++k4) {
       const float4 v = sr[k4];
-      u = fmaf(v.x, w[4 * k4], u);
-      u = fmaf(v.y, w[4 * k4 + 1], u);
-      u = fmaf(v.z, w[4 * k4 + 2], u);
-      u = fmaf(v.w, w[4 * k4 + 3], u);
+      ua[0] = fmaf(v.x, w[4 * k4], ua[0]);
+      ua[1] = fmaf(v.y, w[4 * k4 + 1], ua[1]);
+      ua[2] = fmaf(v.z, w[4 * k4 + 2], ua[2]);
+      ua[3] = fmaf(v.w, w[4 * k4 + 3], ua[3]);
     }
+    const float pre = bc + ((pa[0] + pa[1]) + (pa[2] + pa[3]));
+    const float u = (ua[0] + ua[1]) + (ua[2] + ua[3]);
     const float s = sigmoid_f(pre);
     const int64_t o = (int64_t)(r0 + i) * d + c;
     if constexpr (!BWD) {

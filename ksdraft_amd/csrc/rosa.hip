@@ -1387,27 +1387,49 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
 }
 
 // d loss / d payload = sum over (b, t) of grad * sign (rosa_credit_gpu.py:110), and the
-// Bernoulli map of the credits to projection space (:99-111): one thread per (b, t, s).
+// Bernoulli map of the credits to projection space (:99-111),
+//   g = (credit (1 - 2 bit))_DT * (sigmoid(x) (1 - sigmoid(x)))_DT,  bit = x > 0,
+// each factor rounded to x's dtype as the reference's tensor ops are. The credits are laid
+// out (b, s, m, t) and the projections (b, t, s): a block takes a 64 (t) x 64 (s) tile,
+// reads the three credit tiles along t into LDS (pitch 65) and writes along s.
+constexpr int kCgTile = 64;
+
 template <int DT>
 __global__ void __launch_bounds__(256) rosa_credit_grad_kernel(
     const float *__restrict__ cred, const void *__restrict__ q, const void *__restrict__ k,
     const void *__restrict__ v, int64_t B, int64_t T, int64_t S, void *__restrict__ gq,
     void *__restrict__ gk, void *__restrict__ gv) {
   using E = Elem<DT>;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (b, t, s) flattened
-  if (idx >= B * T * S) return;
-  const int64_t s = idx % S, t = (idx / S) % T, b = idx / (S * T);
-  const float *c = cred + (b * S + s) * 3 * T + t;
+  __shared__ float tile[3][kCgTile][kCgTile + 1];  // [m][s][t]
+  const int64_t s0 = (int64_t)blockIdx.x * kCgTile, t0 = (int64_t)blockIdx.y * kCgTile, b = blockIdx.z;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // load: wave w takes streams s0 + w, w + 4, ...; a lane one position t0 + lane
+  for (int sl = wave; sl < kCgTile; sl += 4) {
+    const int64_t s = s0 + sl, t = t0 + lane;
+    const bool ok = s < S && t < T;
+    const float *c = cred + (b * S + (ok ? s : 0)) * 3 * T + (ok ? t : 0);
+#pragma unroll
+    for (int m = 0; m < 3; ++m) tile[m][sl][lane] = ok ? c[m * T] : 0.0f;
+  }
+  __syncthreads();
   const void *pre[3] = {q, k, v};
   void *out[3] = {gq, gk, gv};
+  // compute: a lane takes stream s0 + lane, wave w positions t0 + w, w + 4, ...
+  const int64_t s = s0 + lane;
+  if (s >= S) return;  // after the block's only barrier
+  for (int tl = wave; tl < kCgTile; tl += 4) {
+    const int64_t t = t0 + tl;
+    if (t >= T) break;
+    const int64_t idx = (b * T + t) * S + s;
 #pragma unroll
-  for (int m = 0; m < 3; ++m) {
-    const float x = E::load((const typename E::T *)pre[m] + idx);
-    const float bit = x > 0.0f ? 1.0f : 0.0f;
-    const float delta = round_to_dt<DT>(c[m * T] * (1.0f - 2.0f * bit));
-    const float sg = 1.0f / (1.0f + expf(-x));
-    const float bern = round_to_dt<DT>(sg * (1.0f - sg));
-    store_out<DT>(out[m], idx, delta * bern);
+    for (int m = 0; m < 3; ++m) {
+      const float x = E::load((const typename E::T *)pre[m] + idx);
+      const float bit = x > 0.0f ? 1.0f : 0.0f;
+      const float delta = round_to_dt<DT>(tile[m][lane][tl] * (1.0f - 2.0f * bit));
+      const float sg = 1.0f / (1.0f + expf(-x));
+      const float bern = round_to_dt<DT>(sg * (1.0f - sg));
+      store_out<DT>(out[m], idx, delta * bern);
+    }
   }
 }
 
@@ -1461,9 +1483,9 @@ extern "C" int ksd_rosa_credit_grads(const float *credits, const void *q, const 
   if (B == 0 || T == 0 || S == 0) return KSD_OK;
   if (!credits || !q || !k || !v || !payload_partial || !gq || !gk || !gv || !gpayload)
     return fail(KSD_EINVAL, "rosa_credit_grads: null pointer");
-  const int64_t n = B * T * S;
+  if (B > 65535 || cdiv(T, kCgTile) > 65535) return fail(KSD_EINVAL, "rosa_credit_grads: too large");
   hipStream_t st = (hipStream_t)stream;
-  dim3 grid((unsigned)cdiv(n, 256));
+  dim3 grid((unsigned)cdiv(S, kCgTile), (unsigned)cdiv(T, kCgTile), (unsigned)B);
   switch (dtype) {
     case KSD_F32: hipLaunchKernelGGL(rosa_credit_grad_kernel<KSD_F32>, grid, dim3(256), 0, st, credits, q, k, v, B, T, S, gq, gk, gv); break;
     case KSD_BF16: hipLaunchKernelGGL(rosa_credit_grad_kernel<KSD_BF16>, grid, dim3(256), 0, st, credits, q, k, v, B, T, S, gq, gk, gv); break;
