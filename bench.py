@@ -340,8 +340,15 @@ def rosa_kernel_times(dev, reps):
                   cred.data_ptr(), part.data_ptr(), _lib.stream_ptr(dev))
 
     BTd, BTS = Bq * T * d, Bq * T * S
+    # the training form on fp32 x (config 5's stream dtype): both layouts of q/k/v_in, and
+    # the shift's backward from three fp32 input gradients
+    x32 = x.float()
+    gin = [torch.randn(Bq, T, d, generator=g).to(dev) for _ in range(3)]
     stages = {
         "rosa_shift_quant": (lambda: R.shift_quantize(x, sig, sig, sig), 2 * BTd + 3 * (BTd + 2 * BTd // 128), None),
+        "rosa_shift_quant_dual_f32": (lambda: R.shift_quantize_dual(x32, sig, sig, sig),
+                                      4 * BTd + 6 * (BTd + 2 * BTd // 128), None),
+        "rosa_shift_backward_f32": (lambda: R.shift_backward(x32, *gin, sig, sig, sig), 20 * BTd, None),
         "rosa_pack_bits_x3": (lambda: [R.pack_bits(t) for t in (q, k, v)], 3 * (4 * BTS + BTS // 8), None),
         "rosa_match": (lambda: R.match_packed(*flat, T, want_j=True), None, pairs),
         "rosa_hard_out": (lambda: R.hard_out(sign.reshape(Bq, S, T), payload), BTS + 4 * BTS, None),
