@@ -327,21 +327,25 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_nt_kernel(
 //     DMA goes out as one scalar-based instruction per 1 KB (64-bit SGPR base + 32-bit
 //     per-lane offset), and the LDS chunk swizzle XORs with (row >> 1) & 7: 16 consecutive
 //     rows of one chunk column fill a 256-byte bank window (64 banks, no conflicts).
+//   * Every wave issues the same five DMA instructions per step: two 1 KB chunks of A,
+//     two of W and one half-wave load of 32 scale rows.
 //   * The step body is instantiated once per ring slot, so every LDS offset is an
-//     immediate. Per wave and step: one barrier, the DMA of step q+3, the fragment reads
-//     of step q, then the VALU epilogue of step q-1 (its partials finished long ago) while
-//     those reads are in flight, then both tiles' MFMA chains and their fp16 scale outer
-//     products.
+//     immediate. Per wave and step: one barrier; the fp16 scale outer products of step
+//     q-1 (two MFMAs, issued first so their results are ready when the epilogue needs
+//     them); the DMA of step q+3; the fragment reads of step q; then step q's eight int8
+//     MFMAs, each followed by 8 VALU of step q-1's epilogue (sched_group_barrier), so the
+//     matrix pipe and the VALU run side by side. The partials ping-pong by step parity.
 //   * The int32 chains start from the bits of 1.5*2^23 (12582912.0f) instead of zero:
 //     |P_g| < 2^22 keeps C + P_g in one binade with unit ulp, so the partial's bits read as
 //     an fp32 are exactly 12582912 + P_g and one exact v_sub_f32 gives float(P_g) (the
 //     half-rate v_cvt_f32_i32 is not needed). The contract is unchanged:
 //     acc = fmaf(float(P_g), sa*sw, acc).
 //   * A finished tile is stored at once (32 buffer stores per lane) through descriptors
-//     that drop rows past M and columns past N.
+//     that drop rows past M and columns past N. Unit ends and DMA re-bases are marked
+//     unlikely, so the hot loop stays compact.
 //   * Waits: a wave's vector-memory operations complete in issue order, so "at most n
 //     outstanding" (n = the instructions issued after step q's DMA) proves that DMA done;
-//     stores issued after it only make such a wait stricter.
+//     the three steps after a unit end count its 32 stores into n.
 namespace g128 {
 constexpr uint32_t SLOT = BM * BK;
 // raw buffer resources: offsets at or past num_records drop stores
@@ -370,6 +374,9 @@ __device__ __forceinline__ void fenced_barrier() {
 // s_waitcnt vmcnt(n) for the counts this kernel uses
 __device__ __forceinline__ void wait_vm(int n) {
   switch (n) {
+    case 42: asm volatile("s_waitcnt vmcnt(42)" ::: "memory"); break;
+    case 37: asm volatile("s_waitcnt vmcnt(37)" ::: "memory"); break;
+    case 32: asm volatile("s_waitcnt vmcnt(32)" ::: "memory"); break;
     case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
     case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
     case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
@@ -411,11 +418,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
   __shared__ __attribute__((aligned(16))) uint32_t sS[NSLOT][256];
   constexpr int DEPTH = NSLOT - 1;
   constexpr int ES = OUT == KSD_F32 ? 4 : 2;
+  constexpr int NW = 5;  // DMA instructions per wave and step: 4 x 1 KB codes + 1 scale
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3, half = lane >> 5, l32 = lane & 31;
-  const int G = K / BK, KT = K / BK;
+  const int KT = K / BK, G = KT;
   const int nunits = ntiles * splits;
 
   int u_begin, u_end;
@@ -430,26 +438,30 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
     return part_lo(pp + 1, KT, splits) - part_lo(pp, KT, splits);
   };
   int T = 0;
-  for (int u = u_begin; u < u_end; ++u) T += unit_len(u);
+  if (splits == 1) T = (u_end - u_begin) * KT;
+  else
+    for (int u = u_begin; u < u_end; ++u) T += unit_len(u);
   if (T == 0) return;
 
+  // DMA: each wave fills 16 rows of the A tile and 16 of the W tile (two 1 KB chunks of
+  // each), and 32 rows of scales (A rows for waves 0-3, W rows for waves 4-7; lanes
+  // 32-63 idle), so every wave issues the same 5 instructions per step.
   const int drow0 = wave * 16 + (lane >> 3), drow1 = drow0 + 8;
   const int dch0 = ((lane & 7) ^ ((drow0 >> 1) & 7)) << 4;
   const int dch1 = ((lane & 7) ^ ((drow1 >> 1) & 7)) << 4;
-  const bool s_load = wave < 4, s_isA = wave < 2;
-  const int NW = s_load ? 5 : 4;
-  const int srow = (wave & 1) * 64 + lane;
+  const bool s_isA = wave < 4;
+  const int srow = (wave & 3) * 32 + l32;
   const uint32_t ldsA = lds_addr(&sA[0][0]) + wave * 2048;
   const uint32_t ldsW = lds_addr(&sW[0][0]) + wave * 2048;
-  const uint32_t ldsS = lds_addr(&sS[0][0]) + ((s_isA ? 0 : 128) + (wave & 1) * 64) * 4;
+  const uint32_t ldsS = lds_addr(&sS[0][0]) + wave * 128;
   const uint16_t *const SB = s_isA ? AS : WS;
   const int8_t *ba, *bw;
   const uint16_t *bs;
   uint32_t oa0, oa1, ow0, ow1, os;
-  int cur_u = u_begin, cur_kt = 0, cur_len = __builtin_amdgcn_readfirstlane(unit_len(u_begin));
+  int is_u = u_begin, is_k = 0, is_len = __builtin_amdgcn_readfirstlane(unit_len(u_begin));
   auto rebase = [&]() __attribute__((always_inline)) {
     // every value here is wave-uniform; readfirstlane keeps the DMA bases in SGPRs
-    const int cu_ = __builtin_amdgcn_readfirstlane(cur_u);
+    const int cu_ = __builtin_amdgcn_readfirstlane(is_u);
     const int t = cu_ / splits, k0 = __builtin_amdgcn_readfirstlane(part_lo(cu_ % splits, KT, splits));
     const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
     ba = A + (int64_t)m0 * K + (int64_t)k0 * BK;
@@ -469,14 +481,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
     dma16(ba, oa1, ldsA + so + 1024);
     dma16(bw, ow0, ldsW + so);
     dma16(bw, ow1, ldsW + so + 1024);
-    if (s_load) dma2(bs, os, ldsS + slot * 1024);
+    if (half == 0) dma2(bs, os, ldsS + slot * 1024);
     ba += BK;
     bw += BK;
     bs += 1;
-    if (++cur_kt == cur_len) {
-      cur_kt = 0;
-      if (++cur_u < u_end) {
-        cur_len = __builtin_amdgcn_readfirstlane(unit_len(cur_u));
+    if (__builtin_expect(++is_k == is_len, 0)) {
+      is_k = 0;
+      if (++is_u < u_end) {
+        is_len = __builtin_amdgcn_readfirstlane(unit_len(is_u));
         rebase();
       }
     }
@@ -497,17 +509,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
   const v16i kSeed = (v16i){kSeedBits, kSeedBits, kSeedBits, kSeedBits, kSeedBits, kSeedBits,
                             kSeedBits, kSeedBits, kSeedBits, kSeedBits, kSeedBits, kSeedBits,
                             kSeedBits, kSeedBits, kSeedBits, kSeedBits};
-
-  // keep the seed in VGPRs (the MFMA reads srcC from VGPRs; left to itself the compiler
-  // keeps the constant in SGPRs and copies it before every chain)
+  // keep the seed in VGPRs (the MFMA reads srcC from VGPRs)
   v16i seedv = kSeed;
   asm volatile("" : "+v"(seedv));
   v16f acc0 = (v16f){}, acc1 = (v16f){};
-  // the previous step's partials and scale products: their epilogue runs one step later,
-  // when the MFMAs that made them have long finished (S* = 0: nothing to add)
-  v16i P0 = seedv, P1 = seedv;
-  v16f S0 = (v16f){}, S1 = (v16f){};
-  int kt = 0, uk = u_begin, klen = unit_len(u_begin);
+  int kt = 0, uk = u_begin, klen = is_len;
 
   auto store_tile = [&](int u) __attribute__((always_inline)) {
     const int t = u / splits;
@@ -567,37 +573,69 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
       }
     }
   };
-  auto epilogue = [&]() __attribute__((always_inline)) {
-    const v16f f0 = __builtin_bit_cast(v16f, P0), f1 = __builtin_bit_cast(v16f, P1);
+  // acc += (P - seed) * S per element: the ordered contract for one group, P the seeded
+  // int32 partials read as fp32, S the scale products
+  auto epilogue = [&](const v16i &Q0, const v16i &Q1, const v16f &T0, const v16f &T1) __attribute__((always_inline)) {
+    const v16f f0 = __builtin_bit_cast(v16f, Q0), f1 = __builtin_bit_cast(v16f, Q1);
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      acc0[e] = fmaf(f0[e] - kSeedF, S0[e], acc0[e]);
-      acc1[e] = fmaf(f1[e] - kSeedF, S1[e], acc1[e]);
+      acc0[e] = fmaf(f0[e] - kSeedF, T0[e], acc0[e]);
+      acc1[e] = fmaf(f1[e] - kSeedF, T1[e], acc1[e]);
     }
+  };
+  // sa (x) sw of a 32x32 tile from one f16 MFMA (k slot 0 only: lanes 32-63 hold zero);
+  // the products of two fp16 values are exact in fp32
+  auto scale_tile = [&](uint32_t sa, uint32_t sw) __attribute__((always_inline)) {
+    const v2u a2 = {sa, 0u}, w2 = {sw, 0u};
+    return __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, a2), __builtin_bit_cast(v4h, w2), (v16f){}, 0, 0, 0);
   };
 
   const int pre = min(DEPTH, T);
   for (int i = 0; i < pre; ++i) dma_step((uint32_t)i);
 
+  // The epilogue of step q runs in step q+1, beside that step's MFMAs: partials ping-pong
+  // by step parity, the scale bits wait in registers, and their products are formed at the
+  // start of step q+1. Zero scales make the deferred epilogue a no-op (first step of a unit).
+  v16i PA0 = seedv, PA1 = seedv, PB0 = seedv, PB1 = seedv;
+  uint32_t qa0 = 0, qa1 = 0, qw = 0;
+  int fresh = 0;  // steps left whose wait may leave the last unit's stores outstanding
+
   auto step = [&](auto slot_c, int q) __attribute__((always_inline)) {
     constexpr int S = decltype(slot_c)::value;
     constexpr uint32_t so = S * SLOT, ss = S * 1024;
-    const int after = min(T - 1 - q, DEPTH - 1);
-    wait_vm(after == 2 ? 2 * NW : (after == 1 ? NW : 0));
+    // This wave's DMA of step q has landed once at most the DMA of the (up to two) later
+    // steps is outstanding. After a unit's 32 stores (issued after the DMA of the next three steps), the waits
+    // of those three steps leave the stores outstanding: vector memory operations
+    // complete in issue order, so "at most n + 32 outstanding" still proves this step's
+    // DMA done.
+    if (__builtin_expect(fresh == 0, 1)) {
+      if (__builtin_expect(q + 2 < T, 1)) wait_vm(2 * NW);
+      else if (q + 1 < T) wait_vm(NW);
+      else wait_vm(0);
+    } else {
+      --fresh;
+      if (q + 2 < T) wait_vm(2 * NW + 32);
+      else if (q + 1 < T) wait_vm(NW + 32);
+      else wait_vm(32);
+    }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     fenced_barrier();
-    if (q + DEPTH < T) dma_step((uint32_t)((S + DEPTH) % NSLOT));
+    // the previous step's scale products first: the epilogue below needs them early
+    const v16f T0 = scale_tile(qa0, qw), T1 = scale_tile(qa1, qw);
+    asm volatile("" ::"v"(T0[0]), "v"(T1[0]));
+    if (__builtin_expect(q + DEPTH < T, 1)) dma_step((uint32_t)((S + DEPTH) % NSLOT));
+    v16i &Pc0 = (S & 1) ? PB0 : PA0;
+    v16i &Pc1 = (S & 1) ? PB1 : PA1;
+    const v16i &Pp0 = (S & 1) ? PA0 : PB0;
+    const v16i &Pp1 = (S & 1) ? PA1 : PB1;
     v4i b[4], a0[4], a1[4];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       b[kk] = lds16(adB[kk] + so);
       a0[kk] = lds16(adA[kk][0] + so);
+      a1[kk] = lds16(adA[kk][1] + so);
     }
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) a1[kk] = lds16(adA[kk][1] + so);
-    const uint32_t sa0 = lds4(adSa + ss), sa1 = lds4(adSa + ss + 128), sw = lds4(adSw + ss);
-    // the previous step's epilogue while this step's fragments are in flight
-    epilogue();
+    const uint32_t sa0 = lds4(adSa + ss) & smask, sa1 = lds4(adSa + ss + 128) & smask, sw = lds4(adSw + ss) & smask;
     v16i p0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0[0], b[0], seedv, 0, 0, 0);
     v16i p1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1[0], b[0], seedv, 0, 0, 0);
 #pragma unroll
@@ -605,19 +643,29 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
       p0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0[kk], b[kk], p0, 0, 0, 0);
       p1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1[kk], b[kk], p1, 0, 0, 0);
     }
-    const v2u sw2 = {sw & smask, 0u};
-    const v2u sa02 = {sa0 & smask, 0u}, sa12 = {sa1 & smask, 0u};
-    S0 = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, sa02), __builtin_bit_cast(v4h, sw2), (v16f){}, 0, 0, 0);
-    S1 = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, sa12), __builtin_bit_cast(v4h, sw2), (v16f){}, 0, 0, 0);
-    P0 = p0;
-    P1 = p1;
-    if (++kt == klen) {  // unit end (uniform): fold in this step, store, restart the sums
-      epilogue();
+    epilogue(Pp0, Pp1, T0, T1);
+    // issue order: fragment reads; the two scale MFMAs and the first int8 MFMA; then
+    // 8 VALU of the previous step's epilogue per int8 MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 14, 0);  // 12 x b128 + 2 scale reads
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+#pragma unroll
+    for (int j = 0; j < 7; ++j) {
+      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    Pc0 = p0;
+    Pc1 = p1;
+    qa0 = sa0;
+    qa1 = sa1;
+    qw = sw;
+    if (__builtin_expect(++kt == klen, 0)) {  // unit end: fold in this step, store, restart
+      const v16f U0 = scale_tile(qa0, qw), U1 = scale_tile(qa1, qw);
+      epilogue(Pc0, Pc1, U0, U1);
       store_tile(uk);
+      fresh = R == nullptr ? 3 : 0;
       acc0 = (v16f){};
       acc1 = (v16f){};
-      S0 = (v16f){};
-      S1 = (v16f){};
+      qa0 = qa1 = qw = 0;
       kt = 0;
       if (++uk < u_end) klen = unit_len(uk);
     }
