@@ -6,10 +6,12 @@ forward + both backward GEMMs, M = 8192 tokens (batch 4 x seq 2048), K = N = 153
 X ~ N(0,1), W ~ N(0,0.02) fp32 master, dY ~ N(0,1e-2), all fp32, seeded (torch CPU
 generator, seed 0) and resident in HBM before timing.
 
-One step = exactly what the training path (W8A8LinearFunction) runs for this layer:
-    quantize W -> quantize X, and X^T requantized along M, in one pass (quantize_dual)
+One step = exactly what the training path (Int8Linear / W8A8LinearFunction) runs for
+this layer when it quantizes its own master:
+    quantize W, and W^T requantized along N, in one pass (quantize_dual)
+    -> quantize X, and X^T requantized along M, in one pass (quantize_dual)
       -> GEMM Y = X W^T (fp32 out)
-    quantize dY along N and along M in one pass (quantize_dual) -> requant W^T
+    quantize dY along N and along M in one pass (quantize_dual)
       -> GEMM dX = dY W -> GEMM dW = dY^T X   (fp32)
 value = algorithmic int8 ops of the three GEMMs (3 * 2*M*N*K) / step time, in TOPS.
 The step runs as a captured HIP graph (no host launch overhead; replays are checked
@@ -103,9 +105,11 @@ def make_inputs(dev):
 
 
 def step(x, w, dy):
-    wq, ws = quantize_last_dim(w)
+    # W's row codes and the requantized W^T that dX needs, from one pass over W
+    wq, ws, wtq, wts = quantize_dual(w, t_from_codes=True)
     y, xtq, xts = w8a8_linear_forward_train(x, wq, ws, None, out_dtype=torch.float32)
-    dx, dw = w8a8_linear_backward(dy, None, None, wq, ws, dx_dtype=torch.float32, xt=(xtq, xts))
+    dx, dw = w8a8_linear_backward(dy, None, None, wq, ws, dx_dtype=torch.float32, xt=(xtq, xts),
+                                  wt=(wtq, wts))
     return y, dx, dw
 
 
@@ -145,14 +149,15 @@ def kernel_times(x, w, dy, reps):
     gtq, gts = quantize_transpose(dy)
     xtq, xts = requant_transpose(xq, xs)
     stages = {
-        "quantize_W": (lambda: quantize_last_dim(w), 4 * N * K + N * K + 2 * N * K // 128),
+        "quantize_W_dual": (lambda: quantize_dual(w, t_from_codes=True), 4 * N * K + 2 * (N * K + 2 * N * K // 128)),
         "quantize_X_dual": (lambda: quantize_dual(x, t_from_codes=True), 4 * M * K + 2 * (M * K + 2 * M * K // 128)),
         "gemm_fwd": (lambda: w8a8_gemm_out(xq, xs, wq, ws), None),
         "quantize_dY_dual": (lambda: quantize_dual(dy), 4 * M * N + 2 * (M * N + 2 * M * N // 128)),
-        "requant_WT": (lambda: requant_transpose(wq, ws), 2 * (N * K + 2 * N * K // 128)),
         "gemm_dX": (lambda: w8a8_gemm_out(gq, gs, wtq, wts), None),
         "gemm_dW": (lambda: w8a8_gemm_out(gtq, gts, xtq, xts), None),
         # the single-layout kernels the dual ones replace in the step (for comparison)
+        "quantize_W": (lambda: quantize_last_dim(w), 4 * N * K + N * K + 2 * N * K // 128),
+        "requant_WT": (lambda: requant_transpose(wq, ws), 2 * (N * K + 2 * N * K // 128)),
         "quantize_X": (lambda: quantize_last_dim(x), 4 * M * K + M * K + 2 * M * K // 128),
         "requant_XT": (lambda: requant_transpose(xq, xs), 2 * (M * K + 2 * M * K // 128)),
         "quantize_dY": (lambda: quantize_last_dim(dy), 4 * M * N + M * N + 2 * M * N // 128),

@@ -284,6 +284,11 @@ __global__ __launch_bounds__(512) void quant_dual_kernel(
   const int tid = threadIdx.x;
   const int64_t c0 = (int64_t)blockIdx.x * 128, r0 = (int64_t)blockIdx.y * 128;
   const int64_t ngC = (C + G - 1) / G, ngR = (R + G - 1) / G;
+  // the tile's rows as wave-uniform buffer descriptors (per-lane offsets below 2^31: the
+  // host checks 128 * C * 4): a per-lane base would wrap every store in a readfirstlane loop
+  const int64_t nrows = min((int64_t)128, R - r0);
+  const auto rq = rsrc(codes + r0 * C, nrows * C);
+  const auto rs = rsrc(scales + r0 * ngC, 2 * nrows * ngC);
 
   // ---- rows: lane (rr, sub) takes rows r0 + 32 p + rr (p = 0..3), columns c0 + 8 sub .. + 8;
   // the four rows' loads are issued before any arithmetic
@@ -314,8 +319,8 @@ __global__ __launch_bounds__(512) void quant_dual_kernel(
       if (ce.dy) {
         typedef float f32x4 __attribute__((ext_vector_type(4)));
         typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        const auto dr = rsrc(ce.dy + (row < R ? row : 0) * C, 4 * C);
-        const uint32_t off = ok ? (uint32_t)col * 4 : kOob;
+        const auto dr = rsrc(ce.dy + r0 * C, 4 * nrows * C);
+        const uint32_t off = ok ? (uint32_t)(lr * C + col) * 4 : kOob;
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{v[0], v[1], v[2], v[3]}), dr, off, 0, 0);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{v[4], v[5], v[6], v[7]}), dr,
                                                ok ? off + 16 : kOob, 0, 0);
@@ -325,14 +330,13 @@ __global__ __launch_bounds__(512) void quant_dual_kernel(
     const float s = group_scale(__builtin_bit_cast(float, am));
     uint32_t w[2];
     codes_rcp_packed<8>(v, s, w);
-    const int64_t rowc = row < R ? row : 0;
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     u32x2 q;
     q.x = w[0];
     q.y = w[1];
-    __builtin_amdgcn_raw_buffer_store_b64(q, rsrc(codes + rowc * C, C), ok ? (uint32_t)col : kOob, 0, 0);
-    __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsrc(scales + rowc * ngC, 2 * ngC),
-                                          ok && sub == 0 ? (uint32_t)(col / G) * 2 : kOob, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(q, rq, ok ? (uint32_t)(lr * C + col) : kOob, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rs,
+                                          ok && sub == 0 ? (uint32_t)(lr * ngC + col / G) * 2 : kOob, 0, 0);
 #pragma unroll
     for (int i = 0; i < 8; ++i) tile[lds_at(sub * 8 + i, lr)] = v[i];
   }
@@ -380,6 +384,9 @@ __global__ __launch_bounds__(512) void quant_dual_codes_kernel(
   const int tid = threadIdx.x;
   const int64_t c0 = (int64_t)blockIdx.x * 128, r0 = (int64_t)blockIdx.y * 128;
   const int64_t ngC = (C + G - 1) / G, ngR = (R + G - 1) / G;
+  const int64_t nrows = min((int64_t)128, R - r0);
+  const auto rq = rsrc(codes + r0 * C, nrows * C);
+  const auto rs = rsrc(scales + r0 * ngC, 2 * nrows * ngC);
 
   // ---- rows, as in quant_dual_kernel
   const int rr = tid >> 4, sub = tid & 15;
@@ -400,14 +407,13 @@ __global__ __launch_bounds__(512) void quant_dual_codes_kernel(
     const float s = group_scale(__builtin_bit_cast(float, am));
     uint32_t w[2];
     codes_rcp_packed<8>(v, s, w);
-    const int64_t rowc = row < R ? row : 0;
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     u32x2 q;
     q.x = w[0];
     q.y = w[1];
-    __builtin_amdgcn_raw_buffer_store_b64(q, rsrc(codes + rowc * C, C), ok ? (uint32_t)col : kOob, 0, 0);
-    __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsrc(scales + rowc * ngC, 2 * ngC),
-                                          ok && sub == 0 ? (uint32_t)(col / G) * 2 : kOob, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(q, rq, ok ? (uint32_t)(lr * C + col) : kOob, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rs,
+                                          ok && sub == 0 ? (uint32_t)(lr * ngC + col / G) * 2 : kOob, 0, 0);
 #pragma unroll
     for (int i = 0; i < 8; ++i) tq[(sub * 8 + i) * PB + lr] = (int8_t)(w[i >> 2] >> (8 * (i & 3)));
     if (sub == 0) srow[lr] = s;  // every row group of the tile has the same scale over its 16 lanes
@@ -951,7 +957,8 @@ extern "C" int ksd_quantize_dual(const void *x, int x_dtype, int64_t R, int64_t 
   hipStream_t st = (hipStream_t)stream;
   const int esz = x_dtype == KSD_F32 ? 4 : 2;
   const bool fast = group == 128 && C % 8 == 0 && ((uintptr_t)x) % 16 == 0 && (C * esz) % 16 == 0 &&
-                    ((uintptr_t)codes) % 8 == 0 && cdiv(R, 128) <= 65535 && cdiv(C, 128) <= 0x7fffffff;
+                    ((uintptr_t)codes) % 8 == 0 && cdiv(R, 128) <= 65535 && cdiv(C, 128) <= 0x7fffffff &&
+                    128 * C * 4 <= 0x7fffffffLL;
   if (!fast) {
     // the two single-layout kernels: row codes, then the transposed codes of x or of them
     int rc = ksd_quantize_lastdim(x, x_dtype, R, C, C, group, codes, scales, nullptr, 0.0f, stream);
@@ -1011,7 +1018,7 @@ extern "C" int ksd_ce_backward_quant_dual(const float *logits, int64_t R, int64_
   const CeSrc ce{row_max, row_inv_sum, targets, ignore_index, grad_scale, dy_out};
   const bool fast = C % 8 == 0 && ((uintptr_t)logits) % 16 == 0 && ((uintptr_t)codes) % 8 == 0 &&
                     (dy_out == nullptr || ((uintptr_t)dy_out) % 16 == 0) && cdiv(R, 128) <= 65535 &&
-                    cdiv(C, 128) <= 0x7fffffff;
+                    cdiv(C, 128) <= 0x7fffffff && 128 * C * 4 <= 0x7fffffffLL;
   if (fast) {
     const dim3 grid((unsigned)cdiv(C, 128), (unsigned)cdiv(R, 128));
     quant_dual_kernel<KSD_F32, true><<<grid, 512, 0, st>>>(logits, R, C, codes, scales, codes_t,

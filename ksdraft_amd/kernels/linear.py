@@ -64,12 +64,14 @@ def w8a8_linear_forward_train(x2: torch.Tensor, wq: torch.Tensor, ws: torch.Tens
 def w8a8_linear_backward(g: torch.Tensor, xq: torch.Tensor | None, xs: torch.Tensor | None,
                          wq: torch.Tensor, ws: torch.Tensor, group: int = GROUP_SIZE,
                          dx_dtype: torch.dtype = torch.float32, need_dx: bool = True,
-                         need_dw: bool = True, xt: tuple | None = None):
+                         need_dw: bool = True, xt: tuple | None = None, wt: tuple | None = None):
     """INT8 backward GEMMs of the linear layer (recipe of ks3_int8.py:403-424).
 
     g (M, N) upstream gradient; xq/xs the forward's activation codes, or ``xt`` =
-    (xtq, xts) the already requantized X^T operand; wq/ws the weight codes. When both
-    gradients are needed, dY is quantized in both layouts in one pass (quantize_dual).
+    (xtq, xts) the already requantized X^T operand; wq/ws the weight codes, and ``wt`` =
+    (wtq, wts) their requantized transpose when the caller already has it (e.g. from
+    quantize_dual(w, t_from_codes=True)). When both gradients are needed, dY is quantized
+    in both layouts in one pass (quantize_dual).
     Returns (dx (M, K) in dx_dtype or None, dw (N, K) fp32 or None)."""
     dx = dw = None
     gq = gs = gtq = gts = None
@@ -78,7 +80,10 @@ def w8a8_linear_backward(g: torch.Tensor, xq: torch.Tensor | None, xs: torch.Ten
     if need_dx:
         if gq is None:
             gq, gs = quantize_last_dim(g, group)                # along N (per token)
-        wtq, wts = requant_transpose(wq, ws, group, group)      # W^T (K, N) along N
+        if wt is not None:
+            wtq, wts = wt
+        else:
+            wtq, wts = requant_transpose(wq, ws, group, group)  # W^T (K, N) along N
         dx = w8a8_gemm_out(gq, gs, wtq, wts, group, out_dtype=_out_dtype(dx_dtype))
     if need_dw:
         if gtq is None:
@@ -97,7 +102,7 @@ class W8A8LinearFunction(torch.autograd.Function):
     is the upstream gradient itself."""
 
     @staticmethod
-    def forward(ctx, x, weight, bias, wq, ws, group, residual=None):
+    def forward(ctx, x, weight, bias, wq, ws, group, residual=None, wt=None):
         K = x.shape[-1]
         N = wq.shape[0]
         x2 = x.reshape(-1, K)
@@ -109,6 +114,7 @@ class W8A8LinearFunction(torch.autograd.Function):
             y, _, _ = w8a8_linear_forward(x2, wq, ws, bias, group, x.dtype, r2)
             xtq = xts = None
         ctx.save_for_backward(xtq, xts, wq, ws)
+        ctx.wt = wt  # (W^T codes, scales) for dX when the caller has them
         ctx.x_shape = x.shape
         ctx.x_dtype = x.dtype
         ctx.group = group
@@ -125,14 +131,14 @@ class W8A8LinearFunction(torch.autograd.Function):
         g = g.contiguous()
         dx, dw = w8a8_linear_backward(g, None, None, wq, ws, ctx.group, ctx.x_dtype,
                                       ctx.needs_input_grad[0], ctx.needs_input_grad[1],
-                                      xt=(xtq, xts) if xtq is not None else None)
+                                      xt=(xtq, xts) if xtq is not None else None, wt=ctx.wt)
         if dx is not None:
             dx = dx.reshape(ctx.x_shape).to(ctx.x_dtype)
         db = None
         if ctx.has_bias and ctx.needs_input_grad[2]:
             db = g.float().sum(0)
         dres = grad_out if len(ctx.needs_input_grad) > 6 and ctx.needs_input_grad[6] else None
-        return dx, dw, db, None, None, None, dres
+        return dx, dw, db, None, None, None, dres, None
 
 
 class Int8Linear(nn.Module):
@@ -168,12 +174,20 @@ class Int8Linear(nn.Module):
         w = self.weight.detach()
         if w.dtype not in (torch.float32, torch.bfloat16, torch.float16):
             w = w.float()
+        wt = None
         if dither > 0:
             codes, scales = quantize_last_dim_dithered(w.float(), GROUP_SIZE, dither)
+        elif self.training and self.weight.requires_grad and w.dim() == 2:
+            # training: the row codes and dX's operand W^T = quant(dequant(W)^T) (the recipe
+            # of ks3_int8.py:349-351) from one pass over the master
+            codes, scales, ct, st = quantize_dual(w.float(), GROUP_SIZE, t_from_codes=True)
+            wt = (ct, st)
         else:
             codes, scales = quantize_last_dim(w.float())
         self.weight_codes = codes
         self.weight_scales = scales
+        self._wt = wt  # valid while weight_codes is these codes
+        self._wt_src = codes
 
     def _quantize_weight_dithered(self, dither: float) -> None:
         self._dither = dither
@@ -221,9 +235,12 @@ class Int8Linear(nn.Module):
             # other float dtypes (float64) go through .float() as the reference's
             # quantize_last_dim(x2.float()) does (linear.py:69); the result is cast back
             xin = x if x.dtype in _OUT_DTYPES else x.float()
+            wt = getattr(self, "_wt", None)
+            if wt is not None and getattr(self, "_wt_src", None) is not self.weight_codes:
+                wt = None  # codes handed over since (optimizer): the backward requantizes
             y = W8A8LinearFunction.apply(xin, self.weight, self.bias, self.weight_codes,
                                          self.weight_scales, GROUP_SIZE,
-                                         residual if fuse_res else None)
+                                         residual if fuse_res else None, wt)
             y = y.to(x.dtype)
             return y if fuse_res or residual is None else residual + y
         # linear.py:68-73: fp32 GEMM, + bias in fp32, then cast to x.dtype (fused)

@@ -83,6 +83,8 @@ def test_training_step_matches_recipe(M, K, N):
         lin.bias.copy_(b)
     xd = x.to(DEV).requires_grad_(True)
     y = lin(xd)
+    # training quantizes W and dX's W^T operand in one dual pass (no requant in backward)
+    assert lin._wt is not None and lin._wt_src is lin.weight_codes
     y.backward(gy.to(DEV))
     ey, edx, edx_ref, edw, edw_ref = _recipe(x.numpy(), w.numpy(), gy.numpy())
     assert np.array_equal(y.detach().cpu().numpy(), (ey + b.numpy()).astype(np.float32))
