@@ -253,7 +253,8 @@ __global__ void __launch_bounds__(kSpineThreads) ks3_spine_kernel(
   const int64_t colc = cok ? col0 : 0;             // a valid column for every lane
   const uint32_t tab_lane = (uint32_t)(uintptr_t)(tab) + (uint32_t)(lane * 4) * (4 * Tab::kPitch);
   const int64_t row_end = min(M, (int64_t)(blockIdx.y + 1) * kSpineRows);
-  const int64_t rfirst = (int64_t)blockIdx.y * kSpineRows + rsub;
+  const int64_t rbase = (int64_t)blockIdx.y * kSpineRows, nrows = row_end - rbase;
+  const int64_t rfirst = rbase + rsub;
   // the two rows (r0, r0 + 16) of an iteration as packed fp16 words: 4 charts each
   auto raw2 = [&](int64_t r0, uint2 (&w)[2]) __attribute__((always_inline)) {
 #pragma unroll
@@ -338,13 +339,15 @@ __global__ void __launch_bounds__(kSpineThreads) ks3_spine_kernel(
         const float s = group_scale(__builtin_bit_cast(float, am));
         uint32_t wq;
         codes_rcp_packed<4>(h[u], s, &wq);
-        const int64_t rowc = rok ? row : 0;
+        // block-uniform descriptors (a per-lane base makes the compiler loop over a wave's
+        // distinct descriptors around every store); the lane's row goes into the offset
+        const int64_t lr = row - rbase;
         const bool lead = rok && cok && (lane & (G / 4 - 1)) == 0;
-        __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsrc(hs + rowc * n_groups, 2 * n_groups),
-                                              lead ? (uint32_t)(col0 / G) * 2 : kOob, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsrc(hs + rbase * n_groups, 2 * nrows * n_groups),
+                                              lead ? (uint32_t)(lr * n_groups + col0 / G) * 2 : kOob, 0, 0);
         if (VEC) {
-          __builtin_amdgcn_raw_buffer_store_b32(wq, rsrc(hq + rowc * F, F),
-                                                rok && cok ? (uint32_t)col0 : kOob, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(wq, rsrc(hq + rbase * F, nrows * F),
+                                                rok && cok ? (uint32_t)(lr * F + col0) : kOob, 0, 0);
         } else if (rok) {
 #pragma unroll
           for (int j = 0; j < 4; ++j)
@@ -395,7 +398,8 @@ __global__ void __launch_bounds__(kSpineThreads) ks3_spine_fused_kernel(
   const int64_t colc = cok ? col0 : 0;
   const uint32_t tab_lane = (uint32_t)(uintptr_t)(tab) + (uint32_t)(lane * 4) * (4 * Tab::kPitch);
   const int64_t row_end = min(M, (int64_t)(blockIdx.y + 1) * kSpineRows);
-  const int64_t rfirst = (int64_t)blockIdx.y * kSpineRows + rsub;
+  const int64_t rbase = (int64_t)blockIdx.y * kSpineRows, nrows = row_end - rbase;
+  const int64_t rfirst = rbase + rsub;
   auto raw2 = [&](int64_t r0, float4 (&w)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -459,13 +463,13 @@ __global__ void __launch_bounds__(kSpineThreads) ks3_spine_fused_kernel(
       const float s = group_scale(__builtin_bit_cast(float, hm));
       uint32_t wq;
       codes_rcp_packed<4>(f, s, &wq);
-      const int64_t rowc = rok ? row : 0;
+      const int64_t lr = row - rbase;  // block-uniform descriptors, as in ks3_spine_kernel
       const bool lead = rok && cok && (lane & (G / 4 - 1)) == 0;
-      __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsrc(hs + rowc * n_groups, 2 * n_groups),
-                                            lead ? (uint32_t)(col0 / G) * 2 : kOob, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsrc(hs + rbase * n_groups, 2 * nrows * n_groups),
+                                            lead ? (uint32_t)(lr * n_groups + col0 / G) * 2 : kOob, 0, 0);
       if (VEC) {
-        __builtin_amdgcn_raw_buffer_store_b32(wq, rsrc(hq + rowc * F, F),
-                                              rok && cok ? (uint32_t)col0 : kOob, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(wq, rsrc(hq + rbase * F, nrows * F),
+                                              rok && cok ? (uint32_t)(lr * F + col0) : kOob, 0, 0);
       } else if (rok) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -1199,7 +1203,8 @@ static int spine_checks(const char *who, const void *in, int64_t M, int64_t F, c
     return fail(KSD_EINVAL, "%s: null input pointer", who);
   if (!table || ((uintptr_t)table & 15) != 0)
     return fail(KSD_EINVAL, "%s: table workspace must be a 16-byte aligned buffer", who);
-  if (F > (1LL << 31) / 256) return fail(KSD_EINVAL, "%s: F too large", who);
+  // stores address a block's kSpineRows rows from one base with 32-bit offsets
+  if (F > (1LL << 31) / (2 * kSpineRows)) return fail(KSD_EINVAL, "%s: F too large", who);
   if (((uintptr_t)tanh_lut & 3) != 0) return fail(KSD_EINVAL, "%s: tanh_lut must be 4-byte aligned", who);
   if (cdiv(M, kSpineRows) > 0x7fffffff) return fail(KSD_EINVAL, "%s: M too large", who);
   return KSD_OK;

@@ -196,6 +196,13 @@ __global__ __launch_bounds__(512) void rosa_shift_dual_kernel(
   cvt_raw8<KSD_F32>(load_raw8<KSD_F32>(sig_q + cc), cok, sg[0]);
   cvt_raw8<KSD_F32>(load_raw8<KSD_F32>(sig_k + cc), cok, sg[1]);
   cvt_raw8<KSD_F32>(load_raw8<KSD_F32>(sig_v + cc), cok, sg[2]);
+  const int64_t nrows = min(128, R - r0);
+  __amdgpu_buffer_rsrc_t rq[3], rsc[3];
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    rq[m] = rsrc(out.codes[m] + (int64_t)r0 * C, nrows * C);
+    rsc[m] = rsrc(out.scales[m] + (int64_t)r0 * ngC, 2 * nrows * ngC);
+  }
   Raw8<DT> raw[4], rawp[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
@@ -220,7 +227,6 @@ __global__ __launch_bounds__(512) void rosa_shift_dual_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) diff[e] = round_to_dt<DT>(diff[e]);
     }
-    const int rowc = row < R ? row : 0;
 #pragma unroll
     for (int m = 0; m < 3; ++m) {
       float v[8];
@@ -234,10 +240,11 @@ __global__ __launch_bounds__(512) void rosa_shift_dual_kernel(
       u32x2 q;
       q.x = w[0];
       q.y = w[1];
-      __builtin_amdgcn_raw_buffer_store_b64(q, rsrc(out.codes[m] + (int64_t)rowc * C, C),
-                                            ok ? (uint32_t)col : kOob, 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsrc(out.scales[m] + (int64_t)rowc * ngC, 2 * ngC),
-                                            ok && sub == 0 ? (uint32_t)(col / G) * 2 : kOob, 0, 0);
+      // one descriptor per tile (a per-lane base would make the compiler loop over the
+      // distinct descriptors of a wave around every store); the lane's row is in the offset
+      __builtin_amdgcn_raw_buffer_store_b64(q, rq[m], ok ? (uint32_t)(lr * C + col) : kOob, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16(scale_bits(s), rsc[m],
+                                            ok && sub == 0 ? (uint32_t)(lr * ngC + col / G) * 2 : kOob, 0, 0);
 #pragma unroll
       for (int i = 0; i < 8; ++i) tq[m][(sub * 8 + i) * PB + lr] = (int8_t)(w[i >> 2] >> (8 * (i & 3)));
       if (sub == 0) srow[m][lr] = s;  // the 16 lanes of a row group share its scale
@@ -598,7 +605,7 @@ extern "C" int ksd_rosa_shift_quant_dual(const void *x, int x_dtype, int64_t B, 
     out.codes_t[m] = codes_t[m];
     out.scales_t[m] = scales_t[m];
   }
-  if (rows > 0x7fffffff - 256 || d > (1 << 24))
+  if (rows > 0x7fffffff - 256 || d >= (1 << 24))
     return fail(KSD_EINVAL, "rosa_shift_quant_dual: too large");
   const size_t esz = x_dtype == KSD_F32 ? 4 : 2;
   auto al = [](const void *p, size_t a) { return ((uintptr_t)p % a) == 0; };
