@@ -667,21 +667,28 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
       acc1 = (v16f){};
       qa0 = qa1 = qw = 0;
       kt = 0;
-      if (++uk < u_end) klen = unit_len(uk);
+      if (++uk < u_end) klen = __builtin_amdgcn_readfirstlane(unit_len(uk));  // SGPR: scalar loop control
     }
   };
   using C0 = std::integral_constant<int, 0>;
   using C1 = std::integral_constant<int, 1>;
   using C2 = std::integral_constant<int, 2>;
   using C3 = std::integral_constant<int, 3>;
-  for (int q = 0; q < T; q += NSLOT) {
+  // whole ring turns without exits, then the tail: an exit between the steps of the loop
+  // body makes the compiler carry placeholder values for it through every step
+  int q = 0;
+  for (; q + NSLOT <= T; q += NSLOT) {
     step(C0{}, q);
-    if (q + 1 >= T) break;
     step(C1{}, q + 1);
-    if (q + 2 >= T) break;
     step(C2{}, q + 2);
-    if (q + 3 >= T) break;
     step(C3{}, q + 3);
+  }
+  if (q < T) {
+    step(C0{}, q);
+    if (q + 1 < T) {
+      step(C1{}, q + 1);
+      if (q + 2 < T) step(C2{}, q + 2);
+    }
   }
 }
 // y = ((p_0 + p_1) + ...) + bias, then the output type: the parts of a split launch in
