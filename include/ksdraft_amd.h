@@ -234,6 +234,24 @@ int ksd_w8a8_gemm_nt_ws(const int8_t *a, const uint16_t *a_scales, const int8_t 
                         int64_t workspace_bytes, void *stream);
 
 /*
+ * Two independent group-128 GEMMs in one persistent launch: the dX = dY . W and
+ * dW = dY^T . X pair of a linear layer's backward (reference ksdraft/kernels/ks3_int8.py:
+ * 403-424, two w8a8_gemm calls of gemm.py:53-90), or any two GEMMs with no data dependence.
+ * Problem i: y_i (M_i, N_i) = a_i (M_i, K_i) . w_i (N_i, K_i)^T in output type y_i_dtype
+ * (KSD_F32, KSD_BF16 or KSD_F16), no bias, no residual, each with exactly the numeric
+ * contract of ksd_w8a8_gemm_nt_ex on its own (including its K split). The workgroups take
+ * balanced runs of both problems' tiles, so a problem with few long tiles (dW) shares the
+ * device with one of many short tiles (dX) instead of leaving CUs idle.
+ *   workspace  16-byte aligned fp32 scratch: the sum over split problems of S*M*N*4 bytes
+ *              (NULL when neither problem splits)
+ */
+int ksd_w8a8_gemm_pair(const int8_t *a0, const uint16_t *a0_scales, const int8_t *w0,
+                       const uint16_t *w0_scales, int64_t M0, int64_t N0, int64_t K0, void *y0,
+                       int y0_dtype, const int8_t *a1, const uint16_t *a1_scales, const int8_t *w1,
+                       const uint16_t *w1_scales, int64_t M1, int64_t N1, int64_t K1, void *y1,
+                       int y1_dtype, float *workspace, int64_t workspace_bytes, void *stream);
+
+/*
  * Test-only export of the exact int32 group partials P_g of the GEMM above
  * (the tl.dot result of reference ksdraft/kernels/gemm.py:42).
  *   partials (K/group, M, N) int32

@@ -44,6 +44,8 @@ SIGNATURES = {
     "ksd_w8a8_gemm_splits": [_I64, _I64, _I64, _INT, _P],
     "ksd_w8a8_gemm_nt_ws": [_P, _P, _P, _P, _I64, _I64, _I64, _INT, _P, _P, _INT, _P, _I64, _P],
     "ksd_w8a8_gemm_nt_ex": [_P, _P, _P, _P, _I64, _I64, _I64, _INT, _P, _P, _P, _INT, _P, _I64, _P],
+    "ksd_w8a8_gemm_pair": [_P, _P, _P, _P, _I64, _I64, _I64, _P, _INT, _P, _P, _P, _P, _I64, _I64, _I64,
+                           _P, _INT, _P, _I64, _P],
     "ksd_w8a8_group_partials": [_P, _P, _I64, _I64, _I64, _INT, _P, _P],
     "ksd_ks3_spine_fwd": [_P, _I64, _I64, _P, _P, _P, _P, _P, _INT, _P, _P, _P, _P, _P],
     "ksd_ks3_spine_fwd_noalloc": [_P, _I64, _I64, _P, _P, _P, _P, _P, _INT, _P, _P, _P, _P],

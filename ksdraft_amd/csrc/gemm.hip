@@ -404,43 +404,83 @@ __host__ __device__ __forceinline__ int part_lo(int p, int KT, int splits) {
   return (int)((int64_t)p * KT / splits);
 }
 
-// Work unit u = (tile u / splits, K-part u % splits). With splits > 1, Y is the fp32
-// workspace: part p of a tile goes to Y + p * part_stride (elements), raw (no bias), and a
-// combine kernel adds the parts in order.
-template <int OUT, bool BIAS>
-__global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
-    const int8_t *__restrict__ A, const uint16_t *__restrict__ AS,
-    const int8_t *__restrict__ W, const uint16_t *__restrict__ WS, int M, int N, int K,
-    int tiles_n, int ntiles, const float *__restrict__ bias, void *__restrict__ Y,
-    int splits, int64_t part_stride, const void *__restrict__ R) {
+// One GEMM of a launch: Y (M, N) = A (M, K) . W (N, K)^T with its scales. Work unit u =
+// (tile u / splits, K-part u % splits). With splits > 1, Y is the fp32 workspace: part p of
+// a tile goes to Y + p * part_stride (elements), raw (no bias), and a combine kernel adds
+// the parts in order. `out` is the output type (read by paired launches; single launches
+// take it as a template argument).
+struct G128Prob {
+  const int8_t *A;
+  const uint16_t *AS;
+  const int8_t *W;
+  const uint16_t *WS;
+  const float *bias;
+  void *Y;
+  const void *R;
+  int64_t part_stride;
+  int M, N, K, tiles_n, ntiles, splits, out;
+};
+// Work split of a paired launch over its grid (logical workgroup c, XCD-ordered): c takes
+// q0 + (c < r0) consecutive units of problem 0 (the one with the longer units), then a run
+// of problem 1's units, kA of them for c < r0 and kB for the others, so every workgroup
+// ends near the same step count.
+struct G128Sched {
+  int q0, r0, kA, kB;
+};
+// Units of problem 1 before logical workgroup c (clamped to its unit count n1).
+__device__ __forceinline__ int pair_start1(int c, const G128Sched &sc, int n1) {
+  const int64_t s = c <= sc.r0 ? (int64_t)c * sc.kA : (int64_t)sc.r0 * sc.kA + (int64_t)(c - sc.r0) * sc.kB;
+  return (int)(s < n1 ? s : n1);
+}
+
+// PAIR = false: one GEMM (p0; p1 is not read), output type OUT. PAIR = true: two
+// independent GEMMs p0 and p1 in one persistent launch (no bias, no residual), each unit
+// stored in its problem's runtime output type (OUT is ignored).
+template <int OUT, bool BIAS, bool PAIR = false>
+__global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(const G128Prob P0, const G128Prob P1,
+                                                                const G128Sched sc) {
   __shared__ __attribute__((aligned(16))) int8_t sA[NSLOT][BM * BK];
   __shared__ __attribute__((aligned(16))) int8_t sW[NSLOT][BN * BK];
   __shared__ __attribute__((aligned(16))) uint32_t sS[NSLOT][256];
   constexpr int DEPTH = NSLOT - 1;
-  constexpr int ES = OUT == KSD_F32 ? 4 : 2;
   constexpr int NW = 5;  // DMA instructions per wave and step: 4 x 1 KB codes + 1 scale
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3, half = lane >> 5, l32 = lane & 31;
-  const int KT = K / BK, G = KT;
-  const int nunits = ntiles * splits;
 
-  int u_begin, u_end;
+  // This workgroup's work list: CU-local units v = 0 .. nbig-1 are problem 0's units
+  // b_begin.., then (paired launches) v = nbig .. v_end-1 are problem 1's units s_begin..
+  int b_begin, nbig, s_begin = 0, v_end;
   {
     const int nb = gridDim.x, per = nb / 8, rem = nb % 8, x = blockIdx.x % 8, i = blockIdx.x / 8;
     const int lb = x * per + min(x, rem) + i;
-    u_begin = (int)((int64_t)nunits * lb / nb);
-    u_end = (int)((int64_t)nunits * (lb + 1) / nb);
+    if constexpr (!PAIR) {
+      const int nunits = P0.ntiles * P0.splits;
+      b_begin = (int)((int64_t)nunits * lb / nb);
+      nbig = (int)((int64_t)nunits * (lb + 1) / nb) - b_begin;
+      v_end = nbig;
+    } else {
+      b_begin = lb * sc.q0 + min(lb, sc.r0);
+      nbig = sc.q0 + (lb < sc.r0 ? 1 : 0);
+      const int n1 = P1.ntiles * P1.splits;
+      s_begin = pair_start1(lb, sc, n1);
+      v_end = nbig + pair_start1(lb + 1, sc, n1) - s_begin;
+    }
   }
-  auto unit_len = [&](int u) __attribute__((always_inline)) {
-    const int pp = u % splits;
-    return part_lo(pp + 1, KT, splits) - part_lo(pp, KT, splits);
+  // problem field of CU-local unit v (wave-uniform)
+#define G128F(v, f) ((!PAIR || (v) < nbig) ? P0.f : P1.f)
+  auto gunit = [&](int v) __attribute__((always_inline)) {
+    return (!PAIR || v < nbig) ? b_begin + v : s_begin + (v - nbig);
+  };
+  auto unit_len = [&](int v) __attribute__((always_inline)) {
+    const int sp = G128F(v, splits), KT = G128F(v, K) / BK, pp = gunit(v) % sp;
+    return part_lo(pp + 1, KT, sp) - part_lo(pp, KT, sp);
   };
   int T = 0;
-  if (splits == 1) T = (u_end - u_begin) * KT;
+  if (!PAIR && P0.splits == 1) T = v_end * (P0.K / BK);
   else
-    for (int u = u_begin; u < u_end; ++u) T += unit_len(u);
+    for (int v = 0; v < v_end; ++v) T += unit_len(v);
   if (T == 0) return;
 
   // DMA: each wave fills 16 rows of the A tile and 16 of the W tile (two 1 KB chunks of
@@ -454,20 +494,21 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
   const uint32_t ldsA = lds_addr(&sA[0][0]) + wave * 2048;
   const uint32_t ldsW = lds_addr(&sW[0][0]) + wave * 2048;
   const uint32_t ldsS = lds_addr(&sS[0][0]) + wave * 128;
-  const uint16_t *const SB = s_isA ? AS : WS;
   const int8_t *ba, *bw;
   const uint16_t *bs;
   uint32_t oa0, oa1, ow0, ow1, os;
-  int is_u = u_begin, is_k = 0, is_len = __builtin_amdgcn_readfirstlane(unit_len(u_begin));
+  int is_u = 0, is_k = 0, is_len = __builtin_amdgcn_readfirstlane(unit_len(0));
   auto rebase = [&]() __attribute__((always_inline)) {
     // every value here is wave-uniform; readfirstlane keeps the DMA bases in SGPRs
-    const int cu_ = __builtin_amdgcn_readfirstlane(is_u);
-    const int t = cu_ / splits, k0 = __builtin_amdgcn_readfirstlane(part_lo(cu_ % splits, KT, splits));
-    const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
-    ba = A + (int64_t)m0 * K + (int64_t)k0 * BK;
-    bw = W + (int64_t)n0 * K + (int64_t)k0 * BK;
+    const int v = __builtin_amdgcn_readfirstlane(is_u);
+    const int u = gunit(v), sp = G128F(v, splits), M = G128F(v, M), N = G128F(v, N), K = G128F(v, K);
+    const int KT = K / BK, G = KT, tn = G128F(v, tiles_n);
+    const int t = u / sp, k0 = __builtin_amdgcn_readfirstlane(part_lo(u % sp, KT, sp));
+    const int m0 = (t / tn) * BM, n0 = (t % tn) * BN;
+    ba = G128F(v, A) + (int64_t)m0 * K + (int64_t)k0 * BK;
+    bw = G128F(v, W) + (int64_t)n0 * K + (int64_t)k0 * BK;
     const int r0 = s_isA ? m0 : n0, rmax = s_isA ? M : N;
-    bs = SB + (int64_t)r0 * G + k0;
+    bs = (s_isA ? G128F(v, AS) : G128F(v, WS)) + (int64_t)r0 * G + k0;
     oa0 = (uint32_t)((min(m0 + drow0, M - 1) - m0) * K + dch0);
     oa1 = (uint32_t)((min(m0 + drow1, M - 1) - m0) * K + dch1);
     ow0 = (uint32_t)((min(n0 + drow0, N - 1) - n0) * K + dch0);
@@ -487,7 +528,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
     bs += 1;
     if (__builtin_expect(++is_k == is_len, 0)) {
       is_k = 0;
-      if (++is_u < u_end) {
+      if (++is_u < v_end) {
         is_len = __builtin_amdgcn_readfirstlane(unit_len(is_u));
         rebase();
       }
@@ -513,12 +554,18 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
   v16i seedv = kSeed;
   asm volatile("" : "+v"(seedv));
   v16f acc0 = (v16f){}, acc1 = (v16f){};
-  int kt = 0, uk = u_begin, klen = is_len;
+  int kt = 0, uk = 0, klen = is_len;
 
-  auto store_tile = [&](int u) __attribute__((always_inline)) {
-    const int t = u / splits;
-    char *const Yp = (char *)Y + (int64_t)(u % splits) * part_stride * ES;
-    const int m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
+  auto store_impl = [&](auto out_c, int v) __attribute__((always_inline)) {
+    constexpr int OT = decltype(out_c)::value;
+    constexpr int ES = OT == KSD_F32 ? 4 : 2;
+    const int u = gunit(v), sp = G128F(v, splits), tn = G128F(v, tiles_n);
+    const int M = G128F(v, M), N = G128F(v, N);
+    const float *const bias = G128F(v, bias);
+    const void *const R = PAIR ? nullptr : P0.R;
+    const int t = u / sp;
+    char *const Yp = (char *)G128F(v, Y) + (int64_t)(u % sp) * G128F(v, part_stride) * ES;
+    const int m0 = (t / tn) * BM, n0 = (t % tn) * BN;
     const int col = n0 + wn * 32 + l32;
     const int64_t r0 = (int64_t)m0 + wm * 64;
     const int64_t rows0 = max((int64_t)0, min((int64_t)32, (int64_t)M - r0));
@@ -536,10 +583,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int vo = voff + ((e >> 2) * 8 + (e & 3)) * N * ES;
-        if constexpr (OUT == KSD_F32) {
+        if constexpr (OT == KSD_F32) {
           r0v[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(q0, vo, 0, 0));
           r1v[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(q1, vo, 0, 0));
-        } else if constexpr (OUT == KSD_BF16) {
+        } else if constexpr (OT == KSD_BF16) {
           r0v[e] = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(q0, vo, 0, 0) << 16);
           r1v[e] = __builtin_bit_cast(float, (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(q1, vo, 0, 0) << 16);
         } else {
@@ -554,23 +601,33 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
       float y0 = BIAS ? acc0[e] + b : acc0[e];
       float y1 = BIAS ? acc1[e] + b : acc1[e];
       if (R != nullptr) {
-        if constexpr (OUT == KSD_BF16) {
+        if constexpr (OT == KSD_BF16) {
           y0 = __builtin_bit_cast(float, (uint32_t)f32_to_bf16(y0) << 16);
           y1 = __builtin_bit_cast(float, (uint32_t)f32_to_bf16(y1) << 16);
-        } else if constexpr (OUT != KSD_F32) {
+        } else if constexpr (OT != KSD_F32) {
           y0 = f16_round(y0);
           y1 = f16_round(y1);
         }
         y0 = y0 + r0v[e];
         y1 = y1 + r1v[e];
       }
-      if constexpr (OUT == KSD_F32) {
+      if constexpr (OT == KSD_F32) {
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y0), r0s, vo, 0, 0);
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y1), r1s, vo, 0, 0);
       } else {
-        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)out_bits<OUT>(y0), r0s, vo, 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)out_bits<OUT>(y1), r1s, vo, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)out_bits<OT>(y0), r0s, vo, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)out_bits<OT>(y1), r1s, vo, 0, 0);
       }
+    }
+  };
+  auto store_tile = [&](int v) __attribute__((always_inline)) {
+    if constexpr (!PAIR) {
+      store_impl(std::integral_constant<int, OUT>{}, v);
+    } else {  // the unit's runtime output type (paired launches: fp32, bf16 or fp16)
+      const int ot = G128F(v, out);
+      if (ot == KSD_F32) store_impl(std::integral_constant<int, KSD_F32>{}, v);
+      else if (ot == KSD_BF16) store_impl(std::integral_constant<int, KSD_BF16>{}, v);
+      else store_impl(std::integral_constant<int, KSD_F16>{}, v);
     }
   };
   // acc += (P - seed) * S per element: the ordered contract for one group, P the seeded
@@ -623,7 +680,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
     // the previous step's scale products first: the epilogue below needs them early
     const v16f T0 = scale_tile(qa0, qw), T1 = scale_tile(qa1, qw);
     asm volatile("" ::"v"(T0[0]), "v"(T1[0]));
-    if (__builtin_expect(q + DEPTH < T, 1)) dma_step((uint32_t)((S + DEPTH) % NSLOT));
     v16i &Pc0 = (S & 1) ? PB0 : PA0;
     v16i &Pc1 = (S & 1) ? PB1 : PA1;
     const v16i &Pp0 = (S & 1) ? PA0 : PB0;
@@ -636,6 +692,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
       a1[kk] = lds16(adA[kk][1] + so);
     }
     const uint32_t sa0 = lds4(adSa + ss) & smask, sa1 = lds4(adSa + ss + 128) & smask, sw = lds4(adSw + ss) & smask;
+    if (__builtin_expect(q + DEPTH < T, 1)) dma_step((uint32_t)((S + DEPTH) % NSLOT));
     v16i p0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0[0], b[0], seedv, 0, 0, 0);
     v16i p1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1[0], b[0], seedv, 0, 0, 0);
 #pragma unroll
@@ -662,12 +719,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(
       const v16f U0 = scale_tile(qa0, qw), U1 = scale_tile(qa1, qw);
       epilogue(Pc0, Pc1, U0, U1);
       store_tile(uk);
-      fresh = R == nullptr ? 3 : 0;
+      fresh = (PAIR || P0.R == nullptr) ? 3 : 0;
       acc0 = (v16f){};
       acc1 = (v16f){};
       qa0 = qa1 = qw = 0;
       kt = 0;
-      if (++uk < u_end) klen = __builtin_amdgcn_readfirstlane(unit_len(uk));  // SGPR: scalar loop control
+      if (++uk < v_end) klen = __builtin_amdgcn_readfirstlane(unit_len(uk));  // SGPR: scalar loop control
     }
   };
   using C0 = std::integral_constant<int, 0>;
@@ -757,18 +814,19 @@ static void launch(const int8_t *a, const uint16_t *as, const int8_t *w, const u
   const int tn = (N + BN - 1) / BN, tm = (M + BM - 1) / BM;
   const int ntiles = tm * tn;
   if constexpr (GROUP == 128 && MODE == 0) {
+    const g128::G128Sched none{0, 0, 0, 0};
     if (splits > 1) {
       const int64_t nel = (int64_t)M * N;
       const int grid = min(ntiles * splits, cu_count());
-      g128::gemm_g128_kernel<KSD_F32, false><<<dim3(grid), dim3(NTHREADS), 0, st>>>(
-          a, as, w, ws, M, N, K, tn, ntiles, nullptr, workspace, splits, nel, nullptr);
+      const g128::G128Prob p{a, as, w, ws, nullptr, workspace, nullptr, nel, M, N, K, tn, ntiles, splits, KSD_F32};
+      g128::gemm_g128_kernel<KSD_F32, false><<<dim3(grid), dim3(NTHREADS), 0, st>>>(p, p, none);
       const int64_t cb = (nel + 1023) / 1024;
       g128::splitk_combine_kernel<OUT, BIAS><<<dim3((unsigned)cb), dim3(256), 0, st>>>(
           workspace, splits, nel, nel, N, bias, y, residual);
     } else {
       const int grid = min(ntiles, cu_count());
-      g128::gemm_g128_kernel<OUT, BIAS><<<dim3(grid), dim3(NTHREADS), 0, st>>>(
-          a, as, w, ws, M, N, K, tn, ntiles, bias, y, 1, 0, residual);
+      const g128::G128Prob p{a, as, w, ws, bias, y, residual, 0, M, N, K, tn, ntiles, 1, OUT};
+      g128::gemm_g128_kernel<OUT, BIAS><<<dim3(grid), dim3(NTHREADS), 0, st>>>(p, p, none);
     }
   } else {
     const int grid = min(ntiles, cu_count());
@@ -798,6 +856,74 @@ static int launch_o(const int8_t *a, const uint16_t *as, const int8_t *w, const 
     default: return fail(KSD_ETYPE, "w8a8_gemm: unsupported output dtype %d", y_dtype);
   }
   return check_launch("w8a8_gemm_nt");
+}
+
+// Balanced work split of a paired launch (see G128Sched): problem 0 has n0 units of at
+// most c0 steps each, problem 1 n1 units of at most c1 steps, c0 >= c1. The smallest
+// per-workgroup step budget T that fits every unit gives kA / kB units of problem 1 to the
+// workgroups with q0 + 1 / q0 units of problem 0.
+static g128::G128Sched pair_sched(int64_t n0, int64_t c0, int64_t n1, int64_t c1, int grid) {
+  g128::G128Sched sc{(int)(n0 / grid), (int)(n0 % grid), 0, 0};
+  auto fill = [&](int64_t budget) { return budget < 0 ? (int64_t)0 : budget / c1; };
+  const int64_t lo = (int64_t)(sc.q0 + (sc.r0 > 0 ? 1 : 0)) * c0;
+  int64_t t = lo > (n0 * c0 + n1 * c1) / grid ? lo : (n0 * c0 + n1 * c1) / grid;
+  for (;; ++t) {
+    const int64_t a = fill(t - (int64_t)(sc.q0 + 1) * c0), b = fill(t - (int64_t)sc.q0 * c0);
+    if (sc.r0 * a + (grid - sc.r0) * b >= n1) {
+      sc.kA = (int)a;
+      sc.kB = (int)b;
+      return sc;
+    }
+  }
+}
+
+// Two GS128 GEMMs in one persistent launch: problem i is y_i (M_i, N_i) = a_i . w_i^T in
+// output type dt_i (fp32, bf16 or fp16), with the same numeric contract (and K split) as
+// its own launch. A problem whose shape splits K sums its parts in ws (fp32), then a
+// combine kernel writes y_i.
+static int launch_pair(const int8_t *const a[2], const uint16_t *const as[2], const int8_t *const w[2],
+                       const uint16_t *const ws[2], const int64_t M[2], const int64_t N[2],
+                       const int64_t K[2], void *const y[2], const int dt[2], float *workspace,
+                       int64_t workspace_bytes, hipStream_t st) {
+  g128::G128Prob p[2];
+  int64_t cost[2], units[2], wsoff[2], need = 0;
+  for (int i = 0; i < 2; ++i) {
+    const int tn = (int)((N[i] + BN - 1) / BN), tm = (int)((M[i] + BM - 1) / BM);
+    const int sp = g128_splits(M[i], N[i], K[i]);
+    const int64_t KT = K[i] / BK;
+    cost[i] = (KT + sp - 1) / sp;
+    units[i] = (int64_t)tm * tn * sp;
+    wsoff[i] = need;
+    if (sp > 1) need += (int64_t)sp * M[i] * N[i] * 4;
+    p[i] = g128::G128Prob{a[i], as[i], w[i], ws[i], nullptr, y[i], nullptr, 0, (int)M[i], (int)N[i],
+                          (int)K[i], tn, tm * tn, sp, dt[i]};
+  }
+  if (need > 0 && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 15) != 0))
+    return fail(KSD_EINVAL, "w8a8_gemm_pair: needs a 16-byte aligned fp32 workspace of %lld bytes, "
+                "got %lld", (long long)need, (long long)workspace_bytes);
+  for (int i = 0; i < 2; ++i)
+    if (p[i].splits > 1) {
+      p[i].Y = (char *)workspace + wsoff[i];
+      p[i].part_stride = M[i] * N[i];
+      p[i].out = KSD_F32;
+    }
+  const int first = cost[1] > cost[0] ? 1 : 0;  // problem 0 of the launch: the longer units
+  const g128::G128Prob &q0 = p[first], &q1 = p[1 - first];
+  const int64_t n0 = units[first], n1 = units[1 - first];
+  const int grid = (int)min((int64_t)cu_count(), n0 + n1);
+  const g128::G128Sched sc = pair_sched(n0, cost[first], n1, cost[1 - first], grid);
+  g128::gemm_g128_kernel<KSD_F32, false, true><<<dim3(grid), dim3(NTHREADS), 0, st>>>(q0, q1, sc);
+  for (int i = 0; i < 2; ++i) {
+    if (p[i].splits <= 1) continue;
+    const int64_t nel = M[i] * N[i], cb = (nel + 1023) / 1024;
+    const float *part = (const float *)((char *)workspace + wsoff[i]);
+    switch (dt[i]) {
+      case KSD_F32: g128::splitk_combine_kernel<KSD_F32, false><<<dim3((unsigned)cb), dim3(256), 0, st>>>(part, p[i].splits, nel, nel, (int)N[i], nullptr, y[i], nullptr); break;
+      case KSD_BF16: g128::splitk_combine_kernel<KSD_BF16, false><<<dim3((unsigned)cb), dim3(256), 0, st>>>(part, p[i].splits, nel, nel, (int)N[i], nullptr, y[i], nullptr); break;
+      default: g128::splitk_combine_kernel<KSD_F16, false><<<dim3((unsigned)cb), dim3(256), 0, st>>>(part, p[i].splits, nel, nel, (int)N[i], nullptr, y[i], nullptr); break;
+    }
+  }
+  return check_launch("w8a8_gemm_pair");
 }
 
 static int gemm_checks(const int8_t *a, const int8_t *w, int64_t M, int64_t N, int64_t K,
@@ -877,6 +1003,36 @@ extern "C" int ksd_w8a8_gemm_nt_ws(const int8_t *a, const uint16_t *a_scales, co
   if (M == 0 || N == 0 || K == 0) return gemm_checks(a, w, M, N, K, group);
   return ksd_w8a8_gemm_nt_ex(a, a_scales, w, w_scales, M, N, K, group, bias, nullptr, y, y_dtype,
                              workspace, workspace_bytes, stream);
+}
+
+extern "C" int ksd_w8a8_gemm_pair(const int8_t *a0, const uint16_t *a0_scales, const int8_t *w0,
+                                  const uint16_t *w0_scales, int64_t M0, int64_t N0, int64_t K0,
+                                  void *y0, int y0_dtype, const int8_t *a1, const uint16_t *a1_scales,
+                                  const int8_t *w1, const uint16_t *w1_scales, int64_t M1, int64_t N1,
+                                  int64_t K1, void *y1, int y1_dtype, float *workspace,
+                                  int64_t workspace_bytes, void *stream) {
+  const int8_t *a[2] = {a0, a1}, *w[2] = {w0, w1};
+  const uint16_t *as[2] = {a0_scales, a1_scales}, *ws[2] = {w0_scales, w1_scales};
+  const int64_t M[2] = {M0, M1}, N[2] = {N0, N1}, K[2] = {K0, K1};
+  void *y[2] = {y0, y1};
+  const int dt[2] = {y0_dtype, y1_dtype};
+  for (int i = 0; i < 2; ++i) {
+    int rc = gemm_checks(a[i], w[i], M[i], N[i], K[i], 128);
+    if (rc != KSD_OK) return rc;
+    if (dt[i] != KSD_F32 && dt[i] != KSD_BF16 && dt[i] != KSD_F16)
+      return fail(KSD_ETYPE, "w8a8_gemm_pair: output dtype %d (fp32, bf16 or fp16 only)", dt[i]);
+    if (M[i] > 0 && N[i] > 0 && K[i] == 0)
+      return fail(KSD_EINVAL, "w8a8_gemm_pair: K = 0 (the host wrapper handles it)");
+  }
+  const bool e0 = M0 == 0 || N0 == 0, e1 = M1 == 0 || N1 == 0;
+  hipStream_t st = (hipStream_t)stream;
+  if (e0 && e1) return KSD_OK;
+  if (e0 || e1) {  // one empty problem: a single launch of the other
+    const int i = e0 ? 1 : 0;
+    return ksd_w8a8_gemm_nt_ex(a[i], as[i], w[i], ws[i], M[i], N[i], K[i], 128, nullptr, nullptr, y[i],
+                               dt[i], workspace, workspace_bytes, stream);
+  }
+  return launch_pair(a, as, w, ws, M, N, K, y, dt, workspace, workspace_bytes, st);
 }
 
 extern "C" int ksd_w8a8_group_partials(const int8_t *a, const int8_t *w, int64_t M, int64_t N,

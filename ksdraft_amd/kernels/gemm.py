@@ -121,6 +121,39 @@ def w8a8_gemm_out(a_codes: torch.Tensor, a_scales: torch.Tensor, w_codes: torch.
     return out
 
 
+def w8a8_gemm_pair(first: tuple, second: tuple, group: int = GROUP_SIZE) -> tuple:
+    """Two independent GEMMs in one launch: each of ``first`` / ``second`` is
+    (a_codes, a_scales, w_codes, w_scales, out_dtype) with out_dtype fp32, bf16 or fp16.
+    Returns (y0, y1), each bit-identical to ``w8a8_gemm_out(a, as, w, ws, out_dtype=...)``.
+    The launch gives the device's workgroups balanced runs of both GEMMs' tiles (e.g. a
+    linear layer's dX, many short tiles, beside its dW, few tiles with K = tokens), where
+    two launches would leave CUs idle through the second one's tail. Group 128 only; other
+    groups run the two GEMMs one after the other."""
+    probs = []
+    for a_codes, a_scales, w_codes, w_scales, out_dtype in (first, second):
+        dev, M, N, K, a, as_, w, ws = _prepare(a_codes, a_scales, w_codes, w_scales, group)
+        code = _OUT_CODE.get(out_dtype)
+        if code is None:
+            raise TypeError(f"unsupported output dtype {out_dtype}")
+        probs.append((dev, M, N, K, a, as_, w, ws, code, out_dtype))
+    if group != GROUP_SIZE or any(p[3] == 0 for p in probs):
+        return tuple(w8a8_gemm_out(a_codes, a_scales, w_codes, w_scales, group, out_dtype=dt)
+                     for a_codes, a_scales, w_codes, w_scales, dt in (first, second))
+    dev = probs[0][0]
+    if probs[1][0] != dev:
+        raise ValueError("w8a8_gemm_pair: both GEMMs must be on one device")
+    outs = [torch.empty((M, N), dtype=dt, device=dev) for _, M, N, _, _, _, _, _, _, dt in probs]
+    need = sum(gemm_splits(M, N, K) * M * N for _, M, N, K, *_ in probs
+               if gemm_splits(M, N, K) > 1)
+    work = torch.empty(need, dtype=torch.float32, device=dev) if need else None
+    args = []
+    for (_, M, N, K, a, as_, w, ws, code, _), y in zip(probs, outs):
+        args += [a.data_ptr(), as_.data_ptr(), w.data_ptr(), ws.data_ptr(), M, N, K, y.data_ptr(), code]
+    _lib.call("ksd_w8a8_gemm_pair", *args, _lib.ptr(work), 0 if work is None else work.numel() * 4,
+              _lib.stream_ptr(dev))
+    return outs[0], outs[1]
+
+
 _SPLITS: dict = {}
 
 

@@ -33,7 +33,7 @@ from torch import nn
 import torch.nn.functional as F
 
 from .. import _lib
-from .gemm import w8a8_gemm, w8a8_gemm_out
+from .gemm import w8a8_gemm, w8a8_gemm_out, w8a8_gemm_pair
 from .quant import (GROUP_SIZE, dequantize_last_dim, quantize_last_dim, quantize_transpose,
                     requant_transpose)
 
@@ -461,11 +461,6 @@ def grad_handoff_device(t: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def _handoff_gemm(a, as_, w, ws, group):
-    """grad_handoff_device(w8a8_gemm(...)): the fp32 GEMM output, handed off on the device."""
-    return grad_handoff_device(w8a8_gemm(a, as_, w, ws, group))
-
-
 class _KS3Int8Train(torch.autograd.Function):
     """Training forward/backward of the all-INT8 cell (ks3_int8.py:317-429): INT8 GEMMs,
     fp16 geometry VJP, fp16 gradient handoff."""
@@ -495,10 +490,15 @@ class _KS3Int8Train(torch.autograd.Function):
         xq, xs, hq, hs, coords16 = ctx.saved_tensors
         g16 = grad_out.reshape(-1, cell.out_features).float().to(FP16)
 
-        # output-projection backward GEMM (ks3_int8.py:345-352)
+        # output-projection backward GEMM (ks3_int8.py:345-352), launched with dup (its
+        # operands are ready already; ks3_int8.py:421-424)
         gq, gs = quantize_last_dim(g16, group)
         upT_q, upT_s = requant_transpose(cell.up_codes, cell.up_scales, group, group)
-        value = w8a8_gemm_out(gq, gs, upT_q, upT_s, group, out_dtype=FP16)
+        gT_q, gT_s = quantize_transpose(g16, group)
+        hT_q, hT_s = requant_transpose(hq, hs, group, group)
+        value, dup = w8a8_gemm_pair((gq, gs, upT_q, upT_s, FP16),
+                                    (gT_q, gT_s, hT_q, hT_s, torch.float32), group)
+        dup = grad_handoff_device(dup)
 
         # geometry VJP (ks3_int8.py:354-401) -> dc in both int8 layouts + column sums
         scale, shift = cell._warp_scalars(FP16)
@@ -510,13 +510,11 @@ class _KS3Int8Train(torch.autograd.Function):
         downT_q, downT_s = requant_transpose(cell.down_codes, cell.down_scales, group, group)
         dx_dtype = grad_out.dtype if grad_out.dtype in (torch.float32, torch.bfloat16,
                                                         torch.float16) else torch.float32
-        dx = w8a8_gemm_out(v["dc_codes"], v["dc_scales"], downT_q, downT_s, group,
-                           out_dtype=dx_dtype)
         xT_q, xT_s = requant_transpose(xq, xs, group, group)
-        ddown = _handoff_gemm(v["dct_codes"], v["dct_scales"], xT_q, xT_s, group)
-        gT_q, gT_s = quantize_transpose(g16, group)
-        hT_q, hT_s = requant_transpose(hq, hs, group, group)
-        dup = _handoff_gemm(gT_q, gT_s, hT_q, hT_s, group)
+        dx, ddown = w8a8_gemm_pair((v["dc_codes"], v["dc_scales"], downT_q, downT_s, dx_dtype),
+                                   (v["dct_codes"], v["dct_scales"], xT_q, xT_s, torch.float32),
+                                   group)
+        ddown = grad_handoff_device(ddown)
 
         dx = dx.reshape(ctx.input_shape).to(grad_out.dtype)
         dres = grad_out if ctx.has_residual and ctx.needs_input_grad[7] else None

@@ -21,7 +21,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from .gemm import w8a8_gemm, w8a8_gemm_out
+from .gemm import w8a8_gemm, w8a8_gemm_out, w8a8_gemm_pair
 from .quant import (GROUP_SIZE, dequantize_last_dim, quantize_dual, quantize_last_dim,
                     quantize_last_dim_dithered, quantize_transpose, requant_transpose)
 
@@ -77,6 +77,11 @@ def w8a8_linear_backward(g: torch.Tensor, xq: torch.Tensor | None, xs: torch.Ten
     gq = gs = gtq = gts = None
     if need_dx and need_dw:
         gq, gs, gtq, gts = quantize_dual(g, group)              # along N and along M
+        if group == GROUP_SIZE:  # dX and dW in one launch (balanced over the CUs)
+            wtq, wts = wt if wt is not None else requant_transpose(wq, ws, group, group)
+            xtq, xts = xt if xt is not None else requant_transpose(xq, xs, group, group)
+            return w8a8_gemm_pair((gq, gs, wtq, wts, _out_dtype(dx_dtype)),
+                                  (gtq, gts, xtq, xts, torch.float32), group)
     if need_dx:
         if gq is None:
             gq, gs = quantize_last_dim(g, group)                # along N (per token)

@@ -12,7 +12,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from ..kernels.gemm import w8a8_gemm, w8a8_gemm_out
+from ..kernels.gemm import w8a8_gemm, w8a8_gemm_out, w8a8_gemm_pair
 from ..kernels.linear import w8a8_linear_forward_train
 from ..kernels.quant import GROUP_SIZE, SCALE_DTYPE, requant_transpose
 
@@ -132,11 +132,16 @@ class LinearCrossEntropyInt8(torch.autograd.Function):
         gsc = grad_loss.to(torch.float32).reshape(1) / n
         gq, gs, gtq, gts = cross_entropy_grad_int8(y, t, rmax, rinv, gsc, ctx.ignore_index, group)
         dx = dw = None
+        out = ctx.x_dtype if ctx.x_dtype in (torch.bfloat16, torch.float16) else torch.float32
         if ctx.needs_input_grad[0]:
             wtq, wts = requant_transpose(wq, ws, group, group)
-            out = ctx.x_dtype if ctx.x_dtype in (torch.bfloat16, torch.float16) else torch.float32
+        if ctx.needs_input_grad[0] and ctx.needs_input_grad[1]:  # one launch for both
+            dx, dw = w8a8_gemm_pair((gq, gs, wtq, wts, out), (gtq, gts, xtq, xts, torch.float32),
+                                    group)
+            dx = dx.reshape(ctx.x_shape)
+        elif ctx.needs_input_grad[0]:
             dx = w8a8_gemm_out(gq, gs, wtq, wts, group, out_dtype=out).reshape(ctx.x_shape)
-        if ctx.needs_input_grad[1]:
+        elif ctx.needs_input_grad[1]:
             dw = w8a8_gemm(gtq, gts, xtq, xts, group)
         return dx, dw, None, None, None, None, None
 
