@@ -416,7 +416,7 @@ __global__ void __launch_bounds__(256) rosa_pack_kernel(const void *__restrict__
 }
 
 // ---------------------------------------------------------------- match
-constexpr int kCH = 8;  // candidate words per chunk
+constexpr int kCH = 16;  // candidate words per chunk
 
 // 64 q bits ending at t in memory order: bit 63 = q[t], bit 63-i = q[t-i] (0 before 0).
 __device__ __forceinline__ uint64_t q_window(const uint32_t *qw, int t) {
@@ -426,65 +426,109 @@ __device__ __forceinline__ uint64_t q_window(const uint32_t *qw, int t) {
   return (m64 << (31 - b)) | (b == 31 ? 0ull : (lo >> (b + 1)));
 }
 
+// One length step of a chunk: dst(j') = src(j'+1) & (k[j'] == q[t-L]) for the chunk's
+// kCH + 2 words (the top word's right neighbour is empty); s = ~0 when q[t-L] = 1, else 0.
+// NEG: the chunk starts at word 0, so its two halo words lie before position 0 and stay
+// empty. Returns the OR of the new words.
+template <bool NEG>
+__device__ __forceinline__ uint32_t match_level(const uint32_t *src, uint32_t *dst, const uint32_t *kw,
+                                                uint32_t s) {
+  uint32_t a2 = 0;
+#pragma unroll
+  for (int c = 0; c < kCH + 2; ++c) {
+    const uint32_t right = c + 1 < kCH + 2 ? src[c + 1] : 0u;
+    uint32_t v = __builtin_amdgcn_alignbit(right, src[c], 1) & ~(kw[c] ^ s);
+    if (NEG && c < 2) v = 0u;
+    dst[c] = v;
+    a2 |= v;
+  }
+  return a2;
+}
+
+// The length walk of one chunk from A = A_1: returns the last non-empty length L (< lmax
+// or = lmax) with A = A_L. Two buffers alternate, so only the exit copies.
+template <bool NEG>
+__device__ __forceinline__ int match_walk(uint32_t *A, const uint32_t *kw, uint64_t qwin, int lmax) {
+  uint32_t B[kCH + 2];
+  uint64_t qs = qwin << 1;  // bit 63 = q[t - L] for the next length step
+  int L = 1;
+  while (L < lmax) {
+    uint32_t s = (uint32_t)((int32_t)(uint32_t)(qs >> 32) >> 31);
+    qs <<= 1;
+    if (!match_level<NEG>(A, B, kw, s)) break;
+    ++L;
+    bool stop = L >= lmax;
+    if (!stop) {
+      s = (uint32_t)((int32_t)(uint32_t)(qs >> 32) >> 31);
+      qs <<= 1;
+      if (match_level<NEG>(B, A, kw, s)) {
+        ++L;
+        continue;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kCH + 2; ++c) A[c] = B[c];
+    break;
+  }
+  return L;
+}
+
 // Best (length, endpoint) for position t >= 1. Returns length (0 = no match), sets *jout.
+// Chunks are walked from the latest candidates down; a later (older) chunk can only win with
+// a strictly longer match, so its survivors are located only when it has one.
 __device__ int match_one(const uint32_t *qw, const uint32_t *kw_all, int W, int t, int lmax,
                          int *jout) {
   const uint64_t qwin = q_window(qw, t);
   const int nw = (t - 1) / 32 + 1;  // words holding candidates j in [0, t-1]
+  const uint32_t nq0 = ((qwin >> 63) & 1) ? 0u : ~0u;  // k ^ nq == (k == q bit)
   int best_l = 0, best_j = -1;
   for (int w0 = ((nw - 1) / kCH) * kCH; w0 >= 0; w0 -= kCH) {
     if (min(lmax, 32 * (w0 + kCH)) <= best_l) break;  // cannot beat a later endpoint
     uint32_t kw[kCH + 2], A[kCH + 2];
-    const uint32_t nq0 = ((qwin >> 63) & 1) ? 0u : ~0u;  // k ^ nq == (k == q bit)
     uint32_t any = 0;
-#pragma unroll
-    for (int c = 0; c < kCH + 2; ++c) {
-      const int w = w0 - 2 + c;
-      kw[c] = (w >= 0 && w < W) ? kw_all[w] : 0u;
-      uint32_t valid = 0u;  // candidates 0 <= j' <= t-1
-      if (w >= 0) {
-        const int hi = t - 1 - 32 * w;  // last valid bit in this word
-        valid = hi >= 31 ? ~0u : (hi < 0 ? 0u : (2u << hi) - 1u);
-      }
-      A[c] = (kw[c] ^ nq0) & valid;
-      any |= A[c];
-    }
-    if (!any) continue;
-    int L = 1;
-    while (L < lmax) {
-      const uint32_t nq = ((qwin >> (63 - L)) & 1) ? 0u : ~0u;  // q[t - L]
-      uint32_t nx[kCH + 2];
-      uint32_t a2 = 0;
+    if (w0 >= 2 && 32 * (w0 + kCH) <= t) {
+      // every word of the chunk lies in [0, t-1]: no validity masks
 #pragma unroll
       for (int c = 0; c < kCH + 2; ++c) {
-        const uint32_t right = c + 1 < kCH + 2 ? A[c + 1] : 0u;
-        const uint32_t shifted = (A[c] >> 1) | (right << 31);  // A_L(j' + 1)
-        nx[c] = shifted & (kw[c] ^ nq) & (w0 - 2 + c >= 0 ? ~0u : 0u);
-        a2 |= nx[c];
+        kw[c] = kw_all[w0 - 2 + c];
+        A[c] = kw[c] ^ nq0;
+        any |= A[c];
       }
-      if (!a2) break;
+    } else {
 #pragma unroll
-      for (int c = 0; c < kCH + 2; ++c) A[c] = nx[c];
-      ++L;
+      for (int c = 0; c < kCH + 2; ++c) {
+        const int w = w0 - 2 + c;
+        const uint32_t kv = kw_all[min(max(w, 0), W - 1)];  // clamped read, masked below
+        kw[c] = (w >= 0 && w < W) ? kv : 0u;
+        const int hi = t - 1 - 32 * w;  // last valid candidate bit in this word
+        const uint32_t valid = w < 0 || hi < 0 ? 0u : (hi >= 31 ? ~0u : (2u << hi) - 1u);
+        A[c] = (kw[c] ^ nq0) & valid;
+        any |= A[c];
+      }
     }
-    // survivors at length L: report the highest j = j' + L - 1 inside this chunk's range
-    const int jlo = 32 * w0, jhi = 32 * (w0 + kCH);  // [jlo, jhi)
-    int found = -1;
+    if (!any) continue;
+    const int L = w0 >= 2 ? match_walk<false>(A, kw, qwin, lmax) : match_walk<true>(A, kw, qwin, lmax);
+    if (L <= best_l) continue;
+    // survivors at length L: the highest j = j' + L - 1 with j >= 32 w0 (the halo words' own
+    // candidates belong to the older chunk; j < 32 (w0 + kCH) holds for every survivor, as
+    // the top word has no right neighbour). In the halo, j >= 32 w0 keeps bits >= 65 - L
+    // of word 0 and bits >= 33 - L of word 1.
+    const int b0 = 65 - L;
+    const uint32_t m0 = b0 >= 32 ? 0u : (~0u << b0);
+    const uint32_t m1 = b0 <= 32 ? ~0u : (b0 >= 64 ? 0u : (~0u << (b0 - 32)));
+    int fc = -1;
+    uint32_t fm = 0u;
 #pragma unroll
-    for (int c = kCH + 1; c >= 0; --c) {
-      if (found >= 0 || A[c] == 0u) continue;
-      const int base = 32 * (w0 - 2 + c) + L - 1;  // j of bit 0
-      // keep bits whose j lies in [jlo, jhi)
-      uint32_t m = A[c];
-      const int lo_bit = jlo - base, hi_bit = jhi - base;  // allowed bit range [lo_bit, hi_bit)
-      if (hi_bit <= 0 || lo_bit >= 32) continue;
-      if (lo_bit > 0) m &= ~0u << lo_bit;
-      if (hi_bit < 32) m &= (1u << hi_bit) - 1u;
-      if (m) found = base + 31 - __clz(m);
+    for (int c = 0; c < kCH + 2; ++c) {
+      const uint32_t m = c == 0 ? (A[0] & m0) : c == 1 ? (A[1] & m1) : A[c];
+      if (m) {
+        fc = c;
+        fm = m;
+      }
     }
-    if (found >= 0 && (L > best_l || (L == best_l && found > best_j))) {
+    if (fc >= 0) {
       best_l = L;
-      best_j = found;
+      best_j = 32 * (w0 - 2 + fc) + L - 1 + 31 - (int)__clz(fm);
     }
   }
   *jout = best_j;
