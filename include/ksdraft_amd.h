@@ -104,6 +104,18 @@ int ksd_requant_transpose(const int8_t *codes, const uint16_t *scales, int64_t R
 int ksd_quantize_dual(const void *x, int x_dtype, int64_t R, int64_t C, int group,
                       int t_from_codes, int8_t *codes, uint16_t *scales, int8_t *codes_t,
                       uint16_t *scales_t, void *stream);
+/*
+ * ksd_quantize_dual (t_from_codes = 0, group 128) of an upstream gradient dY, plus its column
+ * sums: the bias gradient db = dY.float().sum(0) of an Int8Linear's backward (reference
+ * ksdraft/kernels/linear.py:75-97 through autograd's bias grad), from the same read of dY.
+ * Each 128-row tile sums its column in four 32-row parts ((p0 + p1) + (p2 + p3)); the tiles'
+ * sums are added in tile order (an fp32 sum in another order than torch's: TOL).
+ *   colsum     (C,) fp32
+ *   workspace  fp32 scratch of ceil(R/128) * C * 4 bytes; R > 0, C % 8 == 0, aligned rows
+ */
+int ksd_quantize_dual_colsum(const void *x, int x_dtype, int64_t R, int64_t C, int group,
+                             int8_t *codes, uint16_t *scales, int8_t *codes_t, uint16_t *scales_t,
+                             float *colsum, float *workspace, int64_t workspace_bytes, void *stream);
 
 /*
  * Cross entropy over the rows of fp32 logits (R, C) with class targets, the

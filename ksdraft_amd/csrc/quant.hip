@@ -272,11 +272,14 @@ struct CeSrc {
 };
 constexpr float kLog2e = 1.4426950408889634f;
 
+// col_part (optional, not with CE): (ceil(R/128), C) fp32 partial column sums of x, one row
+// per 128-row tile, each the sum of its four 32-row parts ((p0 + p1) + (p2 + p3)), every
+// part summed in row order; colsum_finalize_kernel adds the tiles in order.
 template <int DT, bool CE = false>
 __global__ __launch_bounds__(512) void quant_dual_kernel(
     const void *__restrict__ xv, int64_t R, int64_t C, int8_t *__restrict__ codes,
     uint16_t *__restrict__ scales, int8_t *__restrict__ codes_t, uint16_t *__restrict__ scales_t,
-    CeSrc ce = CeSrc{}) {
+    CeSrc ce = CeSrc{}, float *__restrict__ col_part = nullptr) {
   using T = typename Elem<DT>::T;
   constexpr int G = 128, PITCH = 145;
   __shared__ float tile[128 * PITCH];
@@ -351,6 +354,16 @@ __global__ __launch_bounds__(512) void quant_dual_kernel(
   const uint32_t am = group_max_u32<4>(__builtin_bit_cast(uint32_t, abs_max<RPT>(colv)));
   const float s = group_scale(__builtin_bit_cast(float, am));
   const int64_t gc = c0 + c;
+  if (!CE && col_part != nullptr) {  // this tile's sum of column gc (rows past R are zeros)
+    float ps = colv[0];
+#pragma unroll
+    for (int j = 1; j < RPT; ++j) ps += colv[j];
+    // the four parts of a column sit in one lane quad: pair sums, then the pairs' sum
+    // (a + b == b + a, so both lanes of a pair hold the same value)
+    ps += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, ps), 0xB1, 0xF, 0xF, false));
+    ps += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, ps), 0x4E, 0xF, 0xF, false));
+    if (part == 0 && gc < C) col_part[(int64_t)blockIdx.y * C + gc] = ps;
+  }
   if (gc >= C) return;
   if (part == 0) scales_t[gc * ngR + blockIdx.y] = scale_bits(s);
   uint32_t w[RPT / 4];
@@ -365,6 +378,16 @@ __global__ __launch_bounds__(512) void quant_dual_kernel(
     for (int j = 0; j < RPT; ++j)
       if (rbase + j < R) dst[j] = (int8_t)(w[j / 4] >> (8 * (j % 4)));
   }
+}
+
+// colsum[c] = sum over tiles t = 0, 1, ... of col_part[t, c], in tile order.
+__global__ __launch_bounds__(256) void colsum_finalize_kernel(const float *__restrict__ col_part, int64_t ntiles,
+                                                              int64_t C, float *__restrict__ colsum) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= C) return;
+  float acc = col_part[c];
+  for (int64_t t = 1; t < ntiles; ++t) acc += col_part[t * C + c];
+  colsum[c] = acc;
 }
 
 // Dual-layout quantization of an X operand (t_from_codes: the recipe quant(dequant(quant(
@@ -980,6 +1003,37 @@ extern "C" int ksd_quantize_dual(const void *x, int x_dtype, int64_t R, int64_t 
   }
 #undef KSD_DUAL
   return check_launch("quantize_dual");
+}
+
+extern "C" int ksd_quantize_dual_colsum(const void *x, int x_dtype, int64_t R, int64_t C, int group,
+                                        int8_t *codes, uint16_t *scales, int8_t *codes_t,
+                                        uint16_t *scales_t, float *colsum, float *workspace,
+                                        int64_t workspace_bytes, void *stream) {
+  if (group != 128) return fail(KSD_EINVAL, "quantize_dual_colsum: group must be 128, got %d", group);
+  if (R <= 0 || C < 0) return fail(KSD_EINVAL, "quantize_dual_colsum: needs R > 0 and C >= 0");
+  if (x_dtype != KSD_F32 && x_dtype != KSD_BF16 && x_dtype != KSD_F16)
+    return fail(KSD_ETYPE, "quantize expects float32, bfloat16 or float16 input");
+  if (C == 0) return KSD_OK;
+  if (!x || !codes || !scales || !codes_t || !scales_t || !colsum)
+    return fail(KSD_EINVAL, "quantize_dual_colsum: null pointer");
+  const int esz = x_dtype == KSD_F32 ? 4 : 2;
+  const bool fast = C % 8 == 0 && ((uintptr_t)x) % 16 == 0 && (C * esz) % 16 == 0 &&
+                    ((uintptr_t)codes) % 8 == 0 && cdiv(R, 128) <= 65535 && cdiv(C, 128) <= 0x7fffffff &&
+                    128 * C * 4 <= 0x7fffffffLL;
+  if (!fast) return fail(KSD_EINVAL, "quantize_dual_colsum: needs C %% 8 == 0 and 16-byte aligned rows");
+  const int64_t nt = cdiv(R, 128);
+  if (!workspace || workspace_bytes < nt * C * 4 || ((uintptr_t)workspace) % 4 != 0)
+    return fail(KSD_EINVAL, "quantize_dual_colsum: needs an fp32 workspace of %lld bytes",
+                (long long)(nt * C * 4));
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)cdiv(C, 128), (unsigned)nt);
+  switch (x_dtype) {
+    case KSD_F32: quant_dual_kernel<KSD_F32><<<grid, 512, 0, st>>>(x, R, C, codes, scales, codes_t, scales_t, CeSrc{}, workspace); break;
+    case KSD_BF16: quant_dual_kernel<KSD_BF16><<<grid, 512, 0, st>>>(x, R, C, codes, scales, codes_t, scales_t, CeSrc{}, workspace); break;
+    default: quant_dual_kernel<KSD_F16><<<grid, 512, 0, st>>>(x, R, C, codes, scales, codes_t, scales_t, CeSrc{}, workspace); break;
+  }
+  hipLaunchKernelGGL(colsum_finalize_kernel, dim3((unsigned)cdiv(C, 256)), dim3(256), 0, st, workspace, nt, C, colsum);
+  return check_launch("quantize_dual_colsum");
 }
 
 extern "C" int ksd_ce_row_stats(const float *logits, int64_t R, int64_t C, const int64_t *targets,

@@ -22,8 +22,9 @@ import torch
 from torch import nn
 
 from .gemm import w8a8_gemm, w8a8_gemm_out, w8a8_gemm_pair
-from .quant import (GROUP_SIZE, dequantize_last_dim, quantize_dual, quantize_last_dim,
-                    quantize_last_dim_dithered, quantize_transpose, requant_transpose)
+from .quant import (GROUP_SIZE, dequantize_last_dim, quantize_dual, quantize_dual_colsum,
+                    quantize_last_dim, quantize_last_dim_dithered, quantize_transpose,
+                    requant_transpose)
 
 
 _OUT_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
@@ -64,7 +65,8 @@ def w8a8_linear_forward_train(x2: torch.Tensor, wq: torch.Tensor, ws: torch.Tens
 def w8a8_linear_backward(g: torch.Tensor, xq: torch.Tensor | None, xs: torch.Tensor | None,
                          wq: torch.Tensor, ws: torch.Tensor, group: int = GROUP_SIZE,
                          dx_dtype: torch.dtype = torch.float32, need_dx: bool = True,
-                         need_dw: bool = True, xt: tuple | None = None, wt: tuple | None = None):
+                         need_dw: bool = True, xt: tuple | None = None, wt: tuple | None = None,
+                         want_db: bool = False):
     """INT8 backward GEMMs of the linear layer (recipe of ks3_int8.py:403-424).
 
     g (M, N) upstream gradient; xq/xs the forward's activation codes, or ``xt`` =
@@ -72,16 +74,24 @@ def w8a8_linear_backward(g: torch.Tensor, xq: torch.Tensor | None, xs: torch.Ten
     (wtq, wts) their requantized transpose when the caller already has it (e.g. from
     quantize_dual(w, t_from_codes=True)). When both gradients are needed, dY is quantized
     in both layouts in one pass (quantize_dual).
-    Returns (dx (M, K) in dx_dtype or None, dw (N, K) fp32 or None)."""
-    dx = dw = None
+    Returns (dx (M, K) in dx_dtype or None, dw (N, K) fp32 or None), and with ``want_db``
+    a third entry, the bias gradient g.float().sum(0) (N,) fp32, formed in the dual
+    quantization's pass over g when both GEMMs run."""
+    dx = dw = db = None
     gq = gs = gtq = gts = None
     if need_dx and need_dw:
-        gq, gs, gtq, gts = quantize_dual(g, group)              # along N and along M
+        if want_db:  # the column sums of g come out of the same read
+            gq, gs, gtq, gts, db = quantize_dual_colsum(g, group)
+        else:
+            gq, gs, gtq, gts = quantize_dual(g, group)          # along N and along M
         if group == GROUP_SIZE:  # dX and dW in one launch (balanced over the CUs)
             wtq, wts = wt if wt is not None else requant_transpose(wq, ws, group, group)
             xtq, xts = xt if xt is not None else requant_transpose(xq, xs, group, group)
-            return w8a8_gemm_pair((gq, gs, wtq, wts, _out_dtype(dx_dtype)),
-                                  (gtq, gts, xtq, xts, torch.float32), group)
+            dx, dw = w8a8_gemm_pair((gq, gs, wtq, wts, _out_dtype(dx_dtype)),
+                                    (gtq, gts, xtq, xts, torch.float32), group)
+            return (dx, dw, db) if want_db else (dx, dw)
+    elif want_db:
+        db = g.float().sum(0)
     if need_dx:
         if gq is None:
             gq, gs = quantize_last_dim(g, group)                # along N (per token)
@@ -98,7 +108,7 @@ def w8a8_linear_backward(g: torch.Tensor, xq: torch.Tensor | None, xs: torch.Ten
         else:
             xtq, xts = requant_transpose(xq, xs, group, group)  # X^T (K, M) along M
         dw = w8a8_gemm(gtq, gts, xtq, xts, group)                # (N, K) fp32
-    return dx, dw
+    return (dx, dw, db) if want_db else (dx, dw)
 
 
 class W8A8LinearFunction(torch.autograd.Function):
@@ -134,14 +144,15 @@ class W8A8LinearFunction(torch.autograd.Function):
         if g.dtype not in _OUT_DTYPES:
             g = g.float()
         g = g.contiguous()
-        dx, dw = w8a8_linear_backward(g, None, None, wq, ws, ctx.group, ctx.x_dtype,
-                                      ctx.needs_input_grad[0], ctx.needs_input_grad[1],
-                                      xt=(xtq, xts) if xtq is not None else None, wt=ctx.wt)
+        want_db = ctx.has_bias and ctx.needs_input_grad[2]
+        res = w8a8_linear_backward(g, None, None, wq, ws, ctx.group, ctx.x_dtype,
+                                   ctx.needs_input_grad[0], ctx.needs_input_grad[1],
+                                   xt=(xtq, xts) if xtq is not None else None, wt=ctx.wt,
+                                   want_db=want_db)
+        dx, dw = res[0], res[1]
+        db = res[2] if want_db else None
         if dx is not None:
             dx = dx.reshape(ctx.x_shape).to(ctx.x_dtype)
-        db = None
-        if ctx.has_bias and ctx.needs_input_grad[2]:
-            db = g.float().sum(0)
         dres = grad_out if len(ctx.needs_input_grad) > 6 and ctx.needs_input_grad[6] else None
         return dx, dw, db, None, None, None, dres, None
 

@@ -160,6 +160,33 @@ def quantize_dual(x: torch.Tensor, group: int = GROUP_SIZE, t_from_codes: bool =
     return codes, scales, codes_t, scales_t
 
 
+def quantize_dual_colsum(g: torch.Tensor, group: int = GROUP_SIZE):
+    """quantize_dual(g, group) plus the column sums g.float().sum(0) (a linear layer's bias
+    gradient) from the same read of g: (codes, scales, codes_t, scales_t, colsum). The
+    column sums run in another order than torch's sum (fp32, within rounding). Falls back to
+    quantize_dual + torch's sum where the fused kernel does not apply (group other than 128,
+    C % 8 != 0, no rows)."""
+    g = _float_input(g)
+    dev = _lib.require_gpu(g)
+    if g.dim() != 2:
+        raise ValueError("quantize_dual_colsum expects a 2-D tensor")
+    g = g.contiguous()
+    R, C = g.shape
+    esz = g.element_size()
+    if group != GROUP_SIZE or C % 8 or R == 0 or C == 0 or g.data_ptr() % 16 or (C * esz) % 16:
+        return (*quantize_dual(g, group), g.float().sum(0))
+    codes = torch.empty((R, C), dtype=torch.int8, device=dev)
+    scales = torch.empty((R, -(-C // group)), dtype=SCALE_DTYPE, device=dev)
+    codes_t = torch.empty((C, R), dtype=torch.int8, device=dev)
+    scales_t = torch.empty((C, -(-R // group)), dtype=SCALE_DTYPE, device=dev)
+    colsum = torch.empty(C, dtype=torch.float32, device=dev)
+    work = torch.empty(-(-R // 128) * C, dtype=torch.float32, device=dev)
+    _lib.call("ksd_quantize_dual_colsum", g.data_ptr(), _lib.dtype_code(g.dtype), R, C, group,
+              codes.data_ptr(), scales.data_ptr(), codes_t.data_ptr(), scales_t.data_ptr(),
+              colsum.data_ptr(), work.data_ptr(), work.numel() * 4, _lib.stream_ptr(dev))
+    return codes, scales, codes_t, scales_t, colsum
+
+
 def requant_transpose(codes: torch.Tensor, scales: torch.Tensor,
                       group_in: int = GROUP_SIZE, group: int = GROUP_SIZE):
     """quantize_last_dim(dequantize_last_dim(codes, scales).t(), group) in one pass.

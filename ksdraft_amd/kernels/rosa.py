@@ -148,10 +148,12 @@ class ShiftedInt8Projections(torch.autograd.Function):
             if g is None:
                 g = torch.zeros((B, T, S), dtype=torch.float32, device=x.device)
             g2 = g.reshape(-1, S).float().contiguous()
-            dx_m, dw = w8a8_linear_backward(g2, None, None, wc, ws, need_dx=True,
-                                            need_dw=need[4 + 4 * m], xt=xt)
+            want_db = ctx.has_bias[m] and need[5 + 4 * m]
+            res = w8a8_linear_backward(g2, None, None, wc, ws, need_dx=True,
+                                       need_dw=need[4 + 4 * m], xt=xt, want_db=want_db)
+            dx_m, dw = res[0], res[1]
+            db = res[2] if want_db else None
             dxs.append(dx_m)
-            db = g2.sum(0) if ctx.has_bias[m] and need[5 + 4 * m] else None
             grads.extend([dw, db, None, None])
         dx, dsig = shift_backward(x, *dxs, sig_q, sig_k, sig_v)
         return (dx if need[0] else None, dsig[0], dsig[1], dsig[2], *grads)

@@ -178,3 +178,37 @@ def test_quantize_dual_adversarial_rounding(t_from_codes):
     assert np.array_equal(s.cpu().numpy().view(np.uint16), es.view(np.uint16))
     assert np.array_equal(ct.cpu().numpy(), ect)
     assert np.array_equal(st.cpu().numpy().view(np.uint16), est.view(np.uint16))
+
+
+@pytest.mark.parametrize("shape,dtype", [
+    ((256, 384), torch.float32),      # whole tiles
+    ((300, 136), torch.float32),      # ragged rows (zeros past R) and columns
+    ((8192, 512), torch.float32),     # a Rosa projection's dY at config 4/5
+    ((129, 1024), torch.bfloat16),
+    ((64, 200), torch.float16),
+    ((70, 13), torch.float32),        # C % 8 != 0: quantize_dual + torch's sum
+])
+def test_quantize_dual_colsum(shape, dtype):
+    """The bias-gradient column sums formed in the dual quantization's pass: the codes equal
+    quantize_dual's (bit-exact against the oracle), the sums equal the float64 column sums
+    of the same values within fp32 summation error (the reference's db is torch's fp32
+    g.float().sum(0), another order). Inputs include a NaN-free wide range and exact zeros."""
+    g = torch.Generator().manual_seed(hash(shape) % 2**31)
+    x_cpu = (torch.randn(*shape, generator=g) * 2).to(dtype)
+    x_cpu[:, ::7] = 0
+    c, s, ct, st, cs = kq.quantize_dual_colsum(x_cpu.to(DEV))
+    xf = x_cpu.float().numpy()
+    ec, es = oq.quantize_last_dim(xf, 128)
+    ect, est = oq.quantize_transpose(xf, 128)
+    assert np.array_equal(c.cpu().numpy(), ec)
+    assert np.array_equal(s.cpu().numpy().view(np.uint16), es.view(np.uint16))
+    assert np.array_equal(ct.cpu().numpy(), ect)
+    assert np.array_equal(st.cpu().numpy().view(np.uint16), est.view(np.uint16))
+    want = xf.astype(np.float64).sum(0)
+    bound = np.abs(xf).astype(np.float64).sum(0) * shape[0] * 2.0 ** -24 + 1e-30
+    err = np.abs(cs.cpu().numpy().astype(np.float64) - want)
+    assert (err <= bound).all(), float((err / bound).max())
+    assert np.array_equal(cs.cpu().numpy()[::7], np.zeros_like(want[::7], dtype=np.float32))
+    # torch's fp32 sum (the reference's db) sits within the same bound of the exact sum
+    terr = np.abs(x_cpu.float().sum(0).numpy().astype(np.float64) - cs.cpu().numpy())
+    assert (terr <= 2 * bound).all()
