@@ -385,8 +385,15 @@ __global__ __launch_bounds__(256) void colsum_finalize_kernel(const float *__res
                                                               int64_t C, float *__restrict__ colsum) {
   const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (c >= C) return;
-  float acc = col_part[c];
-  for (int64_t t = 1; t < ntiles; ++t) acc += col_part[t * C + c];
+  float acc = 0.0f;
+  for (int64_t t0 = 0; t0 < ntiles; t0 += 16) {  // 16 loads in flight, then the adds in order
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = t0 + i < ntiles ? col_part[(t0 + i) * C + c] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (t0 + i < ntiles) acc = t0 + i == 0 ? v[i] : acc + v[i];
+  }
   colsum[c] = acc;
 }
 
