@@ -552,26 +552,48 @@ def cpu_baseline(x, w, dy, budget_s):
     as the reference's CPU branch computes it (gemm.py:76-82): dequantize both operands,
     then torch's fp32 matmul. torch uses every core of the process affinity; 2 warm-up
     steps, then the median of at least 5 timed steps (more while the budget lasts)."""
+    from concurrent.futures import ThreadPoolExecutor
     from oracle import quant as oq
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     X, W, DY = x.numpy(), w.numpy(), dy.numpy()
+    pool = ThreadPoolExecutor(cores)
+
+    def rows(fn, *arrs):
+        """fn over row blocks of the arrays on every core (the oracle's numpy ops release
+        the GIL; rows are independent, so the result equals one call)."""
+        n = arrs[0].shape[0]
+        cuts = [n * i // cores for i in range(cores + 1)]
+        parts = list(pool.map(lambda i: fn(*(a[cuts[i]:cuts[i + 1]] for a in arrs)),
+                              [i for i in range(cores) if cuts[i] < cuts[i + 1]]))
+        if isinstance(parts[0], tuple):
+            return tuple(np.concatenate(p) for p in zip(*parts))
+        return np.concatenate(parts)
+
+    def quant(a):  # quant.py:30-52
+        return rows(oq.quantize_last_dim, a)
+
+    def dequant(c, s):  # quant.py:55-67
+        return rows(oq.dequantize_last_dim, c, s)
 
     def mm(aq, as_, wq, ws):  # gemm.py:77-82
-        a = torch.from_numpy(oq.dequantize_last_dim(aq, as_))
-        b = torch.from_numpy(oq.dequantize_last_dim(wq, ws))
-        return a @ b.T
+        return torch.from_numpy(dequant(aq, as_)) @ torch.from_numpy(dequant(wq, ws)).T
 
     def cstep():
-        wq, ws = oq.quantize_last_dim(W)
-        xq, xs = oq.quantize_last_dim(X)
+        wq, ws = quant(W)
+        xq, xs = quant(X)
         mm(xq, xs, wq, ws)
-        gq, gs = oq.quantize_last_dim(DY)
-        wtq, wts = oq.requant_transpose(wq, ws)
+        gq, gs = quant(DY)
+        wtq, wts = quant(np.ascontiguousarray(dequant(wq, ws).T))   # requant W^T
         mm(gq, gs, wtq, wts)
-        gtq, gts = oq.quantize_transpose(DY)
-        xtq, xts = oq.requant_transpose(xq, xs)
+        gtq, gts = quant(np.ascontiguousarray(DY.T))                 # quantize dY^T
+        xtq, xts = quant(np.ascontiguousarray(dequant(xq, xs).T))   # requant X^T
         mm(gtq, gts, xtq, xts)
+
+    # the threaded restatement is the oracle's, block by block
+    chk = quant(X[:512])
+    ref = oq.quantize_last_dim(X[:512])
+    assert np.array_equal(chk[0], ref[0]) and np.array_equal(chk[1].view(np.uint16), ref[1].view(np.uint16))
 
     for _ in range(2):
         cstep()
@@ -581,6 +603,7 @@ def cpu_baseline(x, w, dy, budget_s):
         t0 = time.perf_counter()
         cstep()
         times.append(time.perf_counter() - t0)
+    pool.shutdown()
     t = float(np.median(times))
     cfg = torch.__config__.show()
     blas = "MKL" if "MKL" in cfg else ("OpenBLAS" if "OpenBLAS" in cfg else "torch BLAS")
@@ -591,7 +614,7 @@ def cpu_baseline(x, w, dy, budget_s):
                    f"three dequantize + fp32 matmul GEMMs), median of {len(times)} after 2 "
                    f"warm-ups, {t:.3f} s/step; host {_cpu_model()}, torch "
                    f"{torch.__version__} with {torch.get_num_threads()} threads ({blas}); "
-                   f"numpy quantization single-threaded"),
+                   f"quantizers: the oracle's numpy restatement over {cores} threads of row blocks"),
     }
 
 
