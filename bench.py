@@ -366,7 +366,7 @@ def rosa_kernel_times(dev, reps):
         "rosa_shift_quant_dual_f32": (lambda: R.shift_quantize_dual(x32, sig, sig, sig),
                                       4 * BTd + 6 * (BTd + 2 * BTd // 128), None),
         "rosa_shift_backward_f32": (lambda: R.shift_backward(x32, *gin, sig, sig, sig), 20 * BTd, None),
-        "rosa_pack_bits_x3": (lambda: [R.pack_bits(t) for t in (q, k, v)], 3 * (4 * BTS + BTS // 8), None),
+        "rosa_pack_bits_x3": (lambda: R.pack_bits3(q, k, v), 3 * (4 * BTS + BTS // 8), None),
         "rosa_match": (lambda: R.match_packed(*flat, T, want_j=True), None, pairs),
         "rosa_hard_out": (lambda: R.hard_out(sign.reshape(Bq, S, T), payload), BTS + 4 * BTS, None),
         "rosa_credits": (credits, None, pairs),

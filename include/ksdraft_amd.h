@@ -448,6 +448,11 @@ int ksd_rosa_shift_backward(const void *x, int x_dtype, int64_t B, int64_t T, in
  */
 int ksd_rosa_pack_bits(const void *x, int x_dtype, int64_t B, int64_t T, int64_t S,
                        uint32_t *bits, void *stream);
+/* The same for q, k and v of one shape in one launch (the three pack_bits of
+ * rosa_credit_gpu.py:68-70). */
+int ksd_rosa_pack_bits3(const void *q, const void *k, const void *v, int x_dtype, int64_t B,
+                        int64_t T, int64_t S, uint32_t *q_bits, uint32_t *k_bits, uint32_t *v_bits,
+                        void *stream);
 
 /*
  * R2 — _match_payload_sign (reference ksdraft/model/rosa.py:40-98) on packed bits: for

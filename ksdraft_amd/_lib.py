@@ -64,6 +64,7 @@ SIGNATURES = {
     "ksd_rosa_shift_backward_blocks": [_I64, _I64, _P],
     "ksd_rosa_shift_backward": [_P, _INT, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "ksd_rosa_pack_bits": [_P, _INT, _I64, _I64, _I64, _P, _P],
+    "ksd_rosa_pack_bits3": [_P, _P, _P, _INT, _I64, _I64, _I64, _P, _P, _P, _P],
     "ksd_transfer_cos": [_P, _P, _I64, _I64, _P, _P, _P],
     "ksd_transfer_grad": [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _INT, _P],
     "ksd_injection_update": [_P, _P, _P, _P, _P, _I64, _I64, _P, _P],

@@ -395,14 +395,20 @@ __global__ __launch_bounds__(256) void rosa_shift_bwd_kernel(
 
 // ---------------------------------------------------------------- bit packing
 // (B, T, S) -> words (B, S, W): one thread per (stream s, word w).
+// Up to three projections of one shape in one launch: blockIdx.z = which * B + b.
+struct PackSrc {
+  const void *x[3];
+  uint32_t *bits[3];
+};
 template <int DT>
-__global__ void __launch_bounds__(256) rosa_pack_kernel(const void *__restrict__ x, int64_t T,
-                                                        int64_t S, int64_t W,
-                                                        uint32_t *__restrict__ bits) {
+__global__ void __launch_bounds__(256) rosa_pack_kernel(PackSrc ps, int64_t B, int64_t T,
+                                                        int64_t S, int64_t W) {
   using E = Elem<DT>;
   const int64_t s = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t w = blockIdx.y, b = blockIdx.z;
+  const int64_t w = blockIdx.y, which = blockIdx.z / B, b = blockIdx.z % B;
   if (s >= S) return;
+  const void *x = which == 0 ? ps.x[0] : which == 1 ? ps.x[1] : ps.x[2];
+  uint32_t *bits = which == 0 ? ps.bits[0] : which == 1 ? ps.bits[1] : ps.bits[2];
   const typename E::T *xb = (const typename E::T *)x + b * T * S + s;
   // all 32 loads first (rows past T clamped to a valid row and masked below)
   float v[32];
@@ -560,23 +566,63 @@ __global__ void __launch_bounds__(256) rosa_match_kernel(const uint32_t *__restr
   }
 }
 
-// (B, S, T) int8 sign -> (B, T, S) payload[s] * sign in the output dtype, via a 64x64 tile.
+// (B, S, T) int8 sign -> (B, T, S) payload[s] * sign in the output dtype, via a 64x64 tile:
+// a thread loads 4 positions of a stream as one word (four streams per thread) and stores
+// 4 consecutive streams of a position (16 bytes for fp32, 8 for 16-bit outputs).
 template <int DT>
 __global__ void __launch_bounds__(256) rosa_hard_kernel(const int8_t *__restrict__ sign,
                                                         const float *__restrict__ payload,
                                                         int64_t T, int64_t S, void *__restrict__ out) {
-  __shared__ int8_t tile[64][65];
+  __shared__ __attribute__((aligned(16))) int8_t tile[64][68];  // [stream][position]
   const int64_t b = blockIdx.z;
   const int64_t t0 = (int64_t)blockIdx.x * 64, s0 = (int64_t)blockIdx.y * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int r = ty; r < 64; r += 4) {  // rows = streams, coalesced along t
-    const int64_t s = s0 + r, t = t0 + tx;
-    tile[r][tx] = (s < S && t < T) ? sign[(b * S + s) * T + t] : 0;
+  const int r = threadIdx.x >> 4, c = threadIdx.x & 15;
+  const bool vec_in = (T & 3) == 0 && t0 + 64 <= T;  // whole aligned words of the tile
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int sl = r + 16 * p;
+    const int64_t s = s0 + sl, t = t0 + 4 * c;
+    uint32_t w = 0u;
+    if (s < S) {
+      const int8_t *src = sign + (b * S + s) * T + t;
+      if (vec_in) {
+        w = *(const uint32_t *)src;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (t + j < T) w |= (uint32_t)(uint8_t)src[j] << (8 * j);
+      }
+    }
+    *(uint32_t *)&tile[sl][4 * c] = w;
   }
   __syncthreads();
-  for (int r = ty; r < 64; r += 4) {  // rows = positions, coalesced along s
-    const int64_t t = t0 + r, s = s0 + tx;
-    if (t < T && s < S) store_out<DT>(out, (b * T + t) * S + s, payload[s] * (float)tile[tx][r]);
+  float pay[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) pay[j] = s0 + 4 * c + j < S ? payload[s0 + 4 * c + j] : 0.0f;
+  const bool vec_out = (S & 3) == 0 && s0 + 4 * c + 4 <= S;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int tl = r + 16 * p;
+    const int64_t t = t0 + tl;
+    if (t >= T) continue;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = pay[j] * (float)tile[4 * c + j][tl];
+    const int64_t o = (b * T + t) * S + s0 + 4 * c;
+    if (vec_out) {
+      if constexpr (DT == KSD_F32) {
+        *(float4 *)((float *)out + o) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+        uint16_t h[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) h[j] = DT == KSD_BF16 ? f32_to_bf16(v[j]) : f16_bits(v[j]);
+        *(uint2 *)((uint16_t *)out + o) = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (s0 + 4 * c + j < S) store_out<DT>(out, o + j, v[j]);
+    }
   }
 }
 
@@ -718,6 +764,19 @@ extern "C" int ksd_rosa_shift_backward(const void *x, int x_dtype, int64_t B, in
   return check_launch("rosa_shift_backward");
 }
 
+static int launch_pack(const PackSrc &ps, int n, int x_dtype, int64_t B, int64_t T, int64_t S,
+                       hipStream_t st) {
+  const int64_t W = cdiv(T, 32);
+  if (W > 65535 || n * B > 65535) return fail(KSD_EINVAL, "rosa_pack_bits: T or B too large");
+  dim3 grid((unsigned)cdiv(S, 256), (unsigned)W, (unsigned)(n * B));
+  switch (x_dtype) {
+    case KSD_F32: hipLaunchKernelGGL(rosa_pack_kernel<KSD_F32>, grid, dim3(256), 0, st, ps, B, T, S, W); break;
+    case KSD_BF16: hipLaunchKernelGGL(rosa_pack_kernel<KSD_BF16>, grid, dim3(256), 0, st, ps, B, T, S, W); break;
+    default: hipLaunchKernelGGL(rosa_pack_kernel<KSD_F16>, grid, dim3(256), 0, st, ps, B, T, S, W); break;
+  }
+  return check_launch("rosa_pack_bits");
+}
+
 extern "C" int ksd_rosa_pack_bits(const void *x, int x_dtype, int64_t B, int64_t T, int64_t S,
                                   uint32_t *bits, void *stream) {
   if (B < 0 || T < 0 || S < 0) return fail(KSD_EINVAL, "rosa_pack_bits: negative shape");
@@ -725,16 +784,20 @@ extern "C" int ksd_rosa_pack_bits(const void *x, int x_dtype, int64_t B, int64_t
     return fail(KSD_ETYPE, "rosa_pack_bits: x must be float32, bfloat16 or float16");
   if (B == 0 || T == 0 || S == 0) return KSD_OK;
   if (!x || !bits) return fail(KSD_EINVAL, "rosa_pack_bits: null pointer");
-  const int64_t W = cdiv(T, 32);
-  if (W > 65535 || B > 65535) return fail(KSD_EINVAL, "rosa_pack_bits: T or B too large");
-  dim3 grid((unsigned)cdiv(S, 256), (unsigned)W, (unsigned)B);
-  hipStream_t st = (hipStream_t)stream;
-  switch (x_dtype) {
-    case KSD_F32: hipLaunchKernelGGL(rosa_pack_kernel<KSD_F32>, grid, dim3(256), 0, st, x, T, S, W, bits); break;
-    case KSD_BF16: hipLaunchKernelGGL(rosa_pack_kernel<KSD_BF16>, grid, dim3(256), 0, st, x, T, S, W, bits); break;
-    default: hipLaunchKernelGGL(rosa_pack_kernel<KSD_F16>, grid, dim3(256), 0, st, x, T, S, W, bits); break;
-  }
-  return check_launch("rosa_pack_bits");
+  const PackSrc ps{{x, x, x}, {bits, bits, bits}};
+  return launch_pack(ps, 1, x_dtype, B, T, S, (hipStream_t)stream);
+}
+
+extern "C" int ksd_rosa_pack_bits3(const void *q, const void *k, const void *v, int x_dtype, int64_t B,
+                                   int64_t T, int64_t S, uint32_t *q_bits, uint32_t *k_bits,
+                                   uint32_t *v_bits, void *stream) {
+  if (B < 0 || T < 0 || S < 0) return fail(KSD_EINVAL, "rosa_pack_bits3: negative shape");
+  if (x_dtype != KSD_F32 && x_dtype != KSD_BF16 && x_dtype != KSD_F16)
+    return fail(KSD_ETYPE, "rosa_pack_bits3: inputs must be float32, bfloat16 or float16");
+  if (B == 0 || T == 0 || S == 0) return KSD_OK;
+  if (!q || !k || !v || !q_bits || !k_bits || !v_bits) return fail(KSD_EINVAL, "rosa_pack_bits3: null pointer");
+  const PackSrc ps{{q, k, v}, {q_bits, k_bits, v_bits}};
+  return launch_pack(ps, 3, x_dtype, B, T, S, (hipStream_t)stream);
 }
 
 extern "C" int ksd_rosa_match(const uint32_t *q_bits, const uint32_t *k_bits, const uint32_t *v_bits,

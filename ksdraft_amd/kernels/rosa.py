@@ -174,6 +174,26 @@ def pack_bits(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def pack_bits3(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+    """pack_bits of three (B, T, S) projections of one shape and dtype, in one launch."""
+    dev = _lib.require_gpu(q, k, v)
+    if q.dim() != 3 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("q, k, v must be (B, T, S) tensors of one shape")
+    xs = []
+    for x in (q, k, v):
+        if not torch.is_floating_point(x) or x.dtype == torch.float64:
+            x = x.float()
+        xs.append(x.contiguous())
+    if not (xs[0].dtype == xs[1].dtype == xs[2].dtype):
+        xs = [x.float() for x in xs]
+    B, T, S = q.shape
+    outs = [torch.empty((B, S, -(-T // 32)), dtype=torch.int32, device=dev) for _ in range(3)]
+    _lib.call("ksd_rosa_pack_bits3", xs[0].data_ptr(), xs[1].data_ptr(), xs[2].data_ptr(),
+              _lib.dtype_code(xs[0].dtype), B, T, S, outs[0].data_ptr(), outs[1].data_ptr(),
+              outs[2].data_ptr(), _lib.stream_ptr(dev))
+    return outs
+
+
 def match_packed(q_bits: torch.Tensor, k_bits: torch.Tensor, v_bits: torch.Tensor, T: int,
                  max_match_len: int | None = None, want_j: bool = False):
     """Longest-suffix match on packed bits (n_streams, ceil(T/32)).

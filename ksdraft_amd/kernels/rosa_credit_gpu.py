@@ -28,7 +28,7 @@ class HardRosaGPU(torch.autograd.Function):
         if q.shape[1] > MAX_WINDOW:
             raise ValueError(f"GPU exact credits support T <= {MAX_WINDOW}; got T={q.shape[1]}")
         B, T, S = q.shape
-        bits = [R.pack_bits(t.detach()) for t in (q, k, v)]
+        bits = R.pack_bits3(q.detach(), k.detach(), v.detach())
         sign, mj = R.match_packed(*(b.reshape(B * S, -1) for b in bits), T, want_j=True)
         sign = sign.reshape(B, S, T)
         ctx.save_for_backward(q, k, v, payload, sign, mj, *bits)

@@ -147,7 +147,7 @@ class RosaMixer(nn.Module):
             q_in, k_in, v_in = self._shifted(x)
             q_full, k_full, v_full = self.q_proj(q_in), self.k_proj(k_in), self.v_proj(v_in)
         with torch.no_grad():
-            qb, kb, vb = (R.pack_bits(t.detach()) for t in (q_full, k_full, v_full))
+            qb, kb, vb = R.pack_bits3(q_full.detach(), k_full.detach(), v_full.detach())
             B, T, S = q_full.shape
             sign, _ = R.match_packed(qb.reshape(B * S, -1), kb.reshape(B * S, -1),
                                      vb.reshape(B * S, -1), T)

@@ -83,6 +83,31 @@ def test_pack_bits_dtypes():
             assert np.array_equal(got, bits[..., t]), (dt, t)
 
 
+@pytest.mark.parametrize("shape", [(2, 70, 37), (1, 2048, 512), (3, 64, 64), (1, 5, 3)])
+def test_pack_bits3_equals_three_packs(shape):
+    """One launch for q, k and v gives each projection's pack_bits words."""
+    rng = np.random.default_rng(sum(shape))
+    xs = [_g(rng.standard_normal(shape).astype(np.float32)) for _ in range(3)]
+    got = R.pack_bits3(*xs)
+    for g, x in zip(got, xs):
+        assert torch.equal(g, R.pack_bits(x))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,S,T", [(2, 37, 70), (1, 512, 2048), (3, 64, 64), (1, 3, 5), (2, 130, 66)])
+def test_hard_out_matches_payload_times_sign(B, S, T, dtype):
+    """hard_out = (payload[s] * sign[b, s, t]) transposed to (B, T, S) in the output dtype
+    (rosa_credit_gpu.py:75), including tiles cut by S and T (whole-word and byte loads,
+    vector and scalar stores)."""
+    rng = np.random.default_rng(B * 1000 + S + T)
+    sign = np.where(rng.random((B, S, T)) < 0.5, -1, 1).astype(np.int8)
+    pay = rng.standard_normal(S).astype(np.float32)
+    out = R.hard_out(_g(sign), _g(pay), dtype)
+    want = torch.from_numpy((pay[None, :, None] * sign.astype(np.float32)).transpose(0, 2, 1).copy()).to(dtype)
+    assert out.shape == (B, T, S)
+    assert torch.equal(out.cpu(), want)
+
+
 def test_match_payload_sign_api_kats():
     q, k, v = [[0, 1, 1, 1]], [[1, 0, 1, 1]], [[1, 0, 0, 1]]
     got = _match_payload_sign(_g(np.array(q, np.int8)), _g(np.array(k, np.int8)),
