@@ -39,7 +39,7 @@ sys.path.insert(0, ROOT)
 
 from ksdraft_amd.kernels.linear import (w8a8_linear_backward,  # noqa: E402
                                         w8a8_linear_forward_train)
-from ksdraft_amd.kernels.quant import (quantize_dual, quantize_last_dim,  # noqa: E402
+from ksdraft_amd.kernels.quant import (quantize_dual, quantize_dual2, quantize_last_dim,  # noqa: E402
                                        quantize_transpose, requant_transpose)
 from ksdraft_amd.kernels.gemm import w8a8_gemm_out, w8a8_gemm_pair  # noqa: E402
 from ksdraft_amd.train import adamw_requant_, cross_entropy_grad_int8, cross_entropy_stats  # noqa: E402
@@ -108,9 +108,11 @@ def make_inputs(dev):
 
 
 def step(x, w, dy):
-    # W's row codes and the requantized W^T that dX needs, from one pass over W
-    wq, ws, wtq, wts = quantize_dual(w, t_from_codes=True)
-    y, xtq, xts = w8a8_linear_forward_train(x, wq, ws, None, out_dtype=torch.float32)
+    # W's row codes and the requantized W^T that dX needs, and X's codes and requantized
+    # X^T that dW needs, from one pass over each, in one launch (Int8Linear's training
+    # forward does the same when its codes are stale)
+    (wq, ws, wtq, wts), xpre = quantize_dual2(w, x)
+    y, xtq, xts = w8a8_linear_forward_train(x, wq, ws, None, out_dtype=torch.float32, xpre=xpre)
     # dX and dW in one launch (w8a8_linear_backward pairs them)
     dx, dw = w8a8_linear_backward(dy, None, None, wq, ws, dx_dtype=torch.float32, xt=(xtq, xts),
                                   wt=(wtq, wts))
@@ -156,6 +158,8 @@ def kernel_times(x, w, dy, reps):
         "quantize_W_dual": (lambda: quantize_dual(w, t_from_codes=True), 4 * N * K + 2 * (N * K + 2 * N * K // 128)),
         "quantize_X_dual": (lambda: quantize_dual(x, t_from_codes=True), 4 * M * K + 2 * (M * K + 2 * M * K // 128)),
         "gemm_fwd": (lambda: w8a8_gemm_out(xq, xs, wq, ws), None),
+        # W's and X's dual quantization as one launch (the step's first kernel)
+        "quantize_W_X_dual2": (lambda: quantize_dual2(w, x), 4 * (M + N) * K + 2 * ((M + N) * K + 2 * (M + N) * K // 128)),
         "quantize_dY_dual": (lambda: quantize_dual(dy), 4 * M * N + 2 * (M * N + 2 * M * N // 128)),
         "gemm_dX": (lambda: w8a8_gemm_out(gq, gs, wtq, wts), None),
         "gemm_dW": (lambda: w8a8_gemm_out(gtq, gts, xtq, xts), None),

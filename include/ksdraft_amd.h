@@ -105,6 +105,17 @@ int ksd_quantize_dual(const void *x, int x_dtype, int64_t R, int64_t C, int grou
                       int t_from_codes, int8_t *codes, uint16_t *scales, int8_t *codes_t,
                       uint16_t *scales_t, void *stream);
 /*
+ * ksd_quantize_dual with t_from_codes = 1 (the X-operand recipe) of two tensors of one dtype
+ * in one launch: a linear layer's fp32 weight and its input when both are quantized for a
+ * training forward (reference ksdraft/kernels/linear.py:46-56 and :69 with the X^T recipe of
+ * ks3_int8.py:417-420). The outputs are those of two ksd_quantize_dual calls; shapes the
+ * fused kernel does not take (C % 8 != 0, unaligned rows) run as two calls. Group 128.
+ */
+int ksd_quantize_dual2(const void *x0, int64_t R0, int64_t C0, int8_t *codes0, uint16_t *scales0,
+                       int8_t *codes_t0, uint16_t *scales_t0, const void *x1, int64_t R1,
+                       int64_t C1, int8_t *codes1, uint16_t *scales1, int8_t *codes_t1,
+                       uint16_t *scales_t1, int x_dtype, int group, void *stream);
+/*
  * ksd_quantize_dual (t_from_codes = 0, group 128) of an upstream gradient dY, plus its column
  * sums: the bias gradient db = dY.float().sum(0) of an Int8Linear's backward (reference
  * ksdraft/kernels/linear.py:75-97 through autograd's bias grad), from the same read of dY.

@@ -35,6 +35,7 @@ SIGNATURES = {
     "ksd_quantize_transpose": [_P, _INT, _I64, _I64, _INT, _P, _P, _P],
     "ksd_requant_transpose": [_P, _P, _I64, _I64, _INT, _INT, _P, _P, _P],
     "ksd_quantize_dual": [_P, _INT, _I64, _I64, _INT, _INT, _P, _P, _P, _P, _P],
+    "ksd_quantize_dual2": [_P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _INT, _INT, _P],
     "ksd_quantize_dual_colsum": [_P, _INT, _I64, _I64, _INT, _P, _P, _P, _P, _P, _P, _I64, _P],
     "ksd_ce_row_stats": [_P, _I64, _I64, _P, _I64, _P, _P, _P, _P],
     "ksd_ce_backward_quant_dual": [_P, _I64, _I64, _P, _P, _P, _I64, _P, _INT, _P, _P, _P, _P, _P, _P],

@@ -404,15 +404,16 @@ __global__ __launch_bounds__(256) void colsum_finalize_kernel(const float *__res
 // instead of 74 KB, so four blocks fit a CU. The column pass dequantizes code * scale
 // (exact in fp32, as in quant_dual_kernel) before its amax and codes.
 template <int DT>
-__global__ __launch_bounds__(512) void quant_dual_codes_kernel(
+__device__ __forceinline__ void dual_codes_tile(
     const void *__restrict__ xv, int64_t R, int64_t C, int8_t *__restrict__ codes,
-    uint16_t *__restrict__ scales, int8_t *__restrict__ codes_t, uint16_t *__restrict__ scales_t) {
+    uint16_t *__restrict__ scales, int8_t *__restrict__ codes_t, uint16_t *__restrict__ scales_t,
+    int64_t bx, int64_t by) {
   using T = typename Elem<DT>::T;
   constexpr int G = 128, PB = 132;
   __shared__ __attribute__((aligned(16))) int8_t tq[128 * PB];  // [column][row]
   __shared__ __attribute__((aligned(16))) float srow[128];
   const int tid = threadIdx.x;
-  const int64_t c0 = (int64_t)blockIdx.x * 128, r0 = (int64_t)blockIdx.y * 128;
+  const int64_t c0 = bx * 128, r0 = by * 128;
   const int64_t ngC = (C + G - 1) / G, ngR = (R + G - 1) / G;
   const int64_t nrows = min((int64_t)128, R - r0);
   const auto rq = rsrc(codes + r0 * C, nrows * C);
@@ -468,7 +469,7 @@ __global__ __launch_bounds__(512) void quant_dual_codes_kernel(
   const float s = group_scale(__builtin_bit_cast(float, am));
   const int64_t gc = c0 + c;
   if (gc >= C) return;
-  if (part == 0) scales_t[gc * ngR + blockIdx.y] = scale_bits(s);
+  if (part == 0) scales_t[gc * ngR + by] = scale_bits(s);
   uint32_t w[RPT / 4];
   codes_rcp_packed<RPT>(colv, s, w);
   int8_t *dst = codes_t + gc * R + r0 + part * RPT;
@@ -481,6 +482,33 @@ __global__ __launch_bounds__(512) void quant_dual_codes_kernel(
     for (int j = 0; j < RPT; ++j)
       if (rbase + j < R) dst[j] = (int8_t)(w[j / 4] >> (8 * (j % 4)));
   }
+}
+
+template <int DT>
+__global__ __launch_bounds__(512) void quant_dual_codes_kernel(
+    const void *__restrict__ xv, int64_t R, int64_t C, int8_t *__restrict__ codes,
+    uint16_t *__restrict__ scales, int8_t *__restrict__ codes_t, uint16_t *__restrict__ scales_t) {
+  dual_codes_tile<DT>(xv, R, C, codes, scales, codes_t, scales_t, blockIdx.x, blockIdx.y);
+}
+
+// Two X operands (e.g. a layer's weight and its input) in one launch: blocks
+// [0, tiles of the first) take the first tensor's 128 x 128 tiles in row-major tile order,
+// the rest the second's.
+struct DualOperand {
+  const void *x;
+  int64_t R, C;
+  int8_t *codes;
+  uint16_t *scales;
+  int8_t *codes_t;
+  uint16_t *scales_t;
+};
+template <int DT>
+__global__ __launch_bounds__(512) void quant_dual_codes2_kernel(DualOperand a, DualOperand b) {
+  const int64_t ta = ((a.C + 127) / 128) * ((a.R + 127) / 128);
+  const int64_t i = blockIdx.x;
+  const DualOperand &o = i < ta ? a : b;
+  const int64_t j = i < ta ? i : i - ta, tc = (o.C + 127) / 128;
+  dual_codes_tile<DT>(o.x, o.R, o.C, o.codes, o.scales, o.codes_t, o.scales_t, j % tc, j / tc);
 }
 
 // ---------------------------------------------------------------- cross entropy
@@ -1010,6 +1038,40 @@ extern "C" int ksd_quantize_dual(const void *x, int x_dtype, int64_t R, int64_t 
   }
 #undef KSD_DUAL
   return check_launch("quantize_dual");
+}
+
+extern "C" int ksd_quantize_dual2(const void *x0, int64_t R0, int64_t C0, int8_t *codes0,
+                                  uint16_t *scales0, int8_t *codes_t0, uint16_t *scales_t0,
+                                  const void *x1, int64_t R1, int64_t C1, int8_t *codes1,
+                                  uint16_t *scales1, int8_t *codes_t1, uint16_t *scales_t1,
+                                  int x_dtype, int group, void *stream) {
+  if (group != 128) return fail(KSD_EINVAL, "quantize_dual2: group must be 128, got %d", group);
+  if (R0 < 0 || C0 < 0 || R1 < 0 || C1 < 0) return fail(KSD_EINVAL, "quantize_dual2: negative shape");
+  if (x_dtype != KSD_F32 && x_dtype != KSD_BF16 && x_dtype != KSD_F16)
+    return fail(KSD_ETYPE, "quantize expects float32, bfloat16 or float16 input");
+  const int esz = x_dtype == KSD_F32 ? 4 : 2;
+  auto fast = [&](const void *x, int64_t R, int64_t C, const int8_t *codes) {
+    return R > 0 && C > 0 && C % 8 == 0 && ((uintptr_t)x) % 16 == 0 && (C * esz) % 16 == 0 &&
+           ((uintptr_t)codes) % 8 == 0 && 128 * C * 4 <= 0x7fffffffLL;
+  };
+  if (!fast(x0, R0, C0, codes0) || !fast(x1, R1, C1, codes1) ||
+      cdiv(C0, 128) * cdiv(R0, 128) + cdiv(C1, 128) * cdiv(R1, 128) > 0x7fffffffLL) {
+    int rc = ksd_quantize_dual(x0, x_dtype, R0, C0, group, 1, codes0, scales0, codes_t0, scales_t0, stream);
+    if (rc) return rc;
+    return ksd_quantize_dual(x1, x_dtype, R1, C1, group, 1, codes1, scales1, codes_t1, scales_t1, stream);
+  }
+  if (!codes0 || !scales0 || !codes_t0 || !scales_t0 || !codes1 || !scales1 || !codes_t1 || !scales_t1)
+    return fail(KSD_EINVAL, "quantize_dual2: null pointer");
+  const DualOperand a{x0, R0, C0, codes0, scales0, codes_t0, scales_t0};
+  const DualOperand b{x1, R1, C1, codes1, scales1, codes_t1, scales_t1};
+  const unsigned nblk = (unsigned)(cdiv(C0, 128) * cdiv(R0, 128) + cdiv(C1, 128) * cdiv(R1, 128));
+  hipStream_t st = (hipStream_t)stream;
+  switch (x_dtype) {
+    case KSD_F32: quant_dual_codes2_kernel<KSD_F32><<<nblk, 512, 0, st>>>(a, b); break;
+    case KSD_BF16: quant_dual_codes2_kernel<KSD_BF16><<<nblk, 512, 0, st>>>(a, b); break;
+    default: quant_dual_codes2_kernel<KSD_F16><<<nblk, 512, 0, st>>>(a, b); break;
+  }
+  return check_launch("quantize_dual2");
 }
 
 extern "C" int ksd_quantize_dual_colsum(const void *x, int x_dtype, int64_t R, int64_t C, int group,

@@ -22,9 +22,9 @@ import torch
 from torch import nn
 
 from .gemm import w8a8_gemm, w8a8_gemm_out, w8a8_gemm_pair
-from .quant import (GROUP_SIZE, dequantize_last_dim, quantize_dual, quantize_dual_colsum,
-                    quantize_last_dim, quantize_last_dim_dithered, quantize_transpose,
-                    requant_transpose)
+from .quant import (GROUP_SIZE, dequantize_last_dim, quantize_dual, quantize_dual2,
+                    quantize_dual_colsum, quantize_last_dim, quantize_last_dim_dithered,
+                    quantize_transpose, requant_transpose)
 
 
 _OUT_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
@@ -51,12 +51,14 @@ def w8a8_linear_forward(x2: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
 def w8a8_linear_forward_train(x2: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor,
                               bias: torch.Tensor | None, group: int = GROUP_SIZE,
                               out_dtype: torch.dtype | None = None,
-                              residual: torch.Tensor | None = None):
+                              residual: torch.Tensor | None = None, xpre: tuple | None = None):
     """w8a8_linear_forward that also builds dW's activation operand in the same pass
     over x: X^T requantized along the tokens from the row codes (the double-quant recipe
     of ks3_int8.py:417-420, quantize_dual). The backward needs only that operand, not
-    the row codes. Returns (y, xtq (K, M), xts (K, ceil(M/group)))."""
-    xq, xs, xtq, xts = quantize_dual(x2, group, t_from_codes=True)
+    the row codes. ``xpre``: x's (codes, scales, codes_t, scales_t) when the caller has
+    them already (quantize_dual2 with the weight). Returns (y, xtq (K, M), xts (K,
+    ceil(M/group)))."""
+    xq, xs, xtq, xts = xpre if xpre is not None else quantize_dual(x2, group, t_from_codes=True)
     y = w8a8_gemm_out(xq, xs, wq, ws, group, bias=bias,
                       out_dtype=_out_dtype(out_dtype or x2.dtype), residual=residual)
     return y, xtq, xts
@@ -117,14 +119,14 @@ class W8A8LinearFunction(torch.autograd.Function):
     is the upstream gradient itself."""
 
     @staticmethod
-    def forward(ctx, x, weight, bias, wq, ws, group, residual=None, wt=None):
+    def forward(ctx, x, weight, bias, wq, ws, group, residual=None, wt=None, xpre=None):
         K = x.shape[-1]
         N = wq.shape[0]
         x2 = x.reshape(-1, K)
         r2 = None if residual is None else residual.reshape(-1, N)
         if ctx.needs_input_grad[1]:
             # dW's operand X^T comes out of the same pass over x as the forward's codes
-            y, xtq, xts = w8a8_linear_forward_train(x2, wq, ws, bias, group, x.dtype, r2)
+            y, xtq, xts = w8a8_linear_forward_train(x2, wq, ws, bias, group, x.dtype, r2, xpre)
         else:
             y, _, _ = w8a8_linear_forward(x2, wq, ws, bias, group, x.dtype, r2)
             xtq = xts = None
@@ -154,7 +156,7 @@ class W8A8LinearFunction(torch.autograd.Function):
         if dx is not None:
             dx = dx.reshape(ctx.x_shape).to(ctx.x_dtype)
         dres = grad_out if len(ctx.needs_input_grad) > 6 and ctx.needs_input_grad[6] else None
-        return dx, dw, db, None, None, None, dres, None
+        return dx, dw, db, None, None, None, dres, None, None
 
 
 class Int8Linear(nn.Module):
@@ -238,13 +240,25 @@ class Int8Linear(nn.Module):
         # live fp32 masters stay authoritative (linear.py:66): the codes are rebuilt on every
         # call unless an optimizer handed over the codes of the master as it is now
         # (_codes_current); dithered codes are redrawn every call
+        train = torch.is_grad_enabled() and (self.weight.requires_grad or x.requires_grad
+                                             or (residual is not None and residual.requires_grad))
+        xpre = None
         if not self._codes_current():
             self._codes_key = None
-            self._quantize_weight()
+            w = self.weight.detach()
+            if (train and not self.ste_training and self.training and self.weight.requires_grad
+                    and float(getattr(self, "_dither", 0.0)) == 0.0 and w.dim() == 2
+                    and w.dtype == torch.float32 and x.dtype == torch.float32):
+                # a training forward quantizes the master (both layouts) and x (both
+                # layouts) in one launch
+                (codes, scales, ct, st), xpre = quantize_dual2(w, x.reshape(-1, x.shape[-1]))
+                self.weight_codes, self.weight_scales = codes, scales
+                self._wt, self._wt_src = (ct, st), codes
+            else:
+                self._quantize_weight()
         fuse_res = (residual is not None and x.dtype in _OUT_DTYPES
                     and residual.dtype == x.dtype and not self.ste_training)
-        if torch.is_grad_enabled() and (self.weight.requires_grad or x.requires_grad
-                                        or (residual is not None and residual.requires_grad)):
+        if train:
             if self.ste_training:
                 y = self.fake_quant_forward(x)
                 return y if residual is None else residual + y
@@ -256,7 +270,7 @@ class Int8Linear(nn.Module):
                 wt = None  # codes handed over since (optimizer): the backward requantizes
             y = W8A8LinearFunction.apply(xin, self.weight, self.bias, self.weight_codes,
                                          self.weight_scales, GROUP_SIZE,
-                                         residual if fuse_res else None, wt)
+                                         residual if fuse_res else None, wt, xpre)
             y = y.to(x.dtype)
             return y if fuse_res or residual is None else residual + y
         # linear.py:68-73: fp32 GEMM, + bias in fp32, then cast to x.dtype (fused)

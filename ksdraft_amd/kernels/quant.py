@@ -160,6 +160,32 @@ def quantize_dual(x: torch.Tensor, group: int = GROUP_SIZE, t_from_codes: bool =
     return codes, scales, codes_t, scales_t
 
 
+def quantize_dual2(a: torch.Tensor, b: torch.Tensor, group: int = GROUP_SIZE):
+    """quantize_dual(a, group, t_from_codes=True) and the same of b in one launch (two
+    2-D tensors of one dtype, e.g. a layer's weight and its input): returns the two
+    4-tuples (codes, scales, codes_t, scales_t)."""
+    a = _float_input(a)
+    b = _float_input(b)
+    dev = _lib.require_gpu(a, b)
+    if a.dim() != 2 or b.dim() != 2:
+        raise ValueError("quantize_dual2 expects 2-D tensors")
+    if a.dtype != b.dtype or group != GROUP_SIZE:
+        return (quantize_dual(a, group, t_from_codes=True),
+                quantize_dual(b, group, t_from_codes=True))
+    xs = (a.contiguous(), b.contiguous())  # bound: they must outlive the enqueued kernel
+    outs, args = [], []
+    for x in xs:
+        R, C = x.shape
+        o = (torch.empty((R, C), dtype=torch.int8, device=dev),
+             torch.empty((R, -(-C // group)), dtype=SCALE_DTYPE, device=dev),
+             torch.empty((C, R), dtype=torch.int8, device=dev),
+             torch.empty((C, -(-R // group)), dtype=SCALE_DTYPE, device=dev))
+        outs.append(o)
+        args += [x.data_ptr(), R, C, *(t.data_ptr() for t in o)]
+    _lib.call("ksd_quantize_dual2", *args, _lib.dtype_code(a.dtype), group, _lib.stream_ptr(dev))
+    return outs[0], outs[1]
+
+
 def quantize_dual_colsum(g: torch.Tensor, group: int = GROUP_SIZE):
     """quantize_dual(g, group) plus the column sums g.float().sum(0) (a linear layer's bias
     gradient) from the same read of g: (codes, scales, codes_t, scales_t, colsum). The

@@ -212,3 +212,22 @@ def test_quantize_dual_colsum(shape, dtype):
     # torch's fp32 sum (the reference's db) sits within the same bound of the exact sum
     terr = np.abs(x_cpu.float().sum(0).numpy().astype(np.float64) - cs.cpu().numpy())
     assert (terr <= 2 * bound).all()
+
+
+@pytest.mark.parametrize("sa,sb,dtype", [
+    ((1536, 1536), (8192, 1536), torch.float32),   # config 2's W and X
+    ((300, 136), (129, 1024), torch.float32),      # ragged tiles in both
+    ((64, 200), (256, 384), torch.bfloat16),
+    ((70, 13), (64, 256), torch.float32),          # C % 8 != 0: two launches
+])
+def test_quantize_dual2_equals_two_duals(sa, sb, dtype):
+    """Two X operands in one launch = quantize_dual(t_from_codes=True) of each, bit for bit."""
+    g = torch.Generator().manual_seed(hash((sa, sb)) % 2**31)
+    a = (torch.randn(*sa, generator=g) * 2).to(dtype).to(DEV)
+    b = torch.randn(*sb, generator=g).to(dtype).to(DEV)
+    ra, rb = kq.quantize_dual2(a, b)
+    for got, x in ((ra, a), (rb, b)):
+        want = kq.quantize_dual(x, 128, t_from_codes=True)
+        for u, v in zip(got, want):
+            assert torch.equal(u.view(torch.int8) if u.dtype == torch.int8 else u.view(torch.int16),
+                               v.view(torch.int8) if v.dtype == torch.int8 else v.view(torch.int16))
