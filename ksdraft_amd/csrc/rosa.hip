@@ -1256,8 +1256,18 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
   float *cq = cred + stream * 3 * T, *ck = cq + T, *cv = cq + 2 * T;
   const float pay = payload[s];
   float gsum = 0.0f;
-  for (int t = wave; t < T; t += kCredWaves) {  // wave-uniform
-    const float gr = grad[(b * T + t) * S + s];
+  // This wave's positions t = wave + kCredWaves * k, 64 at a time: the lanes load their
+  // gradients together and only positions with a non-zero gradient are visited (a zero
+  // gradient contributes nothing to any credit, and only a signed zero to the payload sum).
+  for (int kb = 0; wave + kCredWaves * kb < T; kb += 64) {
+    const int tl = wave + kCredWaves * (kb + lane);
+    const float grl = tl < T ? grad[(b * T + tl) * S + s] : 0.0f;
+    uint64_t live = __ballot(grl != 0.0f);  // NaN counts as live
+    while (live) {  // wave-uniform
+    const int li = __builtin_ctzll(live);
+    live &= live - 1;
+    const int t = wave + kCredWaves * (kb + li);
+    const float gr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, grl), li));
     const int jstar = match_j[stream * T + t];
     const uint64_t qwin = q_window(qw, t);
     uint32_t best = 0u;
@@ -1493,6 +1503,7 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
 #pragma unroll
       for (int k = 0; k < 4; ++k) ntab[64 * k + lane] = 0u;  // the event entries they covered
       __builtin_amdgcn_wave_barrier();
+    }
     }
   }
   if (lane == 0) gps[wave] = gsum;
