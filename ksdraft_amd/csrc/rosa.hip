@@ -432,18 +432,26 @@ __device__ __forceinline__ uint64_t q_window(const uint32_t *qw, int t) {
   return (m64 << (31 - b)) | (b == 31 ? 0ull : (lo >> (b + 1)));
 }
 
-// One length step of a chunk: dst(j') = src(j'+1) & (k[j'] == q[t-L]) for the chunk's
-// kCH + 2 words (the top word's right neighbour is empty); s = ~0 when q[t-L] = 1, else 0.
-// NEG: the chunk starts at word 0, so its two halo words lie before position 0 and stay
-// empty. Returns the OR of the new words.
-template <bool NEG>
-__device__ __forceinline__ uint32_t match_level(const uint32_t *src, uint32_t *dst, const uint32_t *kw,
-                                                uint32_t s) {
+// N length steps of a chunk at once (N = 1, 2, 4): from A_L,
+//   A_{L+N}(j') = A_L(j'+N) & AND_{i<N} (k[j'+N-1-i] == q[t-L-i]),
+// since one step is A_{L+1}(j') = A_L(j'+1) & (k[j'] == q[t-L]). ks[d] holds k shifted
+// down by d bits (bit j' of ks[d] = k[j'+d]; zeros past the chunk's top word, where every
+// A bit is zero). qs has q[t-L-i] at bit 63-i. The words cover kCH + 2 words; the top
+// word's right neighbour is empty. NEG: the chunk starts at word 0, so its two halo words
+// lie before position 0 and stay empty. Returns the OR of the new words.
+template <bool NEG, int N>
+__device__ __forceinline__ uint32_t match_steps(const uint32_t *src, uint32_t *dst,
+                                                const uint32_t (&ks)[4][kCH + 2], uint64_t qs) {
+  uint32_t sm[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) sm[i] = (uint32_t)((int32_t)(uint32_t)((qs << i) >> 32) >> 31);
   uint32_t a2 = 0;
 #pragma unroll
   for (int c = 0; c < kCH + 2; ++c) {
     const uint32_t right = c + 1 < kCH + 2 ? src[c + 1] : 0u;
-    uint32_t v = __builtin_amdgcn_alignbit(right, src[c], 1) & ~(kw[c] ^ s);
+    uint32_t v = __builtin_amdgcn_alignbit(right, src[c], N);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v &= ~(ks[N - 1 - i][c] ^ sm[i]);
     if (NEG && c < 2) v = 0u;
     dst[c] = v;
     a2 |= v;
@@ -452,29 +460,37 @@ __device__ __forceinline__ uint32_t match_level(const uint32_t *src, uint32_t *d
 }
 
 // The length walk of one chunk from A = A_1: returns the last non-empty length L (< lmax
-// or = lmax) with A = A_L. Two buffers alternate, so only the exit copies.
+// or = lmax) with A = A_L. Four lengths per step while they fit under lmax and leave a
+// survivor; then one two-length and one one-length step find L among the last four.
 template <bool NEG>
-__device__ __forceinline__ int match_walk(uint32_t *A, const uint32_t *kw, uint64_t qwin, int lmax) {
+__device__ __forceinline__ int match_walk(uint32_t *A, const uint32_t (&ks)[4][kCH + 2], uint64_t qwin,
+                                          int lmax) {
   uint32_t B[kCH + 2];
   uint64_t qs = qwin << 1;  // bit 63 = q[t - L] for the next length step
   int L = 1;
-  while (L < lmax) {
-    uint32_t s = (uint32_t)((int32_t)(uint32_t)(qs >> 32) >> 31);
-    qs <<= 1;
-    if (!match_level<NEG>(A, B, kw, s)) break;
-    ++L;
-    bool stop = L >= lmax;
-    if (!stop) {
-      s = (uint32_t)((int32_t)(uint32_t)(qs >> 32) >> 31);
-      qs <<= 1;
-      if (match_level<NEG>(B, A, kw, s)) {
-        ++L;
-        continue;
-      }
+  for (;;) {
+    if (L + 4 > lmax || !match_steps<NEG, 4>(A, B, ks, qs)) break;
+    qs <<= 4;
+    L += 4;
+    if (L + 4 > lmax || !match_steps<NEG, 4>(B, A, ks, qs)) {
+#pragma unroll
+      for (int c = 0; c < kCH + 2; ++c) A[c] = B[c];
+      break;
     }
+    qs <<= 4;
+    L += 4;
+  }
+  // A = A_L and A_{L+4} is empty (or L + 4 > lmax): L* lies in [L, min(L + 3, lmax)]
+  if (L + 2 <= lmax && match_steps<NEG, 2>(A, B, ks, qs)) {
 #pragma unroll
     for (int c = 0; c < kCH + 2; ++c) A[c] = B[c];
-    break;
+    qs <<= 2;
+    L += 2;
+  }
+  if (L + 1 <= lmax && match_steps<NEG, 1>(A, B, ks, qs)) {
+#pragma unroll
+    for (int c = 0; c < kCH + 2; ++c) A[c] = B[c];
+    L += 1;
   }
   return L;
 }
@@ -513,7 +529,16 @@ __device__ int match_one(const uint32_t *qw, const uint32_t *kw_all, int W, int 
       }
     }
     if (!any) continue;
-    const int L = w0 >= 2 ? match_walk<false>(A, kw, qwin, lmax) : match_walk<true>(A, kw, qwin, lmax);
+    uint32_t ks[4][kCH + 2];
+#pragma unroll
+    for (int c = 0; c < kCH + 2; ++c) {
+      const uint32_t right = c + 1 < kCH + 2 ? kw[c + 1] : 0u;
+      ks[0][c] = kw[c];
+      ks[1][c] = __builtin_amdgcn_alignbit(right, kw[c], 1);
+      ks[2][c] = __builtin_amdgcn_alignbit(right, kw[c], 2);
+      ks[3][c] = __builtin_amdgcn_alignbit(right, kw[c], 3);
+    }
+    const int L = w0 >= 2 ? match_walk<false>(A, ks, qwin, lmax) : match_walk<true>(A, ks, qwin, lmax);
     if (L <= best_l) continue;
     // survivors at length L: the highest j = j' + L - 1 with j >= 32 w0 (the halo words' own
     // candidates belong to the older chunk; j < 32 (w0 + kCH) holds for every survivor, as
