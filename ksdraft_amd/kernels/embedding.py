@@ -49,6 +49,60 @@ def embedding_gather_int8(codes: torch.Tensor, scales: torch.Tensor, ids: torch.
     return out.reshape(*ids.shape, d)
 
 
+class _RowGather(torch.autograd.Function):
+    """weight[ids] (F.embedding) whose backward adds the rows' gradient into a dense
+    gradient that ``weight`` already holds (a tied head's dW), in place, instead of
+    returning a dense (V, d) gradient: the dense embedding backward zero-fills a (V, d)
+    tensor, scatters into it, and autograd then adds all of it.
+
+    The upstream rows are summed per distinct id by torch's embedding backward over a
+    compact table of the distinct ids (the same sorted, position-ordered sums as over the
+    full table), then added once per distinct row (no duplicate indices besides row 0's
+    zero padding slots, so the add is deterministic). Each element thus gets grad + sum, the value autograd's dense
+    accumulation gives. Without a dense gradient on ``weight`` yet, the backward returns
+    the dense gradient built from the same sums."""
+
+    @staticmethod
+    def forward(ctx, weight, ids):
+        ctx.save_for_backward(ids)
+        ctx.weight = weight
+        return torch.nn.functional.embedding(ids, weight)
+
+    @staticmethod
+    def backward(ctx, grad):
+        (ids,) = ctx.saved_tensors
+        weight = ctx.weight
+        d = weight.shape[1]
+        # distinct ids without a host sync: a stable sort, segment heads, their running
+        # count as each position's slot; slots past the distinct count keep id 0 and get
+        # zero sums (adding zeros leaves row 0 as it is)
+        flat = ids.reshape(-1)
+        n = flat.numel()
+        sid, order = torch.sort(flat, stable=True)
+        head = torch.ones(n, dtype=torch.bool, device=flat.device)
+        head[1:] = sid[1:] != sid[:-1]
+        slot = torch.cumsum(head, 0) - 1
+        inv = torch.empty_like(slot)
+        inv[order] = slot
+        uids = torch.zeros(n, dtype=flat.dtype, device=flat.device)
+        uids[slot] = sid
+        sums = torch.ops.aten.embedding_dense_backward(grad.reshape(-1, d), inv, n, -1, False)
+        g = weight.grad
+        if (g is not None and not g.is_sparse and g.is_contiguous() and g.dtype == sums.dtype
+                and g.shape == weight.shape):
+            g.index_add_(0, uids, sums)
+            return None, None
+        dense = torch.zeros_like(weight, memory_format=torch.contiguous_format)
+        dense.index_add_(0, uids, sums)
+        return dense, None
+
+
+def gather_rows_inplace_grad(weight: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
+    """F.embedding(ids, weight); the backward adds the looked-up rows' gradient into the
+    dense gradient ``weight`` already holds, in place (else returns a dense gradient)."""
+    return _RowGather.apply(weight, ids)
+
+
 class _Int8EmbeddingFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, ids, weight, codes, scales, group):

@@ -40,7 +40,12 @@ class KSDraftModel(nn.Module):
 
     def backbone(self, tokens: torch.Tensor, teacher_states: torch.Tensor | None = None):
         """tokens (B, T) -> (output_norm(stream) (B, T, d), per-layer features)."""
-        x = self.input_norm(self.embedding(tokens))
+        if getattr(self, "inplace_embedding_grad", False) and type(self.embedding) is nn.Embedding:
+            from ..kernels.embedding import gather_rows_inplace_grad
+            e = gather_rows_inplace_grad(self.embedding.weight, tokens)
+        else:
+            e = self.embedding(tokens)
+        x = self.input_norm(e)
         if teacher_states is not None:
             if self.teacher_proj is None:
                 raise ValueError("teacher_states passed but teacher_dim=0 at construction")

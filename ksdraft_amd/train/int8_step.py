@@ -37,11 +37,20 @@ def clip_coefficient(params, max_norm: float) -> torch.Tensor:
     return torch.clamp(max_norm / (total + 1e-6), max=1.0).reshape(1)
 
 
-def transfer_space_loss(features, embedding_weight: torch.Tensor, tgt: torch.Tensor):
+def transfer_space_loss(features, embedding_weight: torch.Tensor, tgt: torch.Tensor,
+                        row_grad_in_place: bool = False):
     """distillation_losses' transfer term (train/__init__.py:79-85). On the GPU the
     per-layer cosines and their gradients are two HIP row kernels per layer
-    (kernels.draft.TransferSpaceLoss); the normalized target embeddings stay torch ops."""
-    tgt_emb = F.normalize(embedding_weight[tgt].float(), dim=-1)
+    (kernels.draft.TransferSpaceLoss); the normalized target embeddings stay torch ops.
+    row_grad_in_place: the gather embedding_weight[tgt] adds its row gradients into the
+    dense gradient ``embedding_weight`` already holds, in place (the same values as
+    autograd's dense accumulation), instead of returning a dense (V, d) gradient."""
+    if row_grad_in_place and embedding_weight.requires_grad:
+        from ..kernels.embedding import gather_rows_inplace_grad
+        rows = gather_rows_inplace_grad(embedding_weight, tgt)
+    else:
+        rows = embedding_weight[tgt]
+    tgt_emb = F.normalize(rows.float(), dim=-1)
     if tgt_emb.is_cuda and len(features) and all(f.is_cuda for f in features):
         from ..kernels.draft import TransferSpaceLoss
         d = tgt_emb.shape[-1]
@@ -72,18 +81,24 @@ class Int8DraftTrainer:
         for mod in model.modules():
             if isinstance(mod, Int8Linear) or (isinstance(mod, KS3Int8Cell) and mod.trainable):
                 self.opt.register_int8(mod)
+        # the float embedding's lookups add their row gradients into the tied head's dense
+        # dW in place
+        model.inplace_embedding_grad = True
 
     def loss(self, tokens: torch.Tensor, teacher_states: torch.Tensor | None = None):
         """(loss, ce, transfer) as device tensors, with the graph for backward."""
         model = self.model
         inp, tgt = tokens[:, :-1], tokens[:, 1:]
         h, features = model.backbone(inp, teacher_states)
+        # The transfer term first: its autograd nodes are then older than the head's, so in
+        # backward the head's dense dW reaches the tied weight before the gathers' row
+        # gradients, which add into it in place.
+        ts = transfer_space_loss(features, model.embedding.weight, tgt, row_grad_in_place=True)
         head = model.head
         if not head._codes_current():
             head._quantize_weight()
         ce = LinearCrossEntropyInt8.apply(h, head.weight, head.weight_codes, head.weight_scales,
                                           tgt.reshape(-1), IGNORE_INDEX, 128)
-        ts = transfer_space_loss(features, model.embedding.weight, tgt)
         return ce + self.transfer_weight * ts, ce, ts
 
     def step(self, tokens: torch.Tensor, teacher_states: torch.Tensor | None = None):

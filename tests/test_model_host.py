@@ -86,3 +86,33 @@ def test_injection_stacked_gemms_equal_the_reference_composition():
         ref = z + gate * inj.inject(pp)
         torch.testing.assert_close(got, ref, rtol=1e-12, atol=1e-12)
         torch.testing.assert_close(p, pr, rtol=1e-12, atol=1e-12)
+
+
+def test_inplace_row_gather_gradient_equals_the_dense_embedding_gradient():
+    """The trainer's gathers from the tied weight add their row gradients into the dense
+    gradient the weight already holds (the head's dW), in place. The result must equal
+    autograd's dense accumulation bit for bit, duplicate ids included, and without a
+    gradient on the weight the backward returns the dense embedding gradient."""
+    import torch.nn.functional as F
+    from ksdraft_amd.kernels.embedding import gather_rows_inplace_grad
+    torch.manual_seed(0)
+    w = torch.randn(50, 8, requires_grad=True)
+    ids = torch.tensor([[3, 7, 3], [49, 0, 7], [3, 3, 12]])
+    g = torch.randn(3, 3, 8)
+    head = torch.randn(50, 8)
+    out = gather_rows_inplace_grad(w, ids)
+    assert torch.equal(out, F.embedding(ids, w))
+    w.grad = head.clone()
+    buf = w.grad
+    (out * g).sum().backward()
+    assert w.grad is buf  # added in place
+    got = w.grad.clone()
+    w.grad = head.clone()
+    (F.embedding(ids, w) * g).sum().backward()
+    assert torch.equal(got, w.grad)
+    w.grad = None
+    (gather_rows_inplace_grad(w, ids) * g).sum().backward()
+    dense = w.grad.clone()
+    w.grad = None
+    (F.embedding(ids, w) * g).sum().backward()
+    assert torch.equal(dense, w.grad)
