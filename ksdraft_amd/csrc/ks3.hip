@@ -1189,6 +1189,27 @@ __global__ __launch_bounds__(256) void handoff_select_kernel(const float *__rest
   }
 }
 
+// out != t: one pass writes fp16(t) and raises the flag; the fix-up pass then rewrites t
+// when the flag is set (every block returns at once when it is not). One read of t fewer
+// than the flag + select passes.
+__global__ __launch_bounds__(256) void handoff_round_kernel(const float *__restrict__ t, int64_t n,
+                                                            int *__restrict__ flag, float *__restrict__ out) {
+  bool bad = false;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const float v = t[i];
+    bad |= (f16_bits(v) & 0x7c00u) == 0x7c00u;  // inf or NaN in fp16
+    out[i] = f16_round(v);
+  }
+  if (__syncthreads_or(bad) && threadIdx.x == 0) atomicOr(flag, 1);
+}
+
+__global__ __launch_bounds__(256) void handoff_fixup_kernel(const float *__restrict__ t, int64_t n,
+                                                            const int *__restrict__ flag,
+                                                            float *__restrict__ out) {
+  if (*flag == 0) return;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) out[i] = t[i];
+}
+
 }  // namespace ksd
 
 using namespace ksd;
@@ -1437,7 +1458,12 @@ extern "C" int ksd_grad_handoff(const float *t, int64_t n, int *flag, float *out
   const int64_t blocks = cdiv(n, 256 * 8);
   const unsigned grid = (unsigned)(blocks < 4096 ? blocks : 4096);
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(handoff_flag_kernel, dim3(grid), dim3(256), 0, st, t, n, flag);
-  hipLaunchKernelGGL(handoff_select_kernel, dim3(grid), dim3(256), 0, st, t, n, (const int *)flag, out);
+  if (out != t) {
+    hipLaunchKernelGGL(handoff_round_kernel, dim3(grid), dim3(256), 0, st, t, n, flag, out);
+    hipLaunchKernelGGL(handoff_fixup_kernel, dim3(grid), dim3(256), 0, st, t, n, (const int *)flag, out);
+  } else {  // in place: decide first, then round
+    hipLaunchKernelGGL(handoff_flag_kernel, dim3(grid), dim3(256), 0, st, t, n, flag);
+    hipLaunchKernelGGL(handoff_select_kernel, dim3(grid), dim3(256), 0, st, t, n, (const int *)flag, out);
+  }
   return check_launch("grad_handoff");
 }

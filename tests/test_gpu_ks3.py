@@ -335,3 +335,27 @@ def test_project_and_spine_features_api(gold):
     assert torch.equal(h2.reshape(h.shape), h)
     with pytest.raises(ValueError):
         K.KS3Int8Cell(_Cell(gold).to(DEV), nonlinear="bf16")
+
+
+@pytest.mark.parametrize("case", ["finite", "overflow", "nan", "in_place"])
+def test_grad_handoff_entry_point(case):
+    """ksd_grad_handoff through the C ABI: fp32(fp16(t)) when every element is finite in
+    fp16, else t unchanged (ks3_int8.py:75-84), with out separate from t or aliasing it."""
+    from ksdraft_amd import _lib
+    g = torch.Generator().manual_seed(7)
+    t = torch.randn(3 * 2048 + 37, generator=g) * 100.0
+    if case == "overflow":
+        t[4001] = 70000.0
+    if case == "nan":
+        t[17] = float("nan")
+    want = t.clone() if case in ("overflow", "nan") else t.half().float()
+    td = t.to("cuda")
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = td if case == "in_place" else torch.full_like(td, -1.0)
+    _lib.call("ksd_grad_handoff", td.data_ptr(), td.numel(), flag.data_ptr(), out.data_ptr(),
+              _lib.stream_ptr(td.device))
+    torch.cuda.synchronize()
+    got = out.cpu()
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32)) or (
+        case == "nan" and torch.equal(torch.nan_to_num(got), torch.nan_to_num(want)))
+    assert int(flag.item()) == (1 if case in ("overflow", "nan") else 0)
