@@ -299,11 +299,24 @@ class KS3Int8Cell(nn.Module):
     # ---- scalar dequantization into the active arithmetic domain ----
 
     def _warp_scalars(self, dtype: torch.dtype):
-        """ks3_int8.py:158-165."""
+        """ks3_int8.py:158-165. Kept per dtype while the four warp code/scale tensors are
+        the same objects at the same in-place version (the cache holds them, so their
+        storage cannot be reused under it): a training step dequantizes them once, not in
+        its forward and again in its backward. The returned tensors are not to be modified."""
+        src = (self.warp_scale_codes, self.warp_scale_scales, self.warp_shift_codes,
+               self.warp_shift_scales)
+        cache = getattr(self, "_warp_cache", None)
+        if cache is None:
+            cache = self._warp_cache = {}
+        hit = cache.get(dtype)
+        if (hit is not None and all(a is b for a, b in zip(hit[0], src))
+                and hit[1] == tuple(t._version for t in src)):
+            return hit[2]
         scale = dequantize_last_dim(self.warp_scale_codes, self.warp_scale_scales,
                                     self.group).reshape(-1).to(dtype)
         shift = dequantize_last_dim(self.warp_shift_codes, self.warp_shift_scales,
                                     self.group).reshape(-1).to(dtype)
+        cache[dtype] = (src, tuple(t._version for t in src), (scale, shift))
         return scale, shift
 
     def _check_supported(self):

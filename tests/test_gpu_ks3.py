@@ -359,3 +359,29 @@ def test_grad_handoff_entry_point(case):
     assert torch.equal(got.view(torch.int32), want.view(torch.int32)) or (
         case == "nan" and torch.equal(torch.nan_to_num(got), torch.nan_to_num(want)))
     assert int(flag.item()) == (1 if case in ("overflow", "nan") else 0)
+
+
+def test_warp_scalars_follow_their_codes(gold):
+    """The dequantized warp scale/shift are reused while their code and scale tensors are
+    unchanged, and recomputed after a repack of the masters or an in-place edit."""
+    from ksdraft_amd.kernels.quant import dequantize_last_dim
+    cell = K.KS3Int8Cell(_Cell(gold).to(DEV), group=128, nonlinear="int8", trainable=True)
+
+    def fresh():
+        return (dequantize_last_dim(cell.warp_scale_codes, cell.warp_scale_scales, 128).reshape(-1).half(),
+                dequantize_last_dim(cell.warp_shift_codes, cell.warp_shift_scales, 128).reshape(-1).half())
+
+    s1, h1 = cell._warp_scalars(torch.float16)
+    assert cell._warp_scalars(torch.float16)[0] is s1
+    assert torch.equal(s1, fresh()[0]) and torch.equal(h1, fresh()[1])
+    with torch.no_grad():
+        cell.master_raw_scale.add_(0.5)
+        cell.master_raw_shift.add_(0.25)
+    cell._repack_masters()
+    s2, h2 = cell._warp_scalars(torch.float16)
+    assert torch.equal(s2, fresh()[0]) and torch.equal(h2, fresh()[1])
+    assert not torch.equal(s2, s1)
+    with torch.no_grad():
+        cell.warp_shift_codes.neg_()
+    s3, h3 = cell._warp_scalars(torch.float16)
+    assert torch.equal(h3, fresh()[1]) and not torch.equal(h3, h2)
