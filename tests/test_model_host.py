@@ -14,7 +14,7 @@ from ksdraft_amd.model.spine import AdjacentInjection
 def test_baseline_config_counts():
     cfg = baseline_config()
     assert cfg.charts == 5888 and cfg.d_model == 1536 and cfg.rosa_streams == 512
-    # SURVEY Appendix B figures, from the reference's formulas
+    # the counts the reference's formulas give for this config (ksdraft/config.py:71-95)
     assert cfg.ks3_params() == 18_135_040
     assert cfg.rosa_params() == 3_153_920
     assert cfg.total_params() == 741_556_224
