@@ -423,6 +423,10 @@ __global__ void __launch_bounds__(256) rosa_pack_kernel(PackSrc ps, int64_t B, i
 
 // ---------------------------------------------------------------- match
 constexpr int kCH = 16;  // candidate words per chunk
+#ifndef KSD_MATCH_STEP
+#define KSD_MATCH_STEP 4
+#endif
+constexpr int kStep = KSD_MATCH_STEP;  // match lengths per step of the walk (4 or 2)
 
 // 64 q bits ending at t in memory order: bit 63 = q[t], bit 63-i = q[t-i] (0 before 0).
 __device__ __forceinline__ uint64_t q_window(const uint32_t *qw, int t) {
@@ -441,7 +445,7 @@ __device__ __forceinline__ uint64_t q_window(const uint32_t *qw, int t) {
 // lie before position 0 and stay empty. Returns the OR of the new words.
 template <bool NEG, int N>
 __device__ __forceinline__ uint32_t match_steps(const uint32_t *src, uint32_t *dst,
-                                                const uint32_t (&ks)[4][kCH + 2], uint64_t qs) {
+                                                const uint32_t (&ks)[kStep][kCH + 2], uint64_t qs) {
   uint32_t sm[N];
 #pragma unroll
   for (int i = 0; i < N; ++i) sm[i] = (uint32_t)((int32_t)(uint32_t)((qs << i) >> 32) >> 31);
@@ -463,25 +467,25 @@ __device__ __forceinline__ uint32_t match_steps(const uint32_t *src, uint32_t *d
 // or = lmax) with A = A_L. Four lengths per step while they fit under lmax and leave a
 // survivor; then one two-length and one one-length step find L among the last four.
 template <bool NEG>
-__device__ __forceinline__ int match_walk(uint32_t *A, const uint32_t (&ks)[4][kCH + 2], uint64_t qwin,
+__device__ __forceinline__ int match_walk(uint32_t *A, const uint32_t (&ks)[kStep][kCH + 2], uint64_t qwin,
                                           int lmax) {
   uint32_t B[kCH + 2];
   uint64_t qs = qwin << 1;  // bit 63 = q[t - L] for the next length step
   int L = 1;
   for (;;) {
-    if (L + 4 > lmax || !match_steps<NEG, 4>(A, B, ks, qs)) break;
-    qs <<= 4;
-    L += 4;
-    if (L + 4 > lmax || !match_steps<NEG, 4>(B, A, ks, qs)) {
+    if (L + kStep > lmax || !match_steps<NEG, kStep>(A, B, ks, qs)) break;
+    qs <<= kStep;
+    L += kStep;
+    if (L + kStep > lmax || !match_steps<NEG, kStep>(B, A, ks, qs)) {
 #pragma unroll
       for (int c = 0; c < kCH + 2; ++c) A[c] = B[c];
       break;
     }
-    qs <<= 4;
-    L += 4;
+    qs <<= kStep;
+    L += kStep;
   }
-  // A = A_L and A_{L+4} is empty (or L + 4 > lmax): L* lies in [L, min(L + 3, lmax)]
-  if (L + 2 <= lmax && match_steps<NEG, 2>(A, B, ks, qs)) {
+  // A = A_L and A_{L+kStep} is empty (or past lmax): L* lies in [L, L + kStep - 1]
+  if (kStep == 4 && L + 2 <= lmax && match_steps<NEG, 2>(A, B, ks, qs)) {
 #pragma unroll
     for (int c = 0; c < kCH + 2; ++c) A[c] = B[c];
     qs <<= 2;
@@ -529,14 +533,13 @@ __device__ int match_one(const uint32_t *qw, const uint32_t *kw_all, int W, int 
       }
     }
     if (!any) continue;
-    uint32_t ks[4][kCH + 2];
+    uint32_t ks[kStep][kCH + 2];
 #pragma unroll
     for (int c = 0; c < kCH + 2; ++c) {
       const uint32_t right = c + 1 < kCH + 2 ? kw[c + 1] : 0u;
       ks[0][c] = kw[c];
-      ks[1][c] = __builtin_amdgcn_alignbit(right, kw[c], 1);
-      ks[2][c] = __builtin_amdgcn_alignbit(right, kw[c], 2);
-      ks[3][c] = __builtin_amdgcn_alignbit(right, kw[c], 3);
+#pragma unroll
+      for (int d = 1; d < kStep; ++d) ks[d][c] = __builtin_amdgcn_alignbit(right, kw[c], d);
     }
     const int L = w0 >= 2 ? match_walk<false>(A, ks, qwin, lmax) : match_walk<true>(A, ks, qwin, lmax);
     if (L <= best_l) continue;
