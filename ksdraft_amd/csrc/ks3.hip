@@ -31,7 +31,8 @@ constexpr float kLutDomain = 3.2f;                  // TANH_DOMAIN, ks3_int8.py:
 // The warp step tq * (4/127). Composed (ks3_int8.py:211): a torch fp16 tensor times a
 // Python float is evaluated in fp32 with the constant in fp32. Fused (ks3_triton.py:59):
 // Triton keeps a Python-float scalar out of type promotion (triton/language/semantic.py,
-// computation_type_impl), so the product is an fp16 op and the constant is fp16(4/127).
+// computation_type_impl), so the product is fp16 arithmetic with the constant fp16(4/127),
+// and its compiled form contracts it with the add of the shift into one v_fma_f16.
 constexpr float kTq16Step = (float)(4.0 / 127.0);
 constexpr float kTq16StepFused = 0.031494140625f;  // fp16(4/127) = 2064 * 2^-16
 
@@ -98,10 +99,17 @@ __device__ __forceinline__ SpineCol load_spine_col(const int8_t *codes, const ui
 template <bool FUSED>
 __device__ __forceinline__ int spine_sum(int ti, const SpineCol &c, const int8_t *lut) {
   const int tq = lut_at(lut, ti);
-  // tq * step is exact in fp32 (an int8 code times an fp16 value), so f16_round of it is
-  // the fp16 product
-  float w = f16_round(f16_round((float)tq * (FUSED ? kTq16StepFused : kTq16Step)) + c.sh);
-  w = f16_round(c.sc * w);
+  float w;
+  if constexpr (FUSED) {
+    // ks3_triton.py:59 as Triton compiles it for gfx950: the fp16 product and the add of
+    // the shift are one v_fma_f16 (one rounding), then an fp16 multiply by the scale
+    const _Float16 t16 = __builtin_fmaf16((_Float16)tq, (_Float16)kTq16StepFused, (_Float16)c.sh);
+    w = (float)((_Float16)c.sc * t16);
+  } else {
+    // ks3_int8.py:211: torch's fp16 ops, each evaluated in fp32 and rounded to fp16
+    w = f16_round(f16_round((float)tq * kTq16Step) + c.sh);
+    w = f16_round(c.sc * w);
+  }
   const int zq = lut_at(lut, FUSED ? (int)rintf(fminf(fmaxf(w, -kLutDomain), kLutDomain) * kLutScale)
                                    : lut_index(w));
   int poly = c.a64;
@@ -1002,6 +1010,10 @@ static int64_t vjp_row_blocks(int64_t M) { return cdiv(M, kVjpRowsPerBlock); }
 //          for |th| >= 2^-12 (where the table value is a normal fp16, so the exact scaling
 //          by 4 commutes with the rounding) and 4 th below (tanh(th) rounds to th in
 //          fp32 there). Both forms are checked against torch for every fp16 input.
+// The project_fused contract (SRC == KSD_F32) is the reference's Triton kernel as compiled
+// for gfx950, which contracts multiply/add pairs: there the Horner steps are fused
+// multiply-adds (fp32 in 'fp32', fp16 in 'fp16') and x + (poly + warped) ps is one fp32
+// fused multiply-add (rounded to fp16 after it in 'fp16').
 // A block is 4 waves; a wave walks RT consecutive rows, a lane owns 8 consecutive charts
 // (its per-chart constants stay in registers), a group is G/8 adjacent lanes.
 template <int MODE>
@@ -1084,7 +1096,19 @@ __global__ __launch_bounds__(256) void ks3_spine_float_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float v;
-      if constexpr (MODE == 0) {
+      if constexpr (MODE == 0 && SRC == KSD_F32) {
+        // ks3_triton.py:91-96 as compiled for gfx950: every Horner step and the final
+        // x + s * ps are fused multiply-adds
+        const float t = tanh_fwd<0>(x[e] * 0.25f, tab, true);
+        const float z = tanh_fwd<0>(SC[e] * (t + SH[e]), tab, false);
+        const float poly = fmaf(fmaf(fmaf(A[e], t, B[e]), t, C2[e]), t, C0[e]);
+        float wp = fmaf(4.0f * C5[e], z, 2.0f * C4[e]);
+        wp = fmaf(wp, z, -(3.0f * C5[e]));
+        wp = fmaf(wp, z, -C4[e]);
+        v = fmaf(poly + wp, PS[e], x[e]);
+        v = v < 0.0f ? 0.0f : v;
+        v = v * v;
+      } else if constexpr (MODE == 0) {
         const float t = tanh_fwd<0>(x[e] * 0.25f, tab, true);
         const float z = tanh_fwd<0>(SC[e] * (t + SH[e]), tab, false);
         float poly = A[e] * t + B[e];
@@ -1096,6 +1120,25 @@ __global__ __launch_bounds__(256) void ks3_spine_float_kernel(
         v = x[e] + (poly + wp) * PS[e];
         v = v < 0.0f ? 0.0f : v;
         v = v * v;
+      } else if constexpr (SRC == KSD_F32) {
+        // ks3_triton.py:77-89 as compiled for gfx950: the six Horner steps are fp16 fused
+        // multiply-adds (v_pk_fma_f16) and x + s * ps one fp32 fused multiply-add, rounded
+        // to fp16 after it
+        typedef _Float16 f16t;
+        const float th = f16_round(x[e] * 0.25f);
+        const float t = f16_round(tanh_fwd<1>(th, tab, true));
+        const float warp = f16_round(SC[e] * (t + SH[e]));
+        const float z = tanh_fwd<1>(warp, tab, false);
+        const f16t t16 = (f16t)t, z16 = (f16t)z;
+        f16t poly = __builtin_fmaf16((f16t)A[e], t16, (f16t)B[e]);
+        poly = __builtin_fmaf16(poly, t16, (f16t)C2[e]);
+        poly = __builtin_fmaf16(poly, t16, (f16t)C0[e]);
+        f16t wp = __builtin_fmaf16((f16t)(4.0f * C5[e]), z16, (f16t)(2.0f * C4[e]));
+        wp = __builtin_fmaf16(wp, z16, (f16t)(-3.0f * C5[e]));
+        wp = __builtin_fmaf16(wp, z16, (f16t)(-C4[e]));
+        v = f16_round(fmaf((float)poly + (float)wp, PS[e], x[e]));
+        v = v < 0.0f ? 0.0f : v;
+        v = f16_round(v * v);
       } else {
         const float th = f16_round(x[e] * 0.25f);
         const float t = f16_round(tanh_fwd<1>(th, tab, true));

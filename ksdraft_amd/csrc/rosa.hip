@@ -423,10 +423,7 @@ __global__ void __launch_bounds__(256) rosa_pack_kernel(PackSrc ps, int64_t B, i
 
 // ---------------------------------------------------------------- match
 constexpr int kCH = 16;  // candidate words per chunk
-#ifndef KSD_MATCH_STEP
-#define KSD_MATCH_STEP 4
-#endif
-constexpr int kStep = KSD_MATCH_STEP;  // match lengths per step of the walk (8, 4 or 2)
+constexpr int kStep = 4;  // match lengths per step of the walk
 
 // 64 q bits ending at t in memory order: bit 63 = q[t], bit 63-i = q[t-i] (0 before 0).
 __device__ __forceinline__ uint64_t q_window(const uint32_t *qw, int t) {
@@ -484,15 +481,9 @@ __device__ __forceinline__ int match_walk(uint32_t *A, const uint32_t (&ks)[kSte
     qs <<= kStep;
     L += kStep;
   }
-  // A = A_L and A_{L+kStep} is empty (or past lmax): L* lies in [L, L + kStep - 1];
-  // halving steps find it
-  if (kStep == 8 && L + 4 <= lmax && match_steps<NEG, 4>(A, B, ks, qs)) {
-#pragma unroll
-    for (int c = 0; c < kCH + 2; ++c) A[c] = B[c];
-    qs <<= 4;
-    L += 4;
-  }
-  if (kStep >= 4 && L + 2 <= lmax && match_steps<NEG, 2>(A, B, ks, qs)) {
+  // A = A_L and A_{L+4} is empty (or past lmax): L* lies in [L, L + 3]; a two-length and
+  // a one-length step find it
+  if (L + 2 <= lmax && match_steps<NEG, 2>(A, B, ks, qs)) {
 #pragma unroll
     for (int c = 0; c < kCH + 2; ++c) A[c] = B[c];
     qs <<= 2;

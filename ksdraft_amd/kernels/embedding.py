@@ -50,32 +50,29 @@ def embedding_gather_int8(codes: torch.Tensor, scales: torch.Tensor, ids: torch.
 
 
 class _RowGather(torch.autograd.Function):
-    """weight[ids] (F.embedding) whose backward adds the rows' gradient into a dense
-    gradient that ``weight`` already holds (a tied head's dW), in place, instead of
-    returning a dense (V, d) gradient: the dense embedding backward zero-fills a (V, d)
-    tensor, scatters into it, and autograd then adds all of it.
+    """weight[ids] (F.embedding) whose backward returns a sparse (COO) gradient: the
+    upstream rows summed per distinct id, one entry per distinct row.
 
-    The upstream rows are summed per distinct id by torch's embedding backward over a
-    compact table of the distinct ids (the same sorted, position-ordered sums as over the
-    full table), then added once per distinct row (no duplicate indices besides row 0's
-    zero padding slots, so the add is deterministic). Each element thus gets grad + sum, the value autograd's dense
-    accumulation gives. Without a dense gradient on ``weight`` yet, the backward returns
-    the dense gradient built from the same sums."""
+    A tied weight (embedding lookups beside the LM head) receives a dense gradient from the
+    head; autograd adds the sparse row sums into it (one pass over the dense tensor) instead
+    of zero-filling and adding a dense (V, d) gradient per lookup. The values are the dense
+    embedding backward's: the upstream rows are summed per distinct id by torch's embedding
+    backward over a compact table of the distinct ids (sorted, in position order), found
+    without a host sync. Slots past the distinct count carry id 0 and zero sums, so adding
+    them leaves row 0 unchanged. When the sparse gradient is the weight's only one, its
+    .grad is sparse; the caller that uses this lookup (Int8DraftTrainer) always has the
+    head's dense gradient on the same weight."""
 
     @staticmethod
     def forward(ctx, weight, ids):
         ctx.save_for_backward(ids)
-        ctx.weight = weight
+        ctx.shape = weight.shape
         return torch.nn.functional.embedding(ids, weight)
 
     @staticmethod
     def backward(ctx, grad):
         (ids,) = ctx.saved_tensors
-        weight = ctx.weight
-        d = weight.shape[1]
-        # distinct ids without a host sync: a stable sort, segment heads, their running
-        # count as each position's slot; slots past the distinct count keep id 0 and get
-        # zero sums (adding zeros leaves row 0 as it is)
+        V, d = ctx.shape
         flat = ids.reshape(-1)
         n = flat.numel()
         sid, order = torch.sort(flat, stable=True)
@@ -84,22 +81,14 @@ class _RowGather(torch.autograd.Function):
         slot = torch.cumsum(head, 0) - 1
         inv = torch.empty_like(slot)
         inv[order] = slot
-        uids = torch.zeros(n, dtype=flat.dtype, device=flat.device)
+        uids = torch.zeros(n, dtype=torch.int64, device=flat.device)
         uids[slot] = sid
         sums = torch.ops.aten.embedding_dense_backward(grad.reshape(-1, d), inv, n, -1, False)
-        g = weight.grad
-        if (g is not None and not g.is_sparse and g.is_contiguous() and g.dtype == sums.dtype
-                and g.shape == weight.shape):
-            g.index_add_(0, uids, sums)
-            return None, None
-        dense = torch.zeros_like(weight, memory_format=torch.contiguous_format)
-        dense.index_add_(0, uids, sums)
-        return dense, None
+        return torch.sparse_coo_tensor(uids[None], sums, (V, d), check_invariants=False), None
 
 
-def gather_rows_inplace_grad(weight: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
-    """F.embedding(ids, weight); the backward adds the looked-up rows' gradient into the
-    dense gradient ``weight`` already holds, in place (else returns a dense gradient)."""
+def gather_rows_sparse_grad(weight: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
+    """F.embedding(ids, weight) with a sparse row-sum gradient for ``weight``."""
     return _RowGather.apply(weight, ids)
 
 

@@ -302,13 +302,17 @@ class KS3Int8Cell(nn.Module):
         """ks3_int8.py:158-165. Kept per dtype while the four warp code/scale tensors are
         the same objects at the same in-place version (the cache holds them, so their
         storage cannot be reused under it): a training step dequantizes them once, not in
-        its forward and again in its backward. The returned tensors are not to be modified."""
+        its forward and again in its backward. Inference tensors (made under
+        torch.inference_mode) carry no version counter: with any of those the scalars are
+        dequantized every call and nothing is cached. The returned tensors are not to be
+        modified."""
         src = (self.warp_scale_codes, self.warp_scale_scales, self.warp_shift_codes,
                self.warp_shift_scales)
+        cacheable = not any(t.is_inference() for t in src)
         cache = getattr(self, "_warp_cache", None)
         if cache is None:
             cache = self._warp_cache = {}
-        hit = cache.get(dtype)
+        hit = cache.get(dtype) if cacheable else None
         if (hit is not None and all(a is b for a, b in zip(hit[0], src))
                 and hit[1] == tuple(t._version for t in src)):
             return hit[2]
@@ -316,7 +320,10 @@ class KS3Int8Cell(nn.Module):
                                     self.group).reshape(-1).to(dtype)
         shift = dequantize_last_dim(self.warp_shift_codes, self.warp_shift_scales,
                                     self.group).reshape(-1).to(dtype)
-        cache[dtype] = (src, tuple(t._version for t in src), (scale, shift))
+        if cacheable:
+            cache[dtype] = (src, tuple(t._version for t in src), (scale, shift))
+        else:
+            cache.pop(dtype, None)
         return scale, shift
 
     def _check_supported(self):

@@ -40,9 +40,9 @@ class KSDraftModel(nn.Module):
 
     def backbone(self, tokens: torch.Tensor, teacher_states: torch.Tensor | None = None):
         """tokens (B, T) -> (output_norm(stream) (B, T, d), per-layer features)."""
-        if getattr(self, "inplace_embedding_grad", False) and type(self.embedding) is nn.Embedding:
-            from ..kernels.embedding import gather_rows_inplace_grad
-            e = gather_rows_inplace_grad(self.embedding.weight, tokens)
+        if getattr(self, "sparse_embedding_grad", False) and type(self.embedding) is nn.Embedding:
+            from ..kernels.embedding import gather_rows_sparse_grad
+            e = gather_rows_sparse_grad(self.embedding.weight, tokens)
         else:
             e = self.embedding(tokens)
         x = self.input_norm(e)

@@ -38,16 +38,16 @@ def clip_coefficient(params, max_norm: float) -> torch.Tensor:
 
 
 def transfer_space_loss(features, embedding_weight: torch.Tensor, tgt: torch.Tensor,
-                        row_grad_in_place: bool = False):
+                        sparse_row_grad: bool = False):
     """distillation_losses' transfer term (train/__init__.py:79-85). On the GPU the
     per-layer cosines and their gradients are two HIP row kernels per layer
     (kernels.draft.TransferSpaceLoss); the normalized target embeddings stay torch ops.
-    row_grad_in_place: the gather embedding_weight[tgt] adds its row gradients into the
-    dense gradient ``embedding_weight`` already holds, in place (the same values as
-    autograd's dense accumulation), instead of returning a dense (V, d) gradient."""
-    if row_grad_in_place and embedding_weight.requires_grad:
-        from ..kernels.embedding import gather_rows_inplace_grad
-        rows = gather_rows_inplace_grad(embedding_weight, tgt)
+    sparse_row_grad: the gather embedding_weight[tgt] returns its row gradients as a sparse
+    gradient, which autograd adds into the tied head's dense one (the same values as the
+    dense embedding backward), instead of a dense (V, d) gradient."""
+    if sparse_row_grad and embedding_weight.requires_grad:
+        from ..kernels.embedding import gather_rows_sparse_grad
+        rows = gather_rows_sparse_grad(embedding_weight, tgt)
     else:
         rows = embedding_weight[tgt]
     tgt_emb = F.normalize(rows.float(), dim=-1)
@@ -81,19 +81,16 @@ class Int8DraftTrainer:
         for mod in model.modules():
             if isinstance(mod, Int8Linear) or (isinstance(mod, KS3Int8Cell) and mod.trainable):
                 self.opt.register_int8(mod)
-        # the float embedding's lookups add their row gradients into the tied head's dense
-        # dW in place
-        model.inplace_embedding_grad = True
+        # the float embedding's lookups return sparse row gradients, which autograd adds
+        # into the tied head's dense dW
+        model.sparse_embedding_grad = True
 
     def loss(self, tokens: torch.Tensor, teacher_states: torch.Tensor | None = None):
         """(loss, ce, transfer) as device tensors, with the graph for backward."""
         model = self.model
         inp, tgt = tokens[:, :-1], tokens[:, 1:]
         h, features = model.backbone(inp, teacher_states)
-        # The transfer term first: its autograd nodes are then older than the head's, so in
-        # backward the head's dense dW reaches the tied weight before the gathers' row
-        # gradients, which add into it in place.
-        ts = transfer_space_loss(features, model.embedding.weight, tgt, row_grad_in_place=True)
+        ts = transfer_space_loss(features, model.embedding.weight, tgt, sparse_row_grad=True)
         head = model.head
         if not head._codes_current():
             head._quantize_weight()

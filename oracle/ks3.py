@@ -11,10 +11,11 @@ Follows reference ksdraft/kernels/ks3_int8.py:
   * _KS3Int8Train.backward geometry VJP :354-401
 and reference ksdraft/kernels/ks3_triton.py:
   * the fused (project_fused) spine + requant contract, 'int8' mode :47-75, 137-156
+  * the fused contract of the 'fp32' / 'fp16' modes :76-98
 
-Every fp16 op of the reference is a torch fp16 tensor op: the operation is evaluated in
-fp32 ("opmath") with Python scalars converted to fp32, then rounded to fp16. `h()`
-below applies exactly that rounding. tanh is evaluated in float64 and rounded through
+Every fp16 op of the composed (torch) path is a torch fp16 tensor op: the operation is
+evaluated in fp32 ("opmath") with Python scalars converted to fp32, then rounded to fp16.
+`h()` below applies exactly that rounding. tanh is evaluated in float64 and rounded through
 fp32, i.e. a correctly rounded fp32 tanh, then to fp16.
 
 Pinned by: tests/golden/ks3_int8_golden.npz, written by tests/golden/make_ks3_golden.py
@@ -23,24 +24,21 @@ gradient given identical GEMM outputs); the LUT against an mpmath-free closed fo
 check (float64 tanh, tie distance); _round_div127 by brute force over integer ranges
 (tests/test_oracle_ks3.py).
 
-spine_features_float ('fp32' / 'fp16') is pinned by tests/golden/ks3_modes_golden.npz,
-written by tests/golden/make_ks3_modes_golden.py from the reference's own CPU path: 'fp16'
-bit-exact, 'fp32' within the difference between the float64-based tanh here and torch's
-fp32 tanh (tests/test_oracle_ks3.py). The same function is the fused contract of those
-modes (ks3_triton.py:76-98) when given the clamped fp32 accumulator and fp16 warp scalars;
-there it is parity unpinned at the bit level where Triton's default FMA contraction
-(enable_fp_fusion) may fuse a multiply and an add that the source writes separately.
+spine_features_float ('fp32' / 'fp16', composed) is pinned by
+tests/golden/ks3_modes_golden.npz, written by tests/golden/make_ks3_modes_golden.py from
+the reference's own CPU path: 'fp16' bit-exact, 'fp32' within the difference between the
+float64-based tanh here and torch's fp32 tanh (tests/test_oracle_ks3.py).
 
-spine_fused_int8 (the project_fused contract) follows the Triton source's typing: the
-fp16 warp product with the constant rounded to fp16 (Triton's scalar rule, pinned by
-tests/test_oracle_ks3.py against the installed triton.language.semantic), fp32 LUT
-indices, the untruncated fp32 increment. It stays parity unpinned at the bit level in the
-two places the Triton source leaves to its backend: whether the fp32 `h / pre_scale`
-division of ks3_triton.py:74 and :153 is correctly rounded, and whether the backend
-contracts `x + s * (ps / 64)` (:70) and `tq16 * c + shift16` (:59) into FMAs, which
-Triton's default enable_fp_fusion=True permits but does not force. Those are pinned only by
-the reference's own tolerance against the composed path (rel < 0.05 on the cell output,
-tests/test_ks3_int8.py:82-84), checked on the golden cell.
+The fused contract (spine_fused_int8, and spine_features_float with fused=True) is the
+reference's Triton kernel as Triton compiles it for gfx950. The source text leaves two
+things to the backend: which multiply/add pairs Triton's default enable_fp_fusion
+contracts into one fused multiply-add, and how `/` is lowered. Both are read off the AMD
+assembly of the reference kernel, compiled in the build container by
+tests/golden/make_ks3_fused_contract.py (fixture tests/golden/ks3_fused_contract.json):
+FUSED_CONTRACT below lists the decision for every floating-point line, and
+tests/test_oracle_fused_contract.py checks it against the fixture, the fused
+multiply-adds here against exact rational arithmetic, and the constants (fp16(4/127) on
+ks3_triton.py:59) against the literals the compiler emitted.
 """
 
 from __future__ import annotations
@@ -57,6 +55,42 @@ f16 = np.float16
 def h(x):
     """Round (an fp32 evaluation) to fp16 and return it as fp32 values."""
     return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def fma16(a, b, c):
+    """IEEE fp16 fused multiply-add of fp16-valued inputs, one rounding (v_fma_f16).
+
+    The product of two fp16 values is exact in float64 (22 significant bits). The sum with
+    the fp16 addend is exact there too unless the two are more than ~30 binades apart; then
+    the smaller one lies far below the fp16 rounding point of the larger, which is either an
+    fp16 value (no rounding) or a product with at most 12 significant bits whose tie the
+    smaller one breaks, and that case needs a product past 2^18, where fp16 overflows
+    anyway. So rounding the float64 result to fp16 rounds the exact value once."""
+    r = np.asarray(a, np.float64) * np.asarray(b, np.float64) + np.asarray(c, np.float64)
+    return r.astype(np.float16).astype(np.float32)
+
+
+def fma32(a, b, c):
+    """IEEE fp32 fused multiply-add of fp32 inputs, one rounding (v_fma_f32).
+
+    a*b is exact in float64 (48 bits); the float64 sum hi and its exact error lo (TwoSum)
+    give the exact result hi + lo. Rounding hi to fp32 rounds the exact value correctly
+    unless hi lies exactly halfway between two fp32 values and lo is nonzero: then the
+    exact value is on lo's side of that midpoint."""
+    p = np.asarray(a, np.float32).astype(np.float64) * np.asarray(b, np.float32).astype(np.float64)
+    c = np.asarray(c, np.float32).astype(np.float64)
+    p, c = np.broadcast_arrays(p, c)
+    hi = p + c
+    bb = hi - p
+    lo = (p - (hi - bb)) + (c - bb)
+    with np.errstate(over="ignore", invalid="ignore"):
+        r = hi.astype(np.float32)
+        rd = r.astype(np.float64)
+        nb = np.nextafter(r, np.where(hi > rd, np.inf, -np.inf).astype(np.float32)).astype(np.float64)
+        mid = (hi != rd) & np.isfinite(rd) & np.isfinite(nb) & (hi == (rd + nb) * 0.5)
+        up, dn = np.maximum(rd, nb), np.minimum(rd, nb)
+        r = np.where(mid & (lo > 0), up, np.where(mid & (lo < 0), dn, rd)).astype(np.float32)
+    return r
 
 
 def tanh32(x):
@@ -139,12 +173,19 @@ def spine_features_int8(coords, spine_codes, spine_scale, scale16, shift16, lut)
     return (h(hq16 * hq16) * (pre * pre).astype(np.float32)).astype(np.float32)
 
 
-def spine_features_float(x, spine_codes, spine_scale, scale, shift, mode):
+def spine_features_float(x, spine_codes, spine_scale, scale, shift, mode, fused=False):
     """ks3_int8.py:172-203, the 'fp32' and 'fp16' modes, rank 1 (mean = x).
 
     x (M, F) fp32 coordinates (fp16 values on the composed path); spine_codes (F, 6) int8;
     spine_scale (F,) fp16; scale/shift (F,) the warp scalars in the mode's arithmetic
-    (fp32 values for 'fp32', fp16 values for 'fp16'). Returns h (M, F) fp32."""
+    (fp32 values for 'fp32', fp16 values for 'fp16'). Returns h (M, F) fp32.
+
+    fused=True: the same modes in the fused kernel (ks3_triton.py:76-98) as compiled for
+    gfx950, x being the clamped fp32 accumulator and scale/shift fp16 values. The Horner
+    and warp steps and the final `x + (poly + warped) * ps` are fused multiply-adds there
+    (FUSED_CONTRACT); everything else rounds as in the composed modes."""
+    if fused:
+        return _spine_float_fused(x, spine_codes, spine_scale, scale, shift, mode)
     x = np.asarray(x, np.float32)
     c = np.asarray(spine_codes, np.float32)
     c0, c1, c2, c3, c4, c5 = (c[:, k][None, :] for k in range(6))
@@ -184,6 +225,70 @@ def spine_features_float(x, spine_codes, spine_scale, scale, shift, mode):
     hv = h(x + ((poly + wp).astype(np.float32) * ps).astype(np.float32))
     hv = np.where(hv < 0, f32(0.0), hv)
     return h(hv * hv)
+
+
+def _spine_float_fused(x, spine_codes, spine_scale, scale, shift, mode):
+    """ks3_triton.py:76-98 (NL 1 'fp16', NL 0 'fp32') with FUSED_CONTRACT's gfx950 fusions."""
+    x = np.asarray(x, np.float32)
+    c = np.asarray(spine_codes, np.float32)
+    c0, c1, c2, c3, c4, c5 = (c[:, k][None, :] for k in range(6))
+    ps = np.asarray(spine_scale, np.float16).astype(np.float32)[None, :]
+    sc = np.asarray(scale, np.float32)[None, :]
+    sh = np.asarray(shift, np.float32)[None, :]
+    a = 2 * c0 - 2 * c1 + c2 + c3      # :51-52, small integers: exact whatever the order
+    b = -3 * c0 + 3 * c1 - 2 * c2 - c3
+    if mode == "fp32":
+        t = (f32(4.0) * tanh32((x * f32(0.25)).astype(np.float32))).astype(np.float32)  # :91
+        z = tanh32((sc * (t + sh).astype(np.float32)).astype(np.float32))              # :92
+        poly = fma32(fma32(fma32(a, t, b), t, c2), t, c0)                              # :93
+        wp = fma32(f32(4.0) * c5, z, f32(2.0) * c4)                                    # :94
+        wp = fma32(wp, z, -(f32(3.0) * c5))
+        wp = fma32(wp, z, -c4)
+        hv = fma32((poly + wp).astype(np.float32), ps, x)                              # :95
+        hv = np.where(hv < 0, f32(0.0), hv)
+        return (hv * hv).astype(np.float32)                                            # :96
+    if mode != "fp16":
+        raise ValueError(mode)
+    th = h(x * f32(0.25))                                                              # :77
+    t = h(f32(4.0) * tanh32(th))                                                       # :78
+    warp = h(sc * (t + sh).astype(np.float32))                                         # :79
+    z = h(tanh32(warp))                                                                # :80
+    poly = fma16(fma16(fma16(a, t, b), t, c2), t, c0)                                  # :82-84
+    wp = fma16(f32(4.0) * c5, z, f32(2.0) * c4)                                        # :85
+    wp = fma16(wp, z, -(f32(3.0) * c5))                                                # :86
+    wp = fma16(wp, z, -c4)                                                             # :87
+    hv = h(fma32((poly + wp).astype(np.float32), ps, x))                               # :88
+    hv = np.where(hv < 0, f32(0.0), hv)
+    return h(hv * hv)                                                                  # :89
+
+
+# How Triton (3.6, default enable_fp_fusion) compiles each floating-point line of the
+# reference's fused kernel (ksdraft/kernels/ks3_triton.py) for gfx950, as this oracle
+# computes it. "fma16"/"fma32": the line's multiply and add are one fused multiply-add
+# (v_fma_f16 / v_pk_fma_f16, v_fma_f32 / v_fmac_f32 / v_fma_mix_f32); "mul,add": separately
+# rounded; "ieee_div": `/` is the correctly rounded division (v_div_scale, v_div_fmas,
+# v_div_fixup). Checked against tests/golden/ks3_fused_contract.json by
+# tests/test_oracle_fused_contract.py. Keys: (NL, line).
+FUSED_CONTRACT = {
+    # int8 mode
+    (2, 35): "ieee_div",          # _half_scale: maximum / 127
+    (2, 59): "fma16,mul16",       # fma16(tq16, fp16(4/127), shift16), then * scale16
+    (2, 70): "mul,add",           # x + s * (ps / 64): two fp32 roundings
+    (2, 73): "ieee_div",          # h / pre_scale
+    (2, 153): "ieee_div",         # h / hs, the requantization
+    # fp16 mode
+    (1, 79): "add,mul",           # scale * (t + shift) in fp32, then fp16
+    (1, 82): "fma16", (1, 83): "fma16", (1, 84): "fma16",   # poly Horner steps
+    (1, 85): "fma16", (1, 86): "fma16", (1, 87): "fma16",   # warped Horner steps
+    (1, 88): "add,fma32",         # fp16(fma32(poly + warped, ps, x))
+    (1, 153): "ieee_div",
+    # fp32 mode (line 92, scale * (t + shift), is a multiply after the add and cannot be
+    # contracted; the fixture also attributes the inlined tanh's own FMAs to that line)
+    (0, 93): "fma32",             # poly: three fused steps
+    (0, 94): "fma32",             # warped: three fused steps
+    (0, 95): "add,fma32",         # fma32(poly + warped, ps, x)
+    (0, 153): "ieee_div",
+}
 
 
 def coords_from_gemm(y32):
@@ -295,12 +400,14 @@ def spine_fused_int8(acc32, spine_codes, spine_scale, scale16, shift16, lut, gro
         return np.rint((v * k).astype(np.float32)).astype(np.int64)
 
     tq = lut[np.clip(idx32((x * f32(0.25)).astype(np.float32)) + 128, 0, 255)]
-    # ks3_triton.py:59: `tq.to(tl.float16) * (4. / 127.)` is an fp16 op in Triton (a Python
-    # float scalar does not take part in type promotion, triton/language/semantic.py
-    # computation_type_impl), so the constant is fp16(4/127) and the product is rounded to
-    # fp16; the composed path (spine_features_int8) keeps torch's fp32 constant.
+    # ks3_triton.py:59: `tq.to(tl.float16) * (4. / 127.) + shift.to(tl.float16)` is fp16
+    # arithmetic in Triton (a Python float scalar does not take part in type promotion,
+    # triton/language/semantic.py computation_type_impl), with the constant fp16(4/127)
+    # (0x2808 in the compiled code), and the multiply and the add are contracted into one
+    # v_fma_f16 (FUSED_CONTRACT); then one fp16 multiply by the warp scale. The composed
+    # path (spine_features_int8) keeps torch's fp32 constant and two roundings.
     step16 = f32(np.float16(4.0 / 127.0))
-    warp = h(sc * h(h(tq.astype(np.float32) * step16) + sh))
+    warp = h(sc * fma16(tq.astype(np.float32), step16, sh))
     zq = lut[np.clip(idx32(warp) + 128, 0, 255)]
     a = 2 * c0 - 2 * c1 + c2 + c3
     b = -3 * c0 + 3 * c1 - 2 * c2 - c3

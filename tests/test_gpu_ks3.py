@@ -385,3 +385,21 @@ def test_warp_scalars_follow_their_codes(gold):
         cell.warp_shift_codes.neg_()
     s3, h3 = cell._warp_scalars(torch.float16)
     assert torch.equal(h3, fresh()[1]) and not torch.equal(h3, h2)
+
+
+def test_cell_built_and_run_under_inference_mode(gold):
+    """A cell built, converted and evaluated inside torch.inference_mode (whose tensors
+    carry no version counter) gives the same output as one built outside it; the warp
+    scalars are then dequantized every call instead of cached."""
+    x = _g(gold["std1/x"])
+    ref_cell = K.KS3Int8Cell(_Cell(gold).to(DEV), group=128, nonlinear="int8").eval()
+    with torch.no_grad():
+        ref = ref_cell(x)
+    with torch.inference_mode():
+        cell = K.KS3Int8Cell(_Cell(gold).to(DEV), group=128, nonlinear="int8").eval()
+        y1 = cell(x)
+        y2 = cell(x)
+        yc = K.KS3Int8Cell._forward_composed(cell, x)
+    assert torch.equal(y1, ref) and torch.equal(y2, ref)
+    with torch.no_grad():
+        assert torch.equal(yc, K.KS3Int8Cell._forward_composed(ref_cell, x))

@@ -104,7 +104,7 @@ def test_spine_float_random_against_oracle(mode, fused, M, Fn, group):
                             want_h=True, want_codes=False)
     _, hq, hs = K.spine_float(xin, _g(sq), _g(ss), _g(sc), _g(sh), mode, group)
     h = h.cpu().numpy()
-    exp = ok.spine_features_float(np.clip(x, -65504.0, 65504.0), sq, ss, sc, sh, mode)
+    exp = ok.spine_features_float(np.clip(x, -65504.0, 65504.0), sq, ss, sc, sh, mode, fused=fused)
     _check_h(mode, h, exp)
     eq, es = oq.quantize_last_dim(h, group)
     assert np.array_equal(hq.cpu().numpy(), eq)
@@ -144,7 +144,7 @@ def _mode_chain(gold, mode, x, fused):
     else:
         xin = ok.coords_from_gemm(acc)
         sc, sh = (sc32, sh32) if mode == "fp32" else (ok.h(sc32), ok.h(sh32))
-    hv = ok.spine_features_float(xin, p["spine_codes"], p["spine_scale"], sc, sh, mode)
+    hv = ok.spine_features_float(xin, p["spine_codes"], p["spine_scale"], sc, sh, mode, fused=fused)
     hq, hs = oq.quantize_last_dim(hv)
     return og.gemm_ordered(hq, hs, p["up_codes"], p["up_scales"])
 

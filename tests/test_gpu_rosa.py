@@ -54,6 +54,26 @@ def test_match_vs_pair_bruteforce(T):
     assert np.array_equal(mj.cpu().numpy(), ej)
 
 
+@pytest.mark.parametrize("lmax", [1, 2, 3, 5, 7, 63])
+@pytest.mark.parametrize("T", [100, 300])
+def test_match_explicit_max_match_len(T, lmax):
+    """Caps below and above the default (every residue of the walk's four-length steps and
+    its two/one-length tail, and the 63-bit maximum) against the pair brute force."""
+    rng = np.random.default_rng(T * 64 + lmax)
+    n = 16
+    q = _streams(rng, n, T)
+    k = np.concatenate([q[:6], _streams(rng, n - 6, T)])
+    v = _streams(rng, n, T)
+    proj = [_bits_to_proj(b, rng).T[None] for b in (q, k, v)]
+    packed = [R.pack_bits(_g(p)) for p in proj]
+    sign, mj = R.match_packed(*(p.reshape(n, -1) for p in packed), T, max_match_len=lmax,
+                              want_j=True)
+    es, ej, el = orr.match(q, k, v, max_match_len=lmax)
+    assert el.max() == min(lmax, T - 1)
+    assert np.array_equal(sign.cpu().numpy().astype(np.float32), es)
+    assert np.array_equal(mj.cpu().numpy(), ej)
+
+
 def test_match_t2048_sampled_streams():
     rng = np.random.default_rng(2048)
     n, T = 12, 2048
@@ -237,19 +257,19 @@ def test_rosa_mixer_eval_and_training():
         assert p.grad is not None and torch.isfinite(p.grad).all(), name
 
 
-def _credits_direct(q, k, v, gsign):
+def _credits_direct(q, k, v, gsign, lmax=None):
     """ksd_rosa_credits on (n, T) bit streams, grad_sign (n, T): credits (n, 3, T)."""
     from ksdraft_amd import _lib
     n, T = q.shape
     rng = np.random.default_rng(T)
     proj = [_bits_to_proj(b, rng).T[None] for b in (q, k, v)]  # (1, T, n)
     packed = [R.pack_bits(_g(p)).reshape(n, -1).contiguous() for p in proj]
-    _, mj = R.match_packed(*packed, T, want_j=True)
+    lmax = orr.default_max_match_len(T, lmax)
+    _, mj = R.match_packed(*packed, T, max_match_len=lmax, want_j=True)
     grad = _g(np.ascontiguousarray(gsign.T[None]))  # (1, T, n), payload 1
     pay = torch.ones(n, device=DEV)
     cred = torch.zeros((n, 3, T), device=DEV)
     part = torch.empty((n,), device=DEV)
-    lmax = orr.default_max_match_len(T)
     _lib.call("ksd_rosa_credits", packed[0].data_ptr(), packed[1].data_ptr(), packed[2].data_ptr(),
               mj.contiguous().data_ptr(), grad.data_ptr(), pay.data_ptr(), 1, T, n, lmax,
               cred.data_ptr(), part.data_ptr(), _lib.stream_ptr(torch.device(DEV)))
@@ -270,6 +290,22 @@ def test_credits_structured_streams_bruteforce(T):
     gsign[:, ::7] = 0.0  # positions whose gradient is zero contribute nothing
     got = _credits_direct(q, k, v, gsign)
     exp = orr.credits(q, k, v, gsign)
+    scale = np.abs(exp).max() + 1e-30
+    np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * scale)
+    assert np.array_equal(got == 0, exp == 0)
+
+
+@pytest.mark.parametrize("lmax", [2, 3, 5, 7])
+def test_credits_explicit_max_match_len_bruteforce(lmax):
+    """Short caps: every flip's re-match under the same cap (the definition) at T = 200."""
+    T, n = 200, 12
+    rng = np.random.default_rng(500 + lmax)
+    q = _streams(rng, n, T)
+    k = np.concatenate([q[:4], _streams(rng, n - 4, T)])
+    v = _streams(rng, n, T)
+    gsign = rng.standard_normal((n, T)).astype(np.float32)
+    got = _credits_direct(q, k, v, gsign, lmax)
+    exp = orr.credits(q, k, v, gsign, max_match_len=lmax)
     scale = np.abs(exp).max() + 1e-30
     np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * scale)
     assert np.array_equal(got == 0, exp == 0)

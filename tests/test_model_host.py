@@ -88,31 +88,44 @@ def test_injection_stacked_gemms_equal_the_reference_composition():
         torch.testing.assert_close(p, pr, rtol=1e-12, atol=1e-12)
 
 
-def test_inplace_row_gather_gradient_equals_the_dense_embedding_gradient():
-    """The trainer's gathers from the tied weight add their row gradients into the dense
-    gradient the weight already holds (the head's dW), in place. The result must equal
-    autograd's dense accumulation bit for bit, duplicate ids included, and without a
-    gradient on the weight the backward returns the dense embedding gradient."""
+def test_sparse_row_gather_gradient_equals_the_dense_embedding_gradient():
+    """The trainer's gathers from the tied weight return sparse row-sum gradients, which
+    autograd adds into the head's dense gradient. The weight's .grad must equal the dense
+    embedding backward's accumulation (duplicate ids included); torch.autograd.grad with a
+    preset .grad must return the lookup's own gradient and leave .grad untouched."""
     import torch.nn.functional as F
-    from ksdraft_amd.kernels.embedding import gather_rows_inplace_grad
+    from ksdraft_amd.kernels.embedding import gather_rows_sparse_grad
     torch.manual_seed(0)
     w = torch.randn(50, 8, requires_grad=True)
     ids = torch.tensor([[3, 7, 3], [49, 0, 7], [3, 3, 12]])
-    g = torch.randn(3, 3, 8)
-    head = torch.randn(50, 8)
-    out = gather_rows_inplace_grad(w, ids)
+    ids2 = torch.tensor([[0, 0, 5], [7, 7, 7], [49, 1, 2]])
+    g, g2 = torch.randn(3, 3, 8), torch.randn(3, 3, 8)
+    x, gh = torch.randn(6, 8), torch.randn(6, 50)
+    out = gather_rows_sparse_grad(w, ids)
     assert torch.equal(out, F.embedding(ids, w))
-    w.grad = head.clone()
-    buf = w.grad
-    (out * g).sum().backward()
-    assert w.grad is buf  # added in place
-    got = w.grad.clone()
-    w.grad = head.clone()
-    (F.embedding(ids, w) * g).sum().backward()
-    assert torch.equal(got, w.grad)
+
+    def step(gather):
+        w.grad = None
+        loss = ((x @ w.t()) * gh).sum() + (gather(ids, w) * g).sum() + (gather(ids2, w) * g2).sum()
+        loss.backward()
+        return w.grad
+    got = step(lambda i, ww: gather_rows_sparse_grad(ww, i))
+    assert got.layout == torch.strided and got.shape == w.shape
+    exp = step(F.embedding)
+    torch.testing.assert_close(got, exp, rtol=1e-6, atol=1e-6)
+
+    # one gather beside the head: the same two additions per element, bit for bit
     w.grad = None
-    (gather_rows_inplace_grad(w, ids) * g).sum().backward()
-    dense = w.grad.clone()
+    ((x @ w.t()) * gh).sum().add((gather_rows_sparse_grad(w, ids) * g).sum()).backward()
+    one = w.grad.clone()
     w.grad = None
-    (F.embedding(ids, w) * g).sum().backward()
-    assert torch.equal(dense, w.grad)
+    ((x @ w.t()) * gh).sum().add((F.embedding(ids, w) * g).sum()).backward()
+    assert torch.equal(one, w.grad)
+
+    # autograd.grad with .grad already set: no side effects, the lookup's own gradient
+    preset = torch.randn(50, 8)
+    w.grad = preset.clone()
+    (gr,) = torch.autograd.grad((gather_rows_sparse_grad(w, ids) * g).sum(), w)
+    (ge,) = torch.autograd.grad((F.embedding(ids, w) * g).sum(), w)
+    assert torch.equal(gr.to_dense(), ge)
+    assert torch.equal(w.grad, preset)
