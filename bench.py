@@ -65,6 +65,8 @@ def parse():
     p.add_argument("--no-ln", action="store_true", help="skip the fused LayerNorm + quantize report")
     p.add_argument("--no-c5", action="store_true", help="skip the config-5 draft train step")
     p.add_argument("--c5-steps", type=int, default=3)
+    p.add_argument("--c5-loss-scale", type=float, default=C5_LOSS_SCALE,
+                   help="power-of-two loss scale of the config-5 step (1 = unscaled)")
     p.add_argument("--only-c5", action="store_true", help="run only the config-5 step (profiling)")
     p.add_argument("--pmc-probe", action="store_true",
                    help="for rocprofv3 --pmc runs: a 256 MiB device copy (counter "
@@ -439,19 +441,66 @@ def ln_quant_times(dev, reps):
     return res
 
 
-def draft_c5(dev, steps, warmup):
+# The config-5 step's loss scale. 2^12 gives every GS128 gradient group of the 24 layers
+# a normal or subnormal fp16 scale (the unscaled step leaves every layer's weight gradient
+# exactly zero: the groups' scales clamp to 2^-24 and their codes round to 0). Larger
+# scales overflow the KS3 backward's fp16 column sums of dcoeff (reference
+# ks3_int8.py:379-388 sums in fp16) within two optimizer steps (2^16: inf at step 3).
+C5_LOSS_SCALE = 2.0 ** 12
+
+
+def _zero_tile_fraction(tr, tokens, teacher):
+    """One untimed training step with the backward GEMM launches wrapped: the fraction of
+    the 128 x 128 tiles of their A operands (the int8 codes of the upstream gradients,
+    dY and dY^T, and of the KS3 cell's dc) that hold only zero codes."""
+    import ksdraft_amd.kernels.ks3_int8 as kk
+    import ksdraft_amd.kernels.linear as kl
+    import ksdraft_amd.train as ktr
+    stats = [0, 0]
+    orig = kl.w8a8_gemm_pair
+
+    def counting(first, second, group=128):
+        for prob in (first, second):
+            a = prob[0]
+            M, K = a.shape
+            Mp, Kp = -(-M // 128) * 128, -(-K // 128) * 128
+            nz = torch.nn.functional.pad(a != 0, (0, Kp - K, 0, Mp - M))
+            nz = nz.view(Mp // 128, 128, Kp // 128, 128).any(3).any(1)
+            stats[0] += int((~nz).sum())
+            stats[1] += nz.numel()
+        return orig(first, second, group)
+    mods = (kl, kk, ktr)
+    saved = [m.w8a8_gemm_pair for m in mods]
+    for m in mods:
+        m.w8a8_gemm_pair = counting
+    try:
+        tr.step(tokens, teacher)
+    finally:
+        for m, f in zip(mods, saved):
+            m.w8a8_gemm_pair = f
+    torch.cuda.synchronize()
+    return round(stats[0] / max(1, stats[1]), 4)
+
+
+def draft_c5(dev, steps, warmup, loss_scale=C5_LOSS_SCALE, int8_injection=True):
     """the full KSDraft draft training step, INT8 forward + backward
     through every linear. 24 DraftBlocks (Rosa 512 streams, DSpine injection, KS3 5888
     charts) at d = 1536, vocabulary 150144 with the tied int8 head and the fused
     cross-entropy, a synthetic bf16 teacher state ~N(0,1) (d 1536) on the teacher_proj
     seam, B 4 x T 2048 uniform token ids (T + 1 drawn for the shift), AdamW (lr 3e-4, wd
     0.01) fused with the int8 repack, grad-norm clip 1.0. Random init: the reference's
-    inits with the zero-init surfaces woken to N(0, 0.02). tok/s = 8192 / step time (HIP
-    events over `steps` steps after `warmup`); the forward, backward and optimizer parts
-    of the step are timed with events too."""
+    inits with the zero-init surfaces woken to N(0, 0.02). int8_injection: the DSpine
+    low-rank maps are Int8Linear surfaces too (every linear of the step is INT8).
+    loss_scale: backward runs on loss_scale * loss (a power of two, divided out again in
+    the clip factor); at random init the unscaled mean loss over 8192 tokens leaves most
+    GS128 gradient groups below the fp16 scale floor, so their codes are all zero.
+    tok/s = 8192 / step time (HIP events over `steps` steps after `warmup`); the forward,
+    backward and optimizer parts of the step are timed with events too. The fraction of
+    all-zero 128 x 128 gradient tiles among the backward GEMMs' A operands comes from one
+    extra untimed step."""
     from ksdraft_amd.config import baseline_config
     from ksdraft_amd.model import KSDraftModel, to_int8
-    from ksdraft_amd.train.int8_step import Int8DraftTrainer, clip_coefficient
+    from ksdraft_amd.train.int8_step import Int8DraftTrainer
     cfg = baseline_config()
     torch.manual_seed(0)
     fm = KSDraftModel(cfg, teacher_dim=cfg.d_model, device=dev)
@@ -459,10 +508,11 @@ def draft_c5(dev, steps, warmup):
         for name, p in fm.named_parameters():
             if name.endswith(("up.weight", "out_proj.weight", "teacher_proj.weight")):
                 p.normal_(0, 0.02)
-    model = to_int8(fm, trainable=True)
+    model = to_int8(fm, trainable=True, int8_injection=int8_injection)
     del fm
     torch.cuda.empty_cache()
-    tr = Int8DraftTrainer(model, lr=3e-4, weight_decay=0.01, grad_clip=1.0)
+    tr = Int8DraftTrainer(model, lr=3e-4, weight_decay=0.01, grad_clip=1.0,
+                          loss_scale=loss_scale)
     g = torch.Generator(device=dev).manual_seed(0)
     B, T = 4, 2048
     tokens = torch.randint(0, cfg.vocab_size, (B, T + 1), device=dev, generator=g)
@@ -479,11 +529,9 @@ def draft_c5(dev, steps, warmup):
         tr.model.train()
         loss, ce, ts = tr.loss(tokens, teacher)
         e[1].record()
-        tr.opt.zero_grad(set_to_none=True)
-        loss.backward()
+        tr.backward(loss)
         e[2].record()
-        coef = clip_coefficient(tr.model.parameters(), tr.grad_clip)
-        tr.opt.step(clip_coef=coef)
+        tr.optimizer_step()
         e[3].record()
         losses.append(loss.detach())
     torch.cuda.synchronize()
@@ -504,6 +552,9 @@ def draft_c5(dev, steps, warmup):
         "peak_mem_gb": round(torch.cuda.max_memory_allocated(dev) / 2**30, 2),
         "workload": "BASELINE config 5: 24 layers, d 1536, 512 streams, 5888 charts, vocab "
                     "150144, B 4 x T 2048, teacher state bf16 (d 1536)",
+        "int8_injection": bool(int8_injection),
+        "loss_scale": loss_scale,
+        "zero_grad_tile_frac": _zero_tile_fraction(tr, tokens, teacher),
     }
     res["int8_gemm_tops"] = round(res["int8_gemm_ops_per_step"] / (step_ms * 1e-3) / 1e12, 1)
     # the staged int8 embedding lookup (codes of the tied head) against the float lookup
@@ -644,7 +695,8 @@ def main():
         pmc_probe(x, w, dy)
         return
     if args.only_c5:
-        print(json.dumps({"draft_c5": draft_c5(dev, args.c5_steps, 1)}), flush=True)
+        print(json.dumps({"draft_c5": draft_c5(dev, args.c5_steps, 1, args.c5_loss_scale)}),
+              flush=True)
         return
 
     # eager: warm-up then K timed steps
@@ -735,8 +787,12 @@ def main():
     }
     if not args.no_c5:
         torch.cuda.empty_cache()
-        out["draft_c5"] = draft_c5(dev, args.c5_steps, 1)
+        # the headline step: every linear INT8, live gradients (loss scale 2^12)
+        out["draft_c5"] = draft_c5(dev, args.c5_steps, 1, args.c5_loss_scale)
         out["draft_train_step_tok_s"] = out["draft_c5"]["tok_per_s"]
+        torch.cuda.empty_cache()
+        # beside it: the unscaled loss, whose gradients mostly quantize to zero codes
+        out["draft_c5_unscaled"] = draft_c5(dev, args.c5_steps, 1, 1.0)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(xc, wc, dyc, args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -18,6 +18,8 @@ cross-entropy targets.
 
 from __future__ import annotations
 
+import math
+
 import torch
 import torch.nn.functional as F
 
@@ -26,15 +28,32 @@ from ..kernels.linear import Int8Linear
 from . import IGNORE_INDEX, AdamWRequant, LinearCrossEntropyInt8
 
 
-def clip_coefficient(params, max_norm: float) -> torch.Tensor:
+def clip_coefficient(params, max_norm: float, loss_scale: float = 1.0) -> torch.Tensor:
     """The factor torch.nn.utils.clip_grad_norm_ multiplies every gradient by:
     min(1, max_norm / (||g||_2 + 1e-6)) over all gradients, as a 1-element device tensor.
     The per-tensor norms are one multi-tensor launch (torch._foreach_norm), as in
-    clip_grad_norm_'s own foreach path."""
+    clip_grad_norm_'s own foreach path.
+
+    loss_scale: the gradients hold loss_scale * g (a power of two, so the scaling and the
+    norm's division by it are exact); the factor returned then applies the unscaling too:
+    min(1, max_norm / (||g|| + 1e-6)) / loss_scale."""
     grads = [p.grad for p in params if p.grad is not None]
     norms = torch._foreach_norm(grads, 2.0)
     total = torch.linalg.vector_norm(torch.stack(norms))
-    return torch.clamp(max_norm / (total + 1e-6), max=1.0).reshape(1)
+    if loss_scale != 1.0:
+        total = total / loss_scale
+    coef = torch.clamp(max_norm / (total + 1e-6), max=1.0)
+    if loss_scale != 1.0:
+        coef = coef / loss_scale
+    return coef.reshape(1)
+
+
+def _check_loss_scale(s: float) -> float:
+    s = float(s)
+    m, e = math.frexp(s)
+    if not (s > 0 and m == 0.5):
+        raise ValueError(f"loss_scale must be a positive power of two, got {s}")
+    return s
 
 
 def transfer_space_loss(features, embedding_weight: torch.Tensor, tgt: torch.Tensor,
@@ -66,16 +85,25 @@ class Int8DraftTrainer:
 
     tokens (B, T + 1): inputs tokens[:, :-1], targets tokens[:, 1:] (train/__init__.py:152).
     The model must come from ``to_int8(model, trainable=True)`` (its head is an Int8Linear
-    tied to the embedding)."""
+    tied to the embedding).
+
+    loss_scale (a power of two, default 1): backward runs on loss_scale * loss and the
+    optimizer step divides it out again (through the clip factor). The int8 gradient
+    operands are per-group symmetric codes, so scaling by a power of two leaves every code
+    unchanged wherever the group's fp16 scale stays a normal number, and gives codes to the
+    groups whose scale would otherwise clamp to the 2^-24 minimum and round to zero (a
+    mean loss over 8192 tokens at random init has most vocabulary groups of the logits'
+    gradient near 1e-9)."""
 
     def __init__(self, model, lr: float = 3e-4, betas=(0.9, 0.999), eps: float = 1e-8,
                  weight_decay: float = 0.01, grad_clip: float = 1.0,
-                 transfer_weight: float = 0.5):
+                 transfer_weight: float = 0.5, loss_scale: float = 1.0):
         if not isinstance(getattr(model, "head", None), Int8Linear):
             raise ValueError("Int8DraftTrainer needs to_int8(model, trainable=True)")
         self.model = model
         self.grad_clip = grad_clip
         self.transfer_weight = transfer_weight
+        self.loss_scale = _check_loss_scale(loss_scale)
         self.opt = AdamWRequant(model.parameters(), lr=lr, betas=betas, eps=eps,
                                 weight_decay=weight_decay)
         for mod in model.modules():
@@ -98,11 +126,18 @@ class Int8DraftTrainer:
                                           tgt.reshape(-1), IGNORE_INDEX, 128)
         return ce + self.transfer_weight * ts, ce, ts
 
+    def backward(self, loss: torch.Tensor):
+        """Gradients of loss_scale * loss (the scale is exact: a power of two)."""
+        self.opt.zero_grad(set_to_none=True)
+        (loss * self.loss_scale if self.loss_scale != 1.0 else loss).backward()
+
+    def optimizer_step(self):
+        coef = clip_coefficient(self.model.parameters(), self.grad_clip, self.loss_scale)
+        self.opt.step(clip_coef=coef)
+
     def step(self, tokens: torch.Tensor, teacher_states: torch.Tensor | None = None):
         self.model.train()
         loss, ce, ts = self.loss(tokens, teacher_states)
-        self.opt.zero_grad(set_to_none=True)
-        loss.backward()
-        coef = clip_coefficient(self.model.parameters(), self.grad_clip)
-        self.opt.step(clip_coef=coef)
+        self.backward(loss)
+        self.optimizer_step()
         return loss.detach(), ce.detach(), ts.detach()

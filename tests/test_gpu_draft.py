@@ -248,6 +248,24 @@ def test_clip_coefficient_matches_torch():
         torch.testing.assert_close(g0 * coef, p.grad, rtol=1e-6, atol=1e-7)
 
 
+def test_clip_coefficient_with_loss_scale():
+    """Gradients of a power-of-two scaled loss: the factor returned for them applies the
+    clip and the unscaling at once, bit for bit the unscaled gradients' clip."""
+    torch.manual_seed(4)
+    S = 2.0 ** 12
+    for spread in (3.0, 1e-3):  # clipping active, and inactive
+        ps = [torch.nn.Parameter(torch.randn(n, device=DEV)) for n in (10, 300, 7)]
+        grads = [torch.randn_like(p) * spread for p in ps]
+        for p, g in zip(ps, grads):
+            p.grad = g.clone()
+        coef = clip_coefficient(ps, 1.0)
+        for p, g in zip(ps, grads):
+            p.grad = g * S
+        coef_s = clip_coefficient(ps, 1.0, loss_scale=S)
+        for p, g in zip(ps, grads):
+            assert torch.equal(p.grad * coef_s, g * coef)
+
+
 def test_int8_draft_step_with_int8_embedding():
     """to_int8(int8_embedding=True): the lookup reads the tied head's codes; the looked-up
     rows equal the oracle dequantization of Q(master)[ids], and training steps run."""

@@ -129,3 +129,12 @@ def test_sparse_row_gather_gradient_equals_the_dense_embedding_gradient():
     (ge,) = torch.autograd.grad((F.embedding(ids, w) * g).sum(), w)
     assert torch.equal(gr.to_dense(), ge)
     assert torch.equal(w.grad, preset)
+
+
+def test_loss_scale_must_be_a_power_of_two():
+    from ksdraft_amd.train.int8_step import _check_loss_scale
+    assert _check_loss_scale(1) == 1.0 and _check_loss_scale(4096.0) == 4096.0
+    assert _check_loss_scale(2.0 ** -3) == 0.125
+    for bad in (0, -2.0, 3.0, 1000.0, float("inf"), float("nan")):
+        with pytest.raises(ValueError):
+            _check_loss_scale(bad)
