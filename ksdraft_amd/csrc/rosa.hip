@@ -1144,10 +1144,15 @@ __device__ __forceinline__ uint32_t evt_key16(uint32_t key, int c) {
 }
 // entry p := max(entry p, k16); the word's other entry may be updated by another lane at
 // the same time, hence the compare-and-swap
+// The table lives in LDS; the volatile accesses go through LDS-typed pointers (the low 32
+// bits of a generic pointer into LDS are its LDS offset), so they compile to ds_* and not
+// to flat accesses.
+typedef __attribute__((address_space(3))) volatile uint32_t lds_vu32;
+typedef __attribute__((address_space(3))) volatile uint16_t lds_vu16;
 __device__ __forceinline__ void evt_max16(uint32_t *evt, int p, uint32_t k16) {
   uint32_t *w = evt + (p >> 1);
   const int sh = (p & 1) * 16;
-  uint32_t old = *(volatile uint32_t *)w;
+  uint32_t old = *(lds_vu32 *)(uint32_t)(uintptr_t)w;
   while (((old >> sh) & 0xffffu) < k16) {
     const uint32_t prev = atomicCAS(w, old, (old & ~(0xffffu << sh)) | (k16 << sh));
     if (prev == old) break;
@@ -1155,10 +1160,10 @@ __device__ __forceinline__ void evt_max16(uint32_t *evt, int p, uint32_t k16) {
   }
 }
 __device__ __forceinline__ uint32_t evt_get16(const uint32_t *evt, int p) {
-  return ((const volatile uint16_t *)evt)[p];
+  return ((lds_vu16 *)(uint32_t)(uintptr_t)evt)[p];
 }
 __device__ __forceinline__ void evt_clear16(uint32_t *evt, int p) {
-  ((volatile uint16_t *)evt)[p] = 0;
+  ((lds_vu16 *)(uint32_t)(uintptr_t)evt)[p] = 0;
 }
 
 __device__ __forceinline__ int set_maxbit(uint32_t word) {  // highest candidate of a wave set
@@ -1353,12 +1358,15 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
     auto step = [&](auto hi_c, int L, bool tail) __attribute__((always_inline)) {
       uint32_t D, Dn;
       level_c(hi_c, L, D, Dn);
-      if (L <= imax && __any((A & Dn) != 0u)) hasext |= 1ull << L;
-      if (tail) {
-        if (L >= 1 && L >= Ls - 2 && L <= imax) {  // lower levels: recomputed below when needed
+      if (L <= imax) {
+        if (__any((A & Dn) != 0u)) {
+          hasext |= 1ull << L;
+        } else if (L >= 1) {  // a q flip at offset L without an extension: latest j of A_L
           const int lj = set_maxbit(A);
           if (lane == 0) lat[L] = lj;
         }
+      }
+      if (tail) {
         if (__any((A & farm) != 0u)) {
           farw = A & farm;
           farL = L;
@@ -1446,14 +1454,11 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
         U = unresolved();
       }
     }
-    // Two kinds of bucket i need A_i again, walked in ascending i along one chain:
-    //  U: buckets with every lifted length below the last checkpoint; their candidates
-    //     A_i & Dn_i extended level by level until none survives;
-    //  M: buckets 1 <= i < L* - 2 without an extension (disjoint from U), for the latest
-    //     j of A_i.
-    const uint64_t M = Ls - 3 >= 1 ? ~hasext & (((1ull << min(imax, Ls - 3)) - 1ull) << 1) : 0ull;
+    // U: buckets with every lifted length below the last checkpoint need A_i again: their
+    // candidates A_i & Dn_i are extended level by level until none survives, walked in
+    // ascending i along one chain
     {
-      uint64_t W = U | M;
+      uint64_t W = U;
       uint32_t Ach = valid;  // A_Lch
       int Lch = 0;
       while (W) {
@@ -1463,11 +1468,6 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
         for (; Lch < i; ++Lch) {
           level(Lch, D, Dn);
           Ach &= D;
-        }
-        if ((M >> i) & 1ull) {
-          const int lj = set_maxbit(Ach);
-          if (lane == 0) lat[i] = lj;
-          continue;
         }
         level(i, D, Dn);
         uint32_t Tt = Ach & Dn;
