@@ -354,13 +354,14 @@ def rosa_kernel_times(dev, reps):
     sign, mj = R.match_packed(*flat, T, want_j=True)
     pairs = Bq * S * T * (T - 1) // 2
     from ksdraft_amd import _lib
-    cred = torch.zeros(Bq * S, 3, T, device=dev)
+    cred = torch.empty(Bq * S, 3, T, device=dev)
     part = torch.empty(Bq * S, device=dev)
+    sums = torch.empty(Bq * S, 3, T, dtype=torch.int64, device=dev)
 
     def credits():
         _lib.call("ksd_rosa_credits", flat[0].data_ptr(), flat[1].data_ptr(), flat[2].data_ptr(),
                   mj.data_ptr(), gout.data_ptr(), payload.data_ptr(), Bq, T, S, 62,
-                  cred.data_ptr(), part.data_ptr(), _lib.stream_ptr(dev))
+                  cred.data_ptr(), part.data_ptr(), sums.data_ptr(), _lib.stream_ptr(dev))
 
     BTd, BTS = Bq * T * d, Bq * T * S
     # the training form on fp32 x (config 5's stream dtype): both layouts of q/k/v_in, and

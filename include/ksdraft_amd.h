@@ -496,14 +496,18 @@ int ksd_rosa_hard(const int8_t *sign, const float *payload, int64_t B, int64_t T
  *   q/k/v_bits  (B*S, ceil(T/32)) uint32 from ksd_rosa_pack_bits
  *   match_j     (B*S, T) int32 endpoints from ksd_rosa_match
  *   grad        (B, T, S) fp32 upstream gradient of the hard output
- *   credits     (B*S, 3, T) fp32, zeroed by the caller; accumulated with atomics, so the
- *               summation order (not the flip decisions) varies between runs
+ *   credits     (B*S, 3, T) fp32, written by the call (rows q, k, v)
  *   payload_partial (B*S,) fp32: sum over t of grad * sign per stream (fixed order)
+ *   credit_sums (B*S, 3, T) int64 workspace, or NULL. With it, every credit is an exact
+ *               fixed-point sum of +-2 g(t) (g rounded once, at 2^-48 of the stream's
+ *               largest |grad * payload|), so the credits are identical on every run; a
+ *               stream with a non-finite gradient, or a call without the workspace, adds
+ *               fp32 atomics instead, whose summation order varies between runs
  */
 int ksd_rosa_credits(const uint32_t *q_bits, const uint32_t *k_bits, const uint32_t *v_bits,
                      const int32_t *match_j, const float *grad, const float *payload, int64_t B,
                      int64_t T, int64_t S, int lmax, float *credits, float *payload_partial,
-                     void *stream);
+                     int64_t *credit_sums, void *stream);
 
 /*
  * R5 projection-space gradients (reference ksdraft/kernels/rosa_credit_gpu.py:99-111):

@@ -74,7 +74,7 @@ SIGNATURES = {
     "ksd_injection_update_backward": [_P, _P, _P, _P, _P, _I64, _I64, _P, _P, _P],
     "ksd_rosa_match": [_P, _P, _P, _I64, _I64, _INT, _P, _P, _P],
     "ksd_rosa_hard": [_P, _P, _I64, _I64, _I64, _P, _INT, _P],
-    "ksd_rosa_credits": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P, _P, _P],
+    "ksd_rosa_credits": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P, _P, _P, _P],
     "ksd_rosa_credit_grads": [_P, _P, _P, _P, _INT, _P, _I64, _I64, _I64,
                               _P, _P, _P, _P, _P],
 }

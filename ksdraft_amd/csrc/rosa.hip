@@ -893,6 +893,7 @@ __device__ __forceinline__ float sign_of(uint32_t key, const uint32_t *vw) {
   return key_len(key) >= 1 && getbit(vw, key_j(key) + 1) ? 1.0f : -1.0f;
 }
 
+
 // Block = one stream, 4 waves; wave w handles positions t = w, w + 4, ... and its 64 lanes
 // split the candidates j. Per-wave LDS tables for the current t:
 //   Mw[64]   best key per common-suffix bucket c (c >= 63 pooled)
@@ -902,6 +903,79 @@ __device__ __forceinline__ float sign_of(uint32_t key, const uint32_t *vw) {
 constexpr int kNear = 128;
 constexpr int kCredWaves = 4;
 constexpr int kCredWave32 = 64 + 64 + 128 + 2 * kNear / 4 + 2 * kNear;  // uint32 words per wave
+
+// Credit sums in fixed point. Every contribution to a credit entry is (s' - s) g(t) =
+// +-2 g(t), at most one per position t, so with |g| < 2^e over the stream an entry's sum
+// stays below 2^(1 + ceil(log2 T) + e). Scaled by 2^k, k = 61 - ceil(log2 T) - e, g(t) is
+// rounded once to an integer (an error below 2^-48 of the stream's largest gradient) and
+// the entries are exact int64 sums of +-2 g(t): the result does not depend on
+// the order in which the atomics land, so the credits are bit-identical on every run. A
+// stream whose gradient holds a non-finite value keeps fp32 atomics (its credits are not
+// finite either); so does a call without the int64 workspace.
+struct CredAcc {
+  float *f;               // this stream's (3, T) fp32 credits: q at 0, k at T, v at 2T
+  unsigned long long *a;  // this stream's (3, T) int64 sums, or null
+  double scale;           // 2^k
+  // g(t) in fixed point, once per position
+  __device__ __forceinline__ long long fixed(float g) const {
+    return a ? (long long)rint((double)g * scale) : 0ll;
+  }
+  // contribution d * g(t), d = s' - s = +-2
+  __device__ __forceinline__ void add(int off, float d, float g, long long gi) const {
+    if (a) atomicAdd(a + off, (unsigned long long)((long long)d * gi));
+    else atomicAdd(f + off, d * g);
+  }
+};
+
+// Block-level set-up of one stream's credits: zero the outputs, find the scale. red: LDS
+// scratch of kCredWaves + 1 words. Ends with a barrier.
+__device__ CredAcc cred_prologue(float *f, unsigned long long *a, const float *grad, int64_t b,
+                                 int64_t s, int64_t S, int T, float pay, uint32_t *red) {
+  float m = 0.0f;
+  bool bad = false;
+  for (int t = threadIdx.x; t < T; t += blockDim.x) {
+    const float g = fabsf(grad[(b * T + t) * S + s] * pay);
+    bad |= !(g <= 3.402823466e38f);  // inf or NaN
+    m = fmaxf(m, g);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  const bool wbad = __any(bad);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) red[kCredWaves] = 0u;
+  __syncthreads();
+  if (lane == 0) {
+    red[wave] = __builtin_bit_cast(uint32_t, m);
+    if (wbad) red[kCredWaves] = 1u;
+  }
+  __syncthreads();
+  float mx = 0.0f;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) mx = fmaxf(mx, __builtin_bit_cast(float, red[w]));
+  CredAcc c{f, (a && red[kCredWaves] == 0u) ? a : nullptr, 1.0};
+  if (c.a) {
+    int e = 0;
+    if (mx > 0.0f) frexpf(mx, &e);  // mx < 2^e
+    const int lc = T > 1 ? 32 - __clz(T - 1) : 0;  // ceil(log2 T)
+    c.scale = ldexp(1.0, 61 - lc - e);
+    for (int i = threadIdx.x; i < 3 * T; i += blockDim.x) c.a[i] = 0ull;
+  } else {
+    for (int i = threadIdx.x; i < 3 * T; i += blockDim.x) f[i] = 0.0f;
+  }
+  __threadfence();
+  __syncthreads();
+  return c;
+}
+
+// After every wave's last contribution (behind a barrier): the int64 sums to fp32.
+__device__ void cred_epilogue(const CredAcc &c, int T) {
+  if (!c.a) return;  // block-uniform
+  __threadfence();
+  __syncthreads();
+  for (int i = threadIdx.x; i < 3 * T; i += blockDim.x) {
+    const unsigned long long v = __hip_atomic_load(c.a + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    c.f[i] = (float)((double)(long long)v / c.scale);
+  }
+}
 
 __device__ __forceinline__ uint32_t ext_key(int c, int e, int cap, int j) {
   return mkkey(min(c + 1 + e, cap), j);
@@ -915,7 +989,8 @@ __device__ __forceinline__ uint32_t ext_key(int c, int e, int cap, int j) {
 __device__ __forceinline__ void near_run_flips(int lane, int t, int lmax, int jstar, int trunc_lo,
                                                int trunc_hi, uint32_t farbest, const uint8_t *Cn,
                                                const uint8_t *En, uint32_t *Pref, uint32_t *Suf,
-                                               const uint32_t *vw, float sgn, float g, float *ck) {
+                                               const uint32_t *vw, float sgn, float g, long long gi,
+                                               const CredAcc &ca, int T) {
   const int near0 = jstar - 63;
   const int jlo = max(0, jstar - 62), jhi = min(t - 1, jstar + 62);
   // unchanged near keys, two per lane (r = 2 * lane, 2 * lane + 1), and their max c
@@ -971,14 +1046,15 @@ __device__ __forceinline__ void near_run_flips(int lane, int t, int lmax, int js
       nb = max(nb, k2);
     }
     const float s2 = sign_of(nb, vw);
-    if (s2 != sgn) atomicAdd(ck + p, (s2 - sgn) * g);
+    if (s2 != sgn) ca.add(T + p, s2 - sgn, g, gi);
   }
 }
 
 __global__ void __launch_bounds__(256) rosa_credits_kernel(
     const uint32_t *__restrict__ qb, const uint32_t *__restrict__ kb, const uint32_t *__restrict__ vb,
     const int32_t *__restrict__ match_j, const float *__restrict__ grad, const float *__restrict__ payload,
-    int64_t S, int T, int W, int lmax, float *__restrict__ cred, float *__restrict__ gp_partial) {
+    int64_t S, int T, int W, int lmax, float *__restrict__ cred, float *__restrict__ gp_partial,
+    unsigned long long *__restrict__ cred_acc) {
   extern __shared__ uint32_t sm[];
   uint32_t *qw = sm, *kw = sm + W, *vw = sm + 2 * W;
   const int lane = threadIdx.x & 63;
@@ -995,8 +1071,10 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
     vw[i] = vb[stream * W + i];
   }
   __syncthreads();
-  float *cq = cred + stream * 3 * T, *ck = cq + T, *cv = cq + 2 * T;
   const float pay = payload[s];
+  __shared__ uint32_t red[kCredWaves + 1];
+  const CredAcc ca = cred_prologue(cred + stream * 3 * T, cred_acc ? cred_acc + stream * 3 * T : nullptr,
+                                   grad, b, s, S, T, pay, red);
   float gsum = 0.0f;  // this wave's share of sum_t grad * sign (d loss / d payload)
   __shared__ float gps[kCredWaves];
 
@@ -1015,6 +1093,7 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
     gsum += gr * sgn;
     const float g = gr * pay;
     if (t == 0 || g == 0.0f || lmax < 1) continue;
+    const long long gi = ca.fixed(g);
     const int Lstar = key_len(best);
     // k flips inside the best candidate's matched run, resolved in (b)
     const int trunc_lo = jstar >= 0 ? jstar - min(cstar, capstar) + 1 : 1;
@@ -1062,7 +1141,7 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
           if (v) {
             Rk[p & 127] = 0u;
             const float s2 = sign_of(v, vw);
-            if (s2 != sgn) atomicAdd(ck + p, (s2 - sgn) * g);
+            if (s2 != sgn) ca.add(T + p, s2 - sgn, g, gi);
           }
         }
       }
@@ -1072,7 +1151,7 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
     for (int o = 32; o > 0; o >>= 1) farbest = max(farbest, (uint32_t)__shfl_xor((int)farbest, o));
 
     // v: the endpoint's successor bit
-    if (lane == 0 && Lstar >= 1) atomicAdd(cv + jstar + 1, -2.0f * sgn * g);
+    if (lane == 0 && Lstar >= 1) ca.add(2 * T + jstar + 1, -2.0f * sgn, g, gi);
 
     // q: flip of q[t - i], one lane per i in [0, min(L*, lmax - 1)]. Lane c holds bucket c;
     // g1 = max key over buckets < i (exclusive prefix scan), sj = latest j over buckets > i
@@ -1097,17 +1176,18 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
         uint32_t nb = max(g1, Nw[i]);  // Nw[i]: the candidates with c == i, bit flipped
         if (lane < 63 && sj >= 0) nb = max(nb, mkkey(min(i, min(sj + 1, lmax)), sj));
         const float s2 = sign_of(nb, vw);
-        if (s2 != sgn) atomicAdd(cq + (t - i), (s2 - sgn) * g);
+        if (s2 != sgn) ca.add(t - i, s2 - sgn, g, gi);
       }
     }
 
     // (b) k flips inside the best candidate's run
     if (jstar >= 0)
-      near_run_flips(lane, t, lmax, jstar, trunc_lo, trunc_hi, farbest, Cn, En, Pref, Suf, vw, sgn, g, ck);
+      near_run_flips(lane, t, lmax, jstar, trunc_lo, trunc_hi, farbest, Cn, En, Pref, Suf, vw, sgn, g, gi, ca, T);
   }
   if (lane == 0) gps[wave] = gsum;
   __syncthreads();
   if (threadIdx.x == 0) gp_partial[stream] = ((gps[0] + gps[1]) + gps[2]) + gps[3];
+  cred_epilogue(ca, T);
 }
 
 // Bit-parallel credits for streams of up to 2048 positions (W <= 64 words). Same outputs as
@@ -1203,7 +1283,8 @@ __device__ __forceinline__ uint32_t wave_prefix_max(uint32_t v) {
 __device__ __forceinline__ void near_flips_tables(int lane, int t, int lmax, int jstar, int trunc_lo,
                                                   int trunc_hi, uint32_t farbest, uint64_t qwin,
                                                   const uint32_t *kw, const uint32_t *vw, float sgn,
-                                                  float g, float *ck, uint32_t *tab) {
+                                                  float g, long long gi, const CredAcc &ca, int T,
+                                                  uint32_t *tab) {
   uint32_t *PK = tab, *SU = tab + 64, *TJ = tab + 128, *LF = tab + 192;
   PK[lane] = 0u;  // PK[j - trunc_lo]: the key of j in the run
   SU[lane] = 0u;
@@ -1251,14 +1332,15 @@ __device__ __forceinline__ void near_flips_tables(int lane, int t, int lmax, int
     uint32_t nb = max(max(always, pk), max(su, lf));
     nb = max(nb, mkkey(jt - p, jt));
     const float s2 = sign_of(nb, vw);
-    if (s2 != sgn) atomicAdd(ck + p, (s2 - sgn) * g);
+    if (s2 != sgn) ca.add(T + p, s2 - sgn, g, gi);
   }
 }
 
 __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
     const uint32_t *__restrict__ qb, const uint32_t *__restrict__ kb, const uint32_t *__restrict__ vb,
     const int32_t *__restrict__ match_j, const float *__restrict__ grad, const float *__restrict__ payload,
-    int64_t S, int T, int W, int lmax, float *__restrict__ cred, float *__restrict__ gp_partial) {
+    int64_t S, int T, int W, int lmax, float *__restrict__ cred, float *__restrict__ gp_partial,
+    unsigned long long *__restrict__ cred_acc) {
   __shared__ uint32_t qw[64], kw[64], vw[64];
   __shared__ uint32_t wsm[kCredWaves][kBpWave32];
   __shared__ float gps[kCredWaves];
@@ -1284,8 +1366,10 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
   // p12 >> (64 - L) (L > 32): only words 0 and 1 hold positions below 63
   const uint64_t p01 = lane == 0 ? ~0ull << 32 : ~0ull;
   const uint64_t p12 = lane == 0 ? 0ull : (lane == 1 ? ~0ull << 32 : ~0ull);
-  float *cq = cred + stream * 3 * T, *ck = cq + T, *cv = cq + 2 * T;
   const float pay = payload[s];
+  __shared__ uint32_t red[kCredWaves + 1];
+  const CredAcc ca = cred_prologue(cred + stream * 3 * T, cred_acc ? cred_acc + stream * 3 * T : nullptr,
+                                   grad, b, s, S, T, pay, red);
   float gsum = 0.0f;
   // This wave's positions t = wave + kCredWaves * k, 64 at a time: the lanes load their
   // gradients together and only positions with a non-zero gradient are visited (a zero
@@ -1312,8 +1396,9 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
     gsum += gr * sgn;
     const float g = gr * pay;
     if (t == 0 || g == 0.0f || lmax < 1) continue;
+    const long long gi = ca.fixed(g);
     const int Ls = key_len(best);
-    if (lane == 0 && Ls >= 1) atomicAdd(cv + jstar + 1, -2.0f * sgn * g);  // v flips
+    if (lane == 0 && Ls >= 1) ca.add(2 * T + jstar + 1, -2.0f * sgn, g, gi);  // v flips
     const int imax = min(min(Ls, lmax - 1), t);
     const int trunc_lo = jstar >= 0 ? jstar - min(cstar, capstar) + 1 : 1;
     const int trunc_hi = jstar;
@@ -1488,7 +1573,7 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
       const int i = lane;
       const uint32_t nb = ((hasext >> i) & 1ull) ? Nw[i] : (i >= 1 ? mkkey(i, lat[i]) : 0u);
       const float s2 = sign_of(nb, vw);
-      if (s2 != sgn) atomicAdd(cq + (t - i), (s2 - sgn) * g);
+      if (s2 != sgn) ca.add(t - i, s2 - sgn, g, gi);
     }
     Nw[lane] = 0u;
 
@@ -1515,7 +1600,7 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
           if (!(p >= trunc_lo && p <= trunc_hi) && evt_get16(evt, p) == evt_key16(key, c)) {
             evt_clear16(evt, p);
             const float s2 = sign_of(key, vw);
-            if (s2 != sgn) atomicAdd(ck + p, (s2 - sgn) * g);
+            if (s2 != sgn) ca.add(T + p, s2 - sgn, g, gi);
           }
         }
       }
@@ -1524,7 +1609,7 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
     // k flips inside the best run, from the candidates near j*
     if (jstar >= 0) {
       const uint32_t farbest = farL >= 0 ? mkkey(farL, set_maxbit(farw)) : 0u;
-      near_flips_tables(lane, t, lmax, jstar, trunc_lo, trunc_hi, farbest, qwin, kw, vw, sgn, g, ck, ntab);
+      near_flips_tables(lane, t, lmax, jstar, trunc_lo, trunc_hi, farbest, qwin, kw, vw, sgn, g, gi, ca, T, ntab);
       __builtin_amdgcn_wave_barrier();
 #pragma unroll
       for (int k = 0; k < 4; ++k) ntab[64 * k + lane] = 0u;  // the event entries they covered
@@ -1535,6 +1620,7 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
   if (lane == 0) gps[wave] = gsum;
   __syncthreads();
   if (threadIdx.x == 0) gp_partial[stream] = ((gps[0] + gps[1]) + gps[2]) + gps[3];
+  cred_epilogue(ca, T);
 }
 
 // d loss / d payload = sum over (b, t) of grad * sign (rosa_credit_gpu.py:110), and the
@@ -1602,7 +1688,7 @@ using namespace ksd;
 extern "C" int ksd_rosa_credits(const uint32_t *q_bits, const uint32_t *k_bits, const uint32_t *v_bits,
                                 const int32_t *match_j, const float *grad, const float *payload,
                                 int64_t B, int64_t T, int64_t S, int lmax, float *credits,
-                                float *payload_partial, void *stream) {
+                                float *payload_partial, int64_t *credit_sums, void *stream) {
   if (B < 0 || T < 0 || S < 0) return fail(KSD_EINVAL, "rosa_credits: negative shape");
   if (lmax < 0 || lmax > 63) return fail(KSD_EINVAL, "rosa_credits: lmax must be in [0, 63]");
   if (T > 65535) return fail(KSD_EINVAL, "rosa_credits: T above 65535 is not supported");
@@ -1613,14 +1699,15 @@ extern "C" int ksd_rosa_credits(const uint32_t *q_bits, const uint32_t *k_bits, 
   const size_t lds = (3 * (size_t)W + kCredWaves * (size_t)kCredWave32) * sizeof(uint32_t);
   if (lds > 64 * 1024) return fail(KSD_EINVAL, "rosa_credits: T too large for LDS");
   if (B * S > 0x7fffffff) return fail(KSD_EINVAL, "rosa_credits: too many streams");
+  unsigned long long *sums = (unsigned long long *)credit_sums;
   if (T <= kBpMaxT)  // the bit-parallel kernel: one 32-candidate word per lane
     hipLaunchKernelGGL(rosa_credits_bp_kernel, dim3((unsigned)(B * S)), dim3(256), 0, (hipStream_t)stream,
                        q_bits, k_bits, v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits,
-                       payload_partial);
+                       payload_partial, sums);
   else
     hipLaunchKernelGGL(rosa_credits_kernel, dim3((unsigned)(B * S)), dim3(256), lds, (hipStream_t)stream,
                        q_bits, k_bits, v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits,
-                       payload_partial);
+                       payload_partial, sums);
   return check_launch("rosa_credits");
 }
 

@@ -42,12 +42,14 @@ class HardRosaGPU(torch.autograd.Function):
         grad = grad_out.float().contiguous()
         p32 = payload.detach().float().contiguous()
         lmax = R.resolve_max_match_len(T)
-        cred = torch.zeros((B * S, 3, T), dtype=torch.float32, device=dev)
+        cred = torch.empty((B * S, 3, T), dtype=torch.float32, device=dev)
         part = torch.empty((B * S,), dtype=torch.float32, device=dev)
+        # int64 fixed-point sums: the credits come out the same on every run
+        sums = torch.empty((B * S, 3, T), dtype=torch.int64, device=dev)
         st = _lib.stream_ptr(dev)
         _lib.call("ksd_rosa_credits", qb.data_ptr(), kb.data_ptr(), vb.data_ptr(), mj.data_ptr(),
                   grad.data_ptr(), p32.data_ptr(), B, T, S, lmax, cred.data_ptr(),
-                  part.data_ptr(), st)
+                  part.data_ptr(), sums.data_ptr(), st)
         dt = q.dtype if q.dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
         qc, kc, vc = (t.detach().to(dt).contiguous() for t in (q, k, v))
         gq, gk, gv = (torch.empty((B, T, S), dtype=dt, device=dev) for _ in range(3))

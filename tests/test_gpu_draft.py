@@ -248,6 +248,31 @@ def test_clip_coefficient_matches_torch():
         torch.testing.assert_close(g0 * coef, p.grad, rtol=1e-6, atol=1e-7)
 
 
+def test_training_step_gradients_are_deterministic():
+    """Two backward passes of the INT8 draft step from the same state give bit-identical
+    gradients for every parameter (the Rosa credits are exact fixed-point sums, every other
+    reduction has a fixed order)."""
+    model = _model(int8_injection=True)
+    trainer = Int8DraftTrainer(model, lr=1e-3, loss_scale=2.0 ** 12)
+    g = torch.Generator().manual_seed(5)
+    tokens = torch.randint(0, 512, (2, 97), generator=g).to(DEV)
+    teacher = torch.randn(2, 96, 256, generator=g).to(torch.bfloat16).to(DEV)
+    runs = []
+    for _ in range(3):
+        model.train()
+        loss, _, _ = trainer.loss(tokens, teacher)
+        trainer.backward(loss)
+        torch.cuda.synchronize()
+        runs.append({n: p.grad.detach().clone() for n, p in model.named_parameters()
+                     if p.grad is not None})
+    assert len(runs[0]) > 50
+    for r in runs[1:]:
+        assert r.keys() == runs[0].keys()
+        for n, t in r.items():
+            assert torch.equal(t, runs[0][n]), n
+    assert any(float(t.abs().max()) > 0 for n, t in runs[0].items() if "rosa.q_proj" in n)
+
+
 def test_clip_coefficient_with_loss_scale():
     """Gradients of a power-of-two scaled loss: the factor returned for them applies the
     clip and the unscaling at once, bit for bit the unscaled gradients' clip."""

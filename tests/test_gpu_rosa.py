@@ -257,8 +257,9 @@ def test_rosa_mixer_eval_and_training():
         assert p.grad is not None and torch.isfinite(p.grad).all(), name
 
 
-def _credits_direct(q, k, v, gsign, lmax=None):
-    """ksd_rosa_credits on (n, T) bit streams, grad_sign (n, T): credits (n, 3, T)."""
+def _credits_direct(q, k, v, gsign, lmax=None, fixed=True):
+    """ksd_rosa_credits on (n, T) bit streams, grad_sign (n, T): credits (n, 3, T); fixed:
+    with the int64 workspace (exact, order-independent sums), else fp32 atomics."""
     from ksdraft_amd import _lib
     n, T = q.shape
     rng = np.random.default_rng(T)
@@ -268,11 +269,12 @@ def _credits_direct(q, k, v, gsign, lmax=None):
     _, mj = R.match_packed(*packed, T, max_match_len=lmax, want_j=True)
     grad = _g(np.ascontiguousarray(gsign.T[None]))  # (1, T, n), payload 1
     pay = torch.ones(n, device=DEV)
-    cred = torch.zeros((n, 3, T), device=DEV)
+    cred = torch.full((n, 3, T), float("nan"), device=DEV)  # every entry is written
     part = torch.empty((n,), device=DEV)
+    sums = torch.empty((n, 3, T), dtype=torch.int64, device=DEV) if fixed else None
     _lib.call("ksd_rosa_credits", packed[0].data_ptr(), packed[1].data_ptr(), packed[2].data_ptr(),
               mj.contiguous().data_ptr(), grad.data_ptr(), pay.data_ptr(), 1, T, n, lmax,
-              cred.data_ptr(), part.data_ptr(), _lib.stream_ptr(torch.device(DEV)))
+              cred.data_ptr(), part.data_ptr(), _lib.ptr(sums), _lib.stream_ptr(torch.device(DEV)))
     return cred.cpu().numpy()
 
 
@@ -309,6 +311,50 @@ def test_credits_explicit_max_match_len_bruteforce(lmax):
     scale = np.abs(exp).max() + 1e-30
     np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * scale)
     assert np.array_equal(got == 0, exp == 0)
+
+
+def test_credits_are_deterministic_and_match_the_atomic_sums():
+    """With the int64 workspace every credit is an exact fixed-point sum: two runs give the
+    same bits (structured streams with deep chains, many contributions per entry), and the
+    values agree with the fp32-atomic sums and the definition."""
+    rng = np.random.default_rng(4242)
+    n, T = 24, 2048
+    q = _streams(rng, n, T)
+    k = np.concatenate([q[:8], _streams(rng, n - 8, T)])
+    k[8] = np.roll(q[8], 5)
+    v = _streams(rng, n, T)
+    gsign = (rng.standard_normal((n, T)) * np.exp(rng.uniform(-8, 8, (n, T)))).astype(np.float32)
+    a = _credits_direct(q, k, v, gsign)
+    b = _credits_direct(q, k, v, gsign)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    c = _credits_direct(q, k, v, gsign, fixed=False)
+    scale = np.abs(c).max()
+    np.testing.assert_allclose(a, c, rtol=1e-5, atol=1e-6 * scale)
+    base, _, _ = orr.match(q, k, v)
+    for s in range(0, n, 5):
+        for which in range(3):
+            for p in rng.choice(T, 3, replace=False):
+                fl = [x[s:s + 1].copy() for x in (q, k, v)]
+                fl[which][0, p] ^= 1
+                sp, _, _ = orr.match(*fl)
+                exp = float(((sp[0] - base[s]) * gsign[s].astype(np.float64)).sum())
+                assert abs(a[s, which, p] - exp) <= 1e-5 * max(abs(exp), np.abs(gsign[s]).max()), (s, which, p)
+
+
+def test_credits_nonfinite_gradient_falls_back_to_fp32_sums():
+    """A stream whose gradient holds inf or NaN keeps fp32 atomics (non-finite credits as
+    before); the other streams of the call stay exact."""
+    rng = np.random.default_rng(77)
+    n, T = 6, 300
+    q, k, v = (_streams(rng, n, T) for _ in range(3))
+    gsign = rng.standard_normal((n, T)).astype(np.float32)
+    gsign[1, 17] = np.inf
+    gsign[2, 40] = np.nan
+    got = _credits_direct(q, k, v, gsign)
+    fin = [0, 3, 4, 5]
+    exp = orr.credits(q[fin], k[fin], v[fin], gsign[fin])
+    np.testing.assert_allclose(got[fin], exp, rtol=1e-5, atol=1e-5 * np.abs(exp).max())
+    assert not np.isfinite(got[1]).all() and not np.isfinite(got[2]).all()
 
 
 def test_credits_t2100_sampled_flips():
