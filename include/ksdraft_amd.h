@@ -94,9 +94,11 @@ int ksd_requant_transpose(const int8_t *codes, const uint16_t *scales, int64_t R
  * the column codes quantize_last_dim(x.t(), group) (t_from_codes = 0: the dY and dY^T
  * operands of the linear backward, reference ksdraft/kernels/ks3_int8.py:410, 418), or
  * the column codes of the row-quantized values, quantize_last_dim(dequantize_last_dim(
- * codes, scales).t(), group) (t_from_codes = 1: the X and X^T operands, :417-420).
+ * codes, scales).t(), group) (t_from_codes = 1: the X and X^T operands, :417-420), or both
+ * layouts of x rounded to fp16 first (t_from_codes = 2: the KS3 cell's g16 = grad.to(
+ * float16) operands, :345-348, :421-422; needs group 128, C % 8 == 0, 16-byte rows).
  * No reference counterpart as one call; the results equal those of ksd_quantize_lastdim
- * followed by ksd_quantize_transpose or ksd_requant_transpose.
+ * followed by ksd_quantize_transpose or ksd_requant_transpose (of x.to(float16) for mode 2).
  *   x       (R, C) of type x_dtype (KSD_F32, KSD_BF16, KSD_F16), dense
  *   codes   (R, C) int8;  scales   (R, ceil(C/group)) fp16
  *   codes_t (C, R) int8;  scales_t (C, ceil(R/group)) fp16

@@ -275,7 +275,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 // col_part (optional, not with CE): (ceil(R/128), C) fp32 partial column sums of x, one row
 // per 128-row tile, each the sum of its four 32-row parts ((p0 + p1) + (p2 + p3)), every
 // part summed in row order; colsum_finalize_kernel adds the tiles in order.
-template <int DT, bool CE = false>
+// H16: quantize the fp16 rounding of x (x.to(float16) first: the KS3 cell's backward
+// quantizes its upstream gradient as g16 = grad.to(float16), ks3_int8.py:345-348, :421-422).
+template <int DT, bool CE = false, bool H16 = false>
 __global__ __launch_bounds__(512) void quant_dual_kernel(
     const void *__restrict__ xv, int64_t R, int64_t C, int8_t *__restrict__ codes,
     uint16_t *__restrict__ scales, int8_t *__restrict__ codes_t, uint16_t *__restrict__ scales_t,
@@ -309,6 +311,10 @@ __global__ __launch_bounds__(512) void quant_dual_kernel(
     const bool ok = cok && row < R;
     float v[8];
     cvt_raw8<DT>(raw[p], ok, v);
+    if constexpr (H16) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = f16_round(v[i]);
+    }
     if constexpr (CE) {
       const int64_t rs = row < R ? row : R - 1;
       const int64_t t = ce.tgt[rs];
@@ -1012,11 +1018,14 @@ extern "C" int ksd_quantize_dual(const void *x, int x_dtype, int64_t R, int64_t 
   if (R == 0 || C == 0) return KSD_OK;
   if (!x || !codes || !scales || !codes_t || !scales_t)
     return fail(KSD_EINVAL, "quantize_dual: null pointer");
+  if (t_from_codes < 0 || t_from_codes > 2) return fail(KSD_EINVAL, "quantize_dual: mode must be 0, 1 or 2");
   hipStream_t st = (hipStream_t)stream;
   const int esz = x_dtype == KSD_F32 ? 4 : 2;
   const bool fast = group == 128 && C % 8 == 0 && ((uintptr_t)x) % 16 == 0 && (C * esz) % 16 == 0 &&
                     ((uintptr_t)codes) % 8 == 0 && cdiv(R, 128) <= 65535 && cdiv(C, 128) <= 0x7fffffff &&
                     128 * C * 4 <= 0x7fffffffLL;
+  if (t_from_codes == 2 && !fast)
+    return fail(KSD_EINVAL, "quantize_dual: the fp16 mode needs group 128, C %% 8 == 0 and 16-byte rows");
   if (!fast) {
     // the two single-layout kernels: row codes, then the transposed codes of x or of them
     int rc = ksd_quantize_lastdim(x, x_dtype, R, C, C, group, codes, scales, nullptr, 0.0f, stream);
@@ -1027,8 +1036,10 @@ extern "C" int ksd_quantize_dual(const void *x, int x_dtype, int64_t R, int64_t 
   }
   const dim3 grid((unsigned)cdiv(C, 128), (unsigned)cdiv(R, 128));
 #define KSD_DUAL(DT)                                                                                      \
-  if (t_from_codes)                                                                                       \
+  if (t_from_codes == 1)                                                                                  \
     quant_dual_codes_kernel<DT><<<grid, 512, 0, st>>>(x, R, C, codes, scales, codes_t, scales_t);         \
+  else if (t_from_codes == 2)                                                                             \
+    quant_dual_kernel<DT, false, true><<<grid, 512, 0, st>>>(x, R, C, codes, scales, codes_t, scales_t);  \
   else                                                                                                    \
     quant_dual_kernel<DT><<<grid, 512, 0, st>>>(x, R, C, codes, scales, codes_t, scales_t);
   switch (x_dtype) {

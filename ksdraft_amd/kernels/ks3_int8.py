@@ -12,7 +12,8 @@ Compute runs in libksdraft_amd.so:
     materialised as fp16, ks3_int8.py:241-242, straight from the GEMM epilogue);
   * the fp16 geometry VJP, emitting dc as the two int8 GEMM operands and the eight
     column sums: ksd_ks3_vjp + ksd_ks3_vjp_finalize;
-  * the transposed operands: ksd_requant_transpose / ksd_quantize_transpose.
+  * the transposed operands: ksd_requant_transpose, and the upstream gradient's fp16
+    rounding in both layouts from one pass (ksd_quantize_dual, fp16 mode);
   * the 'fp16' and 'fp32' nonlinear modes (ks3_int8.py:172-203): ksd_ks3_spine_float,
     composed (on the fp16 coordinates) and under the project_fused contract (on the fp32
     accumulator), with the features' requantization in the same pass.
@@ -34,7 +35,7 @@ import torch.nn.functional as F
 
 from .. import _lib
 from .gemm import w8a8_gemm, w8a8_gemm_out, w8a8_gemm_pair
-from .quant import (GROUP_SIZE, dequantize_last_dim, quantize_last_dim, quantize_transpose,
+from .quant import (GROUP_SIZE, dequantize_last_dim, quantize_dual, quantize_last_dim,
                     requant_transpose)
 
 TANH_DOMAIN = 3.2
@@ -508,13 +509,15 @@ class _KS3Int8Train(torch.autograd.Function):
         cell = ctx.cell
         group = cell.group
         xq, xs, hq, hs, coords16 = ctx.saved_tensors
-        g16 = grad_out.reshape(-1, cell.out_features).float().to(FP16)
+        # g16 = grad.to(fp16) in both int8 layouts, from one pass over the gradient: along
+        # the features for the value GEMM (ks3_int8.py:345-348) and along the tokens for
+        # dup (:421-422)
+        gq, gs, gT_q, gT_s = quantize_dual(grad_out.reshape(-1, cell.out_features), group,
+                                           round_fp16=True)
 
         # output-projection backward GEMM (ks3_int8.py:345-352), launched with dup (its
         # operands are ready already; ks3_int8.py:421-424)
-        gq, gs = quantize_last_dim(g16, group)
         upT_q, upT_s = requant_transpose(cell.up_codes, cell.up_scales, group, group)
-        gT_q, gT_s = quantize_transpose(g16, group)
         hT_q, hT_s = requant_transpose(hq, hs, group, group)
         value, dup = w8a8_gemm_pair((gq, gs, upT_q, upT_s, FP16),
                                     (gT_q, gT_s, hT_q, hT_s, torch.float32), group)

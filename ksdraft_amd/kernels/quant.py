@@ -137,25 +137,36 @@ def quantize_transpose(x: torch.Tensor, group: int = GROUP_SIZE):
     return codes, scales
 
 
-def quantize_dual(x: torch.Tensor, group: int = GROUP_SIZE, t_from_codes: bool = False):
+def quantize_dual(x: torch.Tensor, group: int = GROUP_SIZE, t_from_codes: bool = False,
+                  round_fp16: bool = False):
     """Both operand layouts of a 2-D x (R, C) from one read of x.
 
     Returns (codes (R, C), scales (R, ceil(C/group)), codes_t (C, R), scales_t
     (C, ceil(R/group))): codes/scales = quantize_last_dim(x, group); codes_t/scales_t =
     quantize_transpose(x, group), or with ``t_from_codes`` requant_transpose(codes,
-    scales) (the double-quant recipe of reference ksdraft/kernels/ks3_int8.py:417-420)."""
+    scales) (the double-quant recipe of reference ksdraft/kernels/ks3_int8.py:417-420).
+    ``round_fp16``: both layouts of x.to(float16) (the KS3 backward's g16, ks3_int8.py:
+    345-348, 421-422), rounded inside the same pass where the fused kernel applies."""
     x = _float_input(x)
     dev = _lib.require_gpu(x)
     if x.dim() != 2:
         raise ValueError("quantize_dual expects a 2-D tensor")
+    if round_fp16 and t_from_codes:
+        raise ValueError("quantize_dual: round_fp16 and t_from_codes are exclusive")
     x = x.contiguous()
     R, C = x.shape
+    mode = 1 if t_from_codes else 0
+    if round_fp16:
+        if group == GROUP_SIZE and C % 8 == 0 and x.dtype != torch.float16:
+            mode = 2
+        else:
+            x = x.to(torch.float16)
     codes = torch.empty((R, C), dtype=torch.int8, device=dev)
     scales = torch.empty((R, -(-C // group)), dtype=SCALE_DTYPE, device=dev)
     codes_t = torch.empty((C, R), dtype=torch.int8, device=dev)
     scales_t = torch.empty((C, -(-R // group)), dtype=SCALE_DTYPE, device=dev)
     _lib.call("ksd_quantize_dual", x.data_ptr(), _lib.dtype_code(x.dtype), R, C, group,
-              int(bool(t_from_codes)), codes.data_ptr(), scales.data_ptr(), codes_t.data_ptr(),
+              mode, codes.data_ptr(), scales.data_ptr(), codes_t.data_ptr(),
               scales_t.data_ptr(), _lib.stream_ptr(dev))
     return codes, scales, codes_t, scales_t
 

@@ -231,3 +231,22 @@ def test_quantize_dual2_equals_two_duals(sa, sb, dtype):
         for u, v in zip(got, want):
             assert torch.equal(u.view(torch.int8) if u.dtype == torch.int8 else u.view(torch.int16),
                                v.view(torch.int8) if v.dtype == torch.int8 else v.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("R,C", [(256, 1536), (200, 136), (8192, 1536), (33, 24)])
+def test_quantize_dual_fp16_rounding_mode(dtype, R, C):
+    """round_fp16: both layouts of x.to(float16) from one pass, bit-exact against the oracle
+    quantizer of the fp16-rounded values (rows scaled over 16 binades: fp16 subnormals and
+    values that round to zero included)."""
+    from ksdraft_amd.kernels.quant import quantize_dual
+    rng = np.random.default_rng(R + C)
+    x = (rng.standard_normal((R, C)) * np.exp(rng.uniform(-12, 4, (R, 1)))).astype(np.float32)
+    x[::7, ::5] *= 1e-3
+    xd = torch.from_numpy(x).to("cuda").to(dtype)
+    c, s, ct, st = quantize_dual(xd, round_fp16=True)
+    x16 = xd.float().cpu().numpy().astype(np.float16).astype(np.float32)
+    ec, es = oq.quantize_last_dim(x16)
+    et, ets = oq.quantize_last_dim(np.ascontiguousarray(x16.T))
+    assert np.array_equal(c.cpu().numpy(), ec) and np.array_equal(s.cpu().numpy().view(np.uint16), es.view(np.uint16))
+    assert np.array_equal(ct.cpu().numpy(), et) and np.array_equal(st.cpu().numpy().view(np.uint16), ets.view(np.uint16))
