@@ -303,3 +303,150 @@ def test_config4_rosa_step_full_shape():
                 cred = float(((sp[0] - base[0]) * gsign).sum())
                 exp = np.float32(cred * (1.0 - 2.0 * bits[which][0, pos])) * bern[pos]
                 assert abs(grad[b, pos, s] - exp) <= 1e-5 * max(1.0, abs(exp)), (which, b, s, pos)
+
+
+# ------------------------------------------------------------------------------ config 5
+def test_config5_draft_step_full_shape(monkeypatch):
+    """One INT8 draft training step at config-5 dimensions (one layer: d 1536, 512 Rosa
+    streams, 5888 KS3 charts, vocabulary 150144, B 4 x T 2048, teacher state bf16, every
+    linear INT8, loss scale 2^12 so that every gradient group is live), checked on sampled
+    rows against the oracle chains from the recorded surface inputs and the fp32 masters:
+    the Rosa output projection (y with its fused residual, dX, dW), the KS3 cell (y, dx, and
+    ddown / dup on sampled output rows from the device's replayed operands), the head's loss
+    against float64 torch on logits whose sampled rows are bit-exact, and, after the
+    optimizer step, the int8 codes of every registered surface against the oracle
+    quantizer of its updated master."""
+    from ksdraft_amd.config import baseline_config
+    from ksdraft_amd.model import KSDraftModel, to_int8
+    from ksdraft_amd.train.int8_step import Int8DraftTrainer
+    from tests.test_gpu_draft import _Recorder
+
+    cfg = baseline_config()
+    cfg.layers = 1
+    d, Fn, S, V = cfg.d_model, cfg.charts, cfg.rosa_streams, cfg.vocab_size
+    B, Tn = 4, 2048
+    M = B * Tn
+    torch.manual_seed(0)
+    fm = KSDraftModel(cfg, teacher_dim=d, device=DEV)
+    with torch.no_grad():
+        for name, p in fm.named_parameters():
+            if name.endswith(("up.weight", "out_proj.weight", "teacher_proj.weight")):
+                p.normal_(0, 0.02)
+    model = to_int8(fm, trainable=True, int8_injection=True)
+    del fm
+    rec = _Recorder(model, monkeypatch)
+    tr = Int8DraftTrainer(model, lr=3e-4, weight_decay=0.01, grad_clip=1.0, loss_scale=2.0 ** 12)
+    g = torch.Generator(device=DEV).manual_seed(0)
+    tokens = torch.randint(0, V, (B, Tn + 1), device=DEV, generator=g)
+    teacher = torch.randn(B, Tn, d, device=DEV, generator=g).to(torch.bfloat16)
+    masters = {n: p.detach().clone() for n, p in model.named_parameters()}
+    model.train()
+    loss, ce, ts = tr.loss(tokens, teacher)
+    tr.backward(loss)
+    torch.cuda.synchronize()
+    assert torch.isfinite(loss)
+    rows = _rows(M, 12, 20)
+    mnp = lambda k: _np(masters[k]).astype(np.float32)  # noqa: E731
+
+    # Rosa output projection: y = W8A8(x) + b + residual, dX, dW (K = 8192 tokens)
+    r = rec.lin["blocks.0.rosa.out_proj"]
+    mod = r["mod"]
+    x = _np(r["x"]).reshape(M, S).astype(np.float32)
+    gy = _np(r["g"]).reshape(M, d).astype(np.float32)
+    wq, ws = oq.quantize_last_dim(mnp("blocks.0.rosa.out_proj.weight"))
+    bias = mnp("blocks.0.rosa.out_proj.bias")
+    xq, xs = oq.quantize_last_dim(x)
+    ey = og.gemm_ordered(xq, xs, wq, ws, bias=bias, rows=rows, splits=og.splits_for(M, d, S))
+    ey = (ey + _np(r["res"]).reshape(M, d)[rows]).astype(np.float32)
+    assert _eq(_np(r["y"]).reshape(M, d)[rows], ey)
+    gq, gs = oq.quantize_last_dim(gy[rows])
+    edx = og.gemm_ordered(gq, gs, *oq.requant_transpose(wq, ws), splits=og.splits_for(M, S, d))
+    assert _eq(_np(r["dx"]).reshape(M, S)[rows], edx)
+    nrows = _rows(d, 8, 21)
+    gtq, gts = oq.quantize_last_dim(np.ascontiguousarray(gy[:, nrows].T))
+    edw = og.gemm_ordered(gtq, gts, *oq.requant_transpose(xq, xs), splits=og.splits_for(d, S, M))
+    assert _eq(_np(mod.weight.grad)[nrows], edw)
+
+    # KS3 cell, row-local chain: y and dx on sampled tokens
+    r = rec.cell["blocks.0.ffn"]
+    cell = r["mod"]
+    mk = lambda k: mnp(f"blocks.0.ffn.master_{k}")  # noqa: E731
+    p = ok.pack_masters(mk("down"), mk("up"), mk("coefficients"), mk("raw_scale"), mk("raw_shift"))
+    sc, sh = ok.warp_scalars(p["warp_scale_codes"], p["warp_scale_scales"],
+                             p["warp_shift_codes"], p["warp_shift_scales"])
+    coef, _, _ = ok.spine_params(p["spine_codes"], p["spine_scale"], p["warp_scale_codes"],
+                                 p["warp_scale_scales"], p["warp_shift_codes"], p["warp_shift_scales"])
+    xc = _np(r["x"]).reshape(M, d).astype(np.float32)
+    gc = _np(r["g"]).reshape(M, d).astype(np.float32)
+    xq, xs = oq.quantize_last_dim(xc[rows])
+    coords = ok.coords_from_gemm(og.gemm_ordered(xq, xs, p["down_codes"], p["down_scales"],
+                                                 splits=og.splits_for(M, Fn, d)))
+    hfeat = ok.spine_features_int8(coords, p["spine_codes"], p["spine_scale"], sc, sh, ok.make_tanh_lut())
+    hq, hs = oq.quantize_last_dim(hfeat)
+    ey = og.gemm_ordered(hq, hs, p["up_codes"], p["up_scales"], splits=og.splits_for(M, d, Fn))
+    ey = (ey + _np(r["res"]).reshape(M, d)[rows]).astype(np.float32)
+    assert _eq(_np(r["y"]).reshape(M, d)[rows], ey)
+    g16 = ok.h(gc[rows])
+    gq, gs = oq.quantize_last_dim(g16)
+    value = ok.h(og.gemm_ordered(gq, gs, *oq.requant_transpose(p["up_codes"], p["up_scales"]),
+                                 splits=og.splits_for(M, Fn, d)))
+    dc, _, _, _, _ = ok.vjp(value, coords, coef, sc, sh, mk("raw_scale"), mk("raw_shift"))
+    dcq, dcs = oq.quantize_last_dim(dc)
+    edx = og.gemm_ordered(dcq, dcs, *oq.requant_transpose(p["down_codes"], p["down_scales"]),
+                          splits=og.splits_for(M, d, Fn))
+    assert _eq(_np(r["dx"]).reshape(M, d)[rows], edx)
+    # ddown and dup reduce over the 8192 tokens: sampled output rows from the device's own
+    # (replayed, deterministic) operands, each of which the row checks above pin
+    xdev = r["x"].reshape(M, d).float()
+    xq_d, xs_d = kq.quantize_last_dim(xdev)
+    hq_d, hs_d, coords16 = cell._project_codes(xq_d, xs_d)
+    gq_d, gs_d, gtq_d, gts_d = kq.quantize_dual(r["g"].reshape(M, d), round_fp16=True)
+    assert _eq(_np(gq_d[rows]), gq)
+    upTq, upTs = kq.requant_transpose(cell.up_codes, cell.up_scales)
+    value_d = kg.w8a8_gemm_out(gq_d, gs_d, upTq, upTs, out_dtype=torch.float16)
+    scale16, shift16 = cell._warp_scalars(torch.float16)
+    v = K.ks3_vjp(value_d, coords16, cell.spine_codes, cell.spine_scale, scale16, shift16,
+                  cell.warp_scale_raw, cell.warp_shift_raw)
+    frows = _rows(Fn, 6, 22)
+    eddown = og.gemm_ordered(_np(v["dct_codes"][frows]), _np(v["dct_scales"][frows]),
+                             *oq.requant_transpose(_np(xq_d), _np(xs_d)), splits=og.splits_for(Fn, d, M))
+    assert _eq(_np(cell.master_down.grad[frows]), ok.h(eddown))
+    drows = _rows(d, 6, 23)
+    edup = og.gemm_ordered(_np(gtq_d[drows]), _np(gts_d[drows]),
+                           *oq.requant_transpose(_np(hq_d), _np(hs_d)), splits=og.splits_for(d, Fn, M))
+    assert _eq(_np(cell.master_up.grad[drows]), ok.h(edup))
+    del v, value_d, hq_d, coords16
+
+    # the head: sampled logits rows bit-exact, the loss against float64 torch on the logits
+    head = model.head
+    with torch.no_grad():
+        hn, _ = model.backbone(tokens[:, :-1], teacher)
+        hn = hn.reshape(M, d).float()
+        hxq, hxs = kq.quantize_last_dim(hn)
+        logits = kg.w8a8_gemm(hxq, hxs, head.weight_codes, head.weight_scales)
+    vrows = _rows(V, 64, 26)
+    ewq, ews = oq.quantize_last_dim(mnp("embedding.weight")[vrows])
+    assert _eq(_np(head.weight_codes[vrows]), ewq) and _eq(_np(head.weight_scales[vrows]), ews)
+    lrows = rows[:4]
+    el = og.gemm_ordered(_np(hxq), _np(hxs), _np(head.weight_codes), _np(head.weight_scales),
+                         rows=lrows, splits=og.splits_for(M, V, d))
+    assert _eq(_np(logits[lrows]), el)
+    eref = torch.nn.functional.cross_entropy(logits.double(), tokens[:, 1:].reshape(-1))
+    assert abs(ce.item() - eref.item()) <= 2e-5 * abs(eref.item())
+    del logits
+
+    # the optimizer step: every registered surface's codes from its updated master
+    tr.optimizer_step()
+    torch.cuda.synchronize()
+    for name, mod in model.named_modules():
+        if isinstance(mod, Int8Linear):
+            n = mod.weight.shape[0]
+            sel = _rows(n, min(n, 16), 24)
+            eq, es = oq.quantize_last_dim(_np(mod.weight[sel]).astype(np.float32))
+            assert _eq(_np(mod.weight_codes[sel]), eq) and _eq(_np(mod.weight_scales[sel]), es), name
+    for nm in ("down", "up"):
+        w = getattr(cell, "master_" + nm)
+        sel = _rows(w.shape[0], 16, 25)
+        eq, es = oq.quantize_last_dim(_np(w[sel]).astype(np.float32))
+        assert _eq(_np(getattr(cell, nm + "_codes")[sel]), eq), nm
+        assert _eq(_np(getattr(cell, nm + "_scales")[sel]), es), nm
