@@ -14,13 +14,18 @@ this layer when it quantizes its own master:
     quantize dY along N and along M in one pass (quantize_dual)
       -> GEMM dX = dY W -> GEMM dW = dY^T X   (fp32)
 value = algorithmic int8 ops of the three GEMMs (3 * 2*M*N*K) / step time, in TOPS.
-The step runs as a captured HIP graph (no host launch overhead; replays are checked
-bit-equal to the eager step); the eager step time is reported beside it.
+The steps run as a captured HIP graph of G consecutive steps (G the largest divisor of K
+up to 16), replayed K / G times: no host launch overhead, and the ~15 us that each graph
+replay costs beyond its kernels is paid once per G steps. Replays are checked bit-equal to
+the eager step; the one-step graph and the eager step times are reported beside it.
 
-Also reported: per-kernel average launch times (HIP events around graphs of back-to-back
-launches on the launch stream), the GEMM roofline against the 5.0 POPS dense int8 peak,
-and the CPU oracle (the reference's CPU path: dequantize + fp32 matmul) timed on a
-bounded sample on this host.
+Also reported: the step's four launches timed inside the step (HIP events between them
+on the launch stream, eager steps); per-kernel average launch times of back-to-back
+launches (HIP events around graphs of them); the GEMM roofline against the 5.0 POPS
+dense int8 peak, from the in-step GEMM durations (back to back, the same GEMM runs
+slower: the chip holds lower clocks under continuous matrix load than when memory-bound
+quantization launches alternate with it); and the CPU oracle (the reference's CPU path:
+dequantize + fp32 matmul) timed on a bounded sample on this host.
 """
 
 from __future__ import annotations
@@ -119,6 +124,44 @@ def step(x, w, dy):
     dx, dw = w8a8_linear_backward(dy, None, None, wq, ws, dx_dtype=torch.float32, xt=(xtq, xts),
                                   wt=(wtq, wts))
     return y, dx, dw
+
+
+def step_kernel_times(x, w, dy, steps, warmup):
+    """Average duration (us) of each of the step's four launches, measured inside the step:
+    HIP events recorded between the launches on the launch stream over `steps` eager steps
+    (the launches of step() with the backward split into its dual quantization and its
+    paired GEMM launch, checked bit-equal to step()). An interval also holds the dispatch
+    gap before its launch, so it bounds the kernel's own time from above."""
+    f32 = torch.float32
+
+    def run(evs=None):
+        def rec(i):
+            if evs is not None:
+                evs[i].record()
+        rec(0)
+        (wq, ws, wtq, wts), xpre = quantize_dual2(w, x)
+        rec(1)
+        y, xtq, xts = w8a8_linear_forward_train(x, wq, ws, None, out_dtype=f32, xpre=xpre)
+        rec(2)
+        gq, gs, gtq, gts = quantize_dual(dy)
+        rec(3)
+        dx, dw = w8a8_gemm_pair((gq, gs, wtq, wts, f32), (gtq, gts, xtq, xts, f32))
+        rec(4)
+        return y, dx, dw
+
+    for a, b in zip(run(), step(x, w, dy)):
+        if not torch.equal(a, b):
+            raise SystemExit("the instrumented step differs from step()")
+    for _ in range(warmup):
+        run()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for e in evs:
+        run(e)
+    torch.cuda.synchronize()
+    names = ["quantize_W_X_dual2", "gemm_fwd", "quantize_dY_dual", "gemm_dX_dW_pair"]
+    return {n: round(1e3 * sum(e[i].elapsed_time(e[i + 1]) for e in evs) / steps, 3)
+            for i, n in enumerate(names)}
 
 
 def time_graph(fn, reps, warm=3):
@@ -714,31 +757,48 @@ def main():
     eager_ms = e0.elapsed_time(e1) / args.steps
     eager_wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
 
-    # graph: capture one step, check replays against the eager result, time K replays
+    # graphs: one of a single step, and one of G consecutive steps (G the largest divisor
+    # of K up to 16); each replay is checked against the eager result, then K steps are
+    # timed as K replays of the first and K / G replays of the second. A replay costs
+    # ~15 us beyond its kernels (their launches run back to back inside it), so the
+    # G-step graph is the headline.
     ref = [t.clone() for t in step(x, w, dy)]
-    graph, outs, _ = time_graph(lambda: step(x, w, dy), 1)
-    for _ in range(3):
-        graph.replay()
-        step(x, w, dy)           # eager work between replays
-        torch.cuda.synchronize()
-        for a, b in zip(outs, ref):
-            if not torch.equal(a, b):
-                raise SystemExit("graph replay differs from the eager step")
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    g0.record()
-    for _ in range(args.steps):
-        graph.replay()
-    g1.record()
-    torch.cuda.synchronize()
-    ms = g0.elapsed_time(g1) / args.steps
+    G = max(d for d in range(1, 17) if args.steps % d == 0)
 
+    def g_steps():
+        for _ in range(G):
+            out = step(x, w, dy)
+        return out
+
+    def timed_graph(fn, nsteps):
+        graph, outs, _ = time_graph(fn, 1)
+        for _ in range(3):
+            graph.replay()
+            step(x, w, dy)           # eager work between replays
+            torch.cuda.synchronize()
+            for a, b in zip(outs, ref):
+                if not torch.equal(a, b):
+                    raise SystemExit("graph replay differs from the eager step")
+        for _ in range(max(1, args.warmup // nsteps)):
+            graph.replay()
+        torch.cuda.synchronize()
+        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        g0.record()
+        for _ in range(args.steps // nsteps):
+            graph.replay()
+        g1.record()
+        torch.cuda.synchronize()
+        return g0.elapsed_time(g1) / args.steps
+
+    ms1 = timed_graph(lambda: step(x, w, dy), 1)
+    ms = timed_graph(g_steps, G)
+
+    in_step = step_kernel_times(x, w, dy, args.steps, args.warmup)
     kern = kernel_times(x, w, dy, args.kernel_reps)
     gemm_us = [kern[k]["us"] for k in ("gemm_fwd", "gemm_dX", "gemm_dW")]
-    # the step's GEMM launches: the forward, and dX + dW paired in one launch
-    step_gemm_us = kern["gemm_fwd"]["us"] + kern["gemm_dX_dW_pair"]["us"]
+    # the step's GEMM launches, timed inside the step: the forward, and dX + dW paired in
+    # one launch
+    step_gemm_us = in_step["gemm_fwd"] + in_step["gemm_dX_dW_pair"]
     achieved = 3 * GEMM_OPS / (step_gemm_us * 1e-6)
     traffic, tsrc = traffic_from_profiles()
 
@@ -757,16 +817,19 @@ def main():
         "dtype": "int8",
         "data": "synthetic: seeded X~N(0,1), W~N(0,0.02), dY~N(0,1e-2), fp32, resident in HBM",
         "config": {"workload": "BASELINE config 2: W8A8 GS128 linear fwd + dX + dW, "
-                               "M=8192 (4x2048), K=N=1536, fp32 in/out, step as HIP graph",
+                               "M=8192 (4x2048), K=N=1536, fp32 in/out, steps replayed as a HIP graph",
                    "M": M, "K": K, "N": N, "group": 128},
         "pct_int8_peak": round(100 * value * 1e12 / PEAK_INT8, 2),
         "tok_per_s": round(M / (ms * 1e-3), 1),
         "gemm_only_tops": round(achieved / 1e12, 1),
         "gemm_separate_launches_tops": round(3 * GEMM_OPS / (sum(gemm_us) * 1e-6) / 1e12, 1),
+        "graph_steps_per_replay": G,
+        "graph1_ms_per_step": round(ms1, 5),
         "eager_ms_per_step": round(eager_ms, 4),
         "eager_wall_ms_per_step": round(eager_wall_ms, 4),
         "draft_train_step_tok_s": None,
         "draft_c5": None,
+        "step_kernels_us": in_step,
         "kernels": kern,
         "ks3_c4_kernels": None if args.no_ks3 else ks3_kernel_times(dev, args.kernel_reps),
         "rosa_c4_kernels": None if args.no_rosa else rosa_kernel_times(dev, args.kernel_reps),
@@ -774,7 +837,8 @@ def main():
         "ln_quant_c4": None if args.no_ln else ln_quant_times(dev, args.kernel_reps),
         "roofline": {
             "kernel": "ksd::g128::gemm_g128_kernel<f32> (the step's GEMM launches: the forward, "
-                      "and dX + dW paired; ops over summed launch time)",
+                      "and dX + dW paired; ops over their summed durations inside the step, "
+                      "HIP events between the step's launches)",
             "bound": "mfma",
             "achieved": round(achieved / 1e12, 1),
             "peak": PEAK_INT8 / 1e12,
