@@ -500,11 +500,17 @@ int ksd_rosa_hard(const int8_t *sign, const float *payload, int64_t B, int64_t T
  *   grad        (B, T, S) fp32 upstream gradient of the hard output
  *   credits     (B*S, 3, T) fp32, written by the call (rows q, k, v)
  *   payload_partial (B*S,) fp32: sum over t of grad * sign per stream (fixed order)
- *   credit_sums (B*S, 3, T) int64 workspace, or NULL. With it, every credit is an exact
+ *   credit_sums (B*S, 3, T) int64 workspace (required). Every credit is an exact
  *               fixed-point sum of +-2 g(t) (g rounded once, at 2^-48 of the stream's
- *               largest |grad * payload|), so the credits are identical on every run; a
- *               stream with a non-finite gradient, or a call without the workspace, adds
- *               fp32 atomics instead, whose summation order varies between runs
+ *               largest |grad * payload|), so the credits are identical on every run. A
+ *               stream whose g holds inf or NaN gets what the reference's dense sum over t
+ *               of delta * g gives (rosa_credit_gpu.py:48): NaN where any g(t) is NaN or
+ *               some infinite g(t) leaves the entry's sign unchanged (0 * inf), else +-inf
+ *               (NaN if its infinite terms have both signs)
+ * The credits buffer is the call's scratch until it returns (three launches on the stream:
+ * per-stream set-up, the contributions, the conversion to fp32). For T <= 2048 the
+ * contributions are formed by waves that take (stream, 64-position chunk) items from a
+ * counter, so the cost of streams with long matches spreads over the whole device.
  */
 int ksd_rosa_credits(const uint32_t *q_bits, const uint32_t *k_bits, const uint32_t *v_bits,
                      const int32_t *match_j, const float *grad, const float *payload, int64_t B,

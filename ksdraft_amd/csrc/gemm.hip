@@ -792,19 +792,6 @@ static int g128_splits(int64_t M, int64_t N, int64_t K) {
   return s < 1 ? 1 : (int)s;
 }
 
-// one workgroup per CU; the CU count is a device constant, cached per device
-static int cu_count() {
-  static int cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int n = __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
-  if (n <= 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    __atomic_store_n(&cached[dev], n, __ATOMIC_RELAXED);
-  }
-  return n;
-}
 
 template <int GROUP, int OUT, bool BIAS, int MODE>
 static void launch(const int8_t *a, const uint16_t *as, const int8_t *w, const uint16_t *ws,

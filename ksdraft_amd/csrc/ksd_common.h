@@ -40,6 +40,20 @@ inline bool valid_group(int g) { return g == 32 || g == 64 || g == 128; }
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// The device's CU count (persistent launches size their grids by it), cached per device.
+static inline int cu_count() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    __atomic_store_n(&cached[dev], n, __ATOMIC_RELAXED);
+  }
+  return n;
+}
+
 // ---------------------------------------------------------------- device numerics
 constexpr float kScaleMin = 5.9604644775390625e-08f;  // 2**-24, quant.py:22
 constexpr float kScaleMax = 65504.0f;                 // quant.py:23

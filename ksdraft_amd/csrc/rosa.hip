@@ -904,76 +904,171 @@ constexpr int kNear = 128;
 constexpr int kCredWaves = 4;
 constexpr int kCredWave32 = 64 + 64 + 128 + 2 * kNear / 4 + 2 * kNear;  // uint32 words per wave
 
-// Credit sums in fixed point. Every contribution to a credit entry is (s' - s) g(t) =
-// +-2 g(t), at most one per position t, so with |g| < 2^e over the stream an entry's sum
-// stays below 2^(1 + ceil(log2 T) + e). Scaled by 2^k, k = 61 - ceil(log2 T) - e, g(t) is
-// rounded once to an integer (an error below 2^-48 of the stream's largest gradient) and
-// the entries are exact int64 sums of +-2 g(t): the result does not depend on
-// the order in which the atomics land, so the credits are bit-identical on every run. A
-// stream whose gradient holds a non-finite value keeps fp32 atomics (its credits are not
-// finite either); so does a call without the int64 workspace.
+// Credit sums. A call runs three kernels: rosa_cred_setup_kernel (per stream: the mode
+// below, zeroed sums, d loss / d payload), one of the credit kernels (contributions only,
+// into the int64 sums), and rosa_cred_finish_kernel (sums -> fp32 credits). The credits
+// buffer is the call's scratch until the last kernel: entries 0 and 1 of every stream hold
+// its mode and parameter, entry 3 of stream 0 the work counter of the balanced kernel.
+// Modes, for g = grad * payload over the stream:
+//  0  every g finite: every contribution (s' - s) g(t) = +-2 g(t), at most one per position
+//     and entry, so with |g| < 2^e an entry stays below 2^(1 + ceil(log2 T) + e). Scaled
+//     by 2^k, k = 61 - ceil(log2 T) - e, g(t) is rounded once to an integer (an error below
+//     2^-48 of the stream's largest |g|) and the entries are exact int64 sums: the result
+//     does not depend on the order in which the atomics land (bit-identical on every run).
+//  1  some g = +-inf, none NaN: the reference's dense sum over t of delta * g (rosa_credit_
+//     gpu.py:48) makes an entry NaN unless delta != 0 at every infinite position (0 * inf),
+//     and then +-inf, or NaN if the infinite terms have both signs; finite terms do not
+//     matter. Only the infinite positions are visited, and an entry counts its +inf terms
+//     in the high 32 bits and its -inf terms in the low 32 bits.
+//  2  some g NaN: every entry is NaN (delta * NaN); nothing is visited.
 struct CredAcc {
-  float *f;               // this stream's (3, T) fp32 credits: q at 0, k at T, v at 2T
-  unsigned long long *a;  // this stream's (3, T) int64 sums, or null
-  double scale;           // 2^k
+  unsigned long long *a;  // this stream's (3, T) int64 entries: q at 0, k at T, v at 2T
+  double scale;           // 2^k (mode 0)
+  bool fin;               // mode 0
   // g(t) in fixed point, once per position
   __device__ __forceinline__ long long fixed(float g) const {
-    return a ? (long long)rint((double)g * scale) : 0ll;
+    return fin ? (long long)rint((double)g * scale) : 0ll;
   }
   // contribution d * g(t), d = s' - s = +-2
   __device__ __forceinline__ void add(int off, float d, float g, long long gi) const {
-    if (a) atomicAdd(a + off, (unsigned long long)((long long)d * gi));
-    else atomicAdd(f + off, d * g);
+    if (fin) atomicAdd(a + off, (unsigned long long)((long long)d * gi));
+    else atomicAdd(a + off, d * g > 0.0f ? (1ull << 32) : 1ull);
   }
 };
 
-// Block-level set-up of one stream's credits: zero the outputs, find the scale. red: LDS
-// scratch of kCredWaves + 1 words. Ends with a barrier.
-__device__ CredAcc cred_prologue(float *f, unsigned long long *a, const float *grad, int64_t b,
-                                 int64_t s, int64_t S, int T, float pay, uint32_t *red) {
-  float m = 0.0f;
-  bool bad = false;
-  for (int t = threadIdx.x; t < T; t += blockDim.x) {
-    const float g = fabsf(grad[(b * T + t) * S + s] * pay);
-    bad |= !(g <= 3.402823466e38f);  // inf or NaN
-    m = fmaxf(m, g);
+// A stream's mode word in credits entry 0 (a NaN pattern no credit value takes while the
+// sums are formed): 0x7fa00000 | mode << 12 | (k + 2048) for mode 0.
+constexpr uint32_t kCredTag = 0x7fa00000u;
+__device__ __forceinline__ uint32_t cred_mode_word(int mode, int k) {
+  return kCredTag | ((uint32_t)mode << 12) | (uint32_t)((k + 2048) & 0xfff);
+}
+// decodes the stream's mode; false for mode 2 (nothing to visit)
+__device__ __forceinline__ bool cred_acc_of(const float *cred, unsigned long long *sums, int64_t stream,
+                                            int T, CredAcc &ca) {
+  const uint32_t w = ((const uint32_t *)cred)[stream * 3 * T];
+  const int mode = (int)((w >> 12) & 3u);
+  ca.a = sums + stream * 3 * T;
+  ca.fin = mode == 0;
+  ca.scale = ldexp(1.0, (int)(w & 0xfffu) - 2048);
+  return mode != 2;
+}
+// the positions a mode visits: mode 0 every non-zero g, mode 1 the infinite ones
+__device__ __forceinline__ bool cred_live(const CredAcc &ca, float g) {
+  return ca.fin ? g != 0.0f : __builtin_isinf(g);
+}
+
+// One block per stream: mode, zeroed sums and d loss / d payload = sum over t of
+// grad * sign (rosa_credit_gpu.py:110) in a fixed order: wave w sums t = w, w + 4, ... in
+// ascending t, then ((w0 + w1) + w2) + w3. Block 0 also zeroes the work counter.
+__global__ void __launch_bounds__(256) rosa_cred_setup_kernel(
+    const uint32_t *__restrict__ qb, const uint32_t *__restrict__ kb, const uint32_t *__restrict__ vb,
+    const int32_t *__restrict__ match_j, const float *__restrict__ grad, const float *__restrict__ payload,
+    int64_t S, int T, int W, int lmax, float *__restrict__ cred, float *__restrict__ gp_partial,
+    unsigned long long *__restrict__ sums) {
+  extern __shared__ uint32_t sm[];
+  uint32_t *qw = sm, *kw = sm + W, *vw = sm + 2 * W;
+  __shared__ uint32_t red[2 * kCredWaves + 2];
+  __shared__ float gps[kCredWaves];
+  const int64_t stream = blockIdx.x;
+  const int64_t b = stream / S, s = stream % S;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int i = threadIdx.x; i < W; i += blockDim.x) {
+    qw[i] = qb[stream * W + i];
+    kw[i] = kb[stream * W + i];
+    vw[i] = vb[stream * W + i];
+  }
+  __syncthreads();
+  const float pay = payload[s];
+  float m = 0.0f, gsum = 0.0f;
+  int ninf = 0;
+  bool nan = false;
+  for (int t0 = wave; t0 < T; t0 += 64 * kCredWaves) {  // wave-uniform
+    const int t = t0 + kCredWaves * lane;
+    float gr = 0.0f, term = 0.0f;
+    if (t < T) {
+      gr = grad[(b * T + t) * S + s];
+      const float g = gr * pay;
+      if (__builtin_isnan(g)) nan = true;
+      else if (__builtin_isinf(g)) ++ninf;
+      else m = fmaxf(m, fabsf(g));
+      const int jstar = match_j[stream * T + t];
+      uint32_t best = 0u;
+      if (jstar >= 0) {
+        const int cstar = clz64(q_window(qw, t) ^ q_window(kw, jstar));
+        best = mkkey(min(cstar, min(jstar + 1, lmax)), jstar);
+      }
+      term = gr * sign_of(best, vw);
+    }
+    // the wave's positions in ascending t: lane order within a chunk of 64
+    for (int l = 0; l < 64; ++l) {
+      const float v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, term), l));
+      const float gv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gr), l));
+      if (gv != 0.0f || gv != gv) gsum += v;  // the credit kernels skip zero gradients
+    }
   }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-  const bool wbad = __any(bad);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (threadIdx.x == 0) red[kCredWaves] = 0u;
-  __syncthreads();
+  for (int o = 32; o > 0; o >>= 1) {
+    m = fmaxf(m, __shfl_xor(m, o));
+    ninf += __shfl_xor(ninf, o);
+  }
+  const bool wnan = __any(nan);
   if (lane == 0) {
     red[wave] = __builtin_bit_cast(uint32_t, m);
-    if (wbad) red[kCredWaves] = 1u;
+    red[kCredWaves + wave] = (uint32_t)ninf | (wnan ? 0x80000000u : 0u);
+    gps[wave] = gsum;
   }
   __syncthreads();
   float mx = 0.0f;
-  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) mx = fmaxf(mx, __builtin_bit_cast(float, red[w]));
-  CredAcc c{f, (a && red[kCredWaves] == 0u) ? a : nullptr, 1.0};
-  if (c.a) {
+  uint32_t ni = 0u;
+  bool anynan = false;
+  for (int w = 0; w < kCredWaves; ++w) {
+    mx = fmaxf(mx, __builtin_bit_cast(float, red[w]));
+    ni += red[kCredWaves + w] & 0x7fffffffu;
+    anynan |= (red[kCredWaves + w] >> 31) != 0u;
+  }
+  const int mode = anynan ? 2 : (ni ? 1 : 0);
+  int k = 0;
+  if (mode == 0) {
     int e = 0;
     if (mx > 0.0f) frexpf(mx, &e);  // mx < 2^e
     const int lc = T > 1 ? 32 - __clz(T - 1) : 0;  // ceil(log2 T)
-    c.scale = ldexp(1.0, 61 - lc - e);
-    for (int i = threadIdx.x; i < 3 * T; i += blockDim.x) c.a[i] = 0ull;
-  } else {
-    for (int i = threadIdx.x; i < 3 * T; i += blockDim.x) f[i] = 0.0f;
+    k = 61 - lc - e;
   }
-  __threadfence();
-  __syncthreads();
-  return c;
+  unsigned long long *a = sums + stream * 3 * T;
+  if (mode != 2)
+    for (int i = threadIdx.x; i < 3 * T; i += blockDim.x) a[i] = 0ull;
+  if (threadIdx.x == 0) {
+    gp_partial[stream] = ((gps[0] + gps[1]) + gps[2]) + gps[3];
+    uint32_t *cw = (uint32_t *)cred;
+    cw[stream * 3 * T] = cred_mode_word(mode, k);
+    cw[stream * 3 * T + 1] = ni;
+    if (stream == 0 && 3 * T > 3) cw[3] = 0u;  // the balanced kernel's work counter
+  }
 }
 
-// After every wave's last contribution (behind a barrier): the int64 sums to fp32.
-__device__ void cred_epilogue(const CredAcc &c, int T) {
-  if (!c.a) return;  // block-uniform
-  __threadfence();
+// One block per stream: the sums to fp32 credits (the mode read before any entry is
+// written; entry 3 of stream 0 is the spent work counter).
+__global__ void __launch_bounds__(256) rosa_cred_finish_kernel(float *__restrict__ cred,
+                                                               const unsigned long long *__restrict__ sums,
+                                                               int T) {
+  const int64_t stream = blockIdx.x;
+  float *f = cred + stream * 3 * T;
+  const unsigned long long *a = sums + stream * 3 * T;
+  const uint32_t w = ((const uint32_t *)f)[0];
+  const uint32_t ninf = ((const uint32_t *)f)[1];
   __syncthreads();
+  const int mode = (int)((w >> 12) & 3u);
+  const double scale = ldexp(1.0, (int)(w & 0xfffu) - 2048);
+  const float qnan = __builtin_nanf("");
   for (int i = threadIdx.x; i < 3 * T; i += blockDim.x) {
-    const unsigned long long v = __hip_atomic_load(c.a + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    c.f[i] = (float)((double)(long long)v / c.scale);
+    float v = qnan;
+    if (mode == 0) {
+      v = (float)((double)(long long)a[i] / scale);
+    } else if (mode == 1) {
+      const uint32_t np = (uint32_t)(a[i] >> 32), nn = (uint32_t)a[i];
+      if (np + nn == ninf && (np == 0u || nn == 0u)) v = np ? __builtin_inff() : -__builtin_inff();
+    }
+    f[i] = v;
   }
 }
 
@@ -1053,8 +1148,8 @@ __device__ __forceinline__ void near_run_flips(int lane, int t, int lmax, int js
 __global__ void __launch_bounds__(256) rosa_credits_kernel(
     const uint32_t *__restrict__ qb, const uint32_t *__restrict__ kb, const uint32_t *__restrict__ vb,
     const int32_t *__restrict__ match_j, const float *__restrict__ grad, const float *__restrict__ payload,
-    int64_t S, int T, int W, int lmax, float *__restrict__ cred, float *__restrict__ gp_partial,
-    unsigned long long *__restrict__ cred_acc) {
+    int64_t S, int T, int W, int lmax, const float *__restrict__ cred,
+    unsigned long long *__restrict__ sums) {
   extern __shared__ uint32_t sm[];
   uint32_t *qw = sm, *kw = sm + W, *vw = sm + 2 * W;
   const int lane = threadIdx.x & 63;
@@ -1072,11 +1167,8 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
   }
   __syncthreads();
   const float pay = payload[s];
-  __shared__ uint32_t red[kCredWaves + 1];
-  const CredAcc ca = cred_prologue(cred + stream * 3 * T, cred_acc ? cred_acc + stream * 3 * T : nullptr,
-                                   grad, b, s, S, T, pay, red);
-  float gsum = 0.0f;  // this wave's share of sum_t grad * sign (d loss / d payload)
-  __shared__ float gps[kCredWaves];
+  CredAcc ca;
+  if (!cred_acc_of(cred, sums, stream, T, ca)) return;  // block-uniform
 
   for (int t = wave; t < T; t += kCredWaves) {  // wave-uniform
     const float gr = grad[(b * T + t) * S + s];
@@ -1090,9 +1182,8 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
       best = mkkey(min(cstar, capstar), jstar);
     }
     const float sgn = sign_of(best, vw);
-    gsum += gr * sgn;
     const float g = gr * pay;
-    if (t == 0 || g == 0.0f || lmax < 1) continue;
+    if (t == 0 || !cred_live(ca, g) || lmax < 1) continue;
     const long long gi = ca.fixed(g);
     const int Lstar = key_len(best);
     // k flips inside the best candidate's matched run, resolved in (b)
@@ -1184,10 +1275,6 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
     if (jstar >= 0)
       near_run_flips(lane, t, lmax, jstar, trunc_lo, trunc_hi, farbest, Cn, En, Pref, Suf, vw, sgn, g, gi, ca, T);
   }
-  if (lane == 0) gps[wave] = gsum;
-  __syncthreads();
-  if (threadIdx.x == 0) gp_partial[stream] = ((gps[0] + gps[1]) + gps[2]) + gps[3];
-  cred_epilogue(ca, T);
 }
 
 // Bit-parallel credits for streams of up to 2048 positions (W <= 64 words). Same outputs as
@@ -1210,14 +1297,18 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
 //  k flip at p outside the best run: the largest lifted key among the members j of
 //    O_{L*+1} u (O_{L*} & {j > j*}) with j - c_j = p (a per-p table), if any.
 //  k flip inside the best run, and v flips: as in rosa_credits_kernel.
-// LDS per wave: the bucket maxima and latest-j tables (64 words each) and the per-p event
-// table in 16-bit entries, two to a word. For one p the members' keys order as their
-// (lifted length, c) pairs do (j = p + c), so an entry holds (length << 6) | c, at most
-// 12 bits. The near-run flip tables (256 words) reuse the event table's first words: the
-// k-flip pass leaves every event entry zero before they are written, and they are cleared
-// after use. 4.6 KB per wave lets 8 four-wave blocks share a CU.
+// LDS per wave: one 64-word bucket table (the best lifted key of a bucket with members,
+// the latest j of A_i for one without: the two never meet in a bucket), the work item's
+// q/k/v words, and the per-p event table in 16-bit entries, two to a word. For one p the
+// members' keys order as their (lifted length, c) pairs do (j = p + c), so an entry holds
+// (length << 6) | c, at most 12 bits. The near-run flip tables (256 words) reuse the event
+// table's first words: the k-flip pass leaves every event entry zero before they are
+// written, and they are cleared after use. 5 KB per wave lets 8 four-wave blocks share a
+// CU. Every wave works alone (no block barrier): the block is only a unit of launch.
 constexpr int kBpMaxT = 2048;
-constexpr int kBpWave32 = 64 + 64 + kBpMaxT / 2;  // u32 words per wave
+constexpr int kCredChunk = 16;        // positions per work item
+constexpr int kBpWave32 = 64 + 3 * 64 + kBpMaxT / 2;  // u32 words per wave
+constexpr int kBpBlocksPerCu = 8;     // 20 KB of LDS per block: 8 blocks fill a CU's 160 KB
 
 __device__ __forceinline__ uint32_t evt_key16(uint32_t key, int c) {
   return ((uint32_t)key_len(key) << 6) | (uint32_t)c;
@@ -1339,49 +1430,58 @@ __device__ __forceinline__ void near_flips_tables(int lane, int t, int lmax, int
 __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
     const uint32_t *__restrict__ qb, const uint32_t *__restrict__ kb, const uint32_t *__restrict__ vb,
     const int32_t *__restrict__ match_j, const float *__restrict__ grad, const float *__restrict__ payload,
-    int64_t S, int T, int W, int lmax, float *__restrict__ cred, float *__restrict__ gp_partial,
-    unsigned long long *__restrict__ cred_acc) {
-  __shared__ uint32_t qw[64], kw[64], vw[64];
-  __shared__ uint32_t wsm[kCredWaves][kBpWave32];
-  __shared__ float gps[kCredWaves];
+    int64_t S, int T, int W, int lmax, const float *__restrict__ cred, unsigned long long *__restrict__ sums,
+    unsigned int *__restrict__ counter, int nstreams, int nchunks) {
+  __shared__ __attribute__((aligned(16))) uint32_t wsm[kCredWaves][kBpWave32];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint32_t *Nw = wsm[wave];                       // [64] best lifted key per bucket
-  int *lat = (int *)(Nw + 64);                    // [64] latest j of A_i
-  uint32_t *evt = Nw + 128;                       // [kBpMaxT] 16-bit event entries per flip p
+  // [64] per bucket i: the best lifted key when the bucket has members (hasext bit i),
+  // else the latest j of A_i; the two never meet in one bucket
+  uint32_t *Nw = wsm[wave];
+  uint32_t *qw = Nw + 64, *kw = qw + 64, *vw = kw + 64;  // [64] each: the item's stream
+  uint32_t *evt = Nw + 256;                       // [kBpMaxT] 16-bit event entries per flip p
   uint32_t *ntab = evt;                           // [256] near-flip tables (aliasing evt)
-  const int64_t stream = blockIdx.x;
-  const int64_t b = stream / S, s = stream % S;
-  for (int i = threadIdx.x; i < 64; i += 256) {
-    qw[i] = i < W ? qb[stream * W + i] : 0u;
-    kw[i] = i < W ? kb[stream * W + i] : 0u;
-    vw[i] = i < W ? vb[stream * W + i] : 0u;
-  }
-  for (int i = lane; i < 64 + kBpMaxT / 2; i += 64) Nw[i < 64 ? i : 64 + i] = 0u;  // Nw and evt
-  __syncthreads();
-  // this lane's k words: word w and the two below it (zeros before position 0)
-  const uint32_t k0 = kw[lane], k1 = lane >= 1 ? kw[lane - 1] : 0u, k2 = lane >= 2 ? kw[lane - 2] : 0u;
-  const uint64_t k01 = ((uint64_t)k0 << 32) | k1, k12 = ((uint64_t)k1 << 32) | k2;
+  for (int i = lane; i < 64; i += 64) Nw[i] = 0u;
+  for (int i = lane; i < kBpMaxT / 2; i += 64) evt[i] = 0u;
   // {j >= L} for this lane's word as the low 32 bits of p01 >> (32 - L) (L <= 32) or
   // p12 >> (64 - L) (L > 32): only words 0 and 1 hold positions below 63
   const uint64_t p01 = lane == 0 ? ~0ull << 32 : ~0ull;
   const uint64_t p12 = lane == 0 ? 0ull : (lane == 1 ? ~0ull << 32 : ~0ull);
-  const float pay = payload[s];
-  __shared__ uint32_t red[kCredWaves + 1];
-  const CredAcc ca = cred_prologue(cred + stream * 3 * T, cred_acc ? cred_acc + stream * 3 * T : nullptr,
-                                   grad, b, s, S, T, pay, red);
-  float gsum = 0.0f;
-  // This wave's positions t = wave + kCredWaves * k, 64 at a time: the lanes load their
-  // gradients together and only positions with a non-zero gradient are visited (a zero
-  // gradient contributes nothing to any credit, and only a signed zero to the payload sum).
-  for (int kb = 0; wave + kCredWaves * kb < T; kb += 64) {
-    const int tl = wave + kCredWaves * (kb + lane);
-    const float grl = tl < T ? grad[(b * T + tl) * S + s] : 0.0f;
-    uint64_t live = __ballot(grl != 0.0f);  // NaN counts as live
+  const int nitems = nstreams * nchunks;
+  // Work items (stream, chunk of kCredChunk positions), handed out one per wave from a counter:
+  // the cost of a position grows with t and varies widely between streams (long matches
+  // cost far more), so the waves take items dynamically, the later chunks of every stream
+  // first, until none is left.
+  for (;;) {
+    unsigned int it = 0u;
+    if (lane == 0) it = atomicAdd(counter, 1u);
+    const int item = __builtin_amdgcn_readfirstlane((int)it);
+    if (item >= nitems) break;  // wave-uniform
+    const int chunk = nchunks - 1 - item / nstreams;
+    const int64_t stream = item % nstreams;
+    CredAcc ca;
+    if (!cred_acc_of(cred, sums, stream, T, ca)) continue;
+    const int64_t b = stream / S, s = stream % S;
+    __builtin_amdgcn_wave_barrier();
+    qw[lane] = lane < W ? qb[stream * W + lane] : 0u;
+    kw[lane] = lane < W ? kb[stream * W + lane] : 0u;
+    vw[lane] = lane < W ? vb[stream * W + lane] : 0u;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // this lane's k words: word w and the two below it (zeros before position 0)
+    const uint32_t k0 = kw[lane], k1 = lane >= 1 ? kw[lane - 1] : 0u, k2 = lane >= 2 ? kw[lane - 2] : 0u;
+    const uint64_t k01 = ((uint64_t)k0 << 32) | k1, k12 = ((uint64_t)k1 << 32) | k2;
+    const float pay = payload[s];
+    // the chunk's positions: the lanes load their gradients together and only the positions
+    // the stream's mode visits are walked
+    const int tl = chunk * kCredChunk + lane;
+    const float grl = lane < kCredChunk && tl < T ? grad[(b * T + tl) * S + s] : 0.0f;
+    uint64_t live = __ballot(lane < kCredChunk && tl < T && cred_live(ca, grl * pay));
     while (live) {  // wave-uniform
     const int li = __builtin_ctzll(live);
     live &= live - 1;
-    const int t = wave + kCredWaves * (kb + li);
+    const int t = chunk * kCredChunk + li;
     const float gr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, grl), li));
     const int jstar = match_j[stream * T + t];
     const uint64_t qwin = q_window(qw, t);
@@ -1393,9 +1493,8 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
       best = mkkey(min(cstar, capstar), jstar);
     }
     const float sgn = sign_of(best, vw);
-    gsum += gr * sgn;
     const float g = gr * pay;
-    if (t == 0 || g == 0.0f || lmax < 1) continue;
+    if (t == 0 || lmax < 1) continue;
     const long long gi = ca.fixed(g);
     const int Ls = key_len(best);
     if (lane == 0 && Ls >= 1) ca.add(2 * T + jstar + 1, -2.0f * sgn, g, gi);  // v flips
@@ -1448,7 +1547,7 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
           hasext |= 1ull << L;
         } else if (L >= 1) {  // a q flip at offset L without an extension: latest j of A_L
           const int lj = set_maxbit(A);
-          if (lane == 0) lat[L] = lj;
+          if (lane == 0) Nw[L] = (uint32_t)lj;
         }
       }
       if (tail) {
@@ -1493,7 +1592,13 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
     }
 
     // members of a checkpoint set: bucket maxima, and (ev) the lifted keys per flip p
+    // The event updates of one lane are merged while its consecutive members name the same
+    // flip p, and a wave whose last pending updates all name one p sends one update: in a
+    // long run every member's first mismatch is the same k bit, and evt_max16's
+    // compare-and-swap serializes the lanes that update one entry.
     auto members = [&](uint32_t x, bool ev) __attribute__((always_inline)) {
+      int pp = -1;       // this lane's pending event: flip p and its max entry
+      uint32_t pk = 0u;
       while (__any(x != 0u)) {
         if (x != 0u) {
           const int bb = 31 - __clz(x);
@@ -1507,7 +1612,29 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
           const uint32_t key = ext_key(c, e, min(j + 1, lmax), j);
           if (c <= imax) atomicMax(Nw + c, key);
           const int p = j - c;
-          if (ev && key > best && !(p >= trunc_lo && p <= trunc_hi)) evt_max16(evt, p, evt_key16(key, c));
+          if (ev && key > best && !(p >= trunc_lo && p <= trunc_hi)) {
+            const uint32_t k16 = evt_key16(key, c);
+            if (p == pp) {
+              pk = max(pk, k16);
+            } else {
+              if (pp >= 0) evt_max16(evt, pp, pk);
+              pp = p;
+              pk = k16;
+            }
+          }
+        }
+      }
+      const uint64_t pend = __ballot(pp >= 0);
+      if (pend) {  // wave-uniform
+        const int lead = __builtin_ctzll(pend);
+        const int p0 = __builtin_amdgcn_readlane(pp, lead);
+        if (__all(pp < 0 || pp == p0)) {
+          uint32_t m = pp >= 0 ? pk : 0u;
+#pragma unroll
+          for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o));
+          if (lane == lead) evt_max16(evt, p0, m);
+        } else if (pp >= 0) {
+          evt_max16(evt, pp, pk);
         }
       }
     };
@@ -1571,7 +1698,7 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
     // q flips: one lane per offset i
     if (lane <= imax) {
       const int i = lane;
-      const uint32_t nb = ((hasext >> i) & 1ull) ? Nw[i] : (i >= 1 ? mkkey(i, lat[i]) : 0u);
+      const uint32_t nb = ((hasext >> i) & 1ull) ? Nw[i] : (i >= 1 ? mkkey(i, (int)Nw[i]) : 0u);
       const float s2 = sign_of(nb, vw);
       if (s2 != sgn) ca.add(t - i, s2 - sgn, g, gi);
     }
@@ -1617,10 +1744,6 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
     }
     }
   }
-  if (lane == 0) gps[wave] = gsum;
-  __syncthreads();
-  if (threadIdx.x == 0) gp_partial[stream] = ((gps[0] + gps[1]) + gps[2]) + gps[3];
-  cred_epilogue(ca, T);
 }
 
 // d loss / d payload = sum over (b, t) of grad * sign (rosa_credit_gpu.py:110), and the
@@ -1695,19 +1818,32 @@ extern "C" int ksd_rosa_credits(const uint32_t *q_bits, const uint32_t *k_bits, 
   if (B == 0 || T == 0 || S == 0) return KSD_OK;
   if (!q_bits || !k_bits || !v_bits || !match_j || !grad || !payload || !credits || !payload_partial)
     return fail(KSD_EINVAL, "rosa_credits: null pointer");
+  if (!credit_sums) return fail(KSD_EINVAL, "rosa_credits: credit_sums workspace is required");
   const int W = (int)cdiv(T, 32);
   const size_t lds = (3 * (size_t)W + kCredWaves * (size_t)kCredWave32) * sizeof(uint32_t);
   if (lds > 64 * 1024) return fail(KSD_EINVAL, "rosa_credits: T too large for LDS");
-  if (B * S > 0x7fffffff) return fail(KSD_EINVAL, "rosa_credits: too many streams");
+  if (B * S > 0x7fffffff || B * S * cdiv(T, kCredChunk) > 0x7fffffff)
+    return fail(KSD_EINVAL, "rosa_credits: too many streams");
+  hipStream_t st = (hipStream_t)stream;
   unsigned long long *sums = (unsigned long long *)credit_sums;
-  if (T <= kBpMaxT)  // the bit-parallel kernel: one 32-candidate word per lane
-    hipLaunchKernelGGL(rosa_credits_bp_kernel, dim3((unsigned)(B * S)), dim3(256), 0, (hipStream_t)stream,
-                       q_bits, k_bits, v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits,
-                       payload_partial, sums);
-  else
-    hipLaunchKernelGGL(rosa_credits_kernel, dim3((unsigned)(B * S)), dim3(256), lds, (hipStream_t)stream,
-                       q_bits, k_bits, v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits,
-                       payload_partial, sums);
+  const int n = (int)(B * S);
+  hipLaunchKernelGGL(rosa_cred_setup_kernel, dim3((unsigned)n), dim3(256), 3 * (size_t)W * sizeof(uint32_t), st,
+                     q_bits, k_bits, v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits,
+                     payload_partial, sums);
+  if (T >= 2 && lmax >= 1) {  // position 0 has no candidate: T = 1 has no contribution
+    if (T <= kBpMaxT) {  // the bit-parallel kernel: one 32-candidate word per lane
+      const int nchunks = (int)cdiv(T, kCredChunk);
+      const int64_t waves = (int64_t)n * nchunks;
+      const int nblk = (int)min(cdiv(waves, kCredWaves), (int64_t)cu_count() * kBpBlocksPerCu);
+      hipLaunchKernelGGL(rosa_credits_bp_kernel, dim3((unsigned)nblk), dim3(256), 0, st, q_bits, k_bits,
+                         v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits, sums,
+                         (unsigned int *)credits + 3, n, nchunks);
+    } else {
+      hipLaunchKernelGGL(rosa_credits_kernel, dim3((unsigned)n), dim3(256), lds, st, q_bits, k_bits,
+                         v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits, sums);
+    }
+  }
+  hipLaunchKernelGGL(rosa_cred_finish_kernel, dim3((unsigned)n), dim3(256), 0, st, credits, sums, (int)T);
   return check_launch("rosa_credits");
 }
 

@@ -257,9 +257,8 @@ def test_rosa_mixer_eval_and_training():
         assert p.grad is not None and torch.isfinite(p.grad).all(), name
 
 
-def _credits_direct(q, k, v, gsign, lmax=None, fixed=True):
-    """ksd_rosa_credits on (n, T) bit streams, grad_sign (n, T): credits (n, 3, T); fixed:
-    with the int64 workspace (exact, order-independent sums), else fp32 atomics."""
+def _credits_direct(q, k, v, gsign, lmax=None):
+    """ksd_rosa_credits on (n, T) bit streams, grad_sign (n, T): credits (n, 3, T)."""
     from ksdraft_amd import _lib
     n, T = q.shape
     rng = np.random.default_rng(T)
@@ -271,7 +270,7 @@ def _credits_direct(q, k, v, gsign, lmax=None, fixed=True):
     pay = torch.ones(n, device=DEV)
     cred = torch.full((n, 3, T), float("nan"), device=DEV)  # every entry is written
     part = torch.empty((n,), device=DEV)
-    sums = torch.empty((n, 3, T), dtype=torch.int64, device=DEV) if fixed else None
+    sums = torch.empty((n, 3, T), dtype=torch.int64, device=DEV)
     _lib.call("ksd_rosa_credits", packed[0].data_ptr(), packed[1].data_ptr(), packed[2].data_ptr(),
               mj.contiguous().data_ptr(), grad.data_ptr(), pay.data_ptr(), 1, T, n, lmax,
               cred.data_ptr(), part.data_ptr(), _lib.ptr(sums), _lib.stream_ptr(torch.device(DEV)))
@@ -313,10 +312,11 @@ def test_credits_explicit_max_match_len_bruteforce(lmax):
     assert np.array_equal(got == 0, exp == 0)
 
 
-def test_credits_are_deterministic_and_match_the_atomic_sums():
-    """With the int64 workspace every credit is an exact fixed-point sum: two runs give the
-    same bits (structured streams with deep chains, many contributions per entry), and the
-    values agree with the fp32-atomic sums and the definition."""
+def test_credits_are_deterministic():
+    """Every credit is an exact fixed-point sum, formed by waves that take (stream, chunk)
+    items in whatever order they finish: two runs give the same bits (structured streams
+    with deep chains, many contributions per entry), and the values match the definition on
+    sampled flips."""
     rng = np.random.default_rng(4242)
     n, T = 24, 2048
     q = _streams(rng, n, T)
@@ -327,9 +327,6 @@ def test_credits_are_deterministic_and_match_the_atomic_sums():
     a = _credits_direct(q, k, v, gsign)
     b = _credits_direct(q, k, v, gsign)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
-    c = _credits_direct(q, k, v, gsign, fixed=False)
-    scale = np.abs(c).max()
-    np.testing.assert_allclose(a, c, rtol=1e-5, atol=1e-6 * scale)
     base, _, _ = orr.match(q, k, v)
     for s in range(0, n, 5):
         for which in range(3):
@@ -341,20 +338,58 @@ def test_credits_are_deterministic_and_match_the_atomic_sums():
                 assert abs(a[s, which, p] - exp) <= 1e-5 * max(abs(exp), np.abs(gsign[s]).max()), (s, which, p)
 
 
-def test_credits_nonfinite_gradient_falls_back_to_fp32_sums():
-    """A stream whose gradient holds inf or NaN keeps fp32 atomics (non-finite credits as
-    before); the other streams of the call stay exact."""
-    rng = np.random.default_rng(77)
-    n, T = 6, 300
-    q, k, v = (_streams(rng, n, T) for _ in range(3))
+def _dense_entry(q, k, v, g, s, which, p, base):
+    """Credit (which, p) of stream s by definition: the re-match after the flip, then the
+    dense float64 sum of delta * g over every t (IEEE: 0 * inf and NaN give NaN)."""
+    fl = [x[s:s + 1].copy() for x in (q, k, v)]
+    fl[which][0, p] ^= 1
+    sp, _, _ = orr.match(*fl)
+    with np.errstate(invalid="ignore"):
+        return float(((sp[0] - base[s]).astype(np.float64) * g[s].astype(np.float64)).sum())
+
+
+@pytest.mark.parametrize("T", [300, 2100])
+def test_credits_nonfinite_gradient_follows_the_dense_sum(T):
+    """Streams whose gradient holds inf or NaN: the reference sums delta * g over every t
+    (rosa_credit_gpu.py:48), so 0 * inf and NaN make an entry NaN unless every infinite
+    position flips it, which then holds +-inf (NaN if the infinite terms have both signs).
+    T = 300 against the definition on every entry, T = 2100 (the candidate-per-lane kernel)
+    on sampled entries and on every entry the infinite positions flip. The finite streams of
+    the call stay exact."""
+    rng = np.random.default_rng(77 + T)
+    n = 7
+    q = _streams(rng, n, T)
+    k = np.concatenate([q[:3], _streams(rng, n - 3, T)])
+    v = _streams(rng, n, T)
     gsign = rng.standard_normal((n, T)).astype(np.float32)
-    gsign[1, 17] = np.inf
-    gsign[2, 40] = np.nan
+    gsign[1, 17] = np.inf                          # one +inf
+    gsign[2, 40] = np.nan                          # NaN: every entry NaN
+    gsign[3, [50, 90]] = [np.inf, -np.inf]         # both signs
+    gsign[4, 0] = -np.inf                          # at t = 0 (no candidate: every entry NaN)
+    gsign[5, [60, 61]] = np.inf
     got = _credits_direct(q, k, v, gsign)
-    fin = [0, 3, 4, 5]
-    exp = orr.credits(q[fin], k[fin], v[fin], gsign[fin])
-    np.testing.assert_allclose(got[fin], exp, rtol=1e-5, atol=1e-5 * np.abs(exp).max())
-    assert not np.isfinite(got[1]).all() and not np.isfinite(got[2]).all()
+    assert np.isnan(got[2]).all() and np.isnan(got[4]).all()
+    if T <= 300:
+        with np.errstate(invalid="ignore"):
+            exp = orr.credits(q, k, v, gsign)
+        assert np.array_equal(np.isnan(got), np.isnan(exp))
+        assert np.array_equal(np.isposinf(got), np.isposinf(exp))
+        assert np.array_equal(np.isneginf(got), np.isneginf(exp))
+        np.testing.assert_allclose(got[[0, 6]], exp[[0, 6]], rtol=1e-5, atol=1e-5 * np.abs(exp[[0, 6]]).max())
+        assert np.isinf(got[1]).any()
+        return
+    base, _, _ = orr.match(q, k, v)
+    for s in (1, 3, 5):
+        inf_entries = np.argwhere(np.isinf(got[s]))
+        picks = [tuple(e) for e in inf_entries[:6]]
+        picks += [(int(w), int(p)) for w, p in zip(rng.integers(0, 3, 6), rng.integers(0, T, 6))]
+        for which, p in picks:
+            exp = _dense_entry(q, k, v, gsign, s, which, p, base)
+            a = got[s, which, p]
+            assert (np.isnan(a) and np.isnan(exp)) or a == exp, (s, which, p, a, exp)
+    for which, p in zip(rng.integers(0, 3, 6), rng.integers(0, T, 6)):
+        exp = _dense_entry(q, k, v, gsign, 0, which, p, base)
+        assert abs(got[0, which, p] - exp) <= 1e-5 * max(abs(exp), np.abs(gsign[0]).max())
 
 
 def test_credits_t2100_sampled_flips():
