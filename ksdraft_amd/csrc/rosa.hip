@@ -908,7 +908,8 @@ constexpr int kCredWave32 = 64 + 64 + 128 + 2 * kNear / 4 + 2 * kNear;  // uint3
 // below, zeroed sums, d loss / d payload), one of the credit kernels (contributions only,
 // into the int64 sums), and rosa_cred_finish_kernel (sums -> fp32 credits). The credits
 // buffer is the call's scratch until the last kernel: entries 0 and 1 of every stream hold
-// its mode and parameter, entry 3 of stream 0 the work counter of the balanced kernel.
+// its mode and parameter, entry 3 of the first 64 streams the work counters of the
+// balanced kernel.
 // Modes, for g = grad * payload over the stream:
 //  0  every g finite: every contribution (s' - s) g(t) = +-2 g(t), at most one per position
 //     and entry, so with |g| < 2^e an entry stays below 2^(1 + ceil(log2 T) + e). Scaled
@@ -945,7 +946,8 @@ __device__ __forceinline__ uint32_t cred_mode_word(int mode, int k) {
 // decodes the stream's mode; false for mode 2 (nothing to visit)
 __device__ __forceinline__ bool cred_acc_of(const float *cred, unsigned long long *sums, int64_t stream,
                                             int T, CredAcc &ca) {
-  const uint32_t w = ((const uint32_t *)cred)[stream * 3 * T];
+  const uint32_t w = __hip_atomic_load((const uint32_t *)cred + stream * 3 * T, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
   const int mode = (int)((w >> 12) & 3u);
   ca.a = sums + stream * 3 * T;
   ca.fin = mode == 0;
@@ -957,9 +959,12 @@ __device__ __forceinline__ bool cred_live(const CredAcc &ca, float g) {
   return ca.fin ? g != 0.0f : __builtin_isinf(g);
 }
 
+constexpr int kCredCounters = 64;  // work counters of the balanced kernel: entry 3 of streams 0, 1, ...
+
 // One block per stream: mode, zeroed sums and d loss / d payload = sum over t of
 // grad * sign (rosa_credit_gpu.py:110) in a fixed order: wave w sums t = w, w + 4, ... in
-// ascending t, then ((w0 + w1) + w2) + w3. Block 0 also zeroes the work counter.
+// ascending t, then ((w0 + w1) + w2) + w3. Blocks 0 .. kCredCounters - 1 also zero the work
+// counters.
 __global__ void __launch_bounds__(256) rosa_cred_setup_kernel(
     const uint32_t *__restrict__ qb, const uint32_t *__restrict__ kb, const uint32_t *__restrict__ vb,
     const int32_t *__restrict__ match_j, const float *__restrict__ grad, const float *__restrict__ payload,
@@ -1042,21 +1047,27 @@ __global__ void __launch_bounds__(256) rosa_cred_setup_kernel(
     uint32_t *cw = (uint32_t *)cred;
     cw[stream * 3 * T] = cred_mode_word(mode, k);
     cw[stream * 3 * T + 1] = ni;
-    if (stream == 0 && 3 * T > 3) cw[3] = 0u;  // the balanced kernel's work counter
+    if (stream < kCredCounters && 3 * T > 3) cw[stream * 3 * T + 3] = 0u;  // a work counter
   }
 }
 
-// One block per stream: the sums to fp32 credits (the mode read before any entry is
-// written; entry 3 of stream 0 is the spent work counter).
-__global__ void __launch_bounds__(256) rosa_cred_finish_kernel(float *__restrict__ cred,
-                                                               const unsigned long long *__restrict__ sums,
+// One block per stream: the sums to fp32 credits. The stream's mode words are entries of
+// the output: thread 0 reads them and hands them to the block through LDS before any entry
+// is written. (Every wave reading them itself would race with thread 0's first store: the
+// compiler may turn such a uniform load into a scalar-cache load placed after the barrier,
+// since a 32-bit integer load and the float stores do not alias by type.)
+__global__ void __launch_bounds__(256) rosa_cred_finish_kernel(float *cred, const unsigned long long *__restrict__ sums,
                                                                int T) {
+  __shared__ uint32_t mw[2];
   const int64_t stream = blockIdx.x;
-  float *f = cred + stream * 3 * T;
+  uint32_t *f = (uint32_t *)cred + stream * 3 * T;
   const unsigned long long *a = sums + stream * 3 * T;
-  const uint32_t w = ((const uint32_t *)f)[0];
-  const uint32_t ninf = ((const uint32_t *)f)[1];
+  if (threadIdx.x == 0) {
+    mw[0] = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    mw[1] = __hip_atomic_load(f + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   __syncthreads();
+  const uint32_t w = mw[0], ninf = mw[1];
   const int mode = (int)((w >> 12) & 3u);
   const double scale = ldexp(1.0, (int)(w & 0xfffu) - 2048);
   const float qnan = __builtin_nanf("");
@@ -1068,7 +1079,7 @@ __global__ void __launch_bounds__(256) rosa_cred_finish_kernel(float *__restrict
       const uint32_t np = (uint32_t)(a[i] >> 32), nn = (uint32_t)a[i];
       if (np + nn == ninf && (np == 0u || nn == 0u)) v = np ? __builtin_inff() : -__builtin_inff();
     }
-    f[i] = v;
+    f[i] = __builtin_bit_cast(uint32_t, v);
   }
 }
 
@@ -1431,7 +1442,7 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
     const uint32_t *__restrict__ qb, const uint32_t *__restrict__ kb, const uint32_t *__restrict__ vb,
     const int32_t *__restrict__ match_j, const float *__restrict__ grad, const float *__restrict__ payload,
     int64_t S, int T, int W, int lmax, const float *__restrict__ cred, unsigned long long *__restrict__ sums,
-    unsigned int *__restrict__ counter, int nstreams, int nchunks) {
+    unsigned int *__restrict__ counters, int64_t cstride, int ncount, int nstreams, int nchunks) {
   __shared__ __attribute__((aligned(16))) uint32_t wsm[kCredWaves][kBpWave32];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1448,15 +1459,30 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
   const uint64_t p01 = lane == 0 ? ~0ull << 32 : ~0ull;
   const uint64_t p12 = lane == 0 ? 0ull : (lane == 1 ? ~0ull << 32 : ~0ull);
   const int nitems = nstreams * nchunks;
-  // Work items (stream, chunk of kCredChunk positions), handed out one per wave from a counter:
-  // the cost of a position grows with t and varies widely between streams (long matches
-  // cost far more), so the waves take items dynamically, the later chunks of every stream
-  // first, until none is left.
+  // Work items (stream, chunk of kCredChunk positions): the cost of a position grows with t
+  // and varies widely between streams (long matches cost far more), so the waves take
+  // items dynamically, the later chunks of every stream first, until none is left. Item i
+  // belongs to counter i % ncount (the counters sit ncount apart: one counter for all
+  // items would serialize every wave's fetch on one address); a wave starts at its own
+  // counter and moves to the next one once that is spent, reading a counter before adding
+  // to it so that spent ones cost no atomic.
+  const int wid = (int)blockIdx.x * kCredWaves + wave;
+  int cc = wid % ncount, spent = 0;
   for (;;) {
-    unsigned int it = 0u;
-    if (lane == 0) it = atomicAdd(counter, 1u);
-    const int item = __builtin_amdgcn_readfirstlane((int)it);
-    if (item >= nitems) break;  // wave-uniform
+    const int lim = (nitems - cc + ncount - 1) / ncount;  // local indices of counter cc
+    int item = nitems;
+    if (__hip_atomic_load(counters + cc * cstride, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT) < (unsigned int)lim) {
+      unsigned int it = 0u;
+      if (lane == 0) it = atomicAdd(counters + cc * cstride, 1u);
+      const int l = __builtin_amdgcn_readfirstlane((int)it);
+      if (l < lim) item = cc + l * ncount;
+    }
+    if (item >= nitems) {  // wave-uniform: counter cc is spent
+      if (++spent == ncount) break;
+      cc = cc + 1 == ncount ? 0 : cc + 1;
+      continue;
+    }
     const int chunk = nchunks - 1 - item / nstreams;
     const int64_t stream = item % nstreams;
     CredAcc ca;
@@ -1837,7 +1863,7 @@ extern "C" int ksd_rosa_credits(const uint32_t *q_bits, const uint32_t *k_bits, 
       const int nblk = (int)min(cdiv(waves, kCredWaves), (int64_t)cu_count() * kBpBlocksPerCu);
       hipLaunchKernelGGL(rosa_credits_bp_kernel, dim3((unsigned)nblk), dim3(256), 0, st, q_bits, k_bits,
                          v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits, sums,
-                         (unsigned int *)credits + 3, n, nchunks);
+                         (unsigned int *)credits + 3, 3 * T, min(n, kCredCounters), n, nchunks);
     } else {
       hipLaunchKernelGGL(rosa_credits_kernel, dim3((unsigned)n), dim3(256), lds, st, q_bits, k_bits,
                          v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits, sums);

@@ -392,6 +392,32 @@ def test_credits_nonfinite_gradient_follows_the_dense_sum(T):
         assert abs(got[0, which, p] - exp) <= 1e-5 * max(abs(exp), np.abs(gsign[0]).max())
 
 
+def test_credits_repeated_calls_zero_gradient():
+    """Many calls on freshly allocated output buffers filled with NaN beforehand, zero
+    gradient: every credit is exactly zero on every call (the conversion kernel reads each
+    stream's mode words, held in the output buffer, before overwriting them)."""
+    from ksdraft_amd import _lib
+    rng = np.random.default_rng(9)
+    n, T = 256, 2048
+    q, k, v = (_streams(rng, n, T) for _ in range(3))
+    proj = [_bits_to_proj(b, rng).T[None] for b in (q, k, v)]
+    packed = [R.pack_bits(_g(p)).reshape(n, -1).contiguous() for p in proj]
+    _, mj = R.match_packed(*packed, T, want_j=True)
+    grad = torch.zeros((1, T, n), device=DEV)
+    pay = torch.ones(n, device=DEV)
+    bad = []
+    for i in range(100):
+        cred = torch.full((n, 3, T), float("nan"), device=DEV)
+        part = torch.full((n,), float("nan"), device=DEV)
+        sums = torch.full((n, 3, T), -1, dtype=torch.int64, device=DEV)
+        _lib.call("ksd_rosa_credits", packed[0].data_ptr(), packed[1].data_ptr(), packed[2].data_ptr(),
+                  mj.contiguous().data_ptr(), grad.data_ptr(), pay.data_ptr(), 1, T, n, 62,
+                  cred.data_ptr(), part.data_ptr(), sums.data_ptr(), _lib.stream_ptr(torch.device(DEV)))
+        bad.append(torch.stack([(cred != 0).sum(), (part != 0).sum()]))
+    bad = torch.stack(bad).cpu().numpy()
+    assert not bad.any(), np.nonzero(bad.any(1))[0][:5]
+
+
 def test_credits_t2100_sampled_flips():
     """T above 2048 takes the candidate-per-lane kernel: sampled flips by definition."""
     rng = np.random.default_rng(2100)
