@@ -22,10 +22,8 @@ the eager step; the one-step graph and the eager step times are reported beside 
 Also reported: the step's four launches timed inside the step (HIP events between them
 on the launch stream, eager steps); per-kernel average launch times of back-to-back
 launches (HIP events around graphs of them); the GEMM roofline against the 5.0 POPS
-dense int8 peak, from the in-step GEMM durations (back to back, the same GEMM runs
-slower: the chip holds lower clocks under continuous matrix load than when memory-bound
-quantization launches alternate with it); and the CPU oracle (the reference's CPU path:
-dequantize + fp32 matmul) timed on a bounded sample on this host.
+dense int8 peak, from the in-step GEMM durations; and the CPU oracle (the reference's CPU
+path: dequantize + fp32 matmul) timed on a bounded sample on this host.
 """
 
 from __future__ import annotations

@@ -878,7 +878,8 @@ namespace ksd {
 //             lmax flips per t, each resolved from the candidates within 62 of j* (kept in
 //             LDS) and the best key farther away (unchanged by the flip).
 //   v[p]:     the sign at every t whose endpoint is p - 1 flips (closed form).
-// Contributions (sign' - sign) * g(t), g = grad * payload, are added with fp32 atomics.
+// Contributions (sign' - sign) * g(t), g = grad * payload, are added into exact int64
+// fixed-point sums (CredAcc below), which a last kernel converts to fp32.
 
 
 __device__ __forceinline__ int clz64(uint64_t x) { return x ? __clzll((long long)x) : 64; }
