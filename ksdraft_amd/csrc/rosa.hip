@@ -19,6 +19,8 @@
 // non-empty length is the best length and its highest surviving j the latest endpoint.
 // Candidates are walked in chunks of kCH words; each chunk carries two words of halo to
 // its left so every chain j'..j'+61 of its own candidates lies inside the chunk.
+#include <stdlib.h>
+#include <string.h>
 #include <type_traits>
 
 #include "ksd_common.h"
@@ -428,7 +430,10 @@ constexpr int kStep = 4;  // match lengths per step of the walk
 // 64 q bits ending at t in memory order: bit 63 = q[t], bit 63-i = q[t-i] (0 before 0).
 __device__ __forceinline__ uint64_t q_window(const uint32_t *qw, int t) {
   const int w = t >> 5, b = t & 31;
-  const uint64_t hi = qw[w], mid = w >= 1 ? qw[w - 1] : 0u, lo = w >= 2 ? qw[w - 2] : 0u;
+  // every load in bounds and none behind a branch, so the three are in flight together
+  const uint64_t hi = qw[w];
+  const uint64_t mid = qw[max(w - 1, 0)] & (w >= 1 ? ~0u : 0u);
+  const uint64_t lo = qw[max(w - 2, 0)] & (w >= 2 ? ~0u : 0u);
   const uint64_t m64 = (hi << 32) | mid;
   return (m64 << (31 - b)) | (b == 31 ? 0ull : (lo >> (b + 1)));
 }
@@ -895,15 +900,14 @@ __device__ __forceinline__ float sign_of(uint32_t key, const uint32_t *vw) {
 }
 
 
-// Block = one stream, 4 waves; wave w handles positions t = w, w + 4, ... and its 64 lanes
-// split the candidates j. Per-wave LDS tables for the current t:
+// Per-candidate path (scan_position): the 64 lanes of a wave split the candidates j of one
+// position t. Per-wave LDS tables for the current t:
 //   Mw[64]   best key per common-suffix bucket c (c >= 63 pooled)
 //   Nw[64]   best key per bucket after flipping the q bit at the first mismatch
 //   Rk[128]  k-extension events, slot p mod 128: the best lifted key of flip k[p]
-//   Cn/En[128]  c_j and e_j (uint8) of the candidates j in [j* - 63, j* + 64)
-constexpr int kNear = 128;
+//   tab[256] the near-run flip tables (near_flips_tables)
 constexpr int kCredWaves = 4;
-constexpr int kCredWave32 = 64 + 64 + 128 + 2 * kNear / 4 + 2 * kNear;  // uint32 words per wave
+constexpr int kCredWave32 = 64 + 64 + 128 + 256;  // uint32 words per wave
 
 // Credit sums. A call runs three kernels: rosa_cred_setup_kernel (per stream: the mode
 // below, zeroed sums, d loss / d payload), one of the credit kernels (contributions only,
@@ -927,22 +931,25 @@ struct CredAcc {
   unsigned long long *a;  // this stream's (3, T) int64 entries: q at 0, k at T, v at 2T
   double scale;           // 2^k (mode 0)
   bool fin;               // mode 0
+  bool scan;              // the stream's positions take the per-candidate path
   // g(t) in fixed point, once per position
   __device__ __forceinline__ long long fixed(float g) const {
     return fin ? (long long)rint((double)g * scale) : 0ll;
   }
-  // contribution d * g(t), d = s' - s = +-2
-  __device__ __forceinline__ void add(int off, float d, float g, long long gi) const {
-    if (fin) atomicAdd(a + off, (unsigned long long)((long long)d * gi));
-    else atomicAdd(a + off, d * g > 0.0f ? (1ull << 32) : 1ull);
+  // contribution d * g(t), d = s' - s = +2 (up) or -2
+  __device__ __forceinline__ void add(int off, bool up, float g, long long gi) const {
+    if (fin) atomicAdd(a + off, (unsigned long long)(up ? 2 * gi : -2 * gi));
+    else atomicAdd(a + off, up == (g > 0.0f) ? (1ull << 32) : 1ull);
   }
 };
 
 // A stream's mode word in credits entry 0 (a NaN pattern no credit value takes while the
-// sums are formed): 0x7fa00000 | mode << 12 | (k + 2048) for mode 0.
+// sums are formed): 0x7fa00000 | scan << 14 | mode << 12 | (k + 2048) for mode 0, where
+// scan selects the per-candidate path for the stream's positions (cred_scan_stream).
 constexpr uint32_t kCredTag = 0x7fa00000u;
-__device__ __forceinline__ uint32_t cred_mode_word(int mode, int k) {
-  return kCredTag | ((uint32_t)mode << 12) | (uint32_t)((k + 2048) & 0xfff);
+constexpr uint32_t kCredScanBit = 1u << 14;
+__device__ __forceinline__ uint32_t cred_mode_word(int mode, int k, bool scan) {
+  return kCredTag | (scan ? kCredScanBit : 0u) | ((uint32_t)mode << 12) | (uint32_t)((k + 2048) & 0xfff);
 }
 // decodes the stream's mode; false for mode 2 (nothing to visit)
 __device__ __forceinline__ bool cred_acc_of(const float *cred, unsigned long long *sums, int64_t stream,
@@ -952,6 +959,7 @@ __device__ __forceinline__ bool cred_acc_of(const float *cred, unsigned long lon
   const int mode = (int)((w >> 12) & 3u);
   ca.a = sums + stream * 3 * T;
   ca.fin = mode == 0;
+  ca.scan = (w & kCredScanBit) != 0u;
   ca.scale = ldexp(1.0, (int)(w & 0xfffu) - 2048);
   return mode != 2;
 }
@@ -961,6 +969,19 @@ __device__ __forceinline__ bool cred_live(const CredAcc &ca, float g) {
 }
 
 constexpr int kCredCounters = 64;  // work counters of the balanced kernel: entry 3 of streams 0, 1, ...
+
+// Path choice of the balanced kernel. The bit-parallel path's cost grows with the size of
+// the one-mismatch sets it enumerates, which is large on streams with long runs: many
+// positions with a short best match but thousands of one-mismatch candidates, or long
+// matches with long extension chains. The per-candidate path costs about the same per
+// candidate whatever the stream. Measured per position on random and trained-model
+// streams (T 2048), the per-candidate path is the cheaper one when a stream's mean best
+// length exceeds 14 or more than 40% of its positions have a best length below 8, and at
+// every position below 512 (a scan's cost grows with t, the bit-parallel path's hardly).
+constexpr int kScanBelow = 512;
+__device__ __forceinline__ bool cred_scan_stream(int64_t len_sum, int64_t short_cnt, int T) {
+  return len_sum > 14 * (int64_t)T || 10 * short_cnt > 4 * (int64_t)T;
+}
 
 // One block per stream: mode, zeroed sums and d loss / d payload = sum over t of
 // grad * sign (rosa_credit_gpu.py:110) in a fixed order: wave w sums t = w, w + 4, ... in
@@ -974,6 +995,7 @@ __global__ void __launch_bounds__(256) rosa_cred_setup_kernel(
   extern __shared__ uint32_t sm[];
   uint32_t *qw = sm, *kw = sm + W, *vw = sm + 2 * W;
   __shared__ uint32_t red[2 * kCredWaves + 2];
+  __shared__ uint32_t lstat[2 * kCredWaves];  // per wave: sum of best lengths, count below 8
   __shared__ float gps[kCredWaves];
   const int64_t stream = blockIdx.x;
   const int64_t b = stream / S, s = stream % S;
@@ -986,7 +1008,7 @@ __global__ void __launch_bounds__(256) rosa_cred_setup_kernel(
   __syncthreads();
   const float pay = payload[s];
   float m = 0.0f, gsum = 0.0f;
-  int ninf = 0;
+  int ninf = 0, lsum = 0, lshort = 0;
   bool nan = false;
   for (int t0 = wave; t0 < T; t0 += 64 * kCredWaves) {  // wave-uniform
     const int t = t0 + kCredWaves * lane;
@@ -1004,6 +1026,8 @@ __global__ void __launch_bounds__(256) rosa_cred_setup_kernel(
         best = mkkey(min(cstar, min(jstar + 1, lmax)), jstar);
       }
       term = gr * sign_of(best, vw);
+      lsum += key_len(best);
+      lshort += key_len(best) < 8;
     }
     // the wave's positions in ascending t: lane order within a chunk of 64
     for (int l = 0; l < 64; ++l) {
@@ -1016,21 +1040,28 @@ __global__ void __launch_bounds__(256) rosa_cred_setup_kernel(
   for (int o = 32; o > 0; o >>= 1) {
     m = fmaxf(m, __shfl_xor(m, o));
     ninf += __shfl_xor(ninf, o);
+    lsum += __shfl_xor(lsum, o);
+    lshort += __shfl_xor(lshort, o);
   }
   const bool wnan = __any(nan);
   if (lane == 0) {
     red[wave] = __builtin_bit_cast(uint32_t, m);
     red[kCredWaves + wave] = (uint32_t)ninf | (wnan ? 0x80000000u : 0u);
+    lstat[wave] = (uint32_t)lsum;
+    lstat[kCredWaves + wave] = (uint32_t)lshort;
     gps[wave] = gsum;
   }
   __syncthreads();
   float mx = 0.0f;
   uint32_t ni = 0u;
   bool anynan = false;
+  int64_t len_sum = 0, short_cnt = 0;
   for (int w = 0; w < kCredWaves; ++w) {
     mx = fmaxf(mx, __builtin_bit_cast(float, red[w]));
     ni += red[kCredWaves + w] & 0x7fffffffu;
     anynan |= (red[kCredWaves + w] >> 31) != 0u;
+    len_sum += lstat[w];
+    short_cnt += lstat[kCredWaves + w];
   }
   const int mode = anynan ? 2 : (ni ? 1 : 0);
   int k = 0;
@@ -1046,7 +1077,7 @@ __global__ void __launch_bounds__(256) rosa_cred_setup_kernel(
   if (threadIdx.x == 0) {
     gp_partial[stream] = ((gps[0] + gps[1]) + gps[2]) + gps[3];
     uint32_t *cw = (uint32_t *)cred;
-    cw[stream * 3 * T] = cred_mode_word(mode, k);
+    cw[stream * 3 * T] = cred_mode_word(mode, k, cred_scan_stream(len_sum, short_cnt, (int)T));
     cw[stream * 3 * T + 1] = ni;
     if (stream < kCredCounters && 3 * T > 3) cw[stream * 3 * T + 3] = 0u;  // a work counter
   }
@@ -1088,73 +1119,107 @@ __device__ __forceinline__ uint32_t ext_key(int c, int e, int cap, int j) {
   return mkkey(min(c + 1 + e, cap), j);
 }
 
-// k flips inside the best candidate's matched run [trunc_lo, trunc_hi], one lane per flip.
-// Flip p touches only candidates j with j - c_j <= p <= j, all within 62 of j*; keys
-// farther away are unchanged (farbest), and near keys outside [p, p + cmax] enter through
-// prefix / suffix maxima of the unchanged near keys. Cn/En hold c_j and e_j of the
-// candidates j in [j* - 63, j* + 64); Pref/Suf are per-wave scratch of kNear words each.
-__device__ __forceinline__ void near_run_flips(int lane, int t, int lmax, int jstar, int trunc_lo,
-                                               int trunc_hi, uint32_t farbest, const uint8_t *Cn,
-                                               const uint8_t *En, uint32_t *Pref, uint32_t *Suf,
-                                               const uint32_t *vw, float sgn, float g, long long gi,
-                                               const CredAcc &ca, int T) {
-  const int near0 = jstar - 63;
-  const int jlo = max(0, jstar - 62), jhi = min(t - 1, jstar + 62);
-  // unchanged near keys, two per lane (r = 2 * lane, 2 * lane + 1), and their max c
-  uint32_t kr[2];
-  int cmax = 0;
+__device__ __forceinline__ void near_flips_tables(int lane, int t, int lmax, int jstar, int trunc_lo,
+                                                  int trunc_hi, uint32_t farbest, uint64_t qwin,
+                                                  const uint32_t *kw, const uint32_t *vw, float sgn,
+                                                  float g, long long gi, const CredAcc &ca, int T,
+                                                  uint32_t *tab);
+
+// The per-candidate path for one position t, all lanes of the wave: every candidate's
+// common-suffix length from its 64-bit window, 64 candidates per step from the latest down,
+// into the bucket tables (Mw: best key per common-suffix bucket, Nw: per bucket after the
+// q flip at the first mismatch) and the k-extension events Rk; the flips inside the best
+// run from near_flips_tables (tab: 256 words). Writes every table it reads first.
+__device__ __forceinline__ void scan_position(int lane, int t, int T, int lmax, uint64_t qwin, uint32_t best,
+                                              int jstar, int cstar, int capstar, float sgn, float g,
+                                              long long gi, const CredAcc &ca, const uint32_t *kw,
+                                              const uint32_t *vw, uint32_t *Mw, uint32_t *Nw, uint32_t *Rk,
+                                              uint32_t *tab) {
+  const int Lstar = key_len(best);
+  // k flips inside the best candidate's matched run, resolved in (b)
+  const int trunc_lo = jstar >= 0 ? jstar - min(cstar, capstar) + 1 : 1;
+  const int trunc_hi = jstar;
+  const int near0 = jstar - 63;  // the near candidates: j in [near0 + 1, near0 + 125]
+
+  Mw[lane] = Nw[lane] = 0u;
+  Rk[lane] = Rk[lane + 64] = 0u;
+  uint32_t farbest = 0u;  // best key among j outside [j* - 62, j* + 62] (this lane's j)
+  int emit_hi = t - 1;    // k positions above emit_hi are done
+
+  // candidates from the latest down: a bucket's best key is its latest j, so the
+  // bucket tables are written only when a key beats the stored one
+  for (int j0 = ((t - 1) / 64) * 64; j0 >= 0; j0 -= 64) {
+    const int j = j0 + lane;
+    if (j < t) {
+      const uint64_t x = qwin ^ q_window(kw, j);
+      const int c = clz64(x);
+      const int cap = min(j + 1, lmax);
+      const uint32_t key = mkkey(min(c, cap), j);
+      const int cb = min(c, 63);
+      if (key > Mw[cb]) atomicMax(Mw + cb, key);
+      const int r = j - near0;
+      if (r < 1 || r > 125) farbest = max(farbest, key);
+      uint32_t nkey = key;  // after flipping the q bit at j's first mismatch
+      int e = 0;
+      if (c < cap) {
+        e = clz64(x << (c + 1));
+        nkey = ext_key(c, e, cap, j);
+        // (a) flipping k[j - c] extends j past the best
+        const int p = j - c;
+        if (nkey > best && !(p >= trunc_lo && p <= trunc_hi)) atomicMax(Rk + (p & 127), nkey);
+      }
+      if (nkey > Nw[cb]) atomicMax(Nw + cb, nkey);
+    }
+    // events of p come from j in [p, p + 61]: every p >= j0 is now complete
+    {
+      const int p = j0 + lane;
+      if (p <= emit_hi) {
+        const uint32_t v = Rk[p & 127];
+        if (v) {
+          Rk[p & 127] = 0u;
+          const float s2 = sign_of(v, vw);
+          if (s2 != sgn) ca.add(T + p, s2 > 0.0f, g, gi);
+        }
+      }
+    }
+    emit_hi = j0 - 1;
+  }
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int r = 2 * lane + h;
-    const int j2 = near0 + r;
-    kr[h] = 0u;
-    if (j2 >= jlo && j2 <= jhi) {
-      const int c2 = Cn[r];
-      kr[h] = mkkey(min(c2, min(j2 + 1, lmax)), j2);
-      cmax = max(cmax, c2);
+  for (int o = 32; o > 0; o >>= 1) farbest = max(farbest, (uint32_t)__shfl_xor((int)farbest, o));
+
+  // v: the endpoint's successor bit
+  if (lane == 0 && Lstar >= 1) ca.add(2 * T + jstar + 1, sgn < 0.0f, g, gi);
+
+  // q: flip of q[t - i], one lane per i in [0, min(L*, lmax - 1)]. Lane c holds bucket c;
+  // g1 = max key over buckets < i (exclusive prefix scan), sj = latest j over buckets > i
+  // (exclusive suffix scan).
+  {
+    const uint32_t mk = Mw[lane];
+    uint32_t pre = mk;
+    int suf = mk ? key_j(mk) : -1;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t a = (uint32_t)__shfl_up((int)pre, d);
+      const int bsj = __shfl_down(suf, d);
+      if (lane >= d) pre = max(pre, a);
+      if (lane + d < 64) suf = max(suf, bsj);
+    }
+    const uint32_t up1 = (uint32_t)__shfl_up((int)pre, 1);  // all lanes active
+    const uint32_t g1 = lane >= 1 ? up1 : 0u;                 // buckets < lane
+    const int sj = __shfl_down(suf, 1);                                      // buckets > lane
+    const int imax = min(min(Lstar, lmax - 1), t);
+    if (lane <= imax) {
+      const int i = lane;
+      uint32_t nb = max(g1, Nw[i]);  // Nw[i]: the candidates with c == i, bit flipped
+      if (lane < 63 && sj >= 0) nb = max(nb, mkkey(min(i, min(sj + 1, lmax)), sj));
+      const float s2 = sign_of(nb, vw);
+      if (s2 != sgn) ca.add(t - i, s2 > 0.0f, g, gi);
     }
   }
-  uint32_t pre = max(kr[0], kr[1]), suf = pre;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t a = (uint32_t)__shfl_up((int)pre, d);
-    const uint32_t bb = (uint32_t)__shfl_down((int)suf, d);
-    const int cm = __shfl_xor(cmax, d);
-    if (lane >= d) pre = max(pre, a);
-    if (lane + d < 64) suf = max(suf, bb);
-    cmax = max(cmax, cm);
-  }
-  // inclusive prefix / suffix max per near index r. The shuffles run with every lane
-  // active: a cross-lane read from a lane masked off by a branch returns 0.
-  const uint32_t up1 = (uint32_t)__shfl_up((int)pre, 1);
-  const uint32_t down1 = (uint32_t)__shfl_down((int)suf, 1);
-  const uint32_t pre_prev = lane >= 1 ? up1 : 0u;
-  const uint32_t suf_next = lane < 63 ? down1 : 0u;
-  Pref[2 * lane] = max(pre_prev, kr[0]);
-  Pref[2 * lane + 1] = pre;
-  Suf[2 * lane] = suf;
-  Suf[2 * lane + 1] = max(suf_next, kr[1]);
-  const int p = trunc_lo + lane;
-  if (p <= trunc_hi) {
-    uint32_t nb = farbest;
-    const int rl = p - 1 - near0;          // near keys left of the flip
-    if (p - 1 >= jlo) nb = max(nb, Pref[rl]);
-    const int jend = min(jhi, p + cmax);   // candidates that can reach k[p]
-    if (jend + 1 <= jhi) nb = max(nb, Suf[jend + 1 - near0]);
-    for (int j2 = p; j2 <= jend; ++j2) {
-      const int r = j2 - near0;
-      const int c2 = Cn[r], e2 = En[r];
-      const int cap2 = min(j2 + 1, lmax);
-      const int d = j2 - p;
-      uint32_t k2;
-      if (d < min(c2, cap2)) k2 = mkkey(d, j2);
-      else if (d == c2 && c2 < cap2) k2 = ext_key(c2, e2, cap2, j2);
-      else k2 = mkkey(min(c2, cap2), j2);
-      nb = max(nb, k2);
-    }
-    const float s2 = sign_of(nb, vw);
-    if (s2 != sgn) ca.add(T + p, s2 - sgn, g, gi);
-  }
+
+  // (b) k flips inside the best candidate's run
+  if (jstar >= 0)
+    near_flips_tables(lane, t, lmax, jstar, trunc_lo, trunc_hi, farbest, qwin, kw, vw, sgn, g, gi, ca, T, tab);
 }
 
 __global__ void __launch_bounds__(256) rosa_credits_kernel(
@@ -1168,8 +1233,7 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   uint32_t *Mw = sm + 3 * W + wave * kCredWave32;
   uint32_t *Nw = Mw + 64, *Rk = Mw + 128;
-  uint8_t *Cn = (uint8_t *)(Mw + 256), *En = Cn + kNear;
-  uint32_t *Pref = Mw + 256 + kNear / 2, *Suf = Pref + kNear;  // near-key prefix/suffix max
+  uint32_t *tab = Mw + 256;
   const int64_t stream = blockIdx.x;
   const int64_t b = stream / S, s = stream % S;
   for (int i = threadIdx.x; i < W; i += 256) {
@@ -1197,95 +1261,7 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
     const float g = gr * pay;
     if (t == 0 || !cred_live(ca, g) || lmax < 1) continue;
     const long long gi = ca.fixed(g);
-    const int Lstar = key_len(best);
-    // k flips inside the best candidate's matched run, resolved in (b)
-    const int trunc_lo = jstar >= 0 ? jstar - min(cstar, capstar) + 1 : 1;
-    const int trunc_hi = jstar;
-    const int near0 = jstar - 63;  // Cn/En hold j in [near0, near0 + kNear)
-
-    Mw[lane] = Nw[lane] = 0u;
-    Rk[lane] = Rk[lane + 64] = 0u;
-    uint32_t farbest = 0u;  // best key among j outside [j* - 62, j* + 62] (this lane's j)
-    int emit_hi = t - 1;    // k positions above emit_hi are done
-
-    // candidates from the latest down: a bucket's best key is its latest j, so the
-    // bucket tables are written only when a key beats the stored one
-    for (int j0 = ((t - 1) / 64) * 64; j0 >= 0; j0 -= 64) {
-      const int j = j0 + lane;
-      if (j < t) {
-        const uint64_t x = qwin ^ q_window(kw, j);
-        const int c = clz64(x);
-        const int cap = min(j + 1, lmax);
-        const uint32_t key = mkkey(min(c, cap), j);
-        const int cb = min(c, 63);
-        if (key > Mw[cb]) atomicMax(Mw + cb, key);
-        const int r = j - near0;
-        if (r < 1 || r > 125) farbest = max(farbest, key);
-        uint32_t nkey = key;  // after flipping the q bit at j's first mismatch
-        int e = 0;
-        if (c < cap) {
-          e = clz64(x << (c + 1));
-          nkey = ext_key(c, e, cap, j);
-          // (a) flipping k[j - c] extends j past the best
-          const int p = j - c;
-          if (nkey > best && !(p >= trunc_lo && p <= trunc_hi)) atomicMax(Rk + (p & 127), nkey);
-        }
-        if (nkey > Nw[cb]) atomicMax(Nw + cb, nkey);
-        if (r >= 0 && r < kNear) {
-          Cn[r] = (uint8_t)c;
-          En[r] = (uint8_t)e;
-        }
-      }
-      // events of p come from j in [p, p + 61]: every p >= j0 is now complete
-      {
-        const int p = j0 + lane;
-        if (p <= emit_hi) {
-          const uint32_t v = Rk[p & 127];
-          if (v) {
-            Rk[p & 127] = 0u;
-            const float s2 = sign_of(v, vw);
-            if (s2 != sgn) ca.add(T + p, s2 - sgn, g, gi);
-          }
-        }
-      }
-      emit_hi = j0 - 1;
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) farbest = max(farbest, (uint32_t)__shfl_xor((int)farbest, o));
-
-    // v: the endpoint's successor bit
-    if (lane == 0 && Lstar >= 1) ca.add(2 * T + jstar + 1, -2.0f * sgn, g, gi);
-
-    // q: flip of q[t - i], one lane per i in [0, min(L*, lmax - 1)]. Lane c holds bucket c;
-    // g1 = max key over buckets < i (exclusive prefix scan), sj = latest j over buckets > i
-    // (exclusive suffix scan).
-    {
-      const uint32_t mk = Mw[lane];
-      uint32_t pre = mk;
-      int suf = mk ? key_j(mk) : -1;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t a = (uint32_t)__shfl_up((int)pre, d);
-        const int bsj = __shfl_down(suf, d);
-        if (lane >= d) pre = max(pre, a);
-        if (lane + d < 64) suf = max(suf, bsj);
-      }
-      const uint32_t up1 = (uint32_t)__shfl_up((int)pre, 1);  // all lanes active
-      const uint32_t g1 = lane >= 1 ? up1 : 0u;                 // buckets < lane
-      const int sj = __shfl_down(suf, 1);                                      // buckets > lane
-      const int imax = min(min(Lstar, lmax - 1), t);
-      if (lane <= imax) {
-        const int i = lane;
-        uint32_t nb = max(g1, Nw[i]);  // Nw[i]: the candidates with c == i, bit flipped
-        if (lane < 63 && sj >= 0) nb = max(nb, mkkey(min(i, min(sj + 1, lmax)), sj));
-        const float s2 = sign_of(nb, vw);
-        if (s2 != sgn) ca.add(t - i, s2 - sgn, g, gi);
-      }
-    }
-
-    // (b) k flips inside the best candidate's run
-    if (jstar >= 0)
-      near_run_flips(lane, t, lmax, jstar, trunc_lo, trunc_hi, farbest, Cn, En, Pref, Suf, vw, sgn, g, gi, ca, T);
+    scan_position(lane, t, T, lmax, qwin, best, jstar, cstar, capstar, sgn, g, gi, ca, kw, vw, Mw, Nw, Rk, tab);
   }
 }
 
@@ -1435,15 +1411,15 @@ __device__ __forceinline__ void near_flips_tables(int lane, int t, int lmax, int
     uint32_t nb = max(max(always, pk), max(su, lf));
     nb = max(nb, mkkey(jt - p, jt));
     const float s2 = sign_of(nb, vw);
-    if (s2 != sgn) ca.add(T + p, s2 - sgn, g, gi);
+    if (s2 != sgn) ca.add(T + p, s2 > 0.0f, g, gi);
   }
 }
 
-__global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) rosa_credits_bp_kernel(
     const uint32_t *__restrict__ qb, const uint32_t *__restrict__ kb, const uint32_t *__restrict__ vb,
     const int32_t *__restrict__ match_j, const float *__restrict__ grad, const float *__restrict__ payload,
     int64_t S, int T, int W, int lmax, const float *__restrict__ cred, unsigned long long *__restrict__ sums,
-    unsigned int *__restrict__ counters, int64_t cstride, int ncount, int nstreams, int nchunks) {
+    unsigned int *__restrict__ counters, int64_t cstride, int ncount, int nstreams, int nchunks, int force) {
   __shared__ __attribute__((aligned(16))) uint32_t wsm[kCredWaves][kBpWave32];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1523,8 +1499,19 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
     const float g = gr * pay;
     if (t == 0 || lmax < 1) continue;
     const long long gi = ca.fixed(g);
+    if (force == 2 || (force == 0 && (ca.scan || t < kScanBelow))) {  // wave-uniform
+      // the per-candidate path, its tables in the event table's first 448 words
+      scan_position(lane, t, T, lmax, qwin, best, jstar, cstar, capstar, sgn, g, gi, ca, kw, vw, evt, Nw,
+                    evt + 64, evt + 192);
+      __builtin_amdgcn_wave_barrier();
+      Nw[lane] = 0u;  // the bit-parallel path expects both tables zero
+#pragma unroll
+      for (int i = 0; i < 7; ++i) evt[64 * i + lane] = 0u;
+      __builtin_amdgcn_wave_barrier();
+      continue;
+    }
     const int Ls = key_len(best);
-    if (lane == 0 && Ls >= 1) ca.add(2 * T + jstar + 1, -2.0f * sgn, g, gi);  // v flips
+    if (lane == 0 && Ls >= 1) ca.add(2 * T + jstar + 1, sgn < 0.0f, g, gi);  // v flips
     const int imax = min(min(Ls, lmax - 1), t);
     const int trunc_lo = jstar >= 0 ? jstar - min(cstar, capstar) + 1 : 1;
     const int trunc_hi = jstar;
@@ -1727,7 +1714,7 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
       const int i = lane;
       const uint32_t nb = ((hasext >> i) & 1ull) ? Nw[i] : (i >= 1 ? mkkey(i, (int)Nw[i]) : 0u);
       const float s2 = sign_of(nb, vw);
-      if (s2 != sgn) ca.add(t - i, s2 - sgn, g, gi);
+      if (s2 != sgn) ca.add(t - i, s2 > 0.0f, g, gi);
     }
     Nw[lane] = 0u;
 
@@ -1754,7 +1741,7 @@ __global__ void __launch_bounds__(256) rosa_credits_bp_kernel(
           if (!(p >= trunc_lo && p <= trunc_hi) && evt_get16(evt, p) == evt_key16(key, c)) {
             evt_clear16(evt, p);
             const float s2 = sign_of(key, vw);
-            if (s2 != sgn) ca.add(T + p, s2 - sgn, g, gi);
+            if (s2 != sgn) ca.add(T + p, s2 > 0.0f, g, gi);
           }
         }
       }
@@ -1835,6 +1822,16 @@ __global__ void __launch_bounds__(256) rosa_payload_grad_kernel(const float *__r
 
 using namespace ksd;
 
+// KSD_ROSA_CREDITS_PATH = "bits" or "scan" makes every position of the balanced kernel take
+// one path (both give identical sums; for tests and measurement); unset or anything else
+// lets each stream's statistics and the position choose.
+static int credits_path_override() {
+  const char *e = getenv("KSD_ROSA_CREDITS_PATH");
+  if (e && !strcmp(e, "bits")) return 1;
+  if (e && !strcmp(e, "scan")) return 2;
+  return 0;
+}
+
 extern "C" int ksd_rosa_credits(const uint32_t *q_bits, const uint32_t *k_bits, const uint32_t *v_bits,
                                 const int32_t *match_j, const float *grad, const float *payload,
                                 int64_t B, int64_t T, int64_t S, int lmax, float *credits,
@@ -1864,7 +1861,8 @@ extern "C" int ksd_rosa_credits(const uint32_t *q_bits, const uint32_t *k_bits, 
       const int nblk = (int)min(cdiv(waves, kCredWaves), (int64_t)cu_count() * kBpBlocksPerCu);
       hipLaunchKernelGGL(rosa_credits_bp_kernel, dim3((unsigned)nblk), dim3(256), 0, st, q_bits, k_bits,
                          v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits, sums,
-                         (unsigned int *)credits + 3, 3 * T, min(n, kCredCounters), n, nchunks);
+                         (unsigned int *)credits + 3, 3 * T, min(n, kCredCounters), n, nchunks,
+                         credits_path_override());
     } else {
       hipLaunchKernelGGL(rosa_credits_kernel, dim3((unsigned)n), dim3(256), lds, st, q_bits, k_bits,
                          v_bits, match_j, grad, payload, S, (int)T, W, lmax, credits, sums);

@@ -277,10 +277,24 @@ def _credits_direct(q, k, v, gsign, lmax=None):
     return cred.cpu().numpy()
 
 
+# The balanced credits kernel has two paths per position (bit-parallel, per-candidate),
+# chosen from each stream's statistics and the position; KSD_ROSA_CREDITS_PATH forces one.
+PATHS = ["bits", "scan", "auto"]
+
+
+def _set_path(monkeypatch, path):
+    if path == "auto":
+        monkeypatch.delenv("KSD_ROSA_CREDITS_PATH", raising=False)
+    else:
+        monkeypatch.setenv("KSD_ROSA_CREDITS_PATH", path)
+
+
+@pytest.mark.parametrize("path", PATHS)
 @pytest.mark.parametrize("T", [256, 300])
-def test_credits_structured_streams_bruteforce(T):
+def test_credits_structured_streams_bruteforce(T, path, monkeypatch):
     """Constant, periodic and varied-density streams (deep chains, buckets resolved by every
-    checkpoint and by their own chain) against the definition, every flip."""
+    checkpoint and by their own chain) against the definition, every flip, on each path."""
+    _set_path(monkeypatch, path)
     rng = np.random.default_rng(1000 + T)
     n = 16
     q = _streams(rng, n, T)
@@ -296,9 +310,11 @@ def test_credits_structured_streams_bruteforce(T):
     assert np.array_equal(got == 0, exp == 0)
 
 
+@pytest.mark.parametrize("path", ["bits", "scan"])
 @pytest.mark.parametrize("lmax", [2, 3, 5, 7])
-def test_credits_explicit_max_match_len_bruteforce(lmax):
+def test_credits_explicit_max_match_len_bruteforce(lmax, path, monkeypatch):
     """Short caps: every flip's re-match under the same cap (the definition) at T = 200."""
+    _set_path(monkeypatch, path)
     T, n = 200, 12
     rng = np.random.default_rng(500 + lmax)
     q = _streams(rng, n, T)
@@ -310,6 +326,40 @@ def test_credits_explicit_max_match_len_bruteforce(lmax):
     scale = np.abs(exp).max() + 1e-30
     np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * scale)
     assert np.array_equal(got == 0, exp == 0)
+
+
+def test_credits_paths_agree_bitwise(monkeypatch):
+    """T = 2048 streams of every kind (random, long runs, constant, periodic, copies of q): the
+    bit-parallel path alone, the per-candidate path alone and the automatic choice (which
+    takes each path on some streams and positions here) give the same bits, exact sums of
+    the same contributions; sampled flips match the definition."""
+    rng = np.random.default_rng(2048)
+    n, T = 24, 2048
+    q = _streams(rng, n, T)
+    runs = [np.cumsum(rng.uniform(size=T) < pr) % 2 for pr in (0.02, 0.05, 0.1, 0.2)]
+    q[12:16] = np.stack(runs).astype(np.uint8)
+    k = np.concatenate([q[:6], _streams(rng, n - 6, T)])
+    k[12:16] = np.stack([np.cumsum(rng.uniform(size=T) < pr) % 2 for pr in (0.02, 0.05, 0.1, 0.2)])
+    k[8] = np.roll(q[8], 5)
+    v = _streams(rng, n, T)
+    gsign = rng.standard_normal((n, T)).astype(np.float32)
+    out = {}
+    for path in PATHS:
+        _set_path(monkeypatch, path)
+        out[path] = _credits_direct(q, k, v, gsign)
+    assert np.array_equal(out["bits"].view(np.uint32), out["scan"].view(np.uint32))
+    assert np.array_equal(out["bits"].view(np.uint32), out["auto"].view(np.uint32))
+    base, _, _ = orr.match(q, k, v)
+    g64 = gsign.astype(np.float64)
+    for s in (0, 3, 8, 12, 14, 20):
+        for which in range(3):
+            for p in rng.choice(T, 6, replace=False):
+                fl = [b[s:s + 1].copy() for b in (q, k, v)]
+                fl[which][0, p] ^= 1
+                sp, _, _ = orr.match(*fl)
+                exp = float(((sp[0] - base[s]) * g64[s]).sum())
+                got = float(out["auto"][s, which, p])
+                assert abs(got - exp) <= 1e-5 * max(1.0, abs(exp)), (s, which, p, got, exp)
 
 
 def test_credits_are_deterministic():
