@@ -976,11 +976,11 @@ constexpr int kCredCounters = 64;  // work counters of the balanced kernel: entr
 // matches with long extension chains. The per-candidate path costs about the same per
 // candidate whatever the stream. Measured per position on random and trained-model
 // streams (T 2048), the per-candidate path is the cheaper one when a stream's mean best
-// length exceeds 14 or more than 40% of its positions have a best length below 8, and at
-// every position below 512 (a scan's cost grows with t, the bit-parallel path's hardly).
-constexpr int kScanBelow = 512;
+// length exceeds 12 or more than 40% of its positions have a best length below 8, and at
+// every position below 768 (a scan's cost grows with t, the bit-parallel path's hardly).
+constexpr int kScanBelow = 768;
 __device__ __forceinline__ bool cred_scan_stream(int64_t len_sum, int64_t short_cnt, int T) {
-  return len_sum > 14 * (int64_t)T || 10 * short_cnt > 4 * (int64_t)T;
+  return len_sum > 12 * (int64_t)T || 10 * short_cnt > 4 * (int64_t)T;
 }
 
 // One block per stream: mode, zeroed sums and d loss / d payload = sum over t of
@@ -1144,25 +1144,37 @@ __device__ __forceinline__ void scan_position(int lane, int t, int T, int lmax, 
   Mw[lane] = Nw[lane] = 0u;
   Rk[lane] = Rk[lane + 64] = 0u;
   uint32_t farbest = 0u;  // best key among j outside [j* - 62, j* + 62] (this lane's j)
-  int emit_hi = t - 1;    // k positions above emit_hi are done
 
-  // candidates from the latest down: a bucket's best key is its latest j, so the
-  // bucket tables are written only when a key beats the stored one
-  for (int j0 = ((t - 1) / 64) * 64; j0 >= 0; j0 -= 64) {
+  // candidates from the latest down, 64 per step (lane l: j = j0 + l): a bucket's best key is
+  // its latest j, so the bucket tables are written only when a key beats the stored one.
+  // The step template flags: TOP, the first step (lanes j >= t idle, events above t - 1
+  // absent), LOW, the step at j0 = 0 (caps min(j + 1, lmax) below lmax). A lane's window
+  // words sit at a fixed offset from j0 / 32 and its funnel shift (j + 1) mod 32 is fixed.
+  const uint32_t *kwl = kw + ((lane + 1) >> 5);
+  const int sh = (lane + 1) & 31;
+  auto cand_step = [&](int j0, auto top_c, auto low_c) __attribute__((always_inline)) {
+    constexpr bool TOP = decltype(top_c)::value, LOW = decltype(low_c)::value;
     const int j = j0 + lane;
-    if (j < t) {
-      const uint64_t x = qwin ^ q_window(kw, j);
+    const bool near_step = j0 + 63 > near0 && j0 < near0 + 126;  // wave-uniform
+    if (!TOP || j < t) {
+      const uint32_t *kp = kwl + (j0 >> 5);  // words j0 / 32 + (lane + 1) / 32 - 2 ..
+      const uint32_t wa = kp[-2], wb = kp[-1], wc = kp[0];
+      const uint64_t kwin = ((uint64_t)__builtin_amdgcn_alignbit(wc, wb, sh) << 32) |
+                            __builtin_amdgcn_alignbit(wb, wa, sh);
+      const uint64_t x = qwin ^ kwin;
       const int c = clz64(x);
-      const int cap = min(j + 1, lmax);
+      const int cap = LOW ? min(j + 1, lmax) : lmax;  // j >= 64 > lmax - 1 above the last step
       const uint32_t key = mkkey(min(c, cap), j);
       const int cb = min(c, 63);
       if (key > Mw[cb]) atomicMax(Mw + cb, key);
-      const int r = j - near0;
-      if (r < 1 || r > 125) farbest = max(farbest, key);
+      if (near_step) {
+        if ((unsigned)(j - near0 - 1) > 124u) farbest = max(farbest, key);
+      } else {
+        farbest = max(farbest, key);
+      }
       uint32_t nkey = key;  // after flipping the q bit at j's first mismatch
-      int e = 0;
       if (c < cap) {
-        e = clz64(x << (c + 1));
+        const int e = clz64(x << (c + 1));
         nkey = ext_key(c, e, cap, j);
         // (a) flipping k[j - c] extends j past the best
         const int p = j - c;
@@ -1170,10 +1182,10 @@ __device__ __forceinline__ void scan_position(int lane, int t, int T, int lmax, 
       }
       if (nkey > Nw[cb]) atomicMax(Nw + cb, nkey);
     }
-    // events of p come from j in [p, p + 61]: every p >= j0 is now complete
+    // events of p come from j in [p, p + 61]: every p >= j0 is now complete (below t)
     {
       const int p = j0 + lane;
-      if (p <= emit_hi) {
+      if (!TOP || p < t) {
         const uint32_t v = Rk[p & 127];
         if (v) {
           Rk[p & 127] = 0u;
@@ -1182,7 +1194,14 @@ __device__ __forceinline__ void scan_position(int lane, int t, int T, int lmax, 
         }
       }
     }
-    emit_hi = j0 - 1;
+  };
+  const int jtop = ((t - 1) / 64) * 64;
+  if (jtop == 0) {
+    cand_step(0, std::true_type{}, std::true_type{});
+  } else {
+    cand_step(jtop, std::true_type{}, std::false_type{});
+    for (int j0 = jtop - 64; j0 >= 64; j0 -= 64) cand_step(j0, std::false_type{}, std::false_type{});
+    cand_step(0, std::false_type{}, std::true_type{});
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) farbest = max(farbest, (uint32_t)__shfl_xor((int)farbest, o));
@@ -1228,14 +1247,17 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
     int64_t S, int T, int W, int lmax, const float *__restrict__ cred,
     unsigned long long *__restrict__ sums) {
   extern __shared__ uint32_t sm[];
-  uint32_t *qw = sm, *kw = sm + W, *vw = sm + 2 * W;
+  // four zero words before kw: the scan's window loads read kw[-2] and kw[-1] as the
+  // positions before 0
+  uint32_t *kw = sm + 4, *qw = kw + W, *vw = qw + W;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint32_t *Mw = sm + 3 * W + wave * kCredWave32;
+  uint32_t *Mw = sm + 4 + 3 * W + wave * kCredWave32;
   uint32_t *Nw = Mw + 64, *Rk = Mw + 128;
   uint32_t *tab = Mw + 256;
   const int64_t stream = blockIdx.x;
   const int64_t b = stream / S, s = stream % S;
+  if (threadIdx.x < 4) sm[threadIdx.x] = 0u;
   for (int i = threadIdx.x; i < W; i += 256) {
     qw[i] = qb[stream * W + i];
     kw[i] = kb[stream * W + i];
@@ -1415,7 +1437,7 @@ __device__ __forceinline__ void near_flips_tables(int lane, int t, int lmax, int
   }
 }
 
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) rosa_credits_bp_kernel(
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) rosa_credits_bp_kernel(
     const uint32_t *__restrict__ qb, const uint32_t *__restrict__ kb, const uint32_t *__restrict__ vb,
     const int32_t *__restrict__ match_j, const float *__restrict__ grad, const float *__restrict__ payload,
     int64_t S, int T, int W, int lmax, const float *__restrict__ cred, unsigned long long *__restrict__ sums,
@@ -1425,9 +1447,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) r
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // [64] per bucket i: the best lifted key when the bucket has members (hasext bit i),
   // else the latest j of A_i; the two never meet in one bucket
+  // per wave: Nw [64], the item's q and v words [64 each], evt, the item's k words [64]
+  // (after evt, whose last words are zero whenever the per-candidate path runs: the scan's
+  // window loads read kw[-2] and kw[-1] as the positions before 0)
   uint32_t *Nw = wsm[wave];
-  uint32_t *qw = Nw + 64, *kw = qw + 64, *vw = kw + 64;  // [64] each: the item's stream
-  uint32_t *evt = Nw + 256;                       // [kBpMaxT] 16-bit event entries per flip p
+  uint32_t *qw = Nw + 64, *vw = qw + 64;
+  uint32_t *evt = Nw + 192;                       // [kBpMaxT] 16-bit event entries per flip p
+  uint32_t *kw = evt + kBpMaxT / 2;
   uint32_t *ntab = evt;                           // [256] near-flip tables (aliasing evt)
   for (int i = lane; i < 64; i += 64) Nw[i] = 0u;
   for (int i = lane; i < kBpMaxT / 2; i += 64) evt[i] = 0u;
@@ -1844,7 +1870,7 @@ extern "C" int ksd_rosa_credits(const uint32_t *q_bits, const uint32_t *k_bits, 
     return fail(KSD_EINVAL, "rosa_credits: null pointer");
   if (!credit_sums) return fail(KSD_EINVAL, "rosa_credits: credit_sums workspace is required");
   const int W = (int)cdiv(T, 32);
-  const size_t lds = (3 * (size_t)W + kCredWaves * (size_t)kCredWave32) * sizeof(uint32_t);
+  const size_t lds = (4 + 3 * (size_t)W + kCredWaves * (size_t)kCredWave32) * sizeof(uint32_t);
   if (lds > 64 * 1024) return fail(KSD_EINVAL, "rosa_credits: T too large for LDS");
   if (B * S > 0x7fffffff || B * S * cdiv(T, kCredChunk) > 0x7fffffff)
     return fail(KSD_EINVAL, "rosa_credits: too many streams");
