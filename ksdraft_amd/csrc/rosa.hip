@@ -1124,6 +1124,7 @@ __device__ __forceinline__ void near_flips_tables(int lane, int t, int lmax, int
                                                   const uint32_t *kw, const uint32_t *vw, float sgn,
                                                   float g, long long gi, const CredAcc &ca, int T,
                                                   uint32_t *tab);
+__device__ __forceinline__ uint32_t wave_prefix_max(uint32_t v);
 
 // The per-candidate path for one position t, all lanes of the wave: every candidate's
 // common-suffix length from its 64-bit window, 64 candidates per step from the latest down,
@@ -1203,8 +1204,7 @@ __device__ __forceinline__ void scan_position(int lane, int t, int T, int lmax, 
     for (int j0 = jtop - 64; j0 >= 64; j0 -= 64) cand_step(j0, std::false_type{}, std::false_type{});
     cand_step(0, std::false_type{}, std::true_type{});
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) farbest = max(farbest, (uint32_t)__shfl_xor((int)farbest, o));
+  // (farbest stays per lane: near_flips_tables takes the wave maximum of its own terms)
 
   // v: the endpoint's successor bit
   if (lane == 0 && Lstar >= 1) ca.add(2 * T + jstar + 1, sgn < 0.0f, g, gi);
@@ -1213,19 +1213,11 @@ __device__ __forceinline__ void scan_position(int lane, int t, int T, int lmax, 
   // g1 = max key over buckets < i (exclusive prefix scan), sj = latest j over buckets > i
   // (exclusive suffix scan).
   {
-    const uint32_t mk = Mw[lane];
-    uint32_t pre = mk;
-    int suf = mk ? key_j(mk) : -1;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint32_t a = (uint32_t)__shfl_up((int)pre, d);
-      const int bsj = __shfl_down(suf, d);
-      if (lane >= d) pre = max(pre, a);
-      if (lane + d < 64) suf = max(suf, bsj);
-    }
-    const uint32_t up1 = (uint32_t)__shfl_up((int)pre, 1);  // all lanes active
-    const uint32_t g1 = lane >= 1 ? up1 : 0u;                 // buckets < lane
-    const int sj = __shfl_down(suf, 1);                                      // buckets > lane
+    // DPP prefix maxima; the suffix one over the reversed table, turned back by one shuffle
+    // (j + 1 is a key's low half, 0 for an empty bucket)
+    const uint32_t g1 = wave_prefix_max(lane >= 1 ? Mw[lane - 1] : 0u);  // buckets < lane
+    const uint32_t sr = wave_prefix_max(lane >= 1 ? (Mw[64 - lane] & 0xffffu) : 0u);
+    const int sj = (int)(uint32_t)__shfl((int)sr, 63 - lane) - 1;        // buckets > lane
     const int imax = min(min(Lstar, lmax - 1), t);
     if (lane <= imax) {
       const int i = lane;
@@ -1502,17 +1494,18 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) r
     const uint32_t k0 = kw[lane], k1 = lane >= 1 ? kw[lane - 1] : 0u, k2 = lane >= 2 ? kw[lane - 2] : 0u;
     const uint64_t k01 = ((uint64_t)k0 << 32) | k1, k12 = ((uint64_t)k1 << 32) | k2;
     const float pay = payload[s];
-    // the chunk's positions: the lanes load their gradients together and only the positions
+    // the chunk's positions: the lanes load their gradients and endpoints together, and only the positions
     // the stream's mode visits are walked
     const int tl = chunk * kCredChunk + lane;
     const float grl = lane < kCredChunk && tl < T ? grad[(b * T + tl) * S + s] : 0.0f;
+    const int mjl = lane < kCredChunk && tl < T ? match_j[stream * T + tl] : -1;
     uint64_t live = __ballot(lane < kCredChunk && tl < T && cred_live(ca, grl * pay));
     while (live) {  // wave-uniform
     const int li = __builtin_ctzll(live);
     live &= live - 1;
     const int t = chunk * kCredChunk + li;
     const float gr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, grl), li));
-    const int jstar = match_j[stream * T + t];
+    const int jstar = __builtin_amdgcn_readlane(mjl, li);
     const uint64_t qwin = q_window(qw, t);
     uint32_t best = 0u;
     int cstar = 0, capstar = 0;
