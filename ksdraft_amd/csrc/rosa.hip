@@ -901,13 +901,14 @@ __device__ __forceinline__ float sign_of(uint32_t key, const uint32_t *vw) {
 
 
 // Per-candidate path (scan_position): the 64 lanes of a wave split the candidates j of one
-// position t. Per-wave LDS tables for the current t:
-//   Mw[64]   best key per common-suffix bucket c (c >= 63 pooled)
-//   Nw[64]   best key per bucket after flipping the q bit at the first mismatch
+// position t. Per-wave LDS tables for the current t (kScanMw .. words from the base):
+//   Mw[65]   best key per common-suffix length c = 0 .. 64
+//   Nw[65]   best key per c after flipping the q bit at the first mismatch
 //   Rk[128]  k-extension events, slot p mod 128: the best lifted key of flip k[p]
 //   tab[256] the near-run flip tables (near_flips_tables)
 constexpr int kCredWaves = 4;
-constexpr int kCredWave32 = 64 + 64 + 128 + 256;  // uint32 words per wave
+constexpr int kScanMw = 0, kScanNw = 72, kScanRk = 144, kScanTab = 272;
+constexpr int kCredWave32 = kScanTab + 256;  // uint32 words per wave
 
 // Credit sums. A call runs three kernels: rosa_cred_setup_kernel (per stream: the mode
 // below, zeroed sums, d loss / d payload), one of the credit kernels (contributions only,
@@ -1143,6 +1144,7 @@ __device__ __forceinline__ void scan_position(int lane, int t, int T, int lmax, 
   const int near0 = jstar - 63;  // the near candidates: j in [near0 + 1, near0 + 125]
 
   Mw[lane] = Nw[lane] = 0u;
+  if (lane == 0) Mw[64] = Nw[64] = 0u;
   Rk[lane] = Rk[lane + 64] = 0u;
   uint32_t farbest = 0u;  // best key among j outside [j* - 62, j* + 62] (this lane's j)
 
@@ -1166,8 +1168,7 @@ __device__ __forceinline__ void scan_position(int lane, int t, int T, int lmax, 
       const int c = clz64(x);
       const int cap = LOW ? min(j + 1, lmax) : lmax;  // j >= 64 > lmax - 1 above the last step
       const uint32_t key = mkkey(min(c, cap), j);
-      const int cb = min(c, 63);
-      if (key > Mw[cb]) atomicMax(Mw + cb, key);
+      if (key > Mw[c]) atomicMax(Mw + c, key);
       if (near_step) {
         if ((unsigned)(j - near0 - 1) > 124u) farbest = max(farbest, key);
       } else {
@@ -1175,21 +1176,22 @@ __device__ __forceinline__ void scan_position(int lane, int t, int T, int lmax, 
       }
       uint32_t nkey = key;  // after flipping the q bit at j's first mismatch
       if (c < cap) {
-        const int e = clz64(x << (c + 1));
-        nkey = ext_key(c, e, cap, j);
+        // c + 1 + e: the common suffix once the first mismatch (x's top set bit) is gone
+        nkey = mkkey(min(clz64(x ^ (0x8000000000000000ull >> c)), cap), j);
         // (a) flipping k[j - c] extends j past the best
         const int p = j - c;
         if (nkey > best && !(p >= trunc_lo && p <= trunc_hi)) atomicMax(Rk + (p & 127), nkey);
       }
-      if (nkey > Nw[cb]) atomicMax(Nw + cb, nkey);
+      if (nkey > Nw[c]) atomicMax(Nw + c, nkey);
     }
     // events of p come from j in [p, p + 61]: every p >= j0 is now complete (below t)
     {
       const int p = j0 + lane;
       if (!TOP || p < t) {
-        const uint32_t v = Rk[p & 127];
+        uint32_t *slot = Rk + (j0 & 64) + lane;  // slot p mod 128 (j0 is a multiple of 64)
+        const uint32_t v = *slot;
         if (v) {
-          Rk[p & 127] = 0u;
+          *slot = 0u;
           const float s2 = sign_of(v, vw);
           if (s2 != sgn) ca.add(T + p, s2 > 0.0f, g, gi);
         }
@@ -1215,8 +1217,10 @@ __device__ __forceinline__ void scan_position(int lane, int t, int T, int lmax, 
   {
     // DPP prefix maxima; the suffix one over the reversed table, turned back by one shuffle
     // (j + 1 is a key's low half, 0 for an empty bucket)
+    // buckets 63 and 64 pooled: a q flip at offset i <= 62 only asks for c < i or c > i
     const uint32_t g1 = wave_prefix_max(lane >= 1 ? Mw[lane - 1] : 0u);  // buckets < lane
-    const uint32_t sr = wave_prefix_max(lane >= 1 ? (Mw[64 - lane] & 0xffffu) : 0u);
+    const uint32_t mr = lane == 1 ? max(Mw[63], Mw[64]) : Mw[64 - lane];
+    const uint32_t sr = wave_prefix_max(lane >= 1 ? (mr & 0xffffu) : 0u);
     const int sj = (int)(uint32_t)__shfl((int)sr, 63 - lane) - 1;        // buckets > lane
     const int imax = min(min(Lstar, lmax - 1), t);
     if (lane <= imax) {
@@ -1244,9 +1248,9 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
   uint32_t *kw = sm + 4, *qw = kw + W, *vw = qw + W;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  uint32_t *Mw = sm + 4 + 3 * W + wave * kCredWave32;
-  uint32_t *Nw = Mw + 64, *Rk = Mw + 128;
-  uint32_t *tab = Mw + 256;
+  uint32_t *Mw = sm + 4 + 3 * W + wave * kCredWave32 + kScanMw;
+  uint32_t *Nw = Mw + kScanNw, *Rk = Mw + kScanRk;
+  uint32_t *tab = Mw + kScanTab;
   const int64_t stream = blockIdx.x;
   const int64_t b = stream / S, s = stream % S;
   if (threadIdx.x < 4) sm[threadIdx.x] = 0u;
@@ -1310,7 +1314,10 @@ __global__ void __launch_bounds__(256) rosa_credits_kernel(
 constexpr int kBpMaxT = 2048;
 constexpr int kCredChunk = 16;        // positions per work item
 constexpr int kBpWave32 = 64 + 3 * 64 + kBpMaxT / 2;  // u32 words per wave
-constexpr int kBpBlocksPerCu = 8;     // 20 KB of LDS per block: 8 blocks fill a CU's 160 KB
+constexpr int kBpBlocksPerCu = 8;
+// the per-candidate path's tables and their clearing stay below the event table's last
+// two words, which the k words' window loads read as zero
+static_assert(64 * ((kCredWave32 + 63) / 64) <= kBpMaxT / 2 - 2, "scan tables overlap kw[-2..-1]");     // 20 KB of LDS per block: 8 blocks fill a CU's 160 KB
 
 __device__ __forceinline__ uint32_t evt_key16(uint32_t key, int c) {
   return ((uint32_t)key_len(key) << 6) | (uint32_t)c;
@@ -1519,13 +1526,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) r
     if (t == 0 || lmax < 1) continue;
     const long long gi = ca.fixed(g);
     if (force == 2 || (force == 0 && (ca.scan || t < kScanBelow))) {  // wave-uniform
-      // the per-candidate path, its tables in the event table's first 448 words
-      scan_position(lane, t, T, lmax, qwin, best, jstar, cstar, capstar, sgn, g, gi, ca, kw, vw, evt, Nw,
-                    evt + 64, evt + 192);
+      // the per-candidate path, its tables in the event table's first kCredWave32 words
+      scan_position(lane, t, T, lmax, qwin, best, jstar, cstar, capstar, sgn, g, gi, ca, kw, vw,
+                    evt + kScanMw, evt + kScanNw, evt + kScanRk, evt + kScanTab);
       __builtin_amdgcn_wave_barrier();
-      Nw[lane] = 0u;  // the bit-parallel path expects both tables zero
 #pragma unroll
-      for (int i = 0; i < 7; ++i) evt[64 * i + lane] = 0u;
+      for (int i = 0; i < (kCredWave32 + 63) / 64; ++i) evt[64 * i + lane] = 0u;  // the bit-parallel path expects zeros
       __builtin_amdgcn_wave_barrier();
       continue;
     }
