@@ -187,6 +187,27 @@ int ksd_adamw_requant(float *param, const float *grad, float *exp_avg, float *ex
                       uint16_t *scales, void *stream);
 
 /*
+ * ksd_adamw_requant over many masters in a few launches (the optimizer step of a whole
+ * model: torch's foreach AdamW over a parameter group, reference ksdraft/train/__init__.py:
+ * 114-116, 166). Each entry is one master with its own step scalars; the shared scalars
+ * and clip_coef are those of ksd_adamw_requant. Results equal n ksd_adamw_requant calls.
+ * The list is read during the call only. No reference counterpart as one call.
+ */
+typedef struct KsdAdamTensor {
+  float *param;
+  const float *grad;
+  float *exp_avg;
+  float *exp_avg_sq;
+  int8_t *codes;    /* (rows, K) int8, or NULL (no repack; scales NULL too) */
+  uint16_t *scales; /* (rows, ceil(K/128)) fp16 */
+  int64_t rows, K;
+  float step_size, bias_correction2_sqrt;
+} KsdAdamTensor;
+int ksd_adamw_requant_multi(const KsdAdamTensor *tensors, int n, const float *clip_coef, float decay,
+                            float one_minus_beta1, float beta2, float one_minus_beta2, float eps,
+                            int group, void *stream);
+
+/*
  * LayerNorm forward fused with the GS128 quantization of its output: the pre-norm of
  * every block (reference ksdraft/model/block.py:27-41, nn.LayerNorm ln_attn / ln_ffn)
  * followed by the Int8Linear A-operand quantization (ksdraft/kernels/linear.py:69,

@@ -622,15 +622,15 @@ struct AdamArgs {
   float bc2_sqrt;   // (1 - beta2^step)^0.5
 };
 
-// A group of 128 consecutive elements of a row per 16 lanes, 8 per lane. VEC: K % 8 == 0
-// and 16-byte aligned buffers, so a lane's 8 elements are all in range or all out.
+// A group of 128 consecutive elements of a row per 16 lanes, 8 per lane (gid: the
+// (row, group) index of this thread's 16 lanes). VEC: K % 8 == 0 and 16-byte aligned
+// buffers, so a lane's 8 elements are all in range or all out.
 template <bool VEC>
-__global__ __launch_bounds__(256) void adamw_requant_kernel(
+__device__ __forceinline__ void adamw_group(
     float *__restrict__ p, const float *__restrict__ g, float *__restrict__ m, float *__restrict__ v,
-    int64_t rows, int64_t K, int64_t ng, const float *__restrict__ clip, AdamArgs a,
-    int8_t *__restrict__ codes, uint16_t *__restrict__ scales) {
-  const int64_t gid = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);  // (row, group): 16 lanes
-  if (gid >= rows * ng) return;                                      // uniform per 16 lanes
+    int64_t rows, int64_t K, int64_t ng, const float *__restrict__ clip, const AdamArgs &a,
+    int8_t *__restrict__ codes, uint16_t *__restrict__ scales, int64_t gid) {
+  if (gid >= rows * ng) return;  // uniform per 16 lanes
   const int sub = threadIdx.x & 15;
   const int64_t row = gid / ng, grp = gid % ng, col = grp * 128 + sub * 8;
   const int64_t base = row * K + col;
@@ -707,6 +707,52 @@ __global__ __launch_bounds__(256) void adamw_requant_kernel(
     for (int i = 0; i < 8; ++i)
       if (ok[i]) codes[base + i] = (int8_t)(w[i >> 2] >> (8 * (i & 3)));
   }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void adamw_requant_kernel(
+    float *__restrict__ p, const float *__restrict__ g, float *__restrict__ m, float *__restrict__ v,
+    int64_t rows, int64_t K, int64_t ng, const float *__restrict__ clip, AdamArgs a,
+    int8_t *__restrict__ codes, uint16_t *__restrict__ scales) {
+  adamw_group<VEC>(p, g, m, v, rows, K, ng, clip, a, codes, scales,
+                   (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4));
+}
+
+// Many masters in one launch: the optimizer step of a whole model is a few launches instead
+// of one per parameter (each launch costs the host tens of microseconds). A batch travels
+// by value in the kernel arguments; a block finds its master from the prefix of block
+// counts with scalar compares.
+constexpr int kAdamBatch = 24;
+struct AdamTensorArg {
+  float *p;
+  const float *g;
+  float *m, *v;
+  int8_t *codes;
+  uint16_t *scales;
+  int64_t rows, K, ng;
+  float step_size, bc2_sqrt;
+  int32_t first_block, vec;
+};
+struct AdamBatchArg {
+  AdamTensorArg t[kAdamBatch];
+  int32_t n;
+};
+
+__global__ __launch_bounds__(256) void adamw_requant_multi_kernel(const AdamBatchArg b,
+                                                                 const float *__restrict__ clip,
+                                                                 AdamArgs shared) {
+  int i = 0;
+  for (int k = 1; k < b.n; ++k)
+    if (b.t[k].first_block <= (int)blockIdx.x) i = k;
+  const AdamTensorArg &t = b.t[i];
+  AdamArgs a = shared;
+  a.step_size = t.step_size;
+  a.bc2_sqrt = t.bc2_sqrt;
+  const int64_t gid = (int64_t)((int)blockIdx.x - t.first_block) * 16 + (threadIdx.x >> 4);
+  if (t.vec)
+    adamw_group<true>(t.p, t.g, t.m, t.v, t.rows, t.K, t.ng, clip, a, t.codes, t.scales, gid);
+  else
+    adamw_group<false>(t.p, t.g, t.m, t.v, t.rows, t.K, t.ng, clip, a, t.codes, t.scales, gid);
 }
 
 template <int SRC>
@@ -1194,6 +1240,56 @@ extern "C" int ksd_adamw_requant(float *param, const float *grad, float *exp_avg
     adamw_requant_kernel<false><<<(unsigned)blocks, 256, 0, st>>>(param, grad, exp_avg, exp_avg_sq, rows, K, ng,
                                                                   clip_coef, a, codes, scales);
   return check_launch("adamw_requant");
+}
+
+extern "C" int ksd_adamw_requant_multi(const KsdAdamTensor *tensors, int n, const float *clip_coef,
+                                       float decay, float one_minus_beta1, float beta2,
+                                       float one_minus_beta2, float eps, int group, void *stream) {
+  if (group != 128) return fail(KSD_EINVAL, "adamw_requant_multi: group must be 128, got %d", group);
+  if (n < 0 || (n > 0 && !tensors)) return fail(KSD_EINVAL, "adamw_requant_multi: bad tensor list");
+  auto al = [](const void *q, uintptr_t a) { return ((uintptr_t)q) % a == 0; };
+  for (int i = 0; i < n; ++i) {
+    const KsdAdamTensor &t = tensors[i];
+    if (t.rows < 0 || t.K < 0) return fail(KSD_EINVAL, "adamw_requant_multi: tensor %d: negative shape", i);
+    if (t.rows == 0 || t.K == 0) continue;
+    if (!t.param || !t.grad || !t.exp_avg || !t.exp_avg_sq)
+      return fail(KSD_EINVAL, "adamw_requant_multi: tensor %d: null pointer", i);
+    if ((t.codes == nullptr) != (t.scales == nullptr))
+      return fail(KSD_EINVAL, "adamw_requant_multi: tensor %d: codes and scales go together", i);
+    if (cdiv(t.rows * cdiv(t.K, 128), 16) > 0x3fffffffLL)
+      return fail(KSD_EINVAL, "adamw_requant_multi: tensor %d too large", i);
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const AdamArgs shared{decay, one_minus_beta1, beta2, one_minus_beta2, eps, 0.0f, 0.0f};
+  AdamBatchArg b;
+  b.n = 0;
+  int64_t blocks = 0;
+  auto flush = [&]() -> int {
+    if (b.n == 0) return KSD_OK;
+    adamw_requant_multi_kernel<<<(unsigned)blocks, 256, 0, st>>>(b, clip_coef, shared);
+    b.n = 0;
+    blocks = 0;
+    return check_launch("adamw_requant_multi");
+  };
+  for (int i = 0; i < n; ++i) {
+    const KsdAdamTensor &t = tensors[i];
+    if (t.rows == 0 || t.K == 0) continue;
+    const int64_t ng = cdiv(t.K, 128), nb = cdiv(t.rows * ng, 16);
+    if (b.n == kAdamBatch || blocks + nb > 0x7fffffffLL) {
+      const int rc = flush();
+      if (rc) return rc;
+    }
+    AdamTensorArg &a = b.t[b.n++];
+    a.p = t.param, a.g = t.grad, a.m = t.exp_avg, a.v = t.exp_avg_sq;
+    a.codes = t.codes, a.scales = t.scales;
+    a.rows = t.rows, a.K = t.K, a.ng = ng;
+    a.step_size = t.step_size, a.bc2_sqrt = t.bias_correction2_sqrt;
+    a.first_block = (int32_t)blocks;
+    a.vec = t.K % 8 == 0 && al(t.param, 16) && al(t.grad, 16) && al(t.exp_avg, 16) &&
+            al(t.exp_avg_sq, 16) && (t.codes == nullptr || al(t.codes, 8));
+    blocks += nb;
+  }
+  return flush();
 }
 
 extern "C" int ksd_layernorm_quant(const void *x, int x_dtype, int64_t rows, int64_t d,

@@ -186,6 +186,60 @@ def adamw_requant_(param: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tenso
     return None if codes is None else (codes, scales)
 
 
+# KsdAdamTensor of the C ABI: six pointers, rows and K, the two per-master step scalars
+_ADAM_TENSOR = None
+
+
+def _adam_tensor_dtype():
+    global _ADAM_TENSOR
+    if _ADAM_TENSOR is None:
+        import numpy as np
+        _ADAM_TENSOR = np.dtype([("param", "<u8"), ("grad", "<u8"), ("exp_avg", "<u8"),
+                                 ("exp_avg_sq", "<u8"), ("codes", "<u8"), ("scales", "<u8"),
+                                 ("rows", "<i8"), ("K", "<i8"), ("step_size", "<f4"),
+                                 ("bc2_sqrt", "<f4")])
+        assert _ADAM_TENSOR.itemsize == 72
+    return _ADAM_TENSOR
+
+
+def adamw_requant_multi_(items, lr: float, betas=(0.9, 0.999), eps: float = 1e-8,
+                         weight_decay: float = 1e-2, clip_coef: torch.Tensor | None = None,
+                         group: int = GROUP_SIZE):
+    """adamw_requant_ over many masters in a few launches (ksd_adamw_requant_multi).
+
+    items: (param, grad, exp_avg, exp_avg_sq, step, quantize) per master, all fp32,
+    contiguous, on one device; step is that master's incremented step count. Returns one
+    (codes, scales) or None per item, as adamw_requant_ would."""
+    import numpy as np
+    if not items:
+        return []
+    if group != GROUP_SIZE:
+        raise ValueError(f"adamw_requant_multi_ supports group {GROUP_SIZE} only")
+    dev = _lib.require_gpu(*[t for it in items for t in it[:4]], clip_coef)
+    beta1, beta2 = betas
+    arr = np.zeros(len(items), dtype=_adam_tensor_dtype())
+    out = []
+    for i, (param, grad, exp_avg, exp_avg_sq, step, quantize) in enumerate(items):
+        for name, t in (("param", param), ("grad", grad), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
+            if t.dtype != torch.float32 or not t.is_contiguous() or t.shape != param.shape:
+                raise ValueError(f"adamw_requant_multi_: {name} of item {i} must be a contiguous "
+                                 f"float32 tensor of the param's shape")
+        K = param.shape[-1] if param.dim() >= 1 else 1
+        rows = param.numel() // max(K, 1)
+        codes = scales = None
+        if quantize:
+            codes = torch.empty(param.shape, dtype=torch.int8, device=dev)
+            scales = torch.empty((*param.shape[:-1], -(-K // group)), dtype=SCALE_DTYPE, device=dev)
+        out.append(None if codes is None else (codes, scales))
+        arr[i] = (param.data_ptr(), grad.data_ptr(), exp_avg.data_ptr(), exp_avg_sq.data_ptr(),
+                  0 if codes is None else codes.data_ptr(), 0 if scales is None else scales.data_ptr(),
+                  rows, K, lr / (1 - beta1 ** step), (1 - beta2 ** step) ** 0.5)
+    cc = None if clip_coef is None else clip_coef.to(dtype=torch.float32).reshape(1).contiguous()
+    _lib.call("ksd_adamw_requant_multi", arr.ctypes.data, len(items), 0 if cc is None else cc.data_ptr(),
+              1 - lr * weight_decay, 1 - beta1, beta2, 1 - beta2, eps, group, _lib.stream_ptr(dev))
+    return out
+
+
 class AdamWRequant(torch.optim.Optimizer):
     """torch.optim.AdamW (the optimizer of reference ksdraft/train/__init__.py:114-116,
     amsgrad off) whose step also repacks int8 weights.
@@ -224,10 +278,11 @@ class AdamWRequant(torch.optim.Optimizer):
 
     @torch.no_grad()
     def step(self, closure=None, clip_coef: torch.Tensor | None = None):
-        """One AdamW step. Registered Int8Linear masters go through the fused update +
-        int8 repack kernel, one launch each (clip_coef applied on load); every other
-        parameter goes through torch's own multi-tensor AdamW (torch.optim.adamw with
-        foreach), after one multi-tensor multiply by clip_coef, as clip_grad_norm_ does."""
+        """One AdamW step. Registered Int8Linear masters and the other large fp32 parameters
+        go through the fused update (+ int8 repack for the registered ones) kernel, a few
+        launches for the whole group (clip_coef applied on load); every other parameter
+        goes through torch's own multi-tensor AdamW (torch.optim.adamw with foreach), after
+        one multi-tensor multiply by clip_coef, as clip_grad_norm_ does."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
@@ -235,6 +290,7 @@ class AdamWRequant(torch.optim.Optimizer):
         from torch.optim.adamw import adamw as torch_adamw
         for group in self.param_groups:
             fl = ([], [], [], [], [])  # params, grads, exp_avg, exp_avg_sq, steps
+            fused, regs = [], []
             for p in group["params"]:
                 if p.grad is None:
                     continue
@@ -255,10 +311,11 @@ class AdamWRequant(torch.optim.Optimizer):
                 n += 1
                 self._steps[id(p)] = n
                 st["step"].fill_(float(n))  # torch's AdamW state layout: a CPU scalar tensor
-                res = adamw_requant_(p, p.grad.contiguous(), st["exp_avg"], st["exp_avg_sq"],
-                                     n, group["lr"], group["betas"],
-                                     group["eps"], group["weight_decay"], clip_coef,
-                                     quantize=reg is not None)
+                fused.append((p, p.grad.contiguous(), st["exp_avg"], st["exp_avg_sq"], n, reg is not None))
+                regs.append(reg)
+            results = adamw_requant_multi_(fused, group["lr"], group["betas"], group["eps"],
+                                           group["weight_decay"], clip_coef)
+            for (p, *_), reg, res in zip(fused, regs, results):
                 if reg is None:
                     continue
                 # the codes now belong to the master as it is

@@ -55,6 +55,44 @@ def test_adamw_requant_matches_torch(shape, wd, clip):
         _codes_match(p, res)
 
 
+@pytest.mark.parametrize("clip", [None, 0.7])
+def test_adamw_requant_multi_equals_one_call_per_master(clip):
+    """ksd_adamw_requant_multi over 60 masters (more than one launch batch: ragged K, 1-D
+    and 3-D shapes, with and without the int8 repack, different step counts, misaligned
+    views) gives the bits of one ksd_adamw_requant call per master."""
+    g = torch.Generator().manual_seed(11 if clip is None else 12)
+    shapes = [(256, 384), (130, 200), (1536,), (7, 13), (3, 5, 136), (64, 1000), (1, 1)] * 8
+    shapes = shapes[:60]
+    cc = None if clip is None else torch.tensor([clip], device=DEV)
+    items, ref = [], []
+    for i, sh in enumerate(shapes):
+        p0 = (torch.randn(*sh, generator=g) * 0.02).to(DEV)
+        grad = (torch.randn(*sh, generator=g) * 0.01).to(DEV)
+        m0 = (torch.randn(*sh, generator=g) * 1e-3).to(DEV)
+        v0 = (torch.rand(*sh, generator=g) * 1e-5).to(DEV)
+        step = 1 + i % 5
+        quant = i % 3 != 2
+
+        def param_copy():
+            if i % 9 != 4:
+                return p0.clone()
+            buf = torch.zeros(p0.numel() + 1, device=DEV)  # misaligned, contiguous: unvectorised
+            buf[1:] = p0.reshape(-1)
+            return buf[1:].view(sh)
+        items.append((param_copy(), grad, m0.clone(), v0.clone(), step, quant))
+        ref.append((param_copy(), grad, m0.clone(), v0.clone(), step, quant))
+    got = T.adamw_requant_multi_(items, 3e-3, (0.9, 0.95), 1e-8, 0.05, clip_coef=cc)
+    exp = [T.adamw_requant_(p, gr, m, v, st, 3e-3, (0.9, 0.95), 1e-8, 0.05, clip_coef=cc, quantize=q)
+           for p, gr, m, v, st, q in ref]
+    torch.cuda.synchronize()
+    for a, b, ra, rb in zip(items, ref, got, exp):
+        for x, y in zip(a[:4], b[:4]):
+            assert torch.equal(x.view(torch.int32), y.view(torch.int32))
+        assert (ra is None) == (rb is None)
+        if ra is not None:
+            assert torch.equal(ra[0], rb[0]) and torch.equal(ra[1].view(torch.int16), rb[1].view(torch.int16))
+
+
 def test_adamw_requant_optimizer_drives_int8linear():
     """AdamWRequant on an Int8Linear: after the step the module's codes are those of the
     updated master, and the next forward uses them without rebuilding them."""
