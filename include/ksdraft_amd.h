@@ -90,6 +90,23 @@ int ksd_requant_transpose(const int8_t *codes, const uint16_t *scales, int64_t R
                           uint16_t *out_scales, void *stream);
 
 /*
+ * ksd_requant_transpose (group 128 in and out) of many tensors in one launch: the weight
+ * transposes W^T = quant(dequant(W)^T) that a training step's dX GEMMs use (reference
+ * ksdraft/kernels/ks3_int8.py:349-351, 403-424), built for every registered master right
+ * after the optimizer step instead of once per layer inside the backward. Results equal n
+ * ksd_requant_transpose calls; the list is read during the call only. No reference
+ * counterpart as one call.
+ */
+typedef struct KsdRequantT {
+  const int8_t *codes;    /* (R, C) int8 */
+  const uint16_t *scales; /* (R, ceil(C/128)) fp16 */
+  int64_t R, C;
+  int8_t *codes_t;        /* (C, R) int8 */
+  uint16_t *scales_t;     /* (C, ceil(R/128)) fp16 */
+} KsdRequantT;
+int ksd_requant_transpose_multi(const KsdRequantT *list, int n, int group, void *stream);
+
+/*
  * Both layouts of one tensor in one pass: the row codes quantize_last_dim(x, group) and
  * the column codes quantize_last_dim(x.t(), group) (t_from_codes = 0: the dY and dY^T
  * operands of the linear backward, reference ksdraft/kernels/ks3_int8.py:410, 418), or

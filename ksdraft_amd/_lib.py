@@ -41,6 +41,7 @@ SIGNATURES = {
     "ksd_ce_backward_quant_dual": [_P, _I64, _I64, _P, _P, _P, _I64, _P, _INT, _P, _P, _P, _P, _P, _P],
     "ksd_adamw_requant": [_P, _P, _P, _P, _I64, _I64, _P, _F, _F, _F, _F, _F, _F, _F, _INT, _P, _P, _P],
     "ksd_adamw_requant_multi": [_P, _INT, _P, _F, _F, _F, _F, _F, _INT, _P],
+    "ksd_requant_transpose_multi": [_P, _INT, _INT, _P],
     "ksd_layernorm_quant": [_P, _INT, _I64, _I64, _I64, _P, _P, _F, _INT, _P, _P, _P, _P, _P, _P],
     "ksd_embedding_gather_int8": [_P, _P, _P, _I64, _I64, _I64, _INT, _P, _INT, _P],
     "ksd_w8a8_gemm_nt": [_P, _P, _P, _P, _I64, _I64, _I64, _INT, _P, _P, _INT, _P],

@@ -146,10 +146,10 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(
 enum { SRC_F32 = 0, SRC_BF16 = 1, SRC_F16 = 2, SRC_I8 = 3 };
 
 template <int SRC, int G>
-__global__ __launch_bounds__(256) void quant_T_kernel(
+__device__ __forceinline__ void quant_T_tile(
     const void *__restrict__ xv, const uint16_t *__restrict__ in_scales, int64_t nsc_in,
     int gin, int64_t R, int64_t C, int64_t nbc, int64_t ngr, int8_t *__restrict__ codes,
-    uint16_t *__restrict__ scales, bool rows_vec) {
+    uint16_t *__restrict__ scales, bool rows_vec, int64_t bid) {
   // LDS column layout: column c at c * PITCH, row r at + r + SKEW(r). For G = 128 the
   // pitch is 145 (17 mod 64 banks) and rows >= 64 are shifted by 16: the transposing
   // writes (a wave covers 4..16 rows of 16..4 column quads) and the group reads (lanes =
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(256) void quant_T_kernel(
   __shared__ float tile[64 * PITCH];
   auto lds_at = [](int c, int r) { return c * PITCH + r + (G == 128 && r >= 64 ? 16 : 0); };
   const int tid = threadIdx.x;
-  const int64_t bc = blockIdx.x % nbc, br = blockIdx.x / nbc;
+  const int64_t bc = bid % nbc, br = bid / nbc;
   const int64_t r0 = br * G, c0 = bc * 64;
 
   // ---- load: EPV elements per 16-byte vector, LPR lanes per 64-column row segment
@@ -248,6 +248,39 @@ __global__ __launch_bounds__(256) void quant_T_kernel(
     for (int j = 0; j < RPT; ++j)
       if (rbase + j < R) dst[j] = (int8_t)(w[j / 4] >> (8 * (j % 4)));
   }
+}
+
+template <int SRC, int G>
+__global__ __launch_bounds__(256) void quant_T_kernel(
+    const void *__restrict__ xv, const uint16_t *__restrict__ in_scales, int64_t nsc_in,
+    int gin, int64_t R, int64_t C, int64_t nbc, int64_t ngr, int8_t *__restrict__ codes,
+    uint16_t *__restrict__ scales, bool rows_vec) {
+  quant_T_tile<SRC, G>(xv, in_scales, nsc_in, gin, R, C, nbc, ngr, codes, scales, rows_vec, blockIdx.x);
+}
+
+// requant_transpose (group 128 in and out) of many int8 tensors in one launch: the weight
+// transposes a training step's backward needs, built once per optimizer step. A batch
+// travels by value in the kernel arguments; a block finds its tensor with scalar compares.
+constexpr int kRqtBatch = 32;
+struct RqtArg {
+  const int8_t *x;
+  const uint16_t *s;
+  int8_t *codes;
+  uint16_t *scales;
+  int64_t R, C, nbc, ngr;
+  int32_t first_block, rv;
+};
+struct RqtBatchArg {
+  RqtArg t[kRqtBatch];
+  int32_t n;
+};
+__global__ __launch_bounds__(256) void requant_T_multi_kernel(const RqtBatchArg b) {
+  int i = 0;
+  for (int k = 1; k < b.n; ++k)
+    if (b.t[k].first_block <= (int)blockIdx.x) i = k;
+  const RqtArg &t = b.t[i];
+  quant_T_tile<SRC_I8, 128>(t.x, t.s, (t.C + 127) / 128, 128, t.R, t.C, t.nbc, t.ngr, t.codes, t.scales,
+                            t.rv != 0, (int64_t)blockIdx.x - t.first_block);
 }
 
 // ----------------------------------------------------------------------------------
@@ -1287,6 +1320,47 @@ extern "C" int ksd_adamw_requant_multi(const KsdAdamTensor *tensors, int n, cons
     a.first_block = (int32_t)blocks;
     a.vec = t.K % 8 == 0 && al(t.param, 16) && al(t.grad, 16) && al(t.exp_avg, 16) &&
             al(t.exp_avg_sq, 16) && (t.codes == nullptr || al(t.codes, 8));
+    blocks += nb;
+  }
+  return flush();
+}
+
+extern "C" int ksd_requant_transpose_multi(const KsdRequantT *list, int n, int group, void *stream) {
+  if (group != 128) return fail(KSD_EINVAL, "requant_transpose_multi: group must be 128, got %d", group);
+  if (n < 0 || (n > 0 && !list)) return fail(KSD_EINVAL, "requant_transpose_multi: bad list");
+  for (int i = 0; i < n; ++i) {
+    const KsdRequantT &t = list[i];
+    if (t.R < 0 || t.C < 0) return fail(KSD_EINVAL, "requant_transpose_multi: entry %d: negative shape", i);
+    if (t.R == 0 || t.C == 0) continue;
+    if (!t.codes || !t.scales || !t.codes_t || !t.scales_t)
+      return fail(KSD_EINVAL, "requant_transpose_multi: entry %d: null pointer", i);
+    if (cdiv(t.C, 64) * cdiv(t.R, 128) > 0x3fffffffLL)
+      return fail(KSD_EINVAL, "requant_transpose_multi: entry %d too large", i);
+  }
+  hipStream_t st = (hipStream_t)stream;
+  RqtBatchArg b;
+  b.n = 0;
+  int64_t blocks = 0;
+  auto flush = [&]() -> int {
+    if (b.n == 0) return KSD_OK;
+    requant_T_multi_kernel<<<(unsigned)blocks, 256, 0, st>>>(b);
+    b.n = 0;
+    blocks = 0;
+    return check_launch("requant_transpose_multi");
+  };
+  for (int i = 0; i < n; ++i) {
+    const KsdRequantT &t = list[i];
+    if (t.R == 0 || t.C == 0) continue;
+    const int64_t nbc = cdiv(t.C, 64), ngr = cdiv(t.R, 128), nb = nbc * ngr;
+    if (b.n == kRqtBatch || blocks + nb > 0x7fffffffLL) {
+      const int rc = flush();
+      if (rc) return rc;
+    }
+    RqtArg &a = b.t[b.n++];
+    a.x = t.codes, a.s = t.scales, a.codes = t.codes_t, a.scales = t.scales_t;
+    a.R = t.R, a.C = t.C, a.nbc = nbc, a.ngr = ngr;
+    a.first_block = (int32_t)blocks;
+    a.rv = ((uintptr_t)t.codes) % 16 == 0 && t.C % 16 == 0;
     blocks += nb;
   }
   return flush();

@@ -291,6 +291,7 @@ class KS3Int8Cell(nn.Module):
         self.register_buffer("tanh_lut", make_tanh_lut(down.device))
         self.trainable = trainable
         self._master_codes_keys = {}  # master name -> (storage, version) its codes came from
+        self._master_t = {}  # master name -> ((codes_t, scales_t), the codes they came from)
         if trainable:
             for name, value in (("down", down), ("up", up),
                                 ("coefficients", coeffs),
@@ -398,6 +399,14 @@ class KS3Int8Cell(nn.Module):
     def _load_from_state_dict(self, *args, **kwargs):
         self.invalidate_codes()
         return super()._load_from_state_dict(*args, **kwargs)
+
+    def current_transpose(self, name: str):
+        """requant_transpose of the down or up codes (a backward GEMM's operand) when the
+        optimizer built it for the codes the cell holds now, else None."""
+        ent = (getattr(self, "_master_t", None) or {}).get(name)
+        if ent is None or ent[1] is not getattr(self, name + "_codes"):
+            return None
+        return ent[0]
 
     def _master_codes_current(self, name: str) -> bool:
         """True when train.AdamWRequant wrote `name`'s codes in the pass that last updated
@@ -517,7 +526,8 @@ class _KS3Int8Train(torch.autograd.Function):
 
         # output-projection backward GEMM (ks3_int8.py:345-352), launched with dup (its
         # operands are ready already; ks3_int8.py:421-424)
-        upT_q, upT_s = requant_transpose(cell.up_codes, cell.up_scales, group, group)
+        upT_q, upT_s = (cell.current_transpose("up")
+                        or requant_transpose(cell.up_codes, cell.up_scales, group, group))
         hT_q, hT_s = requant_transpose(hq, hs, group, group)
         value, dup = w8a8_gemm_pair((gq, gs, upT_q, upT_s, FP16),
                                     (gT_q, gT_s, hT_q, hT_s, torch.float32), group)
@@ -530,7 +540,8 @@ class _KS3Int8Train(torch.autograd.Function):
         dcoeff = v["dcoeff"].reshape(cell.num_subspaces, cell.subspace_rank, 6)
 
         # INT8 backward GEMMs (ks3_int8.py:403-424)
-        downT_q, downT_s = requant_transpose(cell.down_codes, cell.down_scales, group, group)
+        downT_q, downT_s = (cell.current_transpose("down")
+                            or requant_transpose(cell.down_codes, cell.down_scales, group, group))
         dx_dtype = grad_out.dtype if grad_out.dtype in (torch.float32, torch.bfloat16,
                                                         torch.float16) else torch.float32
         xT_q, xT_s = requant_transpose(xq, xs, group, group)

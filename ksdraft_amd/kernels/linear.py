@@ -226,6 +226,15 @@ class Int8Linear(nn.Module):
                 and getattr(self, "_dither", 0.0) <= 0
                 and key == (self.weight.data_ptr(), self.weight._version))
 
+    def current_transpose(self):
+        """(codes_t, scales_t) = requant_transpose(weight_codes, weight_scales), dX's operand,
+        when it was built for the codes the module holds now (by its training forward or by
+        the optimizer that handed the codes over), else None."""
+        wt = getattr(self, "_wt", None)
+        if wt is None or getattr(self, "_wt_src", None) is not self.weight_codes:
+            return None
+        return wt
+
     def _apply(self, fn, *args, **kwargs):
         self.invalidate_codes()  # .to(), .cuda(), .half() ... may replace the master
         return super()._apply(fn, *args, **kwargs)
@@ -265,9 +274,7 @@ class Int8Linear(nn.Module):
             # other float dtypes (float64) go through .float() as the reference's
             # quantize_last_dim(x2.float()) does (linear.py:69); the result is cast back
             xin = x if x.dtype in _OUT_DTYPES else x.float()
-            wt = getattr(self, "_wt", None)
-            if wt is not None and getattr(self, "_wt_src", None) is not self.weight_codes:
-                wt = None  # codes handed over since (optimizer): the backward requantizes
+            wt = self.current_transpose()  # None: the backward requantizes the codes
             y = W8A8LinearFunction.apply(xin, self.weight, self.bias, self.weight_codes,
                                          self.weight_scales, GROUP_SIZE,
                                          residual if fuse_res else None, wt, xpre)

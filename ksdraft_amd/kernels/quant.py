@@ -246,6 +246,35 @@ def requant_transpose(codes: torch.Tensor, scales: torch.Tensor,
     return out_c, out_s
 
 
+def requant_transpose_multi(pairs, group: int = GROUP_SIZE):
+    """requant_transpose(codes, scales, group, group) of every (codes, scales) pair in a few
+    launches (ksd_requant_transpose_multi); returns the (codes_t, scales_t) pairs in order.
+    Built for the weight transposes of a whole model after an optimizer step."""
+    import numpy as np
+    if not pairs:
+        return []
+    if group != GROUP_SIZE:
+        raise ValueError(f"requant_transpose_multi supports group {GROUP_SIZE} only")
+    dev = _lib.require_gpu(*[t for pr in pairs for t in pr])
+    arr = np.zeros(len(pairs), dtype=np.dtype([("codes", "<u8"), ("scales", "<u8"), ("R", "<i8"),
+                                               ("C", "<i8"), ("codes_t", "<u8"), ("scales_t", "<u8")]))
+    out, keep = [], []
+    for i, (codes, scales) in enumerate(pairs):
+        if codes.dim() != 2 or codes.dtype != torch.int8:
+            raise ValueError("requant_transpose_multi expects 2-D int8 codes")
+        codes, scales = codes.contiguous(), scales.contiguous()
+        R, C = codes.shape
+        if scales.shape != (R, -(-C // group)):
+            raise ValueError(f"scales shape {tuple(scales.shape)} does not match codes {R}x{C}")
+        oc = torch.empty((C, R), dtype=torch.int8, device=dev)
+        osc = torch.empty((C, -(-R // group)), dtype=SCALE_DTYPE, device=dev)
+        keep.append((codes, scales))
+        out.append((oc, osc))
+        arr[i] = (codes.data_ptr(), scales.data_ptr(), R, C, oc.data_ptr(), osc.data_ptr())
+    _lib.call("ksd_requant_transpose_multi", arr.ctypes.data, len(pairs), group, _lib.stream_ptr(dev))
+    return out
+
+
 def layer_norm_quantize(x: torch.Tensor, weight: torch.Tensor | None = None,
                         bias: torch.Tensor | None = None, eps: float = 1e-5,
                         group: int = GROUP_SIZE, return_y: bool = False,

@@ -115,10 +115,11 @@ class ShiftedInt8Projections(torch.autograd.Function):
     The int8 operands, GEMM outputs, dX and dW are those of Int8Linear on the shifted
     inputs; dx and the sigmoid gradients are fp32 sums in this kernel's order.
     Inputs: x, sig_q, sig_k, sig_v, then per projection (weight, bias, weight_codes,
-    weight_scales)."""
+    weight_scales), then optionally the three projections' dX operands (codes_t, scales_t)
+    or None each (Int8Linear.current_transpose)."""
 
     @staticmethod
-    def forward(ctx, x, sig_q, sig_k, sig_v, wq, bq, cq, sq, wk, bk, ck, sk, wv, bv, cv, sv):
+    def forward(ctx, x, sig_q, sig_k, sig_v, wq, bq, cq, sq, wk, bk, ck, sk, wv, bv, cv, sv, wts=None):
         from .gemm import w8a8_gemm_out
         B, T, _ = x.shape
         quant = shift_quantize_dual(x, sig_q, sig_k, sig_v)
@@ -131,6 +132,7 @@ class ShiftedInt8Projections(torch.autograd.Function):
         ctx.save_for_backward(x, sig_q, sig_k, sig_v, quant[0][2], quant[0][3], quant[1][2],
                               quant[1][3], quant[2][2], quant[2][3], cq, sq, ck, sk, cv, sv)
         ctx.has_bias = (bq is not None, bk is not None, bv is not None)
+        ctx.wts = wts if wts is not None else (None, None, None)
         return tuple(outs)
 
     @staticmethod
@@ -150,13 +152,14 @@ class ShiftedInt8Projections(torch.autograd.Function):
             g2 = g.reshape(-1, S).float().contiguous()
             want_db = ctx.has_bias[m] and need[5 + 4 * m]
             res = w8a8_linear_backward(g2, None, None, wc, ws, need_dx=True,
-                                       need_dw=need[4 + 4 * m], xt=xt, want_db=want_db)
+                                       need_dw=need[4 + 4 * m], xt=xt, wt=ctx.wts[m],
+                                       want_db=want_db)
             dx_m, dw = res[0], res[1]
             db = res[2] if want_db else None
             dxs.append(dx_m)
             grads.extend([dw, db, None, None])
         dx, dsig = shift_backward(x, *dxs, sig_q, sig_k, sig_v)
-        return (dx if need[0] else None, dsig[0], dsig[1], dsig[2], *grads)
+        return (dx if need[0] else None, dsig[0], dsig[1], dsig[2], *grads, None)
 
 
 def pack_bits(x: torch.Tensor) -> torch.Tensor:

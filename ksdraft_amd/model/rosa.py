@@ -97,7 +97,8 @@ class RosaMixer(nn.Module):
                 p._quantize_weight()
             args += [p.weight, p.bias, p.weight_codes, p.weight_scales]
         sig = [torch.sigmoid(m) for m in mixes]
-        return R.ShiftedInt8Projections.apply(x, *sig, *args)
+        return R.ShiftedInt8Projections.apply(x, *sig, *args,
+                                              tuple(p.current_transpose() for p in projs))
 
     def _fused_projections(self, x: torch.Tensor):
         """Eval with Int8Linear q/k/v: shift + quantize in one pass, then the W8A8 GEMMs

@@ -14,7 +14,7 @@ import torch
 from .. import _lib
 from ..kernels.gemm import w8a8_gemm, w8a8_gemm_out, w8a8_gemm_pair
 from ..kernels.linear import w8a8_linear_forward_train
-from ..kernels.quant import GROUP_SIZE, SCALE_DTYPE, requant_transpose
+from ..kernels.quant import GROUP_SIZE, SCALE_DTYPE, requant_transpose, requant_transpose_multi
 
 IGNORE_INDEX = -100  # torch.nn.functional.cross_entropy's default
 
@@ -116,13 +116,15 @@ class LinearCrossEntropyInt8(torch.autograd.Function):
     GEMMs. Returns fp32 gradients for x (in x's dtype) and the fp32 master weight."""
 
     @staticmethod
-    def forward(ctx, x, weight, wq, ws, targets, ignore_index, group):
+    def forward(ctx, x, weight, wq, ws, targets, ignore_index, group, wt=None):
+        """wt: (codes_t, scales_t) = requant_transpose(wq, ws) when the caller has it."""
         K = x.shape[-1]
         x2 = x.reshape(-1, K)
         y, xtq, xts = w8a8_linear_forward_train(x2, wq, ws, None, group, torch.float32)
         loss, rmax, rinv, n = cross_entropy_stats(y, targets.reshape(-1), ignore_index)
         ctx.save_for_backward(y, rmax, rinv, n, targets.reshape(-1), xtq, xts, wq, ws)
         ctx.ignore_index, ctx.group, ctx.x_shape, ctx.x_dtype = ignore_index, group, x.shape, x.dtype
+        ctx.wt = wt
         return loss
 
     @staticmethod
@@ -134,7 +136,7 @@ class LinearCrossEntropyInt8(torch.autograd.Function):
         dx = dw = None
         out = ctx.x_dtype if ctx.x_dtype in (torch.bfloat16, torch.float16) else torch.float32
         if ctx.needs_input_grad[0]:
-            wtq, wts = requant_transpose(wq, ws, group, group)
+            wtq, wts = ctx.wt if ctx.wt is not None else requant_transpose(wq, ws, group, group)
         if ctx.needs_input_grad[0] and ctx.needs_input_grad[1]:  # one launch for both
             dx, dw = w8a8_gemm_pair((gq, gs, wtq, wts, out), (gtq, gts, xtq, xts, torch.float32),
                                     group)
@@ -143,7 +145,7 @@ class LinearCrossEntropyInt8(torch.autograd.Function):
             dx = w8a8_gemm_out(gq, gs, wtq, wts, group, out_dtype=out).reshape(ctx.x_shape)
         elif ctx.needs_input_grad[1]:
             dw = w8a8_gemm(gtq, gts, xtq, xts, group)
-        return dx, dw, None, None, None, None, None
+        return dx, dw, None, None, None, None, None, None
 
 
 def adamw_requant_(param: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor,
@@ -275,6 +277,9 @@ class AdamWRequant(torch.optim.Optimizer):
     # parameters at least this large take the fused one-pass kernel; smaller ones (norms,
     # biases, gate vectors) are batched into torch's multi-tensor AdamW
     FUSED_MIN_NUMEL = 1 << 16
+    # after the step, the registered masters' transposed codes (dX's operand) for modules in
+    # training mode, built in a few launches rather than one per layer in the backward
+    build_transposes = True
 
     @torch.no_grad()
     def step(self, closure=None, clip_coef: torch.Tensor | None = None):
@@ -315,6 +320,7 @@ class AdamWRequant(torch.optim.Optimizer):
                 regs.append(reg)
             results = adamw_requant_multi_(fused, group["lr"], group["betas"], group["eps"],
                                            group["weight_decay"], clip_coef)
+            tpairs, towners = [], []
             for (p, *_), reg, res in zip(fused, regs, results):
                 if reg is None:
                     continue
@@ -328,6 +334,17 @@ class AdamWRequant(torch.optim.Optimizer):
                     setattr(mod, name + "_codes", res[0])
                     setattr(mod, name + "_scales", res[1])
                     mod._master_codes_keys[name] = key
+                if self.build_transposes and mod.training and res[0].dim() == 2:
+                    tpairs.append(res)
+                    towners.append((mod, name, res[0]))
+            # the dX operands W^T of the next backward, for all masters in a few launches
+            for (mod, name, codes), wt in zip(towners, requant_transpose_multi(tpairs)):
+                if name is None:
+                    mod._wt, mod._wt_src = wt, codes
+                else:
+                    if getattr(mod, "_master_t", None) is None:
+                        mod._master_t = {}
+                    mod._master_t[name] = (wt, codes)
             if fl[0]:
                 if clip_coef is not None:
                     torch._foreach_mul_(fl[1], clip_coef.reshape(()).to(fl[1][0].dtype))

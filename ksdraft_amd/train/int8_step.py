@@ -123,7 +123,7 @@ class Int8DraftTrainer:
         if not head._codes_current():
             head._quantize_weight()
         ce = LinearCrossEntropyInt8.apply(h, head.weight, head.weight_codes, head.weight_scales,
-                                          tgt.reshape(-1), IGNORE_INDEX, 128)
+                                          tgt.reshape(-1), IGNORE_INDEX, 128, head.current_transpose())
         return ce + self.transfer_weight * ts, ce, ts
 
     def backward(self, loss: torch.Tensor):

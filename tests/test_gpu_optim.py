@@ -93,6 +93,59 @@ def test_adamw_requant_multi_equals_one_call_per_master(clip):
             assert torch.equal(ra[0], rb[0]) and torch.equal(ra[1].view(torch.int16), rb[1].view(torch.int16))
 
 
+def test_requant_transpose_multi_equals_one_call_per_tensor():
+    """ksd_requant_transpose_multi over 70 tensors (more than two launch batches; ragged R
+    and C, one-row and one-column tensors, an unaligned view) gives the bits of one
+    ksd_requant_transpose call per tensor."""
+    from ksdraft_amd.kernels.quant import quantize_last_dim, requant_transpose, requant_transpose_multi
+    g = torch.Generator().manual_seed(5)
+    shapes = [(1536, 1536), (200, 130), (1, 384), (384, 1), (129, 257), (64, 96), (300, 1000)] * 10
+    pairs = []
+    for i, sh in enumerate(shapes):
+        x = (torch.randn(*sh, generator=g) * (0.02 + i)).to(DEV)
+        c, s = quantize_last_dim(x)
+        if i % 11 == 3:  # codes at an odd address: the unvectorised loads
+            buf = torch.empty(c.numel() + 1, dtype=torch.int8, device=DEV)
+            buf[1:] = c.reshape(-1)
+            c = buf[1:].view(sh)
+        pairs.append((c, s))
+    got = requant_transpose_multi(pairs)
+    for (c, s), (ct, st) in zip(pairs, got):
+        ec, es = requant_transpose(c, s)
+        assert torch.equal(ct, ec) and torch.equal(st.view(torch.int16), es.view(torch.int16))
+
+
+def test_optimizer_hands_over_current_transposes():
+    """After AdamWRequant.step, every registered Int8Linear in training mode holds the
+    transposed codes of its new codes (dX's operand), equal to requant_transpose of them;
+    an eval-mode module gets none, and a forward that requantizes drops the stale ones."""
+    from ksdraft_amd.kernels.quant import requant_transpose
+    torch.manual_seed(3)
+    mods = [Int8Linear(256, 384).to(DEV), Int8Linear(384, 128, bias=False).to(DEV),
+            Int8Linear(128, 256).to(DEV)]
+    mods[2].eval()
+    opt = T.AdamWRequant([p for m in mods for p in m.parameters()], lr=1e-3)
+    for m in mods:
+        opt.register_int8(m)
+    x = torch.randn(64, 256, device=DEV)
+    y = mods[1](mods[0](x))
+    y.square().mean().backward()
+    mods[2].weight.grad = torch.randn_like(mods[2].weight)
+    opt.step()
+    for m in mods[:2]:
+        wt = m.current_transpose()
+        assert wt is not None
+        ec, es = requant_transpose(m.weight_codes, m.weight_scales)
+        assert torch.equal(wt[0], ec) and torch.equal(wt[1].view(torch.int16), es.view(torch.int16))
+    assert mods[2].current_transpose() is None
+    with torch.no_grad():
+        mods[0].weight.add_(1e-3)  # versioned write: the next forward requantizes
+    mods[0](x)
+    wt = mods[0].current_transpose()
+    ec, es = requant_transpose(mods[0].weight_codes, mods[0].weight_scales)
+    assert wt is None or (torch.equal(wt[0], ec) and torch.equal(wt[1].view(torch.int16), es.view(torch.int16)))
+
+
 def test_adamw_requant_optimizer_drives_int8linear():
     """AdamWRequant on an Int8Linear: after the step the module's codes are those of the
     updated master, and the next forward uses them without rebuilding them."""
