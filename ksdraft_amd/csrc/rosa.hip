@@ -424,7 +424,7 @@ __global__ void __launch_bounds__(256) rosa_pack_kernel(PackSrc ps, int64_t B, i
 }
 
 // ---------------------------------------------------------------- match
-constexpr int kCH = 16;  // candidate words per chunk
+constexpr int kCH = 8;   // candidate words per chunk
 constexpr int kStep = 4;  // match lengths per step of the walk
 
 // 64 q bits ending at t in memory order: bit 63 = q[t], bit 63-i = q[t-i] (0 before 0).
@@ -572,29 +572,37 @@ __device__ int match_one(const uint32_t *qw, const uint32_t *kw_all, int W, int 
   return best_l;
 }
 
-// One block per stream. sign (streams, T) int8 +-1; match_j (streams, T) int32 or NULL.
-__global__ void __launch_bounds__(256) rosa_match_kernel(const uint32_t *__restrict__ qb,
-                                                         const uint32_t *__restrict__ kb,
-                                                         const uint32_t *__restrict__ vb, int T,
-                                                         int W, int lmax, int8_t *__restrict__ sign,
-                                                         int32_t *__restrict__ match_j) {
+// One block per (stream, 256 consecutive positions), a thread per position. The blocks
+// of the latest positions (the most candidates) come first in the grid, so the hardware's
+// in-order dispatch to free slots balances streams of unequal cost (long-run streams walk
+// more lengths) and leaves the cheap early positions for the end. sign (streams, T) int8
+// +-1; match_j (streams, T) int32 or NULL.
+constexpr int kMatchChunk = 256;
+__global__ void __launch_bounds__(kMatchChunk) rosa_match_kernel(const uint32_t *__restrict__ qb,
+                                                                 const uint32_t *__restrict__ kb,
+                                                                 const uint32_t *__restrict__ vb, int T,
+                                                                 int W, int lmax, int nstreams, int nchunks,
+                                                                 int8_t *__restrict__ sign,
+                                                                 int32_t *__restrict__ match_j) {
   extern __shared__ uint32_t sm[];
   uint32_t *qw = sm, *kw = sm + W, *vw = sm + 2 * W;
-  const int64_t s = blockIdx.x;
-  for (int i = threadIdx.x; i < W; i += 256) {
+  const int64_t item = blockIdx.x;
+  const int chunk = nchunks - 1 - (int)(item / nstreams);
+  const int64_t s = item % nstreams;
+  for (int i = threadIdx.x; i < W; i += kMatchChunk) {
     qw[i] = qb[s * W + i];
     kw[i] = kb[s * W + i];
     vw[i] = vb[s * W + i];
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < T; t += 256) {
-    int j = -1, L = 0;
-    if (t >= 1 && lmax >= 1) L = match_one(qw, kw, W, t, lmax, &j);
-    int8_t sg = -1;
-    if (L >= 1) sg = ((vw[(j + 1) >> 5] >> ((j + 1) & 31)) & 1u) ? 1 : -1;
-    sign[s * T + t] = sg;
-    if (match_j) match_j[s * T + t] = L >= 1 ? j : -1;
-  }
+  const int t = chunk * kMatchChunk + threadIdx.x;
+  if (t >= T) return;
+  int j = -1, L = 0;
+  if (t >= 1 && lmax >= 1) L = match_one(qw, kw, W, t, lmax, &j);
+  int8_t sg = -1;
+  if (L >= 1) sg = ((vw[(j + 1) >> 5] >> ((j + 1) & 31)) & 1u) ? 1 : -1;
+  sign[s * T + t] = sg;
+  if (match_j) match_j[s * T + t] = L >= 1 ? j : -1;
 }
 
 // (B, S, T) int8 sign -> (B, T, S) payload[s] * sign in the output dtype, via a 64x64 tile:
@@ -841,8 +849,11 @@ extern "C" int ksd_rosa_match(const uint32_t *q_bits, const uint32_t *k_bits, co
   if (!q_bits || !k_bits || !v_bits || !sign) return fail(KSD_EINVAL, "rosa_match: null pointer");
   if (n_streams > 0x7fffffff) return fail(KSD_EINVAL, "rosa_match: too many streams");
   const int W = (int)cdiv(T, 32);
-  hipLaunchKernelGGL(rosa_match_kernel, dim3((unsigned)n_streams), dim3(256), 3 * W * sizeof(uint32_t),
-                     (hipStream_t)stream, q_bits, k_bits, v_bits, (int)T, W, lmax, sign, match_j);
+  const int nchunks = (int)cdiv(T, kMatchChunk);
+  if (n_streams * nchunks > 0x7fffffffLL) return fail(KSD_EINVAL, "rosa_match: too many streams");
+  hipLaunchKernelGGL(rosa_match_kernel, dim3((unsigned)(n_streams * nchunks)), dim3(kMatchChunk),
+                     3 * W * sizeof(uint32_t), (hipStream_t)stream, q_bits, k_bits, v_bits, (int)T, W,
+                     lmax, (int)n_streams, nchunks, sign, match_j);
   return check_launch("rosa_match");
 }
 
