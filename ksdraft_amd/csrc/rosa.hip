@@ -956,14 +956,16 @@ struct CredAcc {
 };
 
 // A stream's mode word in credits entry 0 (a NaN pattern no credit value takes while the
-// sums are formed): 0x7fa00000 | scan << 14 | mode << 12 | (k + 2048) for mode 0, where
-// scan selects the per-candidate path for the stream's positions (cred_scan_stream).
+// sums are formed): 0x7fa00000 | idle << 15 | scan << 14 | mode << 12 | (k + 2048) for mode 0,
+// where scan selects the per-candidate path for the stream's positions (cred_scan_stream)
+// and idle marks a mode-0 stream whose every g is zero (no position to visit).
 constexpr uint32_t kCredTag = 0x7fa00000u;
-constexpr uint32_t kCredScanBit = 1u << 14;
-__device__ __forceinline__ uint32_t cred_mode_word(int mode, int k, bool scan) {
-  return kCredTag | (scan ? kCredScanBit : 0u) | ((uint32_t)mode << 12) | (uint32_t)((k + 2048) & 0xfff);
+constexpr uint32_t kCredScanBit = 1u << 14, kCredIdleBit = 1u << 15;
+__device__ __forceinline__ uint32_t cred_mode_word(int mode, int k, bool scan, bool idle) {
+  return kCredTag | (idle ? kCredIdleBit : 0u) | (scan ? kCredScanBit : 0u) | ((uint32_t)mode << 12) |
+         (uint32_t)((k + 2048) & 0xfff);
 }
-// decodes the stream's mode; false for mode 2 (nothing to visit)
+// decodes the stream's mode; false when there is nothing to visit (mode 2, or idle)
 __device__ __forceinline__ bool cred_acc_of(const float *cred, unsigned long long *sums, int64_t stream,
                                             int T, CredAcc &ca) {
   const uint32_t w = __hip_atomic_load((const uint32_t *)cred + stream * 3 * T, __ATOMIC_RELAXED,
@@ -973,7 +975,7 @@ __device__ __forceinline__ bool cred_acc_of(const float *cred, unsigned long lon
   ca.fin = mode == 0;
   ca.scan = (w & kCredScanBit) != 0u;
   ca.scale = ldexp(1.0, (int)(w & 0xfffu) - 2048);
-  return mode != 2;
+  return mode != 2 && (w & kCredIdleBit) == 0u;
 }
 // the positions a mode visits: mode 0 every non-zero g, mode 1 the infinite ones
 __device__ __forceinline__ bool cred_live(const CredAcc &ca, float g) {
@@ -1089,7 +1091,8 @@ __global__ void __launch_bounds__(256) rosa_cred_setup_kernel(
   if (threadIdx.x == 0) {
     gp_partial[stream] = ((gps[0] + gps[1]) + gps[2]) + gps[3];
     uint32_t *cw = (uint32_t *)cred;
-    cw[stream * 3 * T] = cred_mode_word(mode, k, cred_scan_stream(len_sum, short_cnt, (int)T));
+    cw[stream * 3 * T] = cred_mode_word(mode, k, cred_scan_stream(len_sum, short_cnt, (int)T),
+                                        mode == 0 && !(mx > 0.0f));
     cw[stream * 3 * T + 1] = ni;
     if (stream < kCredCounters && 3 * T > 3) cw[stream * 3 * T + 3] = 0u;  // a work counter
   }
@@ -1499,8 +1502,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) r
     const int chunk = nchunks - 1 - item / nstreams;
     const int64_t stream = item % nstreams;
     CredAcc ca;
-    if (!cred_acc_of(cred, sums, stream, T, ca)) continue;
+    if (!cred_acc_of(cred, sums, stream, T, ca)) continue;  // nothing to visit in the stream
     const int64_t b = stream / S, s = stream % S;
+    // the chunk's positions: the lanes load their gradients and endpoints together, and only
+    // the positions the stream's mode visits are walked (an item without one loads no words)
+    const float pay = payload[s];
+    const int tl = chunk * kCredChunk + lane;
+    const float grl = lane < kCredChunk && tl < T ? grad[(b * T + tl) * S + s] : 0.0f;
+    uint64_t live = __ballot(lane < kCredChunk && tl < T && cred_live(ca, grl * pay));
+    if (!live) continue;
+    const int mjl = lane < kCredChunk && tl < T ? match_j[stream * T + tl] : -1;
     __builtin_amdgcn_wave_barrier();
     qw[lane] = lane < W ? qb[stream * W + lane] : 0u;
     kw[lane] = lane < W ? kb[stream * W + lane] : 0u;
@@ -1511,13 +1522,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) r
     // this lane's k words: word w and the two below it (zeros before position 0)
     const uint32_t k0 = kw[lane], k1 = lane >= 1 ? kw[lane - 1] : 0u, k2 = lane >= 2 ? kw[lane - 2] : 0u;
     const uint64_t k01 = ((uint64_t)k0 << 32) | k1, k12 = ((uint64_t)k1 << 32) | k2;
-    const float pay = payload[s];
-    // the chunk's positions: the lanes load their gradients and endpoints together, and only the positions
-    // the stream's mode visits are walked
-    const int tl = chunk * kCredChunk + lane;
-    const float grl = lane < kCredChunk && tl < T ? grad[(b * T + tl) * S + s] : 0.0f;
-    const int mjl = lane < kCredChunk && tl < T ? match_j[stream * T + tl] : -1;
-    uint64_t live = __ballot(lane < kCredChunk && tl < T && cred_live(ca, grl * pay));
     while (live) {  // wave-uniform
     const int li = __builtin_ctzll(live);
     live &= live - 1;
