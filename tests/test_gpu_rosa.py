@@ -398,14 +398,15 @@ def _dense_entry(q, k, v, g, s, which, p, base):
         return float(((sp[0] - base[s]).astype(np.float64) * g[s].astype(np.float64)).sum())
 
 
-@pytest.mark.parametrize("T", [300, 2100])
-def test_credits_nonfinite_gradient_follows_the_dense_sum(T):
+@pytest.mark.parametrize("T,path", [(300, "bits"), (300, "scan"), (2100, "auto")])
+def test_credits_nonfinite_gradient_follows_the_dense_sum(T, path, monkeypatch):
     """Streams whose gradient holds inf or NaN: the reference sums delta * g over every t
     (rosa_credit_gpu.py:48), so 0 * inf and NaN make an entry NaN unless every infinite
     position flips it, which then holds +-inf (NaN if the infinite terms have both signs).
-    T = 300 against the definition on every entry, T = 2100 (the candidate-per-lane kernel)
-    on sampled entries and on every entry the infinite positions flip. The finite streams of
-    the call stay exact."""
+    T = 300 against the definition on every entry (on both paths of the balanced kernel),
+    T = 2100 (the candidate-per-lane kernel) on sampled entries and on every entry the
+    infinite positions flip. The finite streams of the call stay exact."""
+    _set_path(monkeypatch, path)
     rng = np.random.default_rng(77 + T)
     n = 7
     q = _streams(rng, n, T)
