@@ -1522,24 +1522,37 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) r
     // this lane's k words: word w and the two below it (zeros before position 0)
     const uint32_t k0 = kw[lane], k1 = lane >= 1 ? kw[lane - 1] : 0u, k2 = lane >= 2 ? kw[lane - 2] : 0u;
     const uint64_t k01 = ((uint64_t)k0 << 32) | k1, k12 = ((uint64_t)k1 << 32) | k2;
+    // every position's prologue at once, lane l for position chunk * kCredChunk + l: its q
+    // window, the best key from the endpoint, the current sign and g in fixed point
+    uint64_t qwl = 0;
+    uint32_t bestl = 0u;
+    int cstarl = 0;
+    long long gil = 0;
+    if (lane < kCredChunk && tl < T) {
+      qwl = q_window(qw, tl);
+      if (mjl >= 0) {
+        cstarl = clz64(qwl ^ q_window(kw, mjl));
+        bestl = mkkey(min(cstarl, min(mjl + 1, lmax)), mjl);
+      }
+      gil = ca.fixed(grl * pay);
+    }
+    const float sgnl = sign_of(bestl, vw);
     while (live) {  // wave-uniform
     const int li = __builtin_ctzll(live);
     live &= live - 1;
     const int t = chunk * kCredChunk + li;
+    if (t == 0 || lmax < 1) continue;
     const float gr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, grl), li));
     const int jstar = __builtin_amdgcn_readlane(mjl, li);
-    const uint64_t qwin = q_window(qw, t);
-    uint32_t best = 0u;
-    int cstar = 0, capstar = 0;
-    if (jstar >= 0) {
-      cstar = clz64(qwin ^ q_window(kw, jstar));
-      capstar = min(jstar + 1, lmax);
-      best = mkkey(min(cstar, capstar), jstar);
-    }
-    const float sgn = sign_of(best, vw);
+    const uint64_t qwin = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(qwl >> 32), li) << 32) |
+                          (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)qwl, li);
+    const uint32_t best = (uint32_t)__builtin_amdgcn_readlane((int)bestl, li);
+    const int cstar = __builtin_amdgcn_readlane(cstarl, li);
+    const int capstar = jstar >= 0 ? min(jstar + 1, lmax) : 0;
+    const float sgn = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sgnl), li));
     const float g = gr * pay;
-    if (t == 0 || lmax < 1) continue;
-    const long long gi = ca.fixed(g);
+    const long long gi = (long long)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(gil >> 32), li) << 32) |
+                                     (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)gil, li));
     if (force == 2 || (force == 0 && (ca.scan || t < kScanBelow))) {  // wave-uniform
       // the per-candidate path, its tables in the event table's first kCredWave32 words
       scan_position(lane, t, T, lmax, qwin, best, jstar, cstar, capstar, sgn, g, gi, ca, kw, vw,
