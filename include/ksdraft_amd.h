@@ -375,6 +375,28 @@ int ksd_ks3_spine_fused(const float *acc, int64_t M, int64_t F, const int8_t *sp
                         int8_t *h_codes, uint16_t *h_scales, float *table, void *stream);
 
 /*
+ * K8 — project_fused / _fused_gemm_spine, 'int8' mode, group 128, as one GEMM launch
+ * (reference ksdraft/kernels/ks3_triton.py:100-156 and 159-195): the input-projection
+ * GEMM xq . down_codes^T whose epilogue applies the spine, ReLU^2 and the per-group
+ * requantization of ksd_ks3_spine_fused to each finished fp32 accumulator tile, so the
+ * (M, F) accumulator never reaches memory. The accumulator is the ordered sum over all K
+ * groups (K is never split). A small kernel fills the table workspace first.
+ *   a, a_scales     (M, K) int8 codes, 16-byte aligned; (M, K/128) fp16 scales
+ *   w, w_scales     (F, K) int8 down-projection codes, 16-byte aligned; (F, K/128) fp16
+ *   K               a multiple of 128, > 0
+ *   spine/warp buffers and tanh_lut as for ksd_ks3_spine_fwd
+ *   group           128 (groups 32 and 64: ksd_w8a8_gemm_nt, then ksd_ks3_spine_fused)
+ *   h_codes (M, F) int8, h_scales (M, ceil(F/128)) fp16
+ *   table           workspace, (F, 256) fp32, 16-byte aligned, overwritten
+ */
+int ksd_ks3_project_fused(const int8_t *a, const uint16_t *a_scales, const int8_t *w,
+                          const uint16_t *w_scales, int64_t M, int64_t F, int64_t K,
+                          const int8_t *spine_codes, const uint16_t *spine_scale,
+                          const uint16_t *warp_scale, const uint16_t *warp_shift,
+                          const int8_t *tanh_lut, int group, int8_t *h_codes, uint16_t *h_scales,
+                          float *table, void *stream);
+
+/*
  * K6/K8, the 'fp32' and 'fp16' nonlinear modes — _spine_features (reference
  * ksdraft/kernels/ks3_int8.py:172-203, rank 1) followed by quantize_last_dim(h), or the
  * same stage of project_fused for NL = 0 / 1 (ksdraft/kernels/ks3_triton.py:76-98, 137-156).

@@ -54,6 +54,8 @@ SIGNATURES = {
     "ksd_ks3_spine_fwd": [_P, _I64, _I64, _P, _P, _P, _P, _P, _INT, _P, _P, _P, _P, _P],
     "ksd_ks3_spine_fwd_noalloc": [_P, _I64, _I64, _P, _P, _P, _P, _P, _INT, _P, _P, _P, _P],
     "ksd_ks3_spine_fused": [_P, _I64, _I64, _P, _P, _P, _P, _P, _INT, _P, _P, _P, _P],
+    "ksd_ks3_project_fused": [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _INT, _P, _P, _P,
+                              _P],
     "ksd_ks3_spine_float": [_P, _INT, _I64, _I64, _P, _P, _P, _P, _INT, _INT, _P, _P, _P, _P],
     "ksd_ks3_vjp_row_blocks": [_I64, _P],
     "ksd_ks3_vjp": [_P, _P, _I64, _I64, _P, _P, _P, _P, _INT,

@@ -35,6 +35,7 @@ namespace ksd {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
@@ -419,7 +420,14 @@ struct G128Prob {
   const void *R;
   int64_t part_stride;
   int M, N, K, tiles_n, ntiles, splits, out;
+  // kOutSpine launches only: the per-chart increment table (N x 256 fp32) and the h
+  // scales (M x tiles_n fp16); Y holds the h codes (M x N int8)
+  const float *tab;
+  uint16_t *hs;
 };
+// OUT of a launch whose epilogue is the KS3 spine, ReLU^2 and requantization (group 128)
+// instead of a store of the accumulator.
+constexpr int kOutSpine = 16;
 // Work split of a paired launch over its grid (logical workgroup c, XCD-ordered): c takes
 // q0 + (c < r0) consecutive units of problem 0 (the one with the longer units), then a run
 // of problem 1's units, kA of them for c < r0 and kB for the others, so every workgroup
@@ -433,6 +441,21 @@ __device__ __forceinline__ int pair_start1(int c, const G128Sched &sc, int n1) {
   return (int)(s < n1 ? s : n1);
 }
 
+// One stage of a max-butterfly over the 32 lanes of each half-wave: lanes with bit O of
+// their index set keep values [O, 2O), the others [0, O), each maxed with the partner's
+// copy (lane ^ O); after the stages O = 16 .. 1, lane l holds in r[0] the maximum over the
+// half-wave of value index l.
+template <int O>
+__device__ __forceinline__ void bfly_max(uint32_t (&r)[32], int l32) {
+  const bool up = (l32 & O) != 0;
+#pragma unroll
+  for (int k = 0; k < O; ++k) {
+    const uint32_t send = up ? r[k] : r[k + O];
+    const uint32_t keep = up ? r[k + O] : r[k];
+    r[k] = max(keep, (uint32_t)__shfl_xor((int)send, O));
+  }
+}
+
 // PAIR = false: one GEMM (p0; p1 is not read), output type OUT. PAIR = true: two
 // independent GEMMs p0 and p1 in one persistent launch (no bias, no residual), each unit
 // stored in its problem's runtime output type (OUT is ignored).
@@ -442,6 +465,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(const G128Prob P
   __shared__ __attribute__((aligned(16))) int8_t sA[NSLOT][BM * BK];
   __shared__ __attribute__((aligned(16))) int8_t sW[NSLOT][BN * BK];
   __shared__ __attribute__((aligned(16))) uint32_t sS[NSLOT][256];
+  // spine epilogue: [0, 512) per-wave row maxima (4 column waves x 128 rows), then per row
+  // [512, 640) the ReLU^2 pre-scale or the h scale, [640, 768) its reciprocal
+  __shared__ __attribute__((aligned(16))) uint32_t sRed[OUT == kOutSpine ? 768 : 4];
   constexpr int DEPTH = NSLOT - 1;
   constexpr int NW = 5;  // DMA instructions per wave and step: 4 x 1 KB codes + 1 scale
 
@@ -620,8 +646,130 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(const G128Prob P
       }
     }
   };
+  // The KS3 spine of the fused projection (ks3_triton.py:137-156, 'int8' mode) on the
+  // finished tile: per element x = clamp(acc, +-65504), the chart's increment at the LUT
+  // index of x / 4 (table gathered from global memory, L2-resident), h = x + inc; per row
+  // the ReLU^2 pre-scale of max |h| over the tile's 128 charts (one GS128 group), codes
+  // q = clamp(rint(h / pre), 0, 127), features (q * q) * (pre * pre); then the features'
+  // own GS128 scale and int8 codes. The arithmetic is ks3_spine_fused_kernel's, element
+  // for element. Row maxima: a butterfly over the 32 lanes of each half-wave leaves lane
+  // l the maximum of its value index l (one row of the wave), the 4 column waves meet in
+  // LDS, and 128 threads turn each row's maximum into its scale and reciprocal.
+  auto spine_store = [&](int v) __attribute__((always_inline)) {
+    if constexpr (OUT == kOutSpine) {
+      const int t = gunit(v);  // one unit per tile (no K split)
+      const int m0 = __builtin_amdgcn_readfirstlane((t / P0.tiles_n) * BM);
+      const int n0 = __builtin_amdgcn_readfirstlane((t % P0.tiles_n) * BN);
+      // N through an empty asm: the store offsets below are then formed here, at the unit
+      // end, instead of being hoisted out of the K loop into 32 live registers
+      int N = P0.N;
+      asm volatile("" : "+s"(N));
+      N = __builtin_amdgcn_readfirstlane(N);
+      const int M = P0.M, tn = P0.tiles_n;
+      const int cl = wn * 32 + l32;  // this lane's chart within the tile
+      const bool cok = n0 + cl < N;
+      const int ncol = min(N - n0, BN);
+      const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)(P0.tab + (int64_t)n0 * 256), 0, ncol * 1024, kBufFlags);
+      float h[32];
+#pragma unroll
+      for (int k = 0; k < 32; ++k) {
+        const float a = k < 16 ? acc0[k] : acc1[k - 16];
+        const float xc = fminf(fmaxf(a, -kScaleMax), kScaleMax);  // a NaN becomes -65504
+        const int idx = min(max(lut_index_f32(xc * 0.25f) + 128, 0), 255);
+        const float inc = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(trs, cok ? (uint32_t)(cl * 1024 + idx * 4) : kOob, 0, 0));
+        h[k] = cok ? xc + inc : 0.0f;
+      }
+      // value index k of a lane: row wm*64 + (k >> 4)*32 + ((k & 15) >> 2)*8 + half*4 + (k & 3)
+      const int krow = wm * 64 + (l32 >> 4) * 32 + ((l32 & 15) >> 2) * 8 + half * 4 + (l32 & 3);
+      // per row of the tile: max over its 128 charts of the u32 patterns r (magnitudes, NaN
+      // above inf), into sRed[512 + row] as the group scale and sRed[640 + row] as its
+      // reciprocal; then the lane's 32 rows read back
+      auto row_scales = [&](uint32_t (&r)[32], float (&sc)[32], float (&rc)[32]) __attribute__((always_inline)) {
+        bfly_max<16>(r, l32);
+        bfly_max<8>(r, l32);
+        bfly_max<4>(r, l32);
+        bfly_max<2>(r, l32);
+        bfly_max<1>(r, l32);
+        sRed[wn * 128 + krow] = r[0];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        fenced_barrier();
+        if (tid < 128) {
+          const uint32_t m = max(max(sRed[tid], sRed[128 + tid]), max(sRed[256 + tid], sRed[384 + tid]));
+          const float s = group_scale(__builtin_bit_cast(float, m));
+          sRed[512 + tid] = __builtin_bit_cast(uint32_t, s);
+          sRed[640 + tid] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_rcpf(s));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        fenced_barrier();
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int row = wm * 64 + i * 32 + q * 8 + half * 4;
+            // float vectors, read element by element (a __builtin_bit_cast of a vector
+            // element reads element 0 whatever the index: hipcc 7.2, gfx950)
+            const v4f s4 = *(const v4f *)&sRed[512 + row];
+            const v4f r4 = *(const v4f *)&sRed[640 + row];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              sc[i * 16 + q * 4 + j] = s4[j];
+              rc[i * 16 + q * 4 + j] = r4[j];
+            }
+          }
+      };
+      uint32_t r[32];
+      float sc[32], rc[32];
+#pragma unroll
+      for (int k = 0; k < 32; ++k) r[k] = __builtin_bit_cast(uint32_t, fabsf(h[k]));
+      row_scales(r, sc, rc);
+      // ReLU^2 codes and features (the pre-scale pre = sc)
+      float tq[32];
+#pragma unroll
+      for (int k = 0; k < 32; ++k) {
+        const float p = h[k] * rc[k];
+        tq[k] = rintf(p);
+        if (fabsf(fabsf(p - tq[k]) - 0.5f) < 0x1p-14f) tq[k] = rintf(h[k] / sc[k]);
+      }
+#pragma unroll
+      for (int k = 0; k < 32; ++k) {
+        const float q = __builtin_amdgcn_fmed3f(tq[k], 0.0f, 127.0f);  // NaN q: NaN via pre
+        h[k] = (q * q) * (sc[k] * sc[k]);
+        r[k] = __builtin_bit_cast(uint32_t, fabsf(h[k]));
+      }
+      row_scales(r, sc, rc);
+      // the features' codes (codes_rcp_packed, one value per row): rint(f / s) in [-127, 127]
+      // through the reciprocal, the division near a half-integer, 0 for a NaN scale
+      constexpr float kMagic = 12582912.0f;
+      uint32_t code[32];
+#pragma unroll
+      for (int k = 0; k < 32; ++k) {
+        const float c = __builtin_amdgcn_fmed3f(h[k] * rc[k], -127.0f, 127.0f);
+        const float m = c + kMagic;
+        code[k] = __builtin_bit_cast(uint32_t, m);
+        if (fabsf(fabsf(c - (m - kMagic)) - 0.5f) < 0x1p-14f) code[k] = (uint8_t)code_of(h[k] / sc[k]);
+      }
+      // masked global stores: a buffer descriptor here would be held in VGPRs (the kernel's
+      // SGPRs are full) and each store wrapped in a loop over its distinct values
+      const int rows = max(0, min(BM, M - m0));
+      int8_t *const qb = (int8_t *)P0.Y + (int64_t)m0 * N + n0 + cl;
+#pragma unroll
+      for (int k = 0; k < 32; ++k) {
+        const int row = wm * 64 + (k >> 4) * 32 + ((k & 15) >> 2) * 8 + half * 4 + (k & 3);
+        const uint32_t c = sc[k] != sc[k] ? 0u : code[k] & 0xffu;
+        if (cok && row < rows) qb[(int64_t)row * N] = (int8_t)c;
+      }
+      if (tid < rows) {  // waves 0 and 1: row m0 + tid's scale of this group
+        const float s = __builtin_bit_cast(float, sRed[512 + tid]);
+        P0.hs[(int64_t)(m0 + tid) * tn + n0 / BN] = scale_bits(s);
+      }
+    }
+  };
   auto store_tile = [&](int v) __attribute__((always_inline)) {
-    if constexpr (!PAIR) {
+    if constexpr (OUT == kOutSpine) {
+      spine_store(v);
+    } else if constexpr (!PAIR) {
       store_impl(std::integral_constant<int, OUT>{}, v);
     } else {  // the unit's runtime output type (paired launches: fp32, bf16 or fp16)
       const int ot = G128F(v, out);
@@ -1020,6 +1168,39 @@ extern "C" int ksd_w8a8_gemm_pair(const int8_t *a0, const uint16_t *a0_scales, c
                                dt[i], workspace, workspace_bytes, stream);
   }
   return launch_pair(a, as, w, ws, M, N, K, y, dt, workspace, workspace_bytes, st);
+}
+
+extern "C" int ksd_ks3_project_fused(const int8_t *a, const uint16_t *a_scales, const int8_t *w,
+                                     const uint16_t *w_scales, int64_t M, int64_t F, int64_t K,
+                                     const int8_t *spine_codes, const uint16_t *spine_scale,
+                                     const uint16_t *warp_scale, const uint16_t *warp_shift,
+                                     const int8_t *tanh_lut, int group, int8_t *h_codes,
+                                     uint16_t *h_scales, float *table, void *stream) {
+  if (group != 128)
+    return fail(KSD_EINVAL, "ks3_project_fused: group 128 only (groups 32 and 64: w8a8_gemm_nt, "
+                "then ks3_spine_fused)");
+  int rc = gemm_checks(a, w, M, F, K, group);
+  if (rc != KSD_OK) return rc;
+  if (!a_scales || !w_scales || !spine_codes || !spine_scale || !warp_scale || !warp_shift || !tanh_lut)
+    return fail(KSD_EINVAL, "ks3_project_fused: null input pointer");
+  if (!h_codes || !h_scales) return fail(KSD_EINVAL, "ks3_project_fused: null output pointer");
+  if (!table || ((uintptr_t)table & 15) != 0)
+    return fail(KSD_EINVAL, "ks3_project_fused: table workspace must be a 16-byte aligned buffer");
+  if (((uintptr_t)tanh_lut & 3) != 0) return fail(KSD_EINVAL, "ks3_project_fused: tanh_lut must be 4-byte aligned");
+  // code stores address a tile's 128 rows from one base with 32-bit offsets
+  if (F > (1LL << 31) / BM) return fail(KSD_EINVAL, "ks3_project_fused: F too large");
+  if (M == 0 || F == 0) return KSD_OK;
+  if (K == 0) return fail(KSD_EINVAL, "ks3_project_fused: K = 0 (the host wrapper handles it)");
+  hipStream_t st = (hipStream_t)stream;
+  rc = ks3_fused_table(spine_codes, spine_scale, warp_scale, warp_shift, tanh_lut, F, table, st);
+  if (rc != KSD_OK) return rc;
+  const int tn = (int)((F + BN - 1) / BN), tm = (int)((M + BM - 1) / BM);
+  const int grid = min(tm * tn, cu_count());
+  const g128::G128Sched none{0, 0, 0, 0};
+  const g128::G128Prob p{a, a_scales, w, w_scales, nullptr, h_codes, nullptr, 0, (int)M, (int)F, (int)K,
+                         tn, tm * tn, 1, g128::kOutSpine, table, h_scales};
+  g128::gemm_g128_kernel<g128::kOutSpine, false><<<dim3(grid), dim3(NTHREADS), 0, st>>>(p, p, none);
+  return check_launch("ks3_project_fused");
 }
 
 extern "C" int ksd_w8a8_group_partials(const int8_t *a, const int8_t *w, int64_t M, int64_t N,

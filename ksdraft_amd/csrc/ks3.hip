@@ -26,8 +26,6 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
-constexpr float kLutScale = (float)(127.0 / 3.2);   // _lut_index, ks3_int8.py:71
-constexpr float kLutDomain = 3.2f;                  // TANH_DOMAIN, ks3_int8.py:46
 // The warp step tq * (4/127). Composed (ks3_int8.py:211): a torch fp16 tensor times a
 // Python float is evaluated in fp32 with the constant in fp32. Fused (ks3_triton.py:59):
 // Triton keeps a Python-float scalar out of type promotion (triton/language/semantic.py,
@@ -152,10 +150,6 @@ __device__ __forceinline__ int lut_index_x(float x) {
   constexpr float kDom16 = 3.19921875f;  // fp16(3.2)
   const float c = __builtin_amdgcn_fmed3f(x * 0.25f, -kDom16, kDom16);
   return (int)rintf(f16_round(c * kLutScale));
-}
-// _lut_index_f32 of the fused kernel (ks3_triton.py:56): fp32 throughout.
-__device__ __forceinline__ int lut_index_f32(float v) {
-  return (int)rintf(__builtin_amdgcn_fmed3f(v, -kLutDomain, kLutDomain) * kLutScale);
 }
 
 // rint(h / pre) clamped to [0, 127] for the rank-1 ReLU^2 codes (ks3_int8.py:232): the
@@ -1256,6 +1250,16 @@ __global__ __launch_bounds__(256) void handoff_fixup_kernel(const float *__restr
 }  // namespace ksd
 
 using namespace ksd;
+
+// The fused contract's per-chart increment table (F x 256 fp32), for the fused projection
+// GEMM in gemm.hip.
+int ksd::ks3_fused_table(const int8_t *spine_codes, const uint16_t *spine_scale,
+                         const uint16_t *warp_scale, const uint16_t *warp_shift, const int8_t *tanh_lut,
+                         int64_t F, float *table, hipStream_t st) {
+  hipLaunchKernelGGL(ks3_spine_table_kernel<true>, dim3((unsigned)F), dim3(256), 0, st, spine_codes,
+                     spine_scale, warp_scale, warp_shift, tanh_lut, (void *)table);
+  return check_launch("ks3_project_fused (table)");
+}
 
 static int spine_checks(const char *who, const void *in, int64_t M, int64_t F, const int8_t *spine_codes,
                         const uint16_t *spine_scale, const uint16_t *warp_scale,

@@ -54,9 +54,22 @@ static inline int cu_count() {
   return n;
 }
 
+// ks3.hip: launches the fused contract's per-chart increment table kernel (F x 256 fp32).
+int ks3_fused_table(const int8_t *spine_codes, const uint16_t *spine_scale, const uint16_t *warp_scale,
+                    const uint16_t *warp_shift, const int8_t *tanh_lut, int64_t F, float *table,
+                    hipStream_t st);
+
 // ---------------------------------------------------------------- device numerics
 constexpr float kScaleMin = 5.9604644775390625e-08f;  // 2**-24, quant.py:22
 constexpr float kScaleMax = 65504.0f;                 // quant.py:23
+
+// The KS3 tanh LUT's index domain (shared by the spine kernels and the fused projection GEMM).
+constexpr float kLutScale = (float)(127.0 / 3.2);   // _lut_index, ks3_int8.py:71
+constexpr float kLutDomain = 3.2f;                  // TANH_DOMAIN, ks3_int8.py:46
+// _lut_index_f32 of the fused kernel (ks3_triton.py:56): fp32 throughout.
+__device__ __forceinline__ int lut_index_f32(float v) {
+  return (int)rintf(__builtin_amdgcn_fmed3f(v, -kLutDomain, kLutDomain) * kLutScale);
+}
 
 // Materialise v as an fp32 register value. Without this the backend may fuse the op
 // that produced v with the narrowing to fp16 (e.g. fma + cvt -> v_fma_mixlo_f16), which

@@ -137,6 +137,39 @@ def test_spine_fused_contract_bit_exact(M, Fn, group):
     assert _bits_eq(hq.cpu().numpy(), eq) and _bits_eq(hs.cpu().numpy(), es)
 
 
+@pytest.mark.parametrize("M,K,Fn", [(64, 128, 256), (200, 384, 130), (1, 256, 5),
+                                     (333, 1536, 1000), (130, 2048, 300), (1000, 512, 640)])
+def test_project_fused_one_launch_bit_exact(M, K, Fn):
+    """project_fused 'int8', group 128, one_launch: the GEMM whose epilogue runs the spine
+    and both requantizations (one launch after the table) against the oracle chain, the ordered
+    sum over all K groups then the fused contract. Covers ragged M and F (partial tiles,
+    charts past F), a K that the standalone GEMM would split (2048 with 6 tiles), and
+    accumulators beyond the fp16 range (rows with large scales, clamped)."""
+    cell = _random_cell(5 * M + Fn, Fn)
+    rng = np.random.default_rng(M + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[::7] *= 3e5  # large rows: accumulators past +-65504
+    w = (rng.standard_normal((Fn, K)) * 0.05).astype(np.float32)
+    xq, xs = oq.quantize_last_dim(x)
+    wq, ws = oq.quantize_last_dim(w)
+    lut = ok.make_tanh_lut()
+    acc = og.gemm_ordered(xq, xs, wq, ws)
+    assert (np.abs(acc) > 65504).any()
+    eq, es = ok.spine_fused_int8(acc, cell["spine_codes"], cell["spine_scale"], cell["sc"],
+                                 cell["sh"], lut, 128)
+    hq, hs = project_fused(_g(xq), _g(xs), _g(wq), _g(ws), _g(cell["spine_codes"]),
+                           _g(cell["spine_scale"]), _f16(cell["sc"]), _f16(cell["sh"]), _g(lut),
+                           128, "int8", one_launch=True)
+    assert _bits_eq(hq.cpu().numpy(), eq) and _bits_eq(hs.cpu().numpy(), es)
+    # the two-launch default: the same outputs wherever the standalone GEMM does not
+    # split K (its split parts are summed in order, the one launch never splits)
+    hq2, hs2 = project_fused(_g(xq), _g(xs), _g(wq), _g(ws), _g(cell["spine_codes"]),
+                             _g(cell["spine_scale"]), _f16(cell["sc"]), _f16(cell["sh"]), _g(lut),
+                             128, "int8")
+    if K < 2048:
+        assert torch.equal(hq, hq2) and torch.equal(hs, hs2)
+
+
 # ---------------------------------------------------------------- VJP
 def _check_vjp(out, value, coords, coef, sc, sh, raw_scale, raw_shift, group):
     dc, sums, dcoeff, dscale, dshift = ok.vjp(value, coords, coef, sc, sh, raw_scale, raw_shift)
