@@ -748,7 +748,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(const G128Prob P
         const float c = __builtin_amdgcn_fmed3f(h[k] * rc[k], -127.0f, 127.0f);
         const float m = c + kMagic;
         code[k] = __builtin_bit_cast(uint32_t, m);
-        if (fabsf(fabsf(c - (m - kMagic)) - 0.5f) < 0x1p-14f) code[k] = (uint8_t)code_of(h[k] / sc[k]);
+        if (half_dist(c) < 0x1p-14f) code[k] = (uint8_t)code_of(h[k] / sc[k]);
       }
       // masked global stores: a buffer descriptor here would be held in VGPRs (the kernel's
       // SGPRs are full) and each store wrapped in a loop over its distinct values

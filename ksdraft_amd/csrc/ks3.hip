@@ -822,7 +822,7 @@ __global__ void __launch_bounds__(256) ks3_vjp_kernel(
             f[e][c] = (float)dc[i + e][c];
             const float q = __builtin_amdgcn_fmed3f(f[e][c] * r, -127.0f, 127.0f);
             const float mq = q + 12582912.0f;
-            near = fminf(near, fabsf(fabsf(q - (mq - 12582912.0f)) - 0.5f));
+            near = fminf(near, half_dist(q));
             mg[e][c] = __builtin_bit_cast(uint32_t, mq);
             if (s[e] != s[e]) mg[e][c] = 0;  // NaN group: zero codes
           }

@@ -192,6 +192,13 @@ __device__ __forceinline__ int8_t code_of(float v) {
   return v != v ? (int8_t)0 : (int8_t)(int)r;
 }
 
+// Distance from v to the nearest half-integer, |fract(v) - 0.5| (v_fract_f32: v - floor(v),
+// exact for finite v; exact subtraction wherever the result is below 0.25). Equal to
+// ||v - rint(v)| - 0.5|; a NaN v gives NaN, which fminf then ignores.
+__device__ __forceinline__ float half_dist(float v) {
+  return fabsf(__builtin_amdgcn_fractf(v) - 0.5f);
+}
+
 // code_of(x[j] / s) for NV values of one group, s being that group's scale from the
 // NaN-propagating amax over values that include these x (so s is NaN exactly when one of
 // them is, and then every code is 0, as x / NaN is). Otherwise s lies in [2^-24, 65504]
@@ -257,7 +264,7 @@ __device__ __forceinline__ void codes_rcp_packed(const float *x, float s, uint32
     for (int j = c0; j < c0 + CH; ++j) {
       const float c = __builtin_amdgcn_fmed3f(x[j] * r, -127.0f, 127.0f);
       const float m = c + kMagic;
-      near = fminf(near, fabsf(fabsf(c - (m - kMagic)) - 0.5f));
+      near = fminf(near, half_dist(c));
       f[j] = __builtin_bit_cast(uint32_t, m);
     }
     if (near < 0x1p-14f) {
