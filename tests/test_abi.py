@@ -87,6 +87,24 @@ def test_ks3_validation_paths_without_gpu():
     assert b"row blocks" in buf.value
     assert lib.ksd_ks3_vjp_finalize(None, 1, 8, None, None, None, None, None, None, None) == 1
     assert lib.ksd_ks3_tanh16(None, 4, None, None) == 1
+    # the one-launch projection: group 128 only, aligned operands, a table, K > 0
+    a = ctypes.c_void_p(256)
+    assert lib.ksd_ks3_project_fused(a, p, a, p, 64, 256, 128, p, p, p, p, q, 32,
+                                     p, p, a, None) == 1
+    lib.ksd_last_error(buf, 256)
+    assert b"group 128" in buf.value
+    assert lib.ksd_ks3_project_fused(a, p, a, p, 64, 256, 128, p, p, p, p, q, 128,
+                                     p, p, None, None) == 1
+    lib.ksd_last_error(buf, 256)
+    assert b"table" in buf.value
+    assert lib.ksd_ks3_project_fused(a, p, a, p, 64, 256, 0, p, p, p, p, q, 128,
+                                     p, p, a, None) == 1
+    lib.ksd_last_error(buf, 256)
+    assert b"K = 0" in buf.value
+    assert lib.ksd_ks3_project_fused(ctypes.c_void_p(8), p, a, p, 64, 256, 128, p, p, p, p, q,
+                                     128, p, p, a, None) == 1  # A not 16-byte aligned
+    assert lib.ksd_ks3_project_fused(a, p, a, p, 0, 256, 128, p, p, p, p, q, 128,
+                                     p, p, a, None) == 0  # empty: nothing to launch
 
 
 def test_single_hip_runtime_in_process():
