@@ -240,8 +240,10 @@ def ks3_kernel_times(dev, reps):
     F = 5888 charts): average launch time and HBM rate against the algorithmic bytes.
     Synthetic inputs: coordinates ~N(0, 0.8) (x ~N(0,1) through down ~N(0,0.02)),
     value ~N(0, 1e-2), reference inits for the cell (coefficients ~N(0,0.05), raw_scale
-    0.75, raw_shift 0; model/ks3.py:85-88)."""
+    0.75, raw_shift 0; model/ks3.py:85-88). GEMM entries (the down GEMM, and project_fused
+    with the spine in one launch or two) report TOPS against the down GEMM's 2·M·F·d."""
     from ksdraft_amd.kernels import ks3_int8 as K
+    from ksdraft_amd.kernels.ks3_triton import project_fused
     Mk, d, Fc, G = 8192, 1536, 5888, 128
     g = torch.Generator().manual_seed(0)
     coeffs = (torch.randn(Fc, 6, generator=g) * 0.05).to(dev)
@@ -268,6 +270,12 @@ def ks3_kernel_times(dev, reps):
         "ks3_vjp": (lambda: K.ks3_vjp(value16, coords16, sq, ss, sc16, sh16, raw_scale,
                                       raw_shift, G),
                     2 * MF + 2 * MF + MF + MF + 2 * 2 * MF // G + 2 * 8 * Fc * 4 * (Mk // 512)),
+        # project_fused 'int8': the down GEMM with the spine and requantization in its
+        # epilogue (one launch after the table), and the default two-launch form
+        "ks3_project_fused_one_launch": (lambda: project_fused(xq, xs, dq, ds, sq, ss, sc16, sh16, lut,
+                                                               G, "int8", one_launch=True), None),
+        "ks3_project_fused_two_launches": (lambda: project_fused(xq, xs, dq, ds, sq, ss, sc16, sh16,
+                                                                 lut, G, "int8"), None),
     }
     res = {}
     for name, (fn, nbytes) in stages.items():

@@ -12,7 +12,7 @@ arithmetic contract, not the composed one.
   each finished fp32 accumulator tile and stores only the h codes and scales, so the
   (M, F) fp32 accumulator never reaches memory (193 MB at M 8192, F 5888). Its
   accumulator is the unsplit ordered sum over all K groups. It is slower than the two
-  launches (about 300 against 230 us at that shape on MI355X): the per-chart table
+  launches (about 270-300 against 235 us at that shape on MI355X): the per-chart table
   (128 KB per 128-chart tile) cannot be staged in LDS beside the GEMM's 132 KB operand
   ring, so the epilogue gathers it from L2, and the spine's VALU work runs between the
   MFMA steps instead of beside them.
