@@ -257,6 +257,39 @@ def test_config4_ks3_cell_full_shape():
     assert _eq(_np(cell.master_up.grad[drows]), ok.h(edup))
 
 
+def test_config4_project_fused_one_launch_full_shape():
+    """project_fused 'int8' at config 4 (M = 8192, d = 1536, F = 5888): the one-launch
+    kernel (spine in the GEMM's epilogue) equals the two-launch form everywhere (K = 1536
+    is never split), and both equal the oracle chain (ordered GEMM, then the fused
+    contract) on sampled rows."""
+    from ksdraft_amd.kernels.ks3_triton import project_fused
+    M, d, Fn = 8192, 1536, 5888
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(M, d, generator=g)
+    down = torch.randn(Fn, d, generator=g) * 0.02
+    up = torch.randn(d, Fn, generator=g) * 0.02
+    coeffs = torch.randn(Fn, 6, generator=g) * 0.05
+    raw_scale = 0.75 + torch.randn(Fn, generator=g) * 0.3
+    raw_shift = torch.randn(Fn, generator=g) * 0.5
+    cell = K.KS3Int8Cell(_Cell(down, up, coeffs, raw_scale, raw_shift).to(DEV)).eval()
+    xq, xs = kq.quantize_last_dim(x.to(DEV))
+    sc16, sh16 = cell._warp_scalars(torch.float16)
+    args = (xq, xs, cell.down_codes, cell.down_scales, cell.spine_codes, cell.spine_scale,
+            sc16, sh16, cell.tanh_lut, 128, "int8")
+    hq1, hs1 = project_fused(*args, one_launch=True)
+    hq2, hs2 = project_fused(*args)
+    assert torch.equal(hq1, hq2) and torch.equal(hs1, hs2)
+    p = ok.pack_masters(down.numpy(), up.numpy(), coeffs.numpy(), raw_scale.numpy(),
+                        raw_shift.numpy())
+    sc, sh = ok.warp_scalars(p["warp_scale_codes"], p["warp_scale_scales"],
+                             p["warp_shift_codes"], p["warp_shift_scales"])
+    rows = _rows(M, 48, 9)
+    acc = og.gemm_ordered(_np(xq[rows]), _np(xs[rows]), p["down_codes"], p["down_scales"])
+    eq, es = ok.spine_fused_int8(acc, p["spine_codes"], p["spine_scale"], sc, sh,
+                                 ok.make_tanh_lut(), 128)
+    assert _eq(_np(hq1[rows]), eq) and _eq(_np(hs1[rows]), es)
+
+
 def test_config4_rosa_step_full_shape():
     """The Rosa mixer step at B 4 x T 2048, d = 1536, 512 streams: the fused shift +
     quantize on sampled tokens, the hard match on sampled streams (pair brute force) and
