@@ -275,7 +275,7 @@ def ks3_kernel_times(dev, reps):
         "ks3_project_fused_one_launch": (lambda: project_fused(xq, xs, dq, ds, sq, ss, sc16, sh16, lut,
                                                                G, "int8", one_launch=True), None),
         "ks3_project_fused_two_launches": (lambda: project_fused(xq, xs, dq, ds, sq, ss, sc16, sh16,
-                                                                 lut, G, "int8"), None),
+                                                                 lut, G, "int8", one_launch=False), None),
     }
     res = {}
     for name, (fn, nbytes) in stages.items():

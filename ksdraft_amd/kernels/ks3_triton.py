@@ -4,18 +4,21 @@ The reference's Triton kernel fuses the down-projection GEMM, the Horner spine, 
 the per-group requantization (ks3_triton.py:100-156), following the fused kernel's own
 arithmetic contract, not the composed one.
 
-* 'int8' (NL == 2): ksd_w8a8_gemm_nt (fp32 accumulator out), then ksd_ks3_spine_fused
-  (fp32 coordinates and LUT index, no truncation, group pre-scale, second
-  requantization), a per-chart increment table staged in LDS per 128-chart segment.
-* 'int8' with group 128 and ``one_launch=True``: the reference's single-kernel form,
-  ksd_ks3_project_fused, a GEMM whose epilogue runs the same per-element arithmetic on
-  each finished fp32 accumulator tile and stores only the h codes and scales, so the
-  (M, F) fp32 accumulator never reaches memory (193 MB at M 8192, F 5888). Its
-  accumulator is the unsplit ordered sum over all K groups. It is slower than the two
-  launches (about 270-300 against 235 us at that shape on MI355X): the per-chart table
-  (128 KB per 128-chart tile) cannot be staged in LDS beside the GEMM's 132 KB operand
-  ring, so the epilogue gathers it from L2, and the spine's VALU work runs between the
-  MFMA steps instead of beside them.
+* 'int8' (NL == 2) with group 128, up to ONE_LAUNCH_MAX_ROWS rows (the eval path's
+  decode and short-prefill shapes): the reference's single-kernel form,
+  ksd_ks3_project_fused, a GEMM whose epilogue runs the fused contract (fp32 coordinates
+  and LUT index, no truncation, group pre-scale, second requantization) on each finished
+  fp32 accumulator tile and stores only the h codes and scales, after a small kernel has
+  tabulated the per-chart increments. Its accumulator is the unsplit ordered sum over all
+  K groups, so it is taken only where the standalone GEMM would not split K either: the
+  outputs are then identical to the two-launch form's. At d 1536, F 5888 on MI355X it
+  takes about 29 us against 49-53 us for M <= 256 and 53 against 58 us at M = 1024.
+* 'int8' otherwise: ksd_w8a8_gemm_nt (fp32 accumulator out), then ksd_ks3_spine_fused,
+  the same per-element arithmetic with the per-chart table staged in LDS per 128-chart
+  segment. At M >= 2048 this is the faster form (223 against 254 us at M 8192): in one
+  launch the table (128 KB per 128-chart tile) cannot sit in LDS beside the GEMM's
+  132 KB operand ring, so the epilogue gathers it from L2, and the spine's VALU work runs
+  between the MFMA steps instead of beside them. ``one_launch`` forces either form.
 * 'fp16' and 'fp32' (NL == 1, 0; ks3_triton.py:76-98): ksd_ks3_spine_float on the
   accumulator (the coordinates not rounded to fp16, the warp scalars in fp16), every
   fp16/fp32 op of the Triton source rounded separately.
@@ -26,7 +29,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from .gemm import _prepare, w8a8_gemm
+from .gemm import _prepare, gemm_splits, w8a8_gemm
 from .ks3_int8 import spine_float, spine_fused_int8
 
 FP16 = torch.float16
@@ -39,18 +42,20 @@ def project_fused(
     spine_codes: torch.Tensor, spine_scale: torch.Tensor,
     warp_scale: torch.Tensor, warp_shift: torch.Tensor,
     tanh_lut: torch.Tensor,
-    group: int, nonlinear: str, *, one_launch: bool = False,
+    group: int, nonlinear: str, *, one_launch: bool | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Input projection + Horner spine + requant (ks3_triton.py:159-195).
 
-    warp_scale/warp_shift: dequantized fp16 per-chart scalars. one_launch: 'int8' with
-    group 128 as one GEMM launch (no fp32 accumulator in memory; slower, see above).
-    Returns (h_codes int8 (M, N), h_scales fp16 (M, ceil(N/group)))."""
+    warp_scale/warp_shift: dequantized fp16 per-chart scalars. one_launch: None picks the
+    form by shape (see above); True forces the single launch ('int8', group 128 only),
+    False the two launches. Returns (h_codes int8 (M, N), h_scales fp16 (M, ceil(N/group)))."""
     if group & (group - 1):
         raise ValueError("group must be a power of two (32 or 128)")
     nl = {"fp32": 0, "fp16": 1, "int8": 2}[nonlinear]
     if one_launch and (nl != 2 or group != 128):
         raise ValueError("one_launch: 'int8' with group 128 only")
+    if one_launch is None:
+        one_launch = nl == 2 and group == 128 and _one_launch_pays(a_codes, w_codes)
     if one_launch:
         out = _project_fused_int8(a_codes, a_scales, w_codes, w_scales, spine_codes, spine_scale,
                                   warp_scale.to(FP16), warp_shift.to(FP16), tanh_lut)
@@ -63,6 +68,23 @@ def project_fused(
     _, hq, hs = spine_float(acc, spine_codes, spine_scale, warp_scale.to(FP16).float(),
                             warp_shift.to(FP16).float(), nonlinear, group)
     return hq, hs
+
+
+# Largest M for which project_fused takes the single launch by default (measured on MI355X
+# at d 1536, F 5888: 29 against 49-53 us up to M 256, 53 against 58 us at M 1024, 75
+# against 69 us at M 2048).
+ONE_LAUNCH_MAX_ROWS = 1024
+
+
+def _one_launch_pays(a_codes: torch.Tensor, w_codes: torch.Tensor) -> bool:
+    """Few rows, and a GEMM shape the standalone launch would not split along K (so both
+    forms compute the same ordered accumulator)."""
+    if a_codes.dim() != 2 or w_codes.dim() != 2:
+        return False
+    M, K = a_codes.shape
+    N = w_codes.shape[0]
+    K128 = -(-K // 128) * 128
+    return 0 < M <= ONE_LAUNCH_MAX_ROWS and N > 0 and K128 > 0 and gemm_splits(M, N, K128) == 1
 
 
 def _project_fused_int8(a_codes, a_scales, w_codes, w_scales, spine_codes, spine_scale,

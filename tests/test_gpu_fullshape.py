@@ -277,7 +277,7 @@ def test_config4_project_fused_one_launch_full_shape():
     args = (xq, xs, cell.down_codes, cell.down_scales, cell.spine_codes, cell.spine_scale,
             sc16, sh16, cell.tanh_lut, 128, "int8")
     hq1, hs1 = project_fused(*args, one_launch=True)
-    hq2, hs2 = project_fused(*args)
+    hq2, hs2 = project_fused(*args, one_launch=False)
     assert torch.equal(hq1, hq2) and torch.equal(hs1, hs2)
     p = ok.pack_masters(down.numpy(), up.numpy(), coeffs.numpy(), raw_scale.numpy(),
                         raw_shift.numpy())

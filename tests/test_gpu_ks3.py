@@ -161,13 +161,17 @@ def test_project_fused_one_launch_bit_exact(M, K, Fn):
                            _g(cell["spine_scale"]), _f16(cell["sc"]), _f16(cell["sh"]), _g(lut),
                            128, "int8", one_launch=True)
     assert _bits_eq(hq.cpu().numpy(), eq) and _bits_eq(hs.cpu().numpy(), es)
-    # the two-launch default: the same outputs wherever the standalone GEMM does not
-    # split K (its split parts are summed in order, the one launch never splits)
-    hq2, hs2 = project_fused(_g(xq), _g(xs), _g(wq), _g(ws), _g(cell["spine_codes"]),
-                             _g(cell["spine_scale"]), _f16(cell["sc"]), _f16(cell["sh"]), _g(lut),
-                             128, "int8")
+    # the two-launch form: the same outputs wherever the standalone GEMM does not split
+    # K (its split parts are summed in order, the one launch never splits)
+    args = (_g(xq), _g(xs), _g(wq), _g(ws), _g(cell["spine_codes"]), _g(cell["spine_scale"]),
+            _f16(cell["sc"]), _f16(cell["sh"]), _g(lut), 128, "int8")
+    hq2, hs2 = project_fused(*args, one_launch=False)
     if K < 2048:
         assert torch.equal(hq, hq2) and torch.equal(hs, hs2)
+    # the default picks one of the two by shape, with the same outputs as the form it picks
+    hq3, hs3 = project_fused(*args)
+    pick = (hq, hs) if M <= 1024 and K < 2048 else (hq2, hs2)
+    assert torch.equal(hq3, pick[0]) and torch.equal(hs3, pick[1])
 
 
 # ---------------------------------------------------------------- VJP
