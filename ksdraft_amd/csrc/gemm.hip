@@ -752,10 +752,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(const G128Prob P
       }
       // masked global stores: a buffer descriptor here would be held in VGPRs (the kernel's
       // SGPRs are full) and each store wrapped in a loop over its distinct values. The
-      // step waits after a unit end count 32 stores into their vmcnt bound: a lane issues
-      // 32 code stores (waves 0 and 1 one scale store more), and the table gathers above
-      // have already returned (their values were used), so the bound still proves each
-      // step's DMA done.
+      // table gathers above have returned before these stores issue (their values were
+      // used), so every DMA issued before them is complete; the waits of the steps after
+      // the unit end therefore hold whatever number of stores a wave issues here (masked
+      // rows and charts may skip some).
       const int rows = max(0, min(BM, M - m0));
       int8_t *const qb = (int8_t *)P0.Y + (int64_t)m0 * N + n0 + cl;
 #pragma unroll
