@@ -1165,36 +1165,49 @@ __device__ __forceinline__ void scan_position(int lane, int t, int T, int lmax, 
   // candidates from the latest down, 64 per step (lane l: j = j0 + l): a bucket's best key is
   // its latest j, so the bucket tables are written only when a key beats the stored one.
   // The step template flags: TOP, the first step (lanes j >= t idle, events above t - 1
-  // absent), LOW, the step at j0 = 0 (caps min(j + 1, lmax) below lmax). A lane's window
-  // words sit at a fixed offset from j0 / 32 and its funnel shift (j + 1) mod 32 is fixed.
-  const uint32_t *kwl = kw + ((lane + 1) >> 5);
+  // absent), LOW, the step at j0 = 0 (caps min(j + 1, lmax) below lmax), NEAR: 0 for a step
+  // with no candidate in the near range, 1 for one that may have some, 2 to decide at run
+  // time. A lane's window words sit at a fixed offset from j0 / 32 and its funnel shift
+  // (j + 1) mod 32 is fixed.
+  // the lane's window words kw[j0 / 32 + (lane + 1) / 32 - 2 ..], addressed from one LDS
+  // address per step (kept opaque, so every step adds one offset to it)
+  uint32_t kaddr = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint32_t *)(kw + ((lane + 1) >> 5) - 2);
+  asm volatile("" : "+v"(kaddr));
   const int sh = (lane + 1) & 31;
-  auto cand_step = [&](int j0, auto top_c, auto low_c) __attribute__((always_inline)) {
+  auto cand_step = [&](int j0, auto top_c, auto low_c, auto near_c) __attribute__((always_inline)) {
     constexpr bool TOP = decltype(top_c)::value, LOW = decltype(low_c)::value;
-    const int j = j0 + lane;
-    const bool near_step = j0 + 63 > near0 && j0 < near0 + 126;  // wave-uniform
-    if (!TOP || j < t) {
-      const uint32_t *kp = kwl + (j0 >> 5);  // words j0 / 32 + (lane + 1) / 32 - 2 ..
-      const uint32_t wa = kp[-2], wb = kp[-1], wc = kp[0];
+    constexpr int NEAR = decltype(near_c)::value;
+    const int jp1 = (j0 + 1) + lane;  // j + 1, the key's low half
+    if (!TOP || jp1 <= t) {
+      typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+      const uint32_t ka = kaddr + (uint32_t)(j0 >> 5) * 4u;
+      const uint32_t wa = *(lds_u32 *)(uintptr_t)ka, wb = *(lds_u32 *)(uintptr_t)(ka + 4u),
+                     wc = *(lds_u32 *)(uintptr_t)(ka + 8u);
       const uint64_t kwin = ((uint64_t)__builtin_amdgcn_alignbit(wc, wb, sh) << 32) |
                             __builtin_amdgcn_alignbit(wb, wa, sh);
       const uint64_t x = qwin ^ kwin;
       const int c = clz64(x);
-      const int cap = LOW ? min(j + 1, lmax) : lmax;  // j >= 64 > lmax - 1 above the last step
-      const uint32_t key = mkkey(min(c, cap), j);
+      const int cap = LOW ? min(jp1, lmax) : lmax;  // j >= 64 > lmax - 1 above the last step
+      const uint32_t key = ((uint32_t)min(c, cap) << 16) | (uint32_t)jp1;
       if (key > Mw[c]) atomicMax(Mw + c, key);
+      const bool near_step = NEAR == 2 ? (j0 + 63 > near0 && j0 < near0 + 126) : NEAR == 1;
       if (near_step) {
-        if ((unsigned)(j - near0 - 1) > 124u) farbest = max(farbest, key);
+        if ((unsigned)(jp1 - near0 - 2) > 124u) farbest = max(farbest, key);
       } else {
         farbest = max(farbest, key);
       }
-      uint32_t nkey = key;  // after flipping the q bit at j's first mismatch
-      if (c < cap) {
-        // c + 1 + e: the common suffix once the first mismatch (x's top set bit) is gone
-        nkey = mkkey(min(clz64(x ^ (0x8000000000000000ull >> c)), cap), j);
-        // (a) flipping k[j - c] extends j past the best
-        const int p = j - c;
-        if (nkey > best && !(p >= trunc_lo && p <= trunc_hi)) atomicMax(Rk + (p & 127), nkey);
+      // the key after flipping the q bit at j's first mismatch (x's top set bit): the
+      // common suffix c + 1 + e once that mismatch is gone. With c >= cap the flipped bit
+      // lies past the cap and nkey == key; with c = 64 (x = 0, shift taken mod 64) nkey has
+      // length 0: it then only reaches Nw[64], which no flip reads.
+      const uint64_t xb = x ^ (0x8000000000000000ull >> (c & 63));
+      const uint32_t nkey = ((uint32_t)min(clz64(xb), cap) << 16) | (uint32_t)jp1;
+      // (a) flipping k[j - c] extends j past the best (never for c >= cap: nkey == key)
+      if (__builtin_expect(nkey > best, 0)) {
+        int p = jp1 - c;
+        asm volatile("" : "+v"(p));
+        p -= 1;
+        if (!(p >= trunc_lo && p <= trunc_hi)) atomicMax(Rk + (p & 127), nkey);
       }
       if (nkey > Nw[c]) atomicMax(Nw + c, nkey);
     }
@@ -1207,18 +1220,32 @@ __device__ __forceinline__ void scan_position(int lane, int t, int T, int lmax, 
         if (v) {
           *slot = 0u;
           const float s2 = sign_of(v, vw);
-          if (s2 != sgn) ca.add(T + p, s2 > 0.0f, g, gi);
+          // p through an empty asm: the credit address is formed here, not carried as a
+          // pointer through every step
+          int pe = T + p;
+          asm volatile("" : "+v"(pe));
+          if (s2 != sgn) ca.add(pe, s2 > 0.0f, g, gi);
         }
       }
     }
   };
+  using F_ = std::false_type;
+  using T_ = std::true_type;
+  using N0 = std::integral_constant<int, 0>;
+  using N1 = std::integral_constant<int, 1>;
+  using N2 = std::integral_constant<int, 2>;
   const int jtop = ((t - 1) / 64) * 64;
   if (jtop == 0) {
-    cand_step(0, std::true_type{}, std::true_type{});
+    cand_step(0, T_{}, T_{}, N2{});
   } else {
-    cand_step(jtop, std::true_type{}, std::false_type{});
-    for (int j0 = jtop - 64; j0 >= 64; j0 -= 64) cand_step(j0, std::false_type{}, std::false_type{});
-    cand_step(0, std::false_type{}, std::true_type{});
+    cand_step(jtop, T_{}, F_{}, N2{});
+    // the middle steps in three runs: above the near range, the (at most three) steps that
+    // may reach it, and below it
+    int j0 = jtop - 64;
+    for (; j0 >= 64 && j0 >= near0 + 126; j0 -= 64) cand_step(j0, F_{}, F_{}, N0{});
+    for (; j0 >= 64 && j0 + 63 > near0; j0 -= 64) cand_step(j0, F_{}, F_{}, N1{});
+    for (; j0 >= 64; j0 -= 64) cand_step(j0, F_{}, F_{}, N0{});
+    cand_step(0, F_{}, T_{}, N2{});
   }
   // (farbest stays per lane: near_flips_tables takes the wave maximum of its own terms)
 
