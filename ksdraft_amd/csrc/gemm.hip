@@ -400,6 +400,8 @@ template <int OUT> __device__ __forceinline__ uint32_t out_bits(float v) {
 // Cache policy of the output tile stores: nt (non-temporal, the gfx940+ meaning of the slc
 // bit), so the streamed output does not evict the operand panels that other workgroups
 // still read from L2 (config 3's forward: 1.92 -> 1.75 ms; config 2's step 0.154 -> 0.148 ms).
+// K-part partials of a split launch keep the default policy: the combine kernel reads them
+// right after (nt stores made config 5's combines 20% slower).
 constexpr int kStoreNT = 2;
 constexpr int kSeedBits = 0x4B400000;
 constexpr float kSeedF = 12582912.0f;
@@ -642,8 +644,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_g128_kernel(const G128Prob P
         y1 = y1 + r1v[e];
       }
       if constexpr (OT == KSD_F32) {
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y0), r0s, vo, 0, kStoreNT);
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y1), r1s, vo, 0, kStoreNT);
+        if (sp > 1) {  // K-part partials: the combine kernel reads them next, from L2
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y0), r0s, vo, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y1), r1s, vo, 0, 0);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y0), r0s, vo, 0, kStoreNT);
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y1), r1s, vo, 0, kStoreNT);
+        }
       } else {
         __builtin_amdgcn_raw_buffer_store_b16((uint16_t)out_bits<OT>(y0), r0s, vo, 0, kStoreNT);
         __builtin_amdgcn_raw_buffer_store_b16((uint16_t)out_bits<OT>(y1), r1s, vo, 0, kStoreNT);
