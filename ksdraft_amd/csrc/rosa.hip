@@ -899,6 +899,19 @@ namespace ksd {
 
 
 __device__ __forceinline__ int clz64(uint64_t x) { return x ? __clzll((long long)x) : 64; }
+// v_ffbh_u32: leading zeros of a word, ~0 for zero
+__device__ __forceinline__ uint32_t ffbh32(uint32_t a) {
+  uint32_t r;
+  asm("v_ffbh_u32 %0, %1" : "=v"(r) : "v"(a));
+  return r;
+}
+// min(a, b, 64) as one v_min3_u32 (kept whole: the compiler would otherwise move the 64
+// out of the two branches that compute a lifted length)
+__device__ __forceinline__ uint32_t min3_64(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_min3_u32 %0, %1, %2, 64" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 __device__ __forceinline__ int getbit(const uint32_t *w, int pos) { return (w[pos >> 5] >> (pos & 31)) & 1; }
 
 // key = (length << 16) | (j + 1); length 0 reads as "no match" for the sign.
@@ -1186,7 +1199,11 @@ __device__ __forceinline__ void scan_position(int lane, int t, int T, int lmax, 
       const uint64_t kwin = ((uint64_t)__builtin_amdgcn_alignbit(wc, wb, sh) << 32) |
                             __builtin_amdgcn_alignbit(wb, wa, sh);
       const uint64_t x = qwin ^ kwin;
-      const int c = clz64(x);
+      // c = clz64(x) from the two words: v_ffbh gives ~0 for a zero word, so the low word's
+      // count + 32 saturates and the min with 64 covers x = 0
+      const uint32_t xh = (uint32_t)(x >> 32);
+      const uint32_t lo32 = __builtin_elementwise_add_sat(ffbh32((uint32_t)x), 32u);
+      const int c = (int)min(min(ffbh32(xh), lo32), 64u);
       const int cap = LOW ? min(jp1, lmax) : lmax;  // j >= 64 > lmax - 1 above the last step
       const uint32_t key = ((uint32_t)min(c, cap) << 16) | (uint32_t)jp1;
       if (key > Mw[c]) atomicMax(Mw + c, key);
@@ -1200,8 +1217,17 @@ __device__ __forceinline__ void scan_position(int lane, int t, int T, int lmax, 
       // common suffix c + 1 + e once that mismatch is gone. With c >= cap the flipped bit
       // lies past the cap and nkey == key; with c = 64 (x = 0, shift taken mod 64) nkey has
       // length 0: it then only reaches Nw[64], which no flip reads.
-      const uint64_t xb = x ^ (0x8000000000000000ull >> (c & 63));
-      const uint32_t nkey = ((uint32_t)min(clz64(xb), cap) << 16) | (uint32_t)jp1;
+      // When every lane's first mismatch lies in the window's high word (the common case),
+      // the flip leaves the low word as it is, and its leading-zero count is shared with c's.
+      int nlen;
+      if (__all(c < 32)) {
+        nlen = (int)min3_64(ffbh32(xh ^ (0x80000000u >> c)), lo32);
+      } else {
+        const uint64_t xb = x ^ (0x8000000000000000ull >> (c & 63));
+        nlen = (int)min3_64(ffbh32((uint32_t)(xb >> 32)),
+                            __builtin_elementwise_add_sat(ffbh32((uint32_t)xb), 32u));
+      }
+      const uint32_t nkey = ((uint32_t)min(nlen, cap) << 16) | (uint32_t)jp1;
       // (a) flipping k[j - c] extends j past the best (never for c >= cap: nkey == key)
       if (__builtin_expect(nkey > best, 0)) {
         int p = jp1 - c;
